@@ -1,0 +1,381 @@
+"""GPU parity: every tile op through the C ABI vs the CPU oracle (MI355X only).
+
+Inputs are seeded; the HIP result and the oracle see identical bytes.  Full
+BASELINE sizes are checked on deterministic row / head subsets (the oracle on
+the full causal-attention problem would take minutes) plus size-independent
+properties; small and ragged shapes are checked in full.  Tolerances:
+tests/tolerances.py.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import tilers_hip as th
+from oracle import oracle as orc
+from tests.tolerances import (assert_attn_close, assert_gemm_close, assert_softmax_close,
+                              assert_within_ulp16)
+
+pytestmark = pytest.mark.gpu
+
+D = th.TileDtype
+ORC = {D.F32: orc.F32, D.F16: orc.F16, D.BF16: orc.BF16}
+
+
+def upload(dev, stream, arr: np.ndarray, dtype: th.TileDtype) -> th.HipBuffer:
+    buf = dev.alloc(arr.size, dtype)
+    buf.copy_from_host(np.ascontiguousarray(arr).reshape(-1), stream)
+    return buf
+
+
+def rand16(rng, n, dtype, scale=1.0, kind="normal"):
+    x = rng.standard_normal(n) if kind == "normal" else rng.uniform(-1, 1, n)
+    return orc.narrow((x * scale).astype(np.float32), ORC[dtype])
+
+
+def device_random(dev, stream, n, dtype, dist, p0, p1, seed):
+    buf = dev.alloc(n, dtype)
+    th.fill_random(buf, n, dtype, dist, p0, p1, seed, stream)
+    return buf
+
+
+# ---- device / runtime -------------------------------------------------------------
+
+def test_device_properties(dev):
+    assert dev.arch().startswith("gfx950")
+    assert dev.cu_count() > 0
+    mi = dev.mem_info()
+    assert mi.total > 100 * 2 ** 30 and 0 < mi.free <= mi.total
+    print(f"device {dev.name()} {dev.arch()} cus={dev.cu_count()} mem={mi.total / 2**30:.0f} GiB")
+
+
+def test_buffer_round_trip(dev, stream):
+    x = np.arange(1000, dtype=np.float32)
+    b = dev.alloc_from_slice(x, stream)
+    assert len(b) == 1000
+    assert np.array_equal(b.copy_to_host(stream), x)
+
+
+def test_fill_random_moments(dev, stream):
+    n = 1 << 20
+    b = device_random(dev, stream, n, D.F32, "normal", 0.0, 2.0, 0x71130001)
+    x = b.copy_to_host(stream)
+    assert abs(x.mean()) < 0.01 and abs(x.std() - 2.0) < 0.01
+    u = device_random(dev, stream, n, D.BF16, "uniform", -1.0, 1.0, 0x71130002).copy_to_host(stream)
+    uf = orc.widen(u, orc.BF16)
+    assert uf.min() >= -1.0 and uf.max() <= 1.0 and abs(uf.mean()) < 0.01
+    again = device_random(dev, stream, n, D.F32, "normal", 0.0, 2.0, 0x71130001).copy_to_host(stream)
+    assert np.array_equal(again, x)  # counter-based: same seed, same bytes
+
+
+def test_errors_are_hal_errors(dev, stream):
+    with pytest.raises(th.HalError) as e:
+        th.attention_prefill(1, 1, 1, 1, 1, 8, 0, 4, 128, 4, 4, D.BF16, stream)
+    assert e.value.kind == "KernelError" and "max_seq" in str(e.value)
+    with pytest.raises(th.HalError) as e:
+        th.attention_decode(1, 1, 1, 1, 1, 8, 8, 128, 6, 4, D.BF16, stream=stream)
+    assert e.value.kind == "KernelError"
+
+
+# ---- softmax ------------------------------------------------------------------------
+
+def test_softmax_golden_vectors(dev, stream, golden):
+    g = golden("softmax_f32.npz")
+    x = g["x"]
+    xb = upload(dev, stream, x, D.F32)
+    yb = dev.alloc(x.size, D.F32)
+    th.softmax(xb, yb, *x.shape, D.F32, stream)
+    y = yb.copy_to_host(stream).reshape(x.shape)
+    assert_softmax_close(y, g["y"], "softmax golden")
+
+
+def test_softmax_config1_full(dev, stream):
+    """8192 x 1024 f32, X ~ N(0, 2.0), full tensor, rel 1e-5."""
+    rows, cols = 8192, 1024
+    xb = device_random(dev, stream, rows * cols, D.F32, "normal", 0.0, 2.0, 0x71130000 + 1)
+    yb = dev.alloc(rows * cols, D.F32)
+    th.softmax(xb, yb, rows, cols, D.F32, stream)
+    x = xb.copy_to_host(stream).reshape(rows, cols)
+    y = yb.copy_to_host(stream).reshape(rows, cols)
+    ref = orc.softmax(x, rows, cols)
+    assert_softmax_close(y, ref, "softmax config1")
+    assert np.allclose(y.astype(np.float64).sum(axis=1), 1.0, atol=1e-5)
+
+
+@pytest.mark.parametrize("rows,cols", [(3, 1000), (5, 77), (7, 1), (2, 5000), (33, 4096),
+                                       (4, 256), (1, 64), (9, 17000)])
+def test_softmax_f32_shapes(dev, stream, rows, cols):
+    rng = np.random.default_rng(rows * 131 + cols)
+    x = (rng.standard_normal((rows, cols)) * 2).astype(np.float32)
+    xb = upload(dev, stream, x, D.F32)
+    yb = dev.alloc(x.size, D.F32)
+    th.softmax(xb, yb, rows, cols, D.F32, stream)
+    assert_softmax_close(yb.copy_to_host(stream).reshape(rows, cols), orc.softmax(x, rows, cols),
+                         f"softmax {rows}x{cols}")
+
+
+@pytest.mark.parametrize("dtype", [D.F16, D.BF16])
+@pytest.mark.parametrize("rows,cols", [(64, 2048), (3, 100), (4, 8192)])
+def test_softmax_u16(dev, stream, dtype, rows, cols):
+    rng = np.random.default_rng(cols)
+    x = rand16(rng, rows * cols, dtype, 2.0)
+    xb = upload(dev, stream, x, dtype)
+    yb = dev.alloc(x.size, dtype)
+    th.softmax(xb, yb, rows, cols, dtype, stream)
+    y = orc.widen(yb.copy_to_host(stream), ORC[dtype])
+    ref = orc.softmax(orc.widen(x, ORC[dtype]), rows, cols)
+    assert_within_ulp16(y, ref, ORC[dtype], 1.0, f"softmax {dtype.name} {rows}x{cols}")
+
+
+def test_softmax_in_place(dev, stream):
+    rng = np.random.default_rng(99)
+    x = rng.standard_normal((16, 1024)).astype(np.float32)
+    b = upload(dev, stream, x, D.F32)
+    th.softmax(b, b, 16, 1024, D.F32, stream)
+    assert_softmax_close(b.copy_to_host(stream).reshape(16, 1024), orc.softmax(x, 16, 1024))
+
+
+# ---- matmul -------------------------------------------------------------------------
+
+def test_matmul_golden_vectors(dev, stream, golden):
+    for name, dt, trans in (("matmul_bf16.npz", D.BF16, False), ("matmul_f16_t.npz", D.F16, True)):
+        g = golden(name)
+        m, k, n = (int(t) for t in g["mkn"])
+        a = upload(dev, stream, g["a"], dt)
+        b = upload(dev, stream, g["b"], dt)
+        c = dev.alloc(m * n, D.F32)
+        th.matmul(a, b, c, m, k, n, dt, D.F32, trans, stream=stream)
+        assert_gemm_close(c.copy_to_host(stream).reshape(m, n), g["c"], name)
+
+
+@pytest.mark.parametrize("in_dt", [D.BF16, D.F16, D.F32])
+@pytest.mark.parametrize("trans", [False, True])
+@pytest.mark.parametrize("m,k,n", [(256, 256, 256), (300, 72, 136), (1, 8, 8), (513, 1024, 264),
+                                   (64, 33, 40)])
+def test_matmul_integer_bit_exact(dev, stream, in_dt, trans, m, k, n):
+    """Integer-valued inputs make every partial sum exact: any layout/index slip shows."""
+    rng = np.random.default_rng(m + 7 * k + 13 * n)
+    a = rng.integers(-4, 5, (m, k)).astype(np.float32)
+    b = rng.integers(-4, 5, (n, k) if trans else (k, n)).astype(np.float32)
+    ref = (a.astype(np.int64) @ (b.T if trans else b).astype(np.int64)).astype(np.float32)
+    ab = upload(dev, stream, orc.narrow(a, ORC[in_dt]), in_dt)
+    bb = upload(dev, stream, orc.narrow(b, ORC[in_dt]), in_dt)
+    cb = dev.alloc(m * n, D.F32)
+    th.matmul(ab, bb, cb, m, k, n, in_dt, D.F32, trans, stream=stream)
+    got = cb.copy_to_host(stream).reshape(m, n)
+    assert np.array_equal(got, ref), f"max diff {np.abs(got - ref).max()}"
+
+
+@pytest.mark.parametrize("out_dt", [D.F16, D.BF16])
+def test_matmul_u16_output_rounding(dev, stream, out_dt):
+    rng = np.random.default_rng(5)
+    m, k, n = 320, 512, 264
+    a = rand16(rng, m * k, D.F16)
+    b = rand16(rng, k * n, D.F16, 0.02)
+    ab, bb = upload(dev, stream, a, D.F16), upload(dev, stream, b, D.F16)
+    cb = dev.alloc(m * n, out_dt)
+    th.matmul(ab, bb, cb, m, k, n, D.F16, out_dt, False, stream=stream)
+    got = orc.widen(cb.copy_to_host(stream), ORC[out_dt]).reshape(m, n)
+    ref = orc.matmul(a, b, m, k, n, orc.F16, orc.F32)
+    assert_gemm_close(got, orc.widen(orc.narrow(ref, ORC[out_dt]), ORC[out_dt]), "u16 out",
+                      u16_dtype=ORC[out_dt])
+
+
+def test_matmul_batched(dev, stream):
+    rng = np.random.default_rng(6)
+    bsz, m, k, n = 3, 128, 64, 96
+    a = rand16(rng, bsz * m * k, D.BF16)
+    b = rand16(rng, bsz * k * n, D.BF16)
+    ab, bb = upload(dev, stream, a, D.BF16), upload(dev, stream, b, D.BF16)
+    cb = dev.alloc(bsz * m * n, D.F32)
+    th.matmul(ab, bb, cb, m, k, n, D.BF16, D.F32, False, batch=bsz, stream=stream)
+    got = cb.copy_to_host(stream).reshape(bsz, m, n)
+    for i in range(bsz):
+        ref = orc.matmul(a[i * m * k:(i + 1) * m * k], b[i * k * n:(i + 1) * k * n], m, k, n,
+                         orc.BF16)
+        assert_gemm_close(got[i], ref, f"batch {i}")
+
+
+GEMM_ROWS = np.r_[0:64, 1000:1032, 2047:2080, 4032:4096]
+
+
+def test_matmul_config2_full(dev, stream):
+    """4096^3, A,B bf16 U[-1,1], C f32, rel 1e-2 (row subset)."""
+    M = N = K = 4096
+    a = device_random(dev, stream, M * K, D.BF16, "uniform", -1.0, 1.0, 0x71130000 + 2)
+    b = device_random(dev, stream, K * N, D.BF16, "uniform", -1.0, 1.0, 0x71130000 + 102)
+    c = dev.alloc(M * N, D.F32)
+    th.matmul(a, b, c, M, K, N, D.BF16, D.F32, False, stream=stream)
+    ah, bh = a.copy_to_host(stream).reshape(M, K), b.copy_to_host(stream)
+    got = c.copy_to_host(stream).reshape(M, N)
+    rows = GEMM_ROWS
+    ref = orc.matmul(np.ascontiguousarray(ah[rows]), bh, len(rows), K, N, orc.BF16)
+    assert_gemm_close(got[rows], ref, "config2")
+    assert np.isfinite(got).all()
+
+
+def test_matmul_config3_full(dev, stream):
+    """M=8192 K=4096 N=14336, f16, f32 acc, C f16 (row subset)."""
+    M, K, N = 8192, 4096, 14336
+    a = device_random(dev, stream, M * K, D.F16, "normal", 0.0, 1.0, 0x71130000 + 3)
+    b = device_random(dev, stream, K * N, D.F16, "normal", 0.0, 0.02, 0x71130000 + 103)
+    c = dev.alloc(M * N, D.F16)
+    th.matmul(a, b, c, M, K, N, D.F16, D.F16, False, stream=stream)
+    ah, bh = a.copy_to_host(stream).reshape(M, K), b.copy_to_host(stream)
+    got = orc.widen(c.copy_to_host(stream), orc.F16).reshape(M, N)
+    rows = np.r_[0:32, 4095:4111, 8160:8192]
+    ref = orc.matmul(np.ascontiguousarray(ah[rows]), bh, len(rows), K, N, orc.F16, orc.F32)
+    ref16 = orc.widen(orc.narrow(ref, orc.F16), orc.F16)
+    assert_gemm_close(got[rows], ref16, "config3", u16_dtype=orc.F16)
+    assert np.isfinite(got).all()
+
+
+# ---- causal mask / single-head attention ----------------------------------------------
+
+def test_causal_mask_bit_exact(dev, stream):
+    rng = np.random.default_rng(7)
+    x = rng.standard_normal((3, 70, 70)).astype(np.float32)
+    xb = upload(dev, stream, x, D.F32)
+    yb = dev.alloc(x.size, D.F32)
+    th.causal_mask_f32(xb, yb, 70, 70, 3, stream)
+    got = yb.copy_to_host(stream).reshape(3, 70, 70)
+    for t in range(3):
+        assert np.array_equal(got[t].view(np.uint32), orc.causal_mask_f32(x[t], 70, 70).view(np.uint32))
+
+
+def test_attention_f32_golden(dev, stream, golden):
+    g = golden("attention_f32.npz")
+    s, d = (int(t) for t in g["sd"])
+    bufs = [upload(dev, stream, g[n], D.F32) for n in "qkv"]
+    ob = dev.alloc(s * d, D.F32)
+    th.attention(*bufs, ob, s, d, 1, D.F32, stream)
+    got = ob.copy_to_host(stream).reshape(s, d)
+    assert np.abs(got - g["o"]).max() < 1e-4
+    assert np.abs(got - orc.attention_f32(g["q"], g["k"], g["v"], s, d)).max() < 1e-5
+
+
+# ---- prefill ------------------------------------------------------------------------------
+
+def run_prefill(dev, stream, q, k, v, dtype, B, S, start, max_seq, Dh, NH, NKV):
+    qb, kb, vb = (upload(dev, stream, t, dtype) for t in (q, k, v))
+    ob = dev.alloc(B * S * NH * Dh, dtype)
+    th.attention_prefill(qb, kb, vb, ob, B, S, start, max_seq, Dh, NH, NKV, dtype, stream)
+    return orc.widen(ob.copy_to_host(stream), ORC[dtype])
+
+
+def test_prefill_golden_vectors(dev, stream, golden):
+    g = golden("prefill_bf16.npz")
+    B, S, start, max_seq, Dh, NH, NKV = (int(t) for t in g["shape"])
+    got = run_prefill(dev, stream, g["q"], g["k"], g["v"], D.BF16, B, S, start, max_seq, Dh, NH,
+                      NKV)
+    assert_attn_close(got, g["o"].reshape(-1), "prefill golden")
+
+
+@pytest.mark.parametrize("dtype", [D.BF16, D.F16])
+@pytest.mark.parametrize("B,S,start,extra,NH,NKV,Dh", [
+    (1, 256, 0, 0, 2, 2, 128),     # one full query block
+    (2, 300, 0, 4, 4, 1, 128),     # ragged, GQA 4:1
+    (1, 100, 37, 0, 8, 2, 128),    # chunked prefill, start_pos > 0
+    (1, 600, 0, 0, 2, 2, 64),      # head_dim 64 -> general kernel
+    (3, 1, 5, 2, 4, 4, 128),       # single query
+])
+def test_prefill_shapes(dev, stream, dtype, B, S, start, extra, NH, NKV, Dh):
+    rng = np.random.default_rng(S * 7 + start)
+    max_seq = start + S + extra
+    q = rand16(rng, B * S * NH * Dh, dtype)
+    k = rand16(rng, B * NKV * max_seq * Dh, dtype)
+    v = rand16(rng, B * NKV * max_seq * Dh, dtype)
+    got = run_prefill(dev, stream, q, k, v, dtype, B, S, start, max_seq, Dh, NH, NKV)
+    ref = orc.attention_prefill(q, k, v, ORC[dtype], B, S, start, max_seq, Dh, NH, NKV)
+    assert_attn_close(got, ref, f"prefill {dtype.name} B{B} S{S} start{start} G{NH // NKV} D{Dh}")
+
+
+def test_prefill_config4_full(dev, stream):
+    """B=4 H=32 S=4096 D=128 bf16 causal; subsets: 2 (b,h) pairs in
+    full and the first/last 64 query rows of 8 more pairs."""
+    B, H, S, Dh = 4, 32, 4096, 128
+    n = B * S * H * Dh
+    qb = device_random(dev, stream, n, D.BF16, "normal", 0.0, 1.0, 0x71130000 + 4)
+    kb = device_random(dev, stream, n, D.BF16, "normal", 0.0, 1.0, 0x71130000 + 104)
+    vb = device_random(dev, stream, n, D.BF16, "normal", 0.0, 1.0, 0x71130000 + 204)
+    ob = dev.alloc(n, D.BF16)
+    th.attention_prefill(qb, kb, vb, ob, B, S, 0, S, Dh, H, H, D.BF16, stream)
+    q, k, v = (b.copy_to_host(stream) for b in (qb, kb, vb))
+    got = orc.widen(ob.copy_to_host(stream), orc.BF16).reshape(B, S, H, Dh)
+    assert np.isfinite(got).all()
+    for bh in (0, 127):
+        ref = orc.attention_prefill(q, k, v, orc.BF16, B, S, 0, S, Dh, H, H, bh0=bh, nbh=1)
+        b, h = divmod(bh, H)
+        assert_attn_close(got[b, :, h], ref.reshape(B, S, H, Dh)[b, :, h], f"config4 bh={bh}")
+    for bh in (5, 33, 64, 90, 101, 110, 120, 126):
+        b, h = divmod(bh, H)
+        for q0 in (0, S - 64):
+            ref = orc.attention_prefill(q, k, v, orc.BF16, B, S, 0, S, Dh, H, H, bh0=bh, nbh=1,
+                                        q0=q0, nq=64).reshape(B, S, H, Dh)
+            assert_attn_close(got[b, q0:q0 + 64, h], ref[b, q0:q0 + 64, h],
+                              f"config4 bh={bh} rows {q0}..")
+
+
+# ---- decode --------------------------------------------------------------------------------
+
+def run_decode(dev, stream, q, k, v, dtype, B, L, max_seq, Dh, NH, NKV, workspace=False):
+    qb, kb, vb = (upload(dev, stream, t, dtype) for t in (q, k, v))
+    ob = dev.alloc(B * NH * Dh, dtype)
+    ws, wsz = None, 0
+    if workspace:
+        wsz = th.attention_decode_workspace_size(B, L, Dh, NH, NKV)
+        ws = dev.alloc(max(1, wsz // 4), D.F32)
+    th.attention_decode(qb, kb, vb, ob, B, L, max_seq, Dh, NH, NKV, dtype, ws, wsz, stream)
+    return orc.widen(ob.copy_to_host(stream), ORC[dtype])
+
+
+def test_decode_golden_vectors(dev, stream, golden):
+    g = golden("decode_bf16.npz")
+    B, L, max_seq, Dh, NH, NKV = (int(t) for t in g["shape"])
+    got = run_decode(dev, stream, g["q"], g["k"], g["v"], D.BF16, B, L, max_seq, Dh, NH, NKV)
+    assert_attn_close(got, g["o"].reshape(-1), "decode golden")
+
+
+@pytest.mark.parametrize("dtype", [D.BF16, D.F16])
+@pytest.mark.parametrize("B,L,extra,NH,NKV,Dh,ws", [
+    (2, 300, 20, 8, 2, 128, False),
+    (1, 1, 0, 4, 4, 128, True),       # one position
+    (3, 513, 7, 16, 1, 128, True),    # G=16, chunk boundary + 1
+    (2, 1024, 0, 8, 8, 128, False),   # MHA
+    (2, 777, 0, 4, 2, 64, False),     # head_dim 64 -> general kernel
+    (1, 200, 0, 6, 2, 128, False),   # G=3 -> general kernel
+])
+def test_decode_shapes(dev, stream, dtype, B, L, extra, NH, NKV, Dh, ws):
+    rng = np.random.default_rng(L * 3 + NH)
+    max_seq = L + extra
+    q = rand16(rng, B * NH * Dh, dtype)
+    k = rand16(rng, B * NKV * max_seq * Dh, dtype)
+    v = rand16(rng, B * NKV * max_seq * Dh, dtype)
+    got = run_decode(dev, stream, q, k, v, dtype, B, L, max_seq, Dh, NH, NKV, ws)
+    ref = orc.attention_decode(q, k, v, ORC[dtype], B, L, max_seq, Dh, NH, NKV)
+    assert_attn_close(got, ref, f"decode {dtype.name} B{B} L{L} G{NH // NKV} D{Dh}")
+
+
+def test_decode_config5_full(dev, stream):
+    """B=64, NH=32, NKV=8, L=8192, D=128 bf16, all outputs."""
+    B, NH, NKV, L, Dh = 64, 32, 8, 8192, 128
+    qb = device_random(dev, stream, B * NH * Dh, D.BF16, "normal", 0.0, 1.0, 0x71130000 + 5)
+    kb = device_random(dev, stream, B * NKV * L * Dh, D.BF16, "normal", 0.0, 1.0, 0x71130000 + 105)
+    vb = device_random(dev, stream, B * NKV * L * Dh, D.BF16, "normal", 0.0, 1.0, 0x71130000 + 205)
+    ob = dev.alloc(B * NH * Dh, D.BF16)
+    th.attention_decode(qb, kb, vb, ob, B, L, L, Dh, NH, NKV, D.BF16, stream=stream)
+    q, k, v = (b.copy_to_host(stream) for b in (qb, kb, vb))
+    got = orc.widen(ob.copy_to_host(stream), orc.BF16)
+    ref = orc.attention_decode(q, k, v, orc.BF16, B, L, L, Dh, NH, NKV)
+    assert_attn_close(got, ref, "config5")
+
+
+def test_decode_matches_last_prefill_row(dev, stream):
+    rng = np.random.default_rng(21)
+    B, NH, NKV, Dh, L = 2, 8, 2, 128, 700
+    q = rand16(rng, B * NH * Dh, D.BF16)
+    k = rand16(rng, B * NKV * L * Dh, D.BF16)
+    v = rand16(rng, B * NKV * L * Dh, D.BF16)
+    od = run_decode(dev, stream, q, k, v, D.BF16, B, L, L, Dh, NH, NKV)
+    op = run_prefill(dev, stream, q, k, v, D.BF16, B, 1, L - 1, L, Dh, NH, NKV)
+    assert_attn_close(od, op, "decode vs prefill last row")

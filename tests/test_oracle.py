@@ -1,0 +1,252 @@
+"""Pins the CPU oracle (oracle/oracle.c) before it is trusted as the parity checker.
+
+Each check is independent of the oracle's own formulas: golden vectors from an
+independent float64 implementation (tests/golden), exhaustive conversion
+sweeps, closed forms and invariants, and bit-exact brute force on
+integer-valued inputs.  CPU only.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from oracle import oracle as orc
+
+F32, F16, BF16 = orc.F32, orc.F16, orc.BF16
+
+
+def bits_to_f32(u16: np.ndarray) -> np.ndarray:
+    return (u16.astype(np.uint32) << 16).view(np.float32)
+
+
+# ---- 16-bit conversions ---------------------------------------------------------------
+
+def test_bf16_widen_is_exact_shift():
+    allp = np.arange(65536, dtype=np.uint16)
+    w = orc.widen(allp, BF16)
+    assert np.array_equal(w.view(np.uint32), allp.astype(np.uint32) << 16)
+
+
+def test_bf16_round_trip_all_patterns():
+    allp = np.arange(65536, dtype=np.uint16)
+    back = orc.narrow(orc.widen(allp, BF16), BF16)
+    nan = np.isnan(bits_to_f32(allp))
+    assert np.array_equal(back[~nan], allp[~nan])
+    assert np.isnan(bits_to_f32(back[nan])).all()
+
+
+def test_f16_matches_numpy_float16_all_patterns():
+    allp = np.arange(65536, dtype=np.uint16)
+    w = orc.widen(allp, F16)
+    ref = allp.view(np.float16).astype(np.float32)
+    same = (w.view(np.uint32) == ref.view(np.uint32)) | (np.isnan(w) & np.isnan(ref))
+    assert same.all()
+
+
+def test_f32_to_f16_matches_numpy_rounding():
+    rng = np.random.default_rng(1)
+    x = np.concatenate([
+        rng.standard_normal(200000).astype(np.float32) * 10,
+        rng.standard_normal(50000).astype(np.float32) * 1e-6,   # subnormal range of f16
+        rng.standard_normal(50000).astype(np.float32) * 7e4,    # overflow range
+        np.array([0.0, -0.0, np.inf, -np.inf, 65504, 65520, 65519.99, 2 ** -25, 2 ** -24,
+                  3 * 2 ** -26], np.float32),
+    ])
+    got = orc.narrow(x, F16)
+    ref = x.astype(np.float16).view(np.uint16)
+    assert np.array_equal(got, ref)
+
+
+def test_f32_to_bf16_is_nearest_even():
+    rng = np.random.default_rng(2)
+    x = (rng.standard_normal(300000) * np.exp(rng.uniform(-30, 30, 300000))).astype(np.float32)
+    x = np.concatenate([x, np.array([1.0 + 2 ** -8, 1.0 + 3 * 2 ** -8, -(1.0 + 2 ** -8)],
+                                    np.float32)])
+    r = orc.narrow(x, BF16)
+    rv = bits_to_f32(r).astype(np.float64)
+    xv = x.astype(np.float64)
+    up = bits_to_f32((r.astype(np.int32) + 1).astype(np.uint16)).astype(np.float64)
+    dn = bits_to_f32((r.astype(np.int32) - 1).astype(np.uint16)).astype(np.float64)
+    d0 = np.abs(xv - rv)
+    ok = np.isfinite(up) & np.isfinite(dn) & (np.abs(r.astype(np.int32) & 0x7fff) > 1)
+    assert (d0[ok] <= np.abs(xv - up)[ok]).all() and (d0[ok] <= np.abs(xv - dn)[ok]).all()
+    tie = ok & ((d0 == np.abs(xv - up)) | (d0 == np.abs(xv - dn)))
+    assert ((r[tie] & 1) == 0).all()
+    # the explicit ties: 1 + 2^-8 -> 1.0 (even), 1 + 3*2^-8 -> 1 + 2^-6... rounds to even
+    assert bits_to_f32(r[-3:-2])[0] == 1.0
+    assert bits_to_f32(r[-1:])[0] == -1.0
+
+
+# ---- softmax -------------------------------------------------------------------------
+
+def test_softmax_golden(golden):
+    g = golden("softmax_f32.npz")
+    y = orc.softmax(g["x"], *g["x"].shape)
+    assert np.allclose(y, g["y"], rtol=2e-6, atol=0)
+
+
+def test_softmax_invariants():
+    rng = np.random.default_rng(3)
+    x = (rng.standard_normal((64, 1000)) * 2).astype(np.float32)
+    y = orc.softmax(x, 64, 1000)
+    assert np.allclose(y.sum(axis=1), 1.0, atol=2e-6)
+    y2 = orc.softmax((x + 3.0).astype(np.float32), 64, 1000)
+    assert np.allclose(y, y2, rtol=2e-5, atol=1e-9)
+    c = np.full((2, 128), -7.25, np.float32)
+    assert np.all(orc.softmax(c, 2, 128) == np.float32(1 / 128))
+    one_hot = np.zeros((1, 16), np.float32)
+    one_hot[0, 5] = 1000.0
+    yh = orc.softmax(one_hot, 1, 16)
+    assert yh[0, 5] == 1.0 and np.all(np.delete(yh[0], 5) == 0.0)
+
+
+def test_softmax_u16_is_f32_softmax_rounded():
+    rng = np.random.default_rng(4)
+    x = orc.narrow((rng.standard_normal((8, 256)) * 2).astype(np.float32), BF16)
+    y = orc.softmax(x, 8, 256, BF16)
+    ref = orc.softmax(orc.widen(x, BF16), 8, 256)
+    assert np.array_equal(y, orc.narrow(ref, BF16))
+
+
+# ---- matmul --------------------------------------------------------------------------------
+
+def test_matmul_golden_bf16(golden):
+    g = golden("matmul_bf16.npz")
+    m, k, n = g["mkn"]
+    c = orc.matmul(g["a"], g["b"], m, k, n, BF16)
+    rms = np.sqrt(np.mean(g["c"].astype(np.float64) ** 2))
+    assert np.abs(c - g["c"]).max() <= 1e-5 * rms
+
+
+def test_matmul_golden_f16_transposed(golden):
+    g = golden("matmul_f16_t.npz")
+    m, k, n = g["mkn"]
+    c = orc.matmul(g["a"], g["b"], m, k, n, F16, b_trans=True)
+    rms = np.sqrt(np.mean(g["c"].astype(np.float64) ** 2))
+    assert np.abs(c - g["c"]).max() <= 1e-5 * rms
+
+
+@pytest.mark.parametrize("trans", [False, True])
+def test_matmul_integer_inputs_bit_exact(trans):
+    rng = np.random.default_rng(5)
+    m, k, n = 37, 200, 29
+    a = rng.integers(-4, 5, (m, k)).astype(np.float32)
+    b = rng.integers(-4, 5, (n, k) if trans else (k, n)).astype(np.float32)
+    ref = a.astype(np.int64) @ (b.T if trans else b).astype(np.int64)
+    c = orc.matmul(orc.narrow(a, BF16), orc.narrow(b, BF16), m, k, n, BF16, b_trans=trans)
+    assert np.array_equal(c, ref.astype(np.float32))
+    c32 = orc.matmul(a, b, m, k, n, F32, b_trans=trans)
+    assert np.array_equal(c32, ref.astype(np.float32))
+
+
+def test_matmul_identity_and_permutation():
+    rng = np.random.default_rng(6)
+    a = (rng.standard_normal((24, 24))).astype(np.float32)
+    eye = np.eye(24, dtype=np.float32)
+    assert np.array_equal(orc.matmul(a, eye, 24, 24, 24, F32), a)
+    perm = np.eye(24, dtype=np.float32)[rng.permutation(24)]
+    assert np.array_equal(orc.matmul(perm, a, 24, 24, 24, F32), perm @ a)
+
+
+def test_matmul_row_subset_matches_full():
+    rng = np.random.default_rng(7)
+    a = orc.narrow(rng.standard_normal((50, 64)).astype(np.float32), F16)
+    b = orc.narrow(rng.standard_normal((64, 40)).astype(np.float32), F16)
+    full = orc.matmul(a, b, 50, 64, 40, F16, out_dtype=F16)
+    part = orc.matmul(a, b, 50, 64, 40, F16, out_dtype=F16, row0=17, nrows=9)
+    assert np.array_equal(full[17:26], part)
+
+
+# ---- causal mask ------------------------------------------------------------------------
+
+def test_causal_mask_index_rule():
+    x = np.arange(12 * 12, dtype=np.float32).reshape(12, 12)
+    y = orc.causal_mask_f32(x, 12, 12)
+    r, c = np.indices((12, 12))
+    assert np.array_equal(y[c <= r], x[c <= r])
+    assert (y.view(np.uint32)[c > r] == 0xFF800000).all()
+    assert np.isneginf(y).sum() == 12 * 11 // 2
+
+
+# ---- attention -------------------------------------------------------------------------------
+
+def test_attention_f32_golden(golden):
+    g = golden("attention_f32.npz")
+    s, d = g["sd"]
+    o = orc.attention_f32(g["q"], g["k"], g["v"], s, d)
+    assert np.abs(o - g["o"]).max() < 2e-5
+
+
+def test_attention_f32_uniform_keys_average_values():
+    rng = np.random.default_rng(8)
+    s, d = 40, 16
+    q = rng.standard_normal((s, d)).astype(np.float32)
+    k = np.tile(rng.standard_normal((1, d)).astype(np.float32), (s, 1))
+    v = rng.standard_normal((s, d)).astype(np.float32)
+    o = orc.attention_f32(q, k, v, s, d)
+    assert np.allclose(o, np.tile(v.mean(axis=0), (s, 1)), atol=2e-6)
+
+
+def _prefill_args(g):
+    B, S, start, max_seq, D, NH, NKV = (int(t) for t in g["shape"])
+    return B, S, start, max_seq, D, NH, NKV
+
+
+def test_prefill_golden(golden):
+    g = golden("prefill_bf16.npz")
+    B, S, start, max_seq, D, NH, NKV = _prefill_args(g)
+    o = orc.attention_prefill(g["q"], g["k"], g["v"], BF16, B, S, start, max_seq, D, NH, NKV)
+    assert np.abs(o - g["o"].reshape(-1)).max() < 2e-5
+
+
+def test_prefill_first_row_is_first_value():
+    rng = np.random.default_rng(9)
+    B, S, NH, NKV, D = 1, 8, 2, 1, 32
+    q = orc.narrow(rng.standard_normal(B * S * NH * D).astype(np.float32), BF16)
+    k = orc.narrow(rng.standard_normal(B * NKV * S * D).astype(np.float32), BF16)
+    v = orc.narrow(rng.standard_normal(B * NKV * S * D).astype(np.float32), BF16)
+    o = orc.attention_prefill(q, k, v, BF16, B, S, 0, S, D, NH, NKV).reshape(B, S, NH, D)
+    v0 = orc.widen(v, BF16).reshape(B, NKV, S, D)[0, 0, 0]
+    assert np.array_equal(o[0, 0, 0], v0) and np.array_equal(o[0, 0, 1], v0)
+
+
+def test_prefill_gqa_equals_mha_with_repeated_kv():
+    rng = np.random.default_rng(10)
+    B, S, NH, NKV, D = 2, 20, 4, 2, 16
+    q = orc.narrow(rng.standard_normal(B * S * NH * D).astype(np.float32), BF16)
+    k = orc.narrow(rng.standard_normal(B * NKV * S * D).astype(np.float32), BF16)
+    v = orc.narrow(rng.standard_normal(B * NKV * S * D).astype(np.float32), BF16)
+    o_gqa = orc.attention_prefill(q, k, v, BF16, B, S, 0, S, D, NH, NKV)
+    rep = lambda t: np.repeat(t.reshape(B, NKV, S, D), NH // NKV, axis=1).copy()
+    o_mha = orc.attention_prefill(q, rep(k), rep(v), BF16, B, S, 0, S, D, NH, NH)
+    assert np.array_equal(o_gqa, o_mha)
+
+
+def test_decode_golden(golden):
+    g = golden("decode_bf16.npz")
+    B, L, max_seq, D, NH, NKV = (int(t) for t in g["shape"])
+    o = orc.attention_decode(g["q"], g["k"], g["v"], BF16, B, L, max_seq, D, NH, NKV)
+    assert np.abs(o - g["o"].reshape(-1)).max() < 2e-5
+
+
+def test_decode_equals_last_prefill_row():
+    rng = np.random.default_rng(11)
+    B, NH, NKV, D, L, max_seq = 2, 4, 2, 32, 50, 64
+    q = orc.narrow(rng.standard_normal(B * NH * D).astype(np.float32), BF16)
+    k = orc.narrow(rng.standard_normal(B * NKV * max_seq * D).astype(np.float32), BF16)
+    v = orc.narrow(rng.standard_normal(B * NKV * max_seq * D).astype(np.float32), BF16)
+    od = orc.attention_decode(q, k, v, BF16, B, L, max_seq, D, NH, NKV)
+    # one prefill query at absolute position L-1 sees positions 0..L-1
+    op = orc.attention_prefill(q, k, v, BF16, B, 1, L - 1, max_seq, D, NH, NKV)
+    assert np.array_equal(od, op)
+
+
+def test_decode_single_position_returns_value():
+    rng = np.random.default_rng(12)
+    B, NH, NKV, D, max_seq = 1, 4, 1, 16, 8
+    q = orc.narrow(rng.standard_normal(B * NH * D).astype(np.float32), BF16)
+    k = orc.narrow(rng.standard_normal(B * NKV * max_seq * D).astype(np.float32), BF16)
+    v = orc.narrow(rng.standard_normal(B * NKV * max_seq * D).astype(np.float32), BF16)
+    o = orc.attention_decode(q, k, v, BF16, B, 1, max_seq, D, NH, NKV).reshape(NH, D)
+    v0 = orc.widen(v, BF16)[:D]
+    assert all(np.array_equal(o[h], v0) for h in range(NH))

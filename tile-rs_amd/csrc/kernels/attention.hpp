@@ -1,0 +1,574 @@
+// Attention kernels: causal GQA prefill (flash, MFMA), GQA decode (split-KV,
+// MFMA scores), and a general online-softmax kernel for every other shape/dtype.
+//
+// Semantics (reference):
+//   prefill  __tile_attention_prefill_f32  crates/tile_std/src/tile.rs:2136, :3064;
+//            Metal template mlir_to_msl.rs:10928-11009, host params :1851-1859.
+//            query qi of head h sits at absolute position start_pos + qi and sees
+//            KV positions pos <= start_pos + qi of kv_head = h / (NH / NKV);
+//            scale = rsqrt(D).
+//   decode   __tile_attention_decode_f32   tile.rs:2124, :3011; mlir_to_msl.rs:
+//            10747-10816, host params :1816-1823: one query per head, positions
+//            [0, seq_len), same GQA map and scale.
+//   single   __tile_attention_f32          tile.rs:221, :2401; linalg
+//            decomposition mlir_to_linalg.rs:1781-1902 (non-causal, one head,
+//            scale 1/sqrt(D) computed in f64 then rounded to f32).
+// Layouts in HBM: Q, O = [B][S][NH][D]; K, V = [B][NKV][max_seq][D] (the Metal
+// templates' per-batch layout, stacked over the batch).  The Metal templates cap
+// the KV length at 256; these kernels have no cap.
+#pragma once
+
+#include "common.hpp"
+
+namespace th {
+
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+// Hardware round-to-nearest-even packing of two floats (v_cvt_pk_bf16_f32 on gfx950).
+template <int DT>
+__device__ __forceinline__ uint32_t cvt_pk(float lo, float hi) {
+  if constexpr (DT == kBF16) {
+    bf16x2 v = __builtin_convertvector(f32x2{lo, hi}, bf16x2);
+    return __builtin_bit_cast(uint32_t, v);
+  } else {
+    f16x2 v = __builtin_convertvector(f32x2{lo, hi}, f16x2);
+    return __builtin_bit_cast(uint32_t, v);
+  }
+}
+
+// ============================================================================
+// Prefill: flash attention forward, causal, GQA, head_dim 128.
+//
+// Workgroup = 8 waves = 256 query rows of one (batch, head); wave w owns rows
+// [32w, 32w+32).  KV is consumed 64 positions at a time, staged in LDS with two
+// buffers: K as [kv][d] (d contiguous), V transposed as [d][kv-slot].
+// Per wave and KV block:
+//   S^T (64 kv x 32 q)  = K . Q^T          2x8 v_mfma_f32_32x32x16, Q^T in registers
+//   online softmax on S^T columns: lane l owns query l%32; its partner lane l^32
+//   holds the other half of that column, so row statistics need one exchange.
+//   O^T (128 d x 32 q) += V^T . P^T        4x4 MFMAs; P^T is the S^T accumulator
+//   converted to 16-bit in place: accumulator j of lane l (half g = l/32) is KV
+//   row 8*(j/4) + 4g + j%4, and the same KV order is used for the V^T slots, so
+//   the B operand needs no data movement.
+// V^T slot order inside each 16-position group: [0-3, 8-11, 4-7, 12-15], which
+// makes each lane's eight MFMA slots one contiguous 16-byte LDS read.
+// ============================================================================
+namespace fa {
+constexpr int D = 128;
+constexpr int BQ = 256;   // query rows per workgroup
+constexpr int BKV = 64;   // KV positions per LDS stage
+constexpr int NT = 512;   // threads per workgroup (8 waves)
+constexpr float kRescaleThreshold = 8.0f;  // log2 units; see the rescale below
+
+__device__ __forceinline__ int k_swz(int row, int chunk) { return chunk ^ (row & 7); }
+__device__ __forceinline__ int v_swz(int row, int chunk) { return chunk ^ ((row ^ (row >> 3)) & 7); }
+}  // namespace fa
+
+template <int DT>
+__global__ void __launch_bounds__(fa::NT, 1)
+attn_prefill_fa128(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
+                   const uint16_t* __restrict__ V, uint16_t* __restrict__ O, uint32_t batch,
+                   uint32_t seq_len, uint32_t start_pos, uint32_t max_seq, uint32_t nh,
+                   uint32_t nkv, float scale_log2) {
+  using namespace fa;
+  __shared__ u32x4 ks[2][BKV * D / 8];  // 16 KB per stage
+  __shared__ u32x4 vs[2][D * BKV / 8];  // 16 KB per stage
+
+  // ---- work decode: heavy (late) query blocks first, heads dealt to XCDs ----
+  const uint32_t nqb = (seq_len + BQ - 1) / BQ;
+  const uint32_t nbh = batch * nh;
+  uint32_t bh, qb;
+  {
+    const uint32_t bid = blockIdx.x;
+    if (nbh % 8 == 0) {
+      const uint32_t xcd = bid % 8, r = bid / 8, per = nbh / 8;
+      bh = xcd + 8 * (r % per);
+      qb = nqb - 1 - r / per;
+    } else {
+      bh = bid % nbh;
+      qb = nqb - 1 - bid / nbh;
+    }
+  }
+  const uint32_t b = bh / nh, h = bh % nh;
+  const uint32_t kvh = h / (nh / nkv);
+  const uint32_t q0 = qb * BQ;
+  const uint32_t kv_len = start_pos + seq_len;
+
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int l32 = lane & 31, g = lane >> 5;
+  const uint32_t qw0 = q0 + 32 * wave;           // this wave's first query row
+  const uint32_t my_q = qw0 + l32;               // query row owned by this lane
+  const uint32_t qa_lo = start_pos + qw0;        // lowest absolute position in the wave
+  const uint32_t qa_hi = start_pos + qw0 + 31;   // highest
+  const uint32_t my_qa = start_pos + my_q;
+
+  const size_t q_row_stride = static_cast<size_t>(nh) * D;
+  const uint16_t* kbase = K + (static_cast<size_t>(b) * nkv + kvh) * max_seq * D;
+  const uint16_t* vbase = V + (static_cast<size_t>(b) * nkv + kvh) * max_seq * D;
+
+  // Q^T fragments: lane holds query my_q, d = 16*ds + 8*g .. +7.
+  u32x4 qf[8];
+  {
+    const uint16_t* qp = Q + (static_cast<size_t>(b) * seq_len + my_q) * q_row_stride + h * D;
+#pragma unroll
+    for (int ds = 0; ds < 8; ++ds)
+      qf[ds] = (my_q < seq_len) ? ldg128(qp + 16 * ds + 8 * g) : u32x4{0, 0, 0, 0};
+  }
+
+  // KV blocks this workgroup needs: positions [0, start_pos + min(q0 + BQ, S)).
+  const uint32_t q_hi_wg = min(q0 + BQ, seq_len);
+  const uint32_t kv_need = start_pos + q_hi_wg;
+  const uint32_t nkb = (kv_need + BKV - 1) / BKV;
+
+  // ---- staging: waves 0-3 load K (4 x 16 B per thread), waves 4-7 load V as
+  //      8 (kv) x 4 (d) blocks that are transposed on the way into LDS ----
+  u32x4 rk[4];
+  u32x2 rv[8];
+  auto load_kv = [&](uint32_t kv0) {
+    if (t < 256) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int c = t + 256 * i;          // 1024 chunks of 16 B
+        const int row = c >> 4, ch = c & 15;
+        const uint32_t pos = kv0 + row;
+        rk[i] = (pos < kv_len) ? ldg128(kbase + static_cast<size_t>(pos) * D + ch * 8)
+                               : u32x4{0, 0, 0, 0};
+      }
+    } else {
+      const int tt = t - 256;
+      const int db = tt & 31, kvb = tt >> 5;  // d block of 4, kv block of 8
+      const int grp = kvb >> 1, half = kvb & 1;
+#pragma unroll
+      for (int r = 0; r < 8; ++r) {
+        const int kvl = 16 * grp + 4 * half + (r < 4 ? r : 8 + (r - 4));
+        const uint32_t pos = kv0 + kvl;
+        rv[r] = (pos < kv_len)
+                    ? *reinterpret_cast<const u32x2*>(vbase + static_cast<size_t>(pos) * D + 4 * db)
+                    : u32x2{0, 0};
+      }
+    }
+  };
+  auto store_kv = [&](int buf) {
+    if (t < 256) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int c = t + 256 * i;
+        const int row = c >> 4, ch = c & 15;
+        ks[buf][row * 16 + k_swz(row, ch)] = rk[i];
+      }
+    } else {
+      const int tt = t - 256;
+      const int db = tt & 31, kvb = tt >> 5;
+      // rv[r] = 4 d-values of slot r; emit, for each of the 4 d rows, the 8 slots.
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int dw = j >> 1;
+        u32x4 o;
+#pragma unroll
+        for (int p = 0; p < 4; ++p) {
+          const uint32_t lo = rv[2 * p][dw], hi = rv[2 * p + 1][dw];
+          o[p] = (j & 1) ? pack_halves<true>(lo, hi) : pack_halves<false>(lo, hi);
+        }
+        const int row = 4 * db + j;
+        vs[buf][row * 8 + v_swz(row, kvb)] = o;
+      }
+    }
+  };
+
+  f32x16 o_acc[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o_acc[i][r] = 0.0f;
+  float m_run = -INFINITY;  // running max (log2 units) of this lane's query
+  float l_run = 0.0f;       // this lane's partial sum (partner lane holds the rest)
+
+  load_kv(0);
+  store_kv(0);
+  __syncthreads();
+
+  for (uint32_t jb = 0; jb < nkb; ++jb) {
+    const int cur = jb & 1;
+    const uint32_t kv0 = jb * BKV;
+    if (jb + 1 < nkb) load_kv(kv0 + BKV);
+
+    // Skip blocks that lie entirely above this wave's causal diagonal or past
+    // the end of the sequence for all of its rows.
+    const bool active = (kv0 <= qa_hi) && (qw0 < seq_len);
+    if (active) {
+      f32x16 s[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) s[i][r] = 0.0f;
+#pragma unroll
+      for (int ds = 0; ds < 8; ++ds) {
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+          const int row = 32 * kt + l32;
+          const u32x4 kf = ks[cur][row * 16 + k_swz(row, 2 * ds + g)];
+          s[kt] = mfma32x32x16<DT>(kf, qf[ds], s[kt]);
+        }
+      }
+      // Causal mask only where the block crosses the diagonal.
+      if (kv0 + BKV - 1 > qa_lo) {
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const uint32_t pos = kv0 + 32 * kt + 8 * (r >> 2) + 4 * g + (r & 3);
+            if (pos > my_qa) s[kt][r] = -INFINITY;
+          }
+      }
+      float mx = -INFINITY;
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kt][r]);
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      const float m_blk = mx * scale_log2;
+      // Rescale only when the running max grows by more than the threshold: until
+      // then exponents stay <= 2^threshold, which f32 sums and 16-bit P absorb.
+      float m_use = m_run;
+      const bool grow = m_blk > m_run + kRescaleThreshold || m_run == -INFINITY;
+      if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+        const float m_new = fmaxf(m_run, m_blk);
+        const float alpha = exp2_fast(m_run - m_new);
+        l_run *= alpha;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) o_acc[i][r] *= alpha;
+        m_run = m_new;
+        m_use = m_new;
+      }
+      u32x4 pf[4];
+      float ls = 0.0f;
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt) {
+        float p[16];
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          p[r] = exp2_fast(__builtin_fmaf(s[kt][r], scale_log2, -m_use));
+          ls += p[r];
+        }
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+          for (int pp = 0; pp < 4; ++pp)
+            pf[2 * kt + hh][pp] = cvt_pk<DT>(p[8 * hh + 2 * pp], p[8 * hh + 2 * pp + 1]);
+      }
+      l_run += ls;
+#pragma unroll
+      for (int st = 0; st < 4; ++st) {
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) {
+          const int row = 32 * dt + l32;
+          const u32x4 vf = vs[cur][row * 8 + v_swz(row, 2 * st + g)];
+          o_acc[dt] = mfma32x32x16<DT>(vf, pf[st], o_acc[dt]);
+        }
+      }
+    }
+    if (jb + 1 < nkb) store_kv(cur ^ 1);
+    __syncthreads();
+  }
+
+  // ---- epilogue: O[q][d] = O^T[d][q] / l ----
+  const float l_tot = l_run + __shfl_xor(l_run, 32);
+  const float inv = 1.0f / l_tot;
+  if (my_q < seq_len) {
+    uint16_t* op = O + (static_cast<size_t>(b) * seq_len + my_q) * q_row_stride + h * D;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const int d = 32 * dt + 8 * q4 + 4 * g;
+        u32x2 w;
+        w[0] = cvt_pk<DT>(o_acc[dt][4 * q4 + 0] * inv, o_acc[dt][4 * q4 + 1] * inv);
+        w[1] = cvt_pk<DT>(o_acc[dt][4 * q4 + 2] * inv, o_acc[dt][4 * q4 + 3] * inv);
+        *reinterpret_cast<u32x2*>(op + d) = w;
+      }
+  }
+}
+
+// ============================================================================
+// Decode: one query token per head, GQA group G = NH/NKV query heads share each
+// K/V load.  Grid = B * NKV * n_split workgroups of 256 threads; each handles a
+// chunk of up to 512 KV positions of one (batch, kv_head):
+//   A  scores S^T (16 kv x 16 q, G real columns) with v_mfma_f32_16x16x32, K
+//      fragments read straight from HBM (each lane 4 x 16 B of one K row),
+//   B  per-query max / exp / sum over the chunk (in LDS),
+//   C  P.V on the vector ALUs in f32: each lane owns 8 d-values of every 4th row.
+// Partial (m, l, O) per chunk go to a workspace; decode_combine merges them.
+// ============================================================================
+namespace dec {
+constexpr int D = 128;
+constexpr int CHUNK = 512;
+constexpr int NT = 256;
+}  // namespace dec
+
+template <int DT, int G>
+__global__ void __launch_bounds__(dec::NT)
+attn_decode_split(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
+                  const uint16_t* __restrict__ V, float* __restrict__ ws, uint32_t batch,
+                  uint32_t seq_len, uint32_t max_seq, uint32_t nh, uint32_t nkv, uint32_t n_split,
+                  float scale_log2) {
+  using namespace dec;
+  __shared__ float sc[G][CHUNK];       // scores, then probabilities
+  __shared__ float red[4][G][D];       // per-wave partial O
+  __shared__ float stat_m[G], stat_l[G];
+
+  const uint32_t split = blockIdx.x % n_split;
+  const uint32_t bk = blockIdx.x / n_split;  // b * nkv + kvh
+  const uint32_t b = bk / nkv, kvh = bk % nkv;
+  const uint32_t c0 = split * CHUNK;
+  const uint32_t n_here = (c0 < seq_len) ? min(static_cast<uint32_t>(CHUNK), seq_len - c0) : 0u;
+
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int l16 = lane & 15, g4 = lane >> 4;
+  const uint16_t* kb = K + (static_cast<size_t>(bk) * max_seq + c0) * D;
+  const uint16_t* vb = V + (static_cast<size_t>(bk) * max_seq + c0) * D;
+
+  // ---- phase A: scores ----
+  {
+    u32x4 qf[4];
+    const uint32_t hq = kvh * G + l16;
+    const uint16_t* qp = Q + (static_cast<size_t>(b) * nh + hq) * D;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) qf[s] = (l16 < G) ? ldg128(qp + 32 * s + 8 * g4) : u32x4{0, 0, 0, 0};
+    // wave w: rows [w*128, w*128+128) of the chunk, 8 tiles of 16 rows
+    constexpr int TILES = CHUNK / 4 / 16;
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      u32x4 kf[TILES / 2][4];
+#pragma unroll
+      for (int tt = 0; tt < TILES / 2; ++tt) {
+        const uint32_t row = wave * (CHUNK / 4) + (half * (TILES / 2) + tt) * 16 + l16;
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+          kf[tt][s] = (row < n_here) ? ldg128(kb + static_cast<size_t>(row) * D + 32 * s + 8 * g4)
+                                     : u32x4{0, 0, 0, 0};
+      }
+#pragma unroll
+      for (int tt = 0; tt < TILES / 2; ++tt) {
+        f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int s = 0; s < 4; ++s) acc = mfma16x16x32<DT>(kf[tt][s], qf[s], acc);
+        const uint32_t row0 = wave * (CHUNK / 4) + (half * (TILES / 2) + tt) * 16 + 4 * g4;
+        if (l16 < G) {
+          f32x4 w;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) w[i] = (row0 + i < n_here) ? acc[i] * scale_log2 : -INFINITY;
+          *reinterpret_cast<f32x4*>(&sc[l16][row0]) = w;
+        }
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- phase B: per-query max, exp, sum ----
+  for (int q = wave; q < G; q += 4) {
+    float mx = -INFINITY;
+    for (int i = lane; i < CHUNK; i += 64) mx = fmaxf(mx, sc[q][i]);
+    mx = wave_max(mx);
+    float sum = 0.0f;
+    for (int i = lane; i < CHUNK; i += 64) {
+      const float p = (mx == -INFINITY) ? 0.0f : exp2_fast(sc[q][i] - mx);
+      sc[q][i] = p;
+      sum += p;
+    }
+    sum = wave_sum(sum);
+    if (lane == 0) {
+      stat_m[q] = mx;
+      stat_l[q] = sum;
+    }
+  }
+  __syncthreads();
+
+  // ---- phase C: O_partial[q][d] = sum_pos p[q][pos] * V[pos][d] ----
+  {
+    float acc[G][8];
+#pragma unroll
+    for (int q = 0; q < G; ++q)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[q][e] = 0.0f;
+    const int dc = l16;  // d = 8*dc .. 8*dc+7
+    constexpr int ROWS_PER_WAVE = CHUNK / 4;
+    constexpr int UNROLL = 8;
+#pragma unroll 1
+    for (int it = 0; it < ROWS_PER_WAVE / 4; it += UNROLL) {
+      u32x4 vv[UNROLL];
+#pragma unroll
+      for (int u = 0; u < UNROLL; ++u) {
+        const uint32_t row = wave * ROWS_PER_WAVE + 4 * (it + u) + g4;
+        vv[u] = (row < n_here) ? ldg128(vb + static_cast<size_t>(row) * D + 8 * dc)
+                               : u32x4{0, 0, 0, 0};
+      }
+#pragma unroll
+      for (int u = 0; u < UNROLL; ++u) {
+        const int row = wave * ROWS_PER_WAVE + 4 * (it + u) + g4;
+        float vf[8];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          vf[2 * e] = u16_to_f32<DT>(static_cast<uint16_t>(vv[u][e] & 0xffffu));
+          vf[2 * e + 1] = u16_to_f32<DT>(static_cast<uint16_t>(vv[u][e] >> 16));
+        }
+#pragma unroll
+        for (int q = 0; q < G; ++q) {
+          const float p = sc[q][row];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[q][e] = __builtin_fmaf(p, vf[e], acc[q][e]);
+        }
+      }
+    }
+    // reduce the 4 row groups of the wave (lanes l, l^16, l^32, l^48)
+#pragma unroll
+    for (int q = 0; q < G; ++q)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        float v = acc[q][e];
+        v += __shfl_xor(v, 16);
+        v += __shfl_xor(v, 32);
+        acc[q][e] = v;
+      }
+    if (g4 == 0) {
+#pragma unroll
+      for (int q = 0; q < G; ++q)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) red[wave][q][8 * dc + e] = acc[q][e];
+    }
+  }
+  __syncthreads();
+
+  // ---- write the partial result: ws[(bk*G + q)*n_split + split] = {m, l, O[D]} ----
+  for (int i = t; i < G * D; i += NT) {
+    const int q = i / D, d = i % D;
+    const float o = red[0][q][d] + red[1][q][d] + red[2][q][d] + red[3][q][d];
+    float* rec = ws + ((static_cast<size_t>(bk) * G + q) * n_split + split) * (D + 2);
+    rec[2 + d] = o;
+    if (d == 0) {
+      rec[0] = stat_m[q];
+      rec[1] = stat_l[q];
+    }
+  }
+}
+
+// Merge the per-chunk partials: O = sum_s 2^(m_s - M) O_s / sum_s 2^(m_s - M) l_s.
+template <int DT>
+__global__ void __launch_bounds__(128)
+attn_decode_combine(const float* __restrict__ ws, uint16_t* __restrict__ O, uint32_t nh,
+                    uint32_t nkv, uint32_t n_split) {
+  constexpr int D = dec::D;
+  const uint32_t bhq = blockIdx.x;  // b * nh + h
+  const uint32_t b = bhq / nh, h = bhq % nh;
+  const uint32_t G = nh / nkv;
+  const uint32_t kvh = h / G, q = h % G;
+  const float* rec0 = ws + ((static_cast<size_t>(b) * nkv + kvh) * G + q) * n_split * (D + 2);
+  const int d = threadIdx.x;
+  float M = -INFINITY;
+  for (uint32_t s = 0; s < n_split; ++s) M = fmaxf(M, rec0[s * (D + 2)]);
+  float num = 0.0f, den = 0.0f;
+  for (uint32_t s = 0; s < n_split; ++s) {
+    const float* rec = rec0 + s * (D + 2);
+    const float w = (rec[0] == -INFINITY) ? 0.0f : exp2_fast(rec[0] - M);
+    num = __builtin_fmaf(w, rec[2 + d], num);
+    den = __builtin_fmaf(w, rec[1], den);
+  }
+  const float o = (den > 0.0f) ? num / den : 0.0f;
+  O[static_cast<size_t>(bhq) * D + d] = f32_to_u16<DT>(o);
+}
+
+// ============================================================================
+// General attention: any head_dim <= 256, any dtype (f32 / f16 / bf16), causal
+// or not.  One 256-thread workgroup per (batch, query, head); KV streamed in
+// chunks of 1024 scores kept in LDS, online softmax across chunks.  Used for
+// shapes outside the fast kernels and for the f32 single-head op.
+//   kv_visible(q) = causal ? min(start_pos + q + 1, kv_len) : kv_len
+// q_pos_stride is the element stride between consecutive query rows of one head
+// (NH*D for [S][NH][D]); kv tensors are [B][NKV][max_seq][D].
+// ============================================================================
+template <int DT>
+__global__ void __launch_bounds__(256)
+attn_general(const void* __restrict__ Q, const void* __restrict__ K, const void* __restrict__ V,
+             void* __restrict__ O, uint32_t batch, uint32_t seq_len, uint32_t start_pos,
+             uint32_t max_seq, uint32_t kv_len, uint32_t head_dim, uint32_t nh, uint32_t nkv,
+             int causal, float scale) {
+  constexpr int CH = 1024;
+  __shared__ float qs[256];
+  __shared__ float sc[CH];
+  __shared__ float red[4];
+  const uint32_t h = blockIdx.x % nh;
+  const uint32_t qi = (blockIdx.x / nh) % seq_len;
+  const uint32_t b = blockIdx.x / (nh * seq_len);
+  const uint32_t kvh = h / (nh / nkv);
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  auto ld = [&](const void* p, size_t i) -> float {
+    if constexpr (DT == kF32) return static_cast<const float*>(p)[i];
+    else return u16_to_f32<DT>(static_cast<const uint16_t*>(p)[i]);
+  };
+  const size_t q_off = ((static_cast<size_t>(b) * seq_len + qi) * nh + h) * head_dim;
+  const size_t kv_off = (static_cast<size_t>(b) * nkv + kvh) * max_seq * head_dim;
+  for (uint32_t d = t; d < head_dim; d += 256) qs[d] = ld(Q, q_off + d);
+  __syncthreads();
+  const uint32_t visible = causal ? min(start_pos + qi + 1, kv_len) : kv_len;
+  float m_run = -INFINITY, l_run = 0.0f, acc = 0.0f;  // acc: d = t
+  for (uint32_t c0 = 0; c0 < visible; c0 += CH) {
+    const uint32_t n = min(static_cast<uint32_t>(CH), visible - c0);
+    for (uint32_t p = t; p < n; p += 256) {
+      const size_t kr = kv_off + static_cast<size_t>(c0 + p) * head_dim;
+      float dot = 0.0f;
+      for (uint32_t d = 0; d < head_dim; ++d) dot = __builtin_fmaf(qs[d], ld(K, kr + d), dot);
+      sc[p] = dot * scale;
+    }
+    __syncthreads();
+    float mx = -INFINITY;
+    for (uint32_t p = t; p < n; p += 256) mx = fmaxf(mx, sc[p]);
+    mx = wave_max(mx);
+    if (lane == 0) red[wave] = mx;
+    __syncthreads();
+    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    __syncthreads();
+    const float m_new = fmaxf(m_run, mx);
+    const float alpha = expf(m_run - m_new);
+    float sum = 0.0f;
+    for (uint32_t p = t; p < n; p += 256) {
+      const float e = expf(sc[p] - m_new);
+      sc[p] = e;
+      sum += e;
+    }
+    sum = wave_sum(sum);
+    if (lane == 0) red[wave] = sum;
+    __syncthreads();
+    sum = (red[0] + red[1]) + (red[2] + red[3]);
+    l_run = l_run * alpha + sum;
+    if (static_cast<uint32_t>(t) < head_dim) {
+      float a = acc * alpha;
+      for (uint32_t p = 0; p < n; ++p)
+        a = __builtin_fmaf(sc[p], ld(V, kv_off + static_cast<size_t>(c0 + p) * head_dim + t), a);
+      acc = a;
+    }
+    m_run = m_new;
+    __syncthreads();
+  }
+  if (static_cast<uint32_t>(t) < head_dim) {
+    const float o = (l_run > 0.0f) ? acc / l_run : 0.0f;
+    if constexpr (DT == kF32) static_cast<float*>(O)[q_off + t] = o;
+    else static_cast<uint16_t*>(O)[q_off + t] = f32_to_u16<DT>(o);
+  }
+}
+
+// Causal mask on an f32 tile (mlir_to_linalg.rs:1191-1247): y = x where col <= row,
+// else -inf.  Bit-exact.  Rows are `rows` long tiles stacked `tiles` deep.
+__global__ void __launch_bounds__(256)
+causal_mask_f32(const float* __restrict__ x, float* __restrict__ y, uint32_t rows, uint32_t cols,
+                uint64_t total) {
+  const uint64_t i = static_cast<uint64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= total) return;
+  const uint32_t c = static_cast<uint32_t>(i % cols);
+  const uint32_t r = static_cast<uint32_t>((i / cols) % rows);
+  y[i] = (c <= r) ? x[i] : __uint_as_float(0xff800000u);
+}
+
+}  // namespace th

@@ -1,0 +1,162 @@
+// Device-side helpers shared by every tile-op kernel (gfx950 / CDNA4 only).
+//
+// The tile ops carry f16 and bf16 in the same u16 carrier
+// (reference: crates/tile_std/src/lib.rs:182); the dtype is a runtime tag here.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace th {
+
+// Element-type tags; numerically equal to TH_DTYPE_* in include/tilers_hip.h.
+enum Dtype : int { kF32 = 0, kF16 = 1, kBF16 = 2 };
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+// ---- 16-bit float conversions ------------------------------------------------
+// Widening is exact; narrowing rounds to nearest even, matching `arith.extf` /
+// `arith.truncf` in the reference's linalg bridge (mlir_to_linalg.rs:1249-1303).
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) {
+  return __uint_as_float(static_cast<uint32_t>(h) << 16);
+}
+
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) {
+    return static_cast<uint16_t>((u >> 16) | 0x0040u);
+  }
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+__device__ __forceinline__ float f16_to_f32(uint16_t h) {
+  _Float16 v = __builtin_bit_cast(_Float16, h);
+  return static_cast<float>(v);
+}
+
+__device__ __forceinline__ uint16_t f32_to_f16(float f) {
+  _Float16 v = static_cast<_Float16>(f);  // v_cvt_f16_f32: round to nearest even
+  return __builtin_bit_cast(uint16_t, v);
+}
+
+template <int DT>
+__device__ __forceinline__ float u16_to_f32(uint16_t h) {
+  if constexpr (DT == kBF16) return bf16_to_f32(h);
+  else return f16_to_f32(h);
+}
+
+template <int DT>
+__device__ __forceinline__ uint16_t f32_to_u16(float f) {
+  if constexpr (DT == kBF16) return f32_to_bf16(f);
+  else return f32_to_f16(f);
+}
+
+// Two f32 -> packed pair of 16-bit values (lo in bits 0..15).
+template <int DT>
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+  return static_cast<uint32_t>(f32_to_u16<DT>(lo)) |
+         (static_cast<uint32_t>(f32_to_u16<DT>(hi)) << 16);
+}
+
+// ---- wavefront (64-lane) reductions ---------------------------------------------
+// Lanes within a 16-lane row use DPP; the two cross-row steps use ds_swizzle-free
+// lane shuffles.
+
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float v) {
+  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), CTRL, 0xf, 0xf, true));
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+  v = fmaxf(v, dpp_f32<0xb1>(v));   // quad_perm [1,0,3,2]
+  v = fmaxf(v, dpp_f32<0x4e>(v));   // quad_perm [2,3,0,1]
+  v = fmaxf(v, dpp_f32<0x141>(v));  // row_half_mirror
+  v = fmaxf(v, dpp_f32<0x140>(v));  // row_mirror
+  v = fmaxf(v, __shfl_xor(v, 16));
+  v = fmaxf(v, __shfl_xor(v, 32));
+  return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+  v += dpp_f32<0xb1>(v);
+  v += dpp_f32<0x4e>(v);
+  v += dpp_f32<0x141>(v);
+  v += dpp_f32<0x140>(v);
+  v += __shfl_xor(v, 16);
+  v += __shfl_xor(v, 32);
+  return v;
+}
+
+// exp(x) for x <= 0 via the hardware base-2 exponential.
+__device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// ---- MFMA wrappers (gfx950) ---------------------------------------------------
+
+template <int DT>
+__device__ __forceinline__ f32x16 mfma32x32x16(u32x4 a, u32x4 b, f32x16 c) {
+  if constexpr (DT == kBF16) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                    __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                   __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+}
+
+template <int DT>
+__device__ __forceinline__ f32x4 mfma16x16x32(u32x4 a, u32x4 b, f32x4 c) {
+  if constexpr (DT == kBF16) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                    __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                   __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+}
+
+// Dword built from the low (SEL_HI=false) or high 16-bit halves of two dwords:
+// result = lo_src.half | (hi_src.half << 16).
+template <bool SEL_HI>
+__device__ __forceinline__ uint32_t pack_halves(uint32_t lo_src, uint32_t hi_src) {
+  return __builtin_amdgcn_perm(hi_src, lo_src, SEL_HI ? 0x07060302u : 0x05040100u);
+}
+
+// Transpose an 8x8 block of 16-bit values held as 8 rows of 4 dwords:
+// in[r] holds row r (elements c=0..7), out[c] receives column c (elements r=0..7).
+__device__ __forceinline__ void transpose8x8_b16(const u32x4 (&in)[8], u32x4 (&out)[8]) {
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    const int dw = c >> 1;
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      const uint32_t lo = in[2 * p][dw];
+      const uint32_t hi = in[2 * p + 1][dw];
+      out[c][p] = (c & 1) ? pack_halves<true>(lo, hi) : pack_halves<false>(lo, hi);
+    }
+  }
+}
+
+// ---- global memory helpers -----------------------------------------------------
+
+__device__ __forceinline__ u32x4 ldg128(const void* p) {
+  return *reinterpret_cast<const u32x4*>(p);
+}
+__device__ __forceinline__ void stg128(void* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
+
+__device__ __forceinline__ u32x4 ldg128_nt(const void* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
+__device__ __forceinline__ void stg128_nt(void* p, u32x4 v) {
+  __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(p));
+}
+
+}  // namespace th

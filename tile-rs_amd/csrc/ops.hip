@@ -1,0 +1,408 @@
+// Tile-op entry points of the C ABI (include/tilers_hip.h, section 2).
+//
+// Each entry point checks shapes and pointers on the host, picks the
+// hand-written gfx950 kernel for the shape, and enqueues it on the caller's
+// stream.  There is no CPU fallback: a shape no kernel takes is an error.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdint>
+#include <string>
+
+#include "kernels/attention.hpp"
+#include "kernels/common.hpp"
+#include "kernels/gemm.hpp"
+#include "kernels/softmax.hpp"
+#include "runtime.hpp"
+
+using th::fail;
+
+namespace {
+
+hipStream_t as_stream(th_stream s) { return static_cast<hipStream_t>(s); }
+
+int launch_status(const char* what) {
+  return th::check_hip(hipGetLastError(), what, TH_KERNEL_ERROR);
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int dtype_size(th_dtype d) { return d == TH_F32 ? 4 : 2; }
+
+bool valid_dtype(th_dtype d) { return d == TH_F32 || d == TH_F16 || d == TH_BF16; }
+
+// ---- softmax ----------------------------------------------------------------
+
+template <int DT>
+int softmax_launch(const void* x, void* y, uint32_t rows, uint32_t cols, hipStream_t s) {
+  constexpr int E = th::SoftmaxVec<DT>::kElems;
+  const bool vec_ok = (cols % E == 0) && aligned16(x) && aligned16(y);
+  const uint32_t nvec = cols / E;
+  if (vec_ok && nvec <= 64u * 16u) {
+    const uint32_t rows_per_wg = 4;
+    const dim3 grid((rows + rows_per_wg - 1) / rows_per_wg), block(256);
+    if (nvec <= 64)
+      hipLaunchKernelGGL((th::softmax_rows_reg<DT, 1>), grid, block, 0, s, x, y, rows, cols);
+    else if (nvec <= 128)
+      hipLaunchKernelGGL((th::softmax_rows_reg<DT, 2>), grid, block, 0, s, x, y, rows, cols);
+    else if (nvec <= 256)
+      hipLaunchKernelGGL((th::softmax_rows_reg<DT, 4>), grid, block, 0, s, x, y, rows, cols);
+    else if (nvec <= 512)
+      hipLaunchKernelGGL((th::softmax_rows_reg<DT, 8>), grid, block, 0, s, x, y, rows, cols);
+    else
+      hipLaunchKernelGGL((th::softmax_rows_reg<DT, 16>), grid, block, 0, s, x, y, rows, cols);
+  } else {
+    hipLaunchKernelGGL((th::softmax_rows_generic<DT>), dim3(rows), dim3(256), 0, s, x, y, rows,
+                       cols);
+  }
+  return launch_status("softmax launch");
+}
+
+// ---- matmul -------------------------------------------------------------------
+
+template <int DT, int DTO>
+int gemm_mfma_launch(const void* a, const void* b, void* c, uint32_t m, uint32_t k, uint32_t n,
+                     bool bt, uint32_t batch, uint64_t sa, uint64_t sb, uint64_t sc,
+                     hipStream_t s) {
+  const uint32_t tiles = ((m + 255) / 256) * ((n + 255) / 256);
+  const dim3 grid(tiles, batch), block(th::gemm::NT);
+  auto A = static_cast<const uint16_t*>(a);
+  auto B = static_cast<const uint16_t*>(b);
+  if (bt)
+    hipLaunchKernelGGL((th::gemm_mfma_256<DT, DTO, true>), grid, block, 0, s, A, B, c, m, n, k, sa,
+                       sb, sc);
+  else
+    hipLaunchKernelGGL((th::gemm_mfma_256<DT, DTO, false>), grid, block, 0, s, A, B, c, m, n, k, sa,
+                       sb, sc);
+  return launch_status("matmul (MFMA) launch");
+}
+
+template <int DT, int DTO>
+int gemm_fma_launch(const void* a, const void* b, void* c, uint32_t m, uint32_t k, uint32_t n,
+                    bool bt, uint32_t batch, uint64_t sa, uint64_t sb, uint64_t sc,
+                    hipStream_t s) {
+  const uint32_t tiles = ((m + 63) / 64) * ((n + 63) / 64);
+  const dim3 grid(tiles, batch), block(256);
+  if (bt)
+    hipLaunchKernelGGL((th::gemm_fma_64<DT, DTO, true>), grid, block, 0, s, a, b, c, m, n, k, sa,
+                       sb, sc);
+  else
+    hipLaunchKernelGGL((th::gemm_fma_64<DT, DTO, false>), grid, block, 0, s, a, b, c, m, n, k, sa,
+                       sb, sc);
+  return launch_status("matmul (FMA) launch");
+}
+
+template <int DT>
+int gemm_dispatch_out(const void* a, const void* b, void* c, uint32_t m, uint32_t k, uint32_t n,
+                      th_dtype out, bool bt, uint32_t batch, uint64_t sa, uint64_t sb, uint64_t sc,
+                      hipStream_t s, bool mfma) {
+  switch (out) {
+    case TH_F32:
+      return mfma ? gemm_mfma_launch<DT, th::kF32>(a, b, c, m, k, n, bt, batch, sa, sb, sc, s)
+                  : gemm_fma_launch<DT, th::kF32>(a, b, c, m, k, n, bt, batch, sa, sb, sc, s);
+    case TH_F16:
+      return mfma ? gemm_mfma_launch<DT, th::kF16>(a, b, c, m, k, n, bt, batch, sa, sb, sc, s)
+                  : gemm_fma_launch<DT, th::kF16>(a, b, c, m, k, n, bt, batch, sa, sb, sc, s);
+    default:
+      return mfma ? gemm_mfma_launch<DT, th::kBF16>(a, b, c, m, k, n, bt, batch, sa, sb, sc, s)
+                  : gemm_fma_launch<DT, th::kBF16>(a, b, c, m, k, n, bt, batch, sa, sb, sc, s);
+  }
+}
+
+// ---- random fill ------------------------------------------------------------------
+
+__device__ __forceinline__ uint64_t splitmix64(uint64_t x) {
+  x += 0x9e3779b97f4a7c15ull;
+  x = (x ^ (x >> 30)) * 0xbf58476d1ce4e5b9ull;
+  x = (x ^ (x >> 27)) * 0x94d049bb133111ebull;
+  return x ^ (x >> 31);
+}
+
+template <int DT>
+__global__ void __launch_bounds__(256)
+fill_random_kernel(void* dst, uint64_t n, int dist, float p0, float p1, uint64_t seed) {
+  const uint64_t i = static_cast<uint64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= n) return;
+  const uint64_t r = splitmix64(seed ^ splitmix64(i));
+  const float u1 = (static_cast<float>(r >> 40) + 0.5f) * (1.0f / 16777216.0f);           // (0,1)
+  const float u2 = static_cast<float>((r >> 16) & 0xffffffu) * (1.0f / 16777216.0f);     // [0,1)
+  float v;
+  if (dist == 0) {
+    v = p0 + (p1 - p0) * u2;
+  } else {
+    v = p0 + p1 * sqrtf(-2.0f * logf(u1)) * cosf(6.283185307179586f * u2);
+  }
+  if constexpr (DT == th::kF32) static_cast<float*>(dst)[i] = v;
+  else static_cast<uint16_t*>(dst)[i] = th::f32_to_u16<DT>(v);
+}
+
+}  // namespace
+
+extern "C" {
+
+int th_softmax(const void* x, void* y, uint32_t rows, uint32_t cols, th_dtype dtype, th_stream s) {
+  if (!valid_dtype(dtype)) return fail(TH_KERNEL_ERROR, "softmax: unknown dtype");
+  if (rows == 0 || cols == 0) return TH_OK;
+  if (!x || !y) return fail(TH_KERNEL_ERROR, "softmax: null pointer");
+  switch (dtype) {
+    case TH_F32: return softmax_launch<th::kF32>(x, y, rows, cols, as_stream(s));
+    case TH_F16: return softmax_launch<th::kF16>(x, y, rows, cols, as_stream(s));
+    default: return softmax_launch<th::kBF16>(x, y, rows, cols, as_stream(s));
+  }
+}
+
+int th_matmul(const void* a, const void* b, void* c, uint32_t m, uint32_t k, uint32_t n,
+              th_dtype in_dtype, th_dtype out_dtype, int b_transposed, uint32_t batch, uint64_t sa,
+              uint64_t sb, uint64_t sc, th_stream s) {
+  if (!valid_dtype(in_dtype) || !valid_dtype(out_dtype))
+    return fail(TH_KERNEL_ERROR, "matmul: unknown dtype");
+  if (m == 0 || n == 0 || batch == 0) return TH_OK;
+  if (!a || !b || !c) return fail(TH_KERNEL_ERROR, "matmul: null pointer");
+  if (batch > 65535) return fail(TH_KERNEL_ERROR, "matmul: batch > 65535");
+  const bool bt = b_transposed != 0;
+  if (sa == 0) sa = static_cast<uint64_t>(m) * k;
+  if (sb == 0) sb = static_cast<uint64_t>(k) * n;
+  if (sc == 0) sc = static_cast<uint64_t>(m) * n;
+  if (k == 0) {
+    // empty contraction: C = 0 (linalg.fill 0 with nothing accumulated)
+    const size_t esz = dtype_size(out_dtype);
+    for (uint32_t i = 0; i < batch; ++i)
+      TH_TRY(th::check_hip(hipMemsetAsync(static_cast<char*>(c) + i * sc * esz, 0,
+                                          static_cast<size_t>(m) * n * esz, as_stream(s)),
+                           "hipMemsetAsync", TH_MEMORY_ERROR));
+    return TH_OK;
+  }
+  const bool mfma = in_dtype != TH_F32 && (k % 8 == 0) && (bt || n % 8 == 0) && aligned16(a) &&
+                    aligned16(b) && (sa % 8 == 0) && (sb % 8 == 0);
+  switch (in_dtype) {
+    case TH_F32:
+      return gemm_dispatch_out<th::kF32>(a, b, c, m, k, n, out_dtype, bt, batch, sa, sb, sc,
+                                         as_stream(s), false);
+    case TH_F16:
+      return gemm_dispatch_out<th::kF16>(a, b, c, m, k, n, out_dtype, bt, batch, sa, sb, sc,
+                                         as_stream(s), mfma);
+    default:
+      return gemm_dispatch_out<th::kBF16>(a, b, c, m, k, n, out_dtype, bt, batch, sa, sb, sc,
+                                          as_stream(s), mfma);
+  }
+}
+
+int th_causal_mask_f32(const float* x, float* y, uint32_t rows, uint32_t cols, uint32_t tiles,
+                       th_stream s) {
+  const uint64_t total = static_cast<uint64_t>(rows) * cols * tiles;
+  if (total == 0) return TH_OK;
+  if (!x || !y) return fail(TH_KERNEL_ERROR, "causal_mask: null pointer");
+  const uint64_t blocks = (total + 255) / 256;
+  if (blocks > 0x7fffffffu) return fail(TH_KERNEL_ERROR, "causal_mask: too large");
+  hipLaunchKernelGGL(th::causal_mask_f32, dim3(static_cast<uint32_t>(blocks)), dim3(256), 0,
+                     as_stream(s), x, y, rows, cols, total);
+  return launch_status("causal_mask launch");
+}
+
+static int attn_general_launch(const void* q, const void* k, const void* v, void* o,
+                               uint32_t batch, uint32_t seq_len, uint32_t start_pos,
+                               uint32_t max_seq, uint32_t kv_len, uint32_t head_dim, uint32_t nh,
+                               uint32_t nkv, int causal, float scale, th_dtype dtype,
+                               hipStream_t s) {
+  if (head_dim > 256) return fail(TH_KERNEL_ERROR, "attention: head_dim > 256 is not supported");
+  const uint64_t blocks = static_cast<uint64_t>(batch) * seq_len * nh;
+  if (blocks > 0x7fffffffu) return fail(TH_KERNEL_ERROR, "attention: grid too large");
+  const dim3 grid(static_cast<uint32_t>(blocks)), block(256);
+  switch (dtype) {
+    case TH_F32:
+      hipLaunchKernelGGL(th::attn_general<th::kF32>, grid, block, 0, s, q, k, v, o, batch, seq_len,
+                         start_pos, max_seq, kv_len, head_dim, nh, nkv, causal, scale);
+      break;
+    case TH_F16:
+      hipLaunchKernelGGL(th::attn_general<th::kF16>, grid, block, 0, s, q, k, v, o, batch, seq_len,
+                         start_pos, max_seq, kv_len, head_dim, nh, nkv, causal, scale);
+      break;
+    default:
+      hipLaunchKernelGGL(th::attn_general<th::kBF16>, grid, block, 0, s, q, k, v, o, batch,
+                         seq_len, start_pos, max_seq, kv_len, head_dim, nh, nkv, causal, scale);
+      break;
+  }
+  return launch_status("attention (general) launch");
+}
+
+int th_attention(const void* q, const void* k, const void* v, void* o, uint32_t seq_len,
+                 uint32_t head_dim, uint32_t tiles, th_dtype dtype, th_stream s) {
+  if (!valid_dtype(dtype)) return fail(TH_KERNEL_ERROR, "attention: unknown dtype");
+  if (seq_len == 0 || head_dim == 0 || tiles == 0) return TH_OK;
+  if (!q || !k || !v || !o) return fail(TH_KERNEL_ERROR, "attention: null pointer");
+  // scale printed by the linalg bridge: 1.0f64 / sqrt(d), then used as f32
+  const float scale = static_cast<float>(1.0 / std::sqrt(static_cast<double>(head_dim)));
+  return attn_general_launch(q, k, v, o, tiles, seq_len, 0, seq_len, seq_len, head_dim, 1, 1, 0,
+                             scale, dtype, as_stream(s));
+}
+
+int th_attention_prefill(const void* q, const void* k, const void* v, void* o, uint32_t batch,
+                         uint32_t seq_len, uint32_t start_pos, uint32_t max_seq,
+                         uint32_t head_dim, uint32_t num_heads, uint32_t num_kv_heads,
+                         th_dtype dtype, th_stream s) {
+  if (!valid_dtype(dtype)) return fail(TH_KERNEL_ERROR, "attention_prefill: unknown dtype");
+  if (batch == 0 || seq_len == 0 || num_heads == 0) return TH_OK;
+  if (!q || !k || !v || !o) return fail(TH_KERNEL_ERROR, "attention_prefill: null pointer");
+  if (num_kv_heads == 0 || num_heads % num_kv_heads != 0)
+    return fail(TH_KERNEL_ERROR, "attention_prefill: num_heads must be a multiple of num_kv_heads");
+  if (static_cast<uint64_t>(start_pos) + seq_len > max_seq)
+    return fail(TH_KERNEL_ERROR, "attention_prefill: start_pos + seq_len exceeds max_seq");
+  if (head_dim == 0) return fail(TH_KERNEL_ERROR, "attention_prefill: head_dim == 0");
+  const float scale = 1.0f / std::sqrt(static_cast<float>(head_dim));  // rsqrt(float(head_dim))
+  const bool fast = dtype != TH_F32 && head_dim == th::fa::D && aligned16(q) && aligned16(k) &&
+                    aligned16(v) && aligned16(o);
+  if (fast) {
+    const uint64_t nqb = (seq_len + th::fa::BQ - 1) / th::fa::BQ;
+    const uint64_t blocks = nqb * batch * num_heads;
+    if (blocks > 0x7fffffffu) return fail(TH_KERNEL_ERROR, "attention_prefill: grid too large");
+    const dim3 grid(static_cast<uint32_t>(blocks)), block(th::fa::NT);
+    const float sl2 = scale * th::kLog2e;
+    auto Q = static_cast<const uint16_t*>(q);
+    auto K = static_cast<const uint16_t*>(k);
+    auto V = static_cast<const uint16_t*>(v);
+    auto O = static_cast<uint16_t*>(o);
+    if (dtype == TH_BF16)
+      hipLaunchKernelGGL(th::attn_prefill_fa128<th::kBF16>, grid, block, 0, as_stream(s), Q, K, V, O,
+                         batch, seq_len, start_pos, max_seq, num_heads, num_kv_heads, sl2);
+    else
+      hipLaunchKernelGGL(th::attn_prefill_fa128<th::kF16>, grid, block, 0, as_stream(s), Q, K, V, O,
+                         batch, seq_len, start_pos, max_seq, num_heads, num_kv_heads, sl2);
+    return launch_status("attention_prefill launch");
+  }
+  return attn_general_launch(q, k, v, o, batch, seq_len, start_pos, max_seq, start_pos + seq_len,
+                             head_dim, num_heads, num_kv_heads, 1, scale, dtype, as_stream(s));
+}
+
+static uint32_t decode_splits(uint32_t seq_len) {
+  return (seq_len + th::dec::CHUNK - 1) / th::dec::CHUNK;
+}
+
+static bool decode_fast(uint32_t head_dim, uint32_t nh, uint32_t nkv, th_dtype dtype) {
+  if (dtype == TH_F32 || head_dim != th::dec::D || nkv == 0 || nh % nkv != 0) return false;
+  const uint32_t g = nh / nkv;
+  return g == 1 || g == 2 || g == 4 || g == 8 || g == 16;
+}
+
+size_t th_attention_decode_workspace_size(uint32_t batch, uint32_t seq_len, uint32_t head_dim,
+                                          uint32_t num_heads, uint32_t num_kv_heads) {
+  (void)num_kv_heads;
+  if (head_dim != th::dec::D) return 0;
+  return static_cast<size_t>(batch) * num_heads * decode_splits(seq_len) * (th::dec::D + 2) *
+         sizeof(float);
+}
+
+}  // extern "C"
+
+template <int DT, int G>
+static void decode_split_launch(const void* q, const void* k, const void* v, float* ws,
+                                uint32_t batch, uint32_t seq_len, uint32_t max_seq, uint32_t nh,
+                                uint32_t nkv, uint32_t n_split, float sl2, hipStream_t s) {
+  const dim3 grid(batch * nkv * n_split), block(th::dec::NT);
+  hipLaunchKernelGGL((th::attn_decode_split<DT, G>), grid, block, 0, s,
+                     static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
+                     static_cast<const uint16_t*>(v), ws, batch, seq_len, max_seq, nh, nkv,
+                     n_split, sl2);
+}
+
+template <int DT>
+static void decode_launch_g(uint32_t g, const void* q, const void* k, const void* v, float* ws,
+                            uint32_t batch, uint32_t seq_len, uint32_t max_seq, uint32_t nh,
+                            uint32_t nkv, uint32_t n_split, float sl2, hipStream_t s) {
+  switch (g) {
+    case 1: decode_split_launch<DT, 1>(q, k, v, ws, batch, seq_len, max_seq, nh, nkv, n_split, sl2, s); break;
+    case 2: decode_split_launch<DT, 2>(q, k, v, ws, batch, seq_len, max_seq, nh, nkv, n_split, sl2, s); break;
+    case 4: decode_split_launch<DT, 4>(q, k, v, ws, batch, seq_len, max_seq, nh, nkv, n_split, sl2, s); break;
+    case 8: decode_split_launch<DT, 8>(q, k, v, ws, batch, seq_len, max_seq, nh, nkv, n_split, sl2, s); break;
+    default: decode_split_launch<DT, 16>(q, k, v, ws, batch, seq_len, max_seq, nh, nkv, n_split, sl2, s); break;
+  }
+}
+
+extern "C" {
+
+int th_attention_decode(const void* q, const void* k, const void* v, void* o, uint32_t batch,
+                        uint32_t seq_len, uint32_t max_seq, uint32_t head_dim, uint32_t num_heads,
+                        uint32_t num_kv_heads, th_dtype dtype, void* workspace,
+                        size_t workspace_bytes, th_stream s) {
+  if (!valid_dtype(dtype)) return fail(TH_KERNEL_ERROR, "attention_decode: unknown dtype");
+  if (batch == 0 || num_heads == 0) return TH_OK;
+  if (!q || !k || !v || !o) return fail(TH_KERNEL_ERROR, "attention_decode: null pointer");
+  if (num_kv_heads == 0 || num_heads % num_kv_heads != 0)
+    return fail(TH_KERNEL_ERROR, "attention_decode: num_heads must be a multiple of num_kv_heads");
+  if (seq_len > max_seq) return fail(TH_KERNEL_ERROR, "attention_decode: seq_len exceeds max_seq");
+  if (head_dim == 0) return fail(TH_KERNEL_ERROR, "attention_decode: head_dim == 0");
+  const float scale = 1.0f / std::sqrt(static_cast<float>(head_dim));
+  if (seq_len == 0) {
+    // no positions: the output is zero (nothing to weight)
+    const size_t bytes = static_cast<size_t>(batch) * num_heads * head_dim * dtype_size(dtype);
+    return th::check_hip(hipMemsetAsync(o, 0, bytes, as_stream(s)), "hipMemsetAsync",
+                         TH_MEMORY_ERROR);
+  }
+  const bool fast = decode_fast(head_dim, num_heads, num_kv_heads, dtype) && aligned16(q) &&
+                    aligned16(k) && aligned16(v);
+  if (!fast) {
+    // one query per (batch, head): Q/O [B][1][NH][D]
+    return attn_general_launch(q, k, v, o, batch, 1, 0, max_seq, seq_len, head_dim, num_heads,
+                               num_kv_heads, 0, scale, dtype, as_stream(s));
+  }
+  const uint32_t n_split = decode_splits(seq_len);
+  const size_t need = th_attention_decode_workspace_size(batch, seq_len, head_dim, num_heads,
+                                                         num_kv_heads);
+  void* ws = workspace;
+  if (ws) {
+    if (workspace_bytes < need)
+      return fail(TH_MEMORY_ERROR, "attention_decode: workspace of " +
+                                       std::to_string(workspace_bytes) + " bytes < required " +
+                                       std::to_string(need));
+  } else {
+    TH_TRY(th::device_scratch(need, &ws));
+  }
+  const uint64_t blocks = static_cast<uint64_t>(batch) * num_kv_heads * n_split;
+  if (blocks > 0x7fffffffu) return fail(TH_KERNEL_ERROR, "attention_decode: grid too large");
+  const float sl2 = scale * th::kLog2e;
+  const uint32_t g = num_heads / num_kv_heads;
+  if (dtype == TH_BF16)
+    decode_launch_g<th::kBF16>(g, q, k, v, static_cast<float*>(ws), batch, seq_len, max_seq,
+                               num_heads, num_kv_heads, n_split, sl2, as_stream(s));
+  else
+    decode_launch_g<th::kF16>(g, q, k, v, static_cast<float*>(ws), batch, seq_len, max_seq,
+                              num_heads, num_kv_heads, n_split, sl2, as_stream(s));
+  TH_TRY(launch_status("attention_decode launch"));
+  const dim3 cgrid(batch * num_heads), cblock(th::dec::D);
+  if (dtype == TH_BF16)
+    hipLaunchKernelGGL(th::attn_decode_combine<th::kBF16>, cgrid, cblock, 0, as_stream(s),
+                       static_cast<const float*>(ws), static_cast<uint16_t*>(o), num_heads,
+                       num_kv_heads, n_split);
+  else
+    hipLaunchKernelGGL(th::attn_decode_combine<th::kF16>, cgrid, cblock, 0, as_stream(s),
+                       static_cast<const float*>(ws), static_cast<uint16_t*>(o), num_heads,
+                       num_kv_heads, n_split);
+  return launch_status("attention_decode combine launch");
+}
+
+int th_fill_random(void* dst, uint64_t n, th_dtype dtype, int dist, float p0, float p1,
+                   uint64_t seed, th_stream s) {
+  if (!valid_dtype(dtype)) return fail(TH_KERNEL_ERROR, "fill_random: unknown dtype");
+  if (dist != 0 && dist != 1) return fail(TH_KERNEL_ERROR, "fill_random: dist must be 0 or 1");
+  if (n == 0) return TH_OK;
+  if (!dst) return fail(TH_KERNEL_ERROR, "fill_random: null pointer");
+  const uint64_t blocks = (n + 255) / 256;
+  if (blocks > 0x7fffffffu) return fail(TH_KERNEL_ERROR, "fill_random: too large");
+  const dim3 grid(static_cast<uint32_t>(blocks)), block(256);
+  switch (dtype) {
+    case TH_F32:
+      hipLaunchKernelGGL(fill_random_kernel<th::kF32>, grid, block, 0, as_stream(s), dst, n, dist, p0,
+                         p1, seed);
+      break;
+    case TH_F16:
+      hipLaunchKernelGGL(fill_random_kernel<th::kF16>, grid, block, 0, as_stream(s), dst, n, dist, p0,
+                         p1, seed);
+      break;
+    default:
+      hipLaunchKernelGGL(fill_random_kernel<th::kBF16>, grid, block, 0, as_stream(s), dst, n, dist,
+                         p0, p1, seed);
+      break;
+  }
+  return launch_status("fill_random launch");
+}
+
+}  // extern "C"
