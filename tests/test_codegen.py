@@ -1,0 +1,200 @@
+"""The `hip` CodegenTarget and the TargetRegistry (CPU only).
+
+Mirrors the reference's registry/trait tests (crates/tile_codegen/src/lib.rs:
+69-148) and its behaviour specs (crates/tile_spec/features/
+backend_emit_purity.feature, core_op_lowering.feature,
+registry_add_target.feature): empty-module rejection, byte-identical re-emit,
+per-op lowering, and adding a target by registration.
+"""
+from __future__ import annotations
+
+from pathlib import Path
+
+import pytest
+
+import tilers_hip as th
+from tilers_hip import _build
+
+EXAMPLES = Path(_build.EXAMPLES_DIR)
+
+
+def mlir_one(op_line: str, loads: int = 1, store: str = "__tile_store_f32",
+             load: str = "__tile_load_f32", name: str = "k", rows: int = 1, cols: int = 1024,
+             extra_consts: str = "") -> str:
+    args = ", ".join(f"%arg{i}: !llvm.ptr<1>" for i in range(loads + 1))
+    body = [f"    %r = llvm.mlir.constant({rows} : i32) : i32",
+            f"    %c = llvm.mlir.constant({cols} : i32) : i32", extra_consts]
+    for i in range(loads):
+        body.append(f"    %t{i} = llvm.call @{load}(%arg{i}, %r, %c) : (!llvm.ptr<1>, i32, i32) -> i32")
+    body.append(op_line)
+    body.append(f"    llvm.call @{store}(%arg{loads}, %y, %r, %c) : (!llvm.ptr<1>, i32, i32, i32) -> ()")
+    body.append("    llvm.return")
+    return ("module {\n  llvm.func @" + name + "(" + args + ") attributes {hacc.entry} {\n    ^bb0:\n"
+            + "\n".join(l for l in body if l) + "\n  }\n}\n")
+
+
+# ---- registry (crates/tile_codegen/src/lib.rs:69-148) ---------------------------------
+
+def test_builtin_registry_has_debug_and_hip():
+    r = th.TargetRegistry.with_builtin()
+    assert r.names() == ["debug", "hip"]
+    assert len(r) == 2 and not r.is_empty()
+    assert r.select("hip").name() == "hip"
+    assert r.select("cuda") is None
+    assert th.TargetRegistry.new().is_empty()
+
+
+def test_debug_target_echoes_module():
+    r = th.TargetRegistry.with_builtin()
+    out = r.select("debug").emit("func.func @a\nfunc.func @b\n")
+    assert out.source == "// tile-rs debug target\n// 2 MLIR lines, 2 func.func op(s)\nfunc.func @a\nfunc.func @b\n\n"
+    assert out.ext == "mlir.txt"
+
+
+@pytest.mark.parametrize("target", ["debug", "hip"])
+def test_empty_module_is_an_error(target):
+    r = th.TargetRegistry.with_builtin()
+    with pytest.raises(th.HalError) as e:
+        r.select(target).emit("   \n ")
+    assert "empty MLIR module" in str(e.value)
+
+
+def test_module_without_entry_kernel_is_an_error():
+    src = mlir_one("    %y = llvm.call @__tile_softmax_f32(%t0, %t0, %r, %c) : (i32, i32, i32, i32) -> i32")
+    with pytest.raises(th.HalError) as e:
+        th.emit(src.replace("attributes {hacc.entry}", ""))
+    assert "No entry-point kernel functions" in str(e.value)
+
+
+def test_register_custom_target_and_select_by_codegen_path(monkeypatch):
+    # registry_add_target.feature: register a target, select it by TILERS_CODEGEN_PATH
+    r = th.TargetRegistry.with_builtin()
+    r.register(th.EmitterTarget("myaccel", "acc", lambda m: "// myaccel\n" + m))
+    monkeypatch.setenv("TILERS_CODEGEN_PATH", "myaccel")
+    import os
+    t = r.select(os.environ["TILERS_CODEGEN_PATH"])
+    out = t.emit("x")
+    assert out.source == "// myaccel\nx" and out.ext == "acc"
+    r.register(th.EmitterTarget("failing", "x", lambda m: (_ for _ in ()).throw(ValueError("nope"))))
+    with pytest.raises(th.HalError) as e:
+        r.select("failing").emit("x")
+    assert "nope" in str(e.value)
+
+
+def test_select_returns_first_registered_of_a_name():
+    r = th.TargetRegistry.new()
+    r.register(th.EmitterTarget("dup", "a", lambda m: "first"))
+    r.register(th.EmitterTarget("dup", "b", lambda m: "second"))
+    assert r.select("dup").emit("x").source == "first"
+
+
+# ---- hip target: purity and lowering -------------------------------------------------------
+
+@pytest.mark.parametrize("path", sorted(EXAMPLES.glob("*.mlir")), ids=lambda p: p.stem)
+def test_emit_is_deterministic(path):
+    text = path.read_text()
+    a, b = th.emit(text), th.emit(text)
+    assert a.source == b.source and a.ext == "hip" and a.meta == b.meta
+    assert a.meta.kernel_names and not a.meta.has_cube_kernel
+    for name in a.meta.kernel_names:
+        assert f'extern "C" __global__' in a.source and f"__th_desc_{name}" in a.source
+
+
+def test_registry_hip_matches_direct_emit():
+    text = (EXAMPLES / "softmax_rows.mlir").read_text()
+    assert th.TargetRegistry.with_builtin().select("hip").emit(text).source == th.emit(text).source
+
+
+@pytest.mark.parametrize("example,entry", [
+    ("softmax_rows", "th::entry::softmax_rows<th::kF32, 4>"),
+    ("softmax_generic", "th::entry::softmax_rows<th::kBF16, 4>"),
+    ("matmul_bf16", "th::entry::gemm<th::kBF16, th::kF32, false>"),
+    ("matmul_f16_t", "th::entry::gemm<th::kF16, th::kF16, true>"),
+    ("matmul_f32", "th::entry::gemm_fma<th::kF32, th::kF32, false>"),
+    ("attention_f32", "th::entry::attention_tiles<th::kF32, 256>"),
+    ("prefill_bf16", "th::entry::prefill<th::kBF16>"),
+    ("decode_bf16", "th::entry::decode<th::kBF16>"),
+])
+def test_hot_ops_lower_to_hand_written_kernels(example, entry):
+    out = th.emit((EXAMPLES / f"{example}.mlir").read_text())
+    assert entry in out.source
+
+
+def test_matmul_shape_and_tile_offsets_are_exact():
+    out = th.emit((EXAMPLES / "matmul_bf16.mlir").read_text())
+    # M=512 K=256 N=384: th::entry::gemm(..., M, N, K, tiles); 2 x 2 workgroups per tile
+    assert "512u, 384u, 256u, th_tiles" in out.source
+    assert "__th_desc_matmul_bf16_acc_f32 = {th::kLaunchDescMagic, 256u, 4u, 1u" in out.source
+
+
+def test_attention_runtime_params_follow_metal_order():
+    pre = th.emit((EXAMPLES / "prefill_bf16.mlir").read_text()).source
+    assert ("uint32_t seq_len, uint32_t start_pos, uint32_t max_seq, uint32_t head_dim, "
+            "uint32_t num_heads, uint32_t num_kv_heads, uint32_t th_tiles") in pre
+    dec = th.emit((EXAMPLES / "decode_bf16.mlir").read_text()).source
+    assert ("uint32_t seq_len, uint32_t max_seq, uint32_t head_dim, uint32_t num_heads, "
+            "uint32_t num_kv_heads, uint32_t th_tiles") in dec
+
+
+def test_elementwise_fallback():
+    out = th.emit((EXAMPLES / "swiglu_mask.mlir").read_text())
+    assert out.meta.kernel_names == ["swiglu", "scaled_causal"]
+    assert "/ (1.0f + expf(-" in out.source            # silu
+    assert "(col <= row ?" in out.source                 # causal mask: keep col <= row
+    assert "0x1p-3f" in out.source                       # scale 0.125, exact
+    assert "fminf(fmaxf(" in out.source                  # clamp
+
+
+def test_bf16_side_channel_from_names():
+    body = "    %y = llvm.call @__tile_softmax_f16(%t0, %t0, %r, %c) : (i32, i32, i32, i32) -> i32"
+    f16 = th.emit(mlir_one(body, load="__tile_load_f16", store="__tile_store_f16", name="sm"))
+    assert "th::kF16" in f16.source and "th::kBF16" not in f16.source
+    bf = th.emit(mlir_one(body, load="__tile_load_f16", store="__tile_store_f16", name="sm_bf16"))
+    assert "th::kBF16" in bf.source
+    explicit = th.emit(mlir_one(body, load="__tile_load_bf16", store="__tile_store_bf16", name="sm"))
+    assert "th::kBF16" in explicit.source
+
+
+def test_generic_form_matches_pretty_form():
+    gen = th.emit((EXAMPLES / "softmax_generic.mlir").read_text())
+    assert gen.meta.kernel_names == ["softmax_bf16_generic"]
+    assert "th_tiles * 4u, 2048u" in gen.source
+
+
+def test_unsupported_intrinsic_is_an_error():
+    body = "    %y = llvm.call @__tile_topk_f32(%t0, %t0, %r, %c) : (i32, i32, i32, i32) -> i32"
+    with pytest.raises(th.HalError) as e:
+        th.emit(mlir_one(body))
+    assert "unsupported intrinsic __tile_topk_f32" in str(e.value)
+    assert e.value.kind == "KernelError"
+
+
+def test_hot_op_must_be_fed_by_loads():
+    body = ("    %e = llvm.call @__tile_exp_f32(%t0, %t0, %r, %c) : (i32, i32, i32, i32) -> i32\n"
+            "    %y = llvm.call @__tile_softmax_f32(%e, %e, %r, %c) : (i32, i32, i32, i32) -> i32")
+    with pytest.raises(th.HalError) as e:
+        th.emit(mlir_one(body))
+    assert "operands must come straight from loads" in str(e.value)
+
+
+def test_constant_gep_offsets_are_applied():
+    src = mlir_one("    %y = llvm.call @__tile_softmax_f32(%t0, %t0, %r, %c) : (i32, i32, i32, i32) -> i32")
+    src = src.replace("    %t0 = llvm.call @__tile_load_f32(%arg0,",
+                      "    %o = llvm.mlir.constant(4096 : i64) : i64\n"
+                      "    %p = llvm.getelementptr %arg0[%o] : (!llvm.ptr<1>, i64) -> !llvm.ptr<1>, f32\n"
+                      "    %t0 = llvm.call @__tile_load_f32(%p,")
+    out = th.emit(src)
+    assert "(reinterpret_cast<const float*>(p0) + 4096ll)" in out.source
+
+
+def test_emitted_module_compiles_for_gfx950(tmp_path):
+    out = th.emit((EXAMPLES / "swiglu_mask.mlir").read_text())
+    co = tmp_path / "swiglu.hsaco"
+    th.compile_source(out.source, co)
+    assert co.stat().st_size > 1000
+
+
+def test_compile_error_is_reported(tmp_path):
+    with pytest.raises(th.HalError) as e:
+        th.compile_source("this is not C++", tmp_path / "bad.hsaco")
+    assert "hipcc failed" in str(e.value)

@@ -1,0 +1,177 @@
+"""Kernels emitted by the `hip` target, launched through the HAL launcher.
+
+The example modules (tile-rs_amd/tilers_hip/examples/*.mlir) are emitted and
+compiled to gfx950 code objects by build(); here each is loaded with
+hipModuleLoad, launched by name on a 1-D grid of logical tiles (the launch
+descriptor expands it to the hardware grid), and compared with the CPU oracle.
+"""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import tilers_hip as th
+from oracle import oracle as orc
+from tests.tolerances import (assert_attn_close, assert_gemm_close, assert_softmax_close,
+                              assert_within_ulp16)
+from tilers_hip import _build
+
+pytestmark = pytest.mark.gpu
+D = th.TileDtype
+
+
+@pytest.fixture(scope="module")
+def launcher(dev):
+    lau = dev.create_launcher()
+    for stem in ("softmax_rows", "softmax_generic", "matmul_bf16", "matmul_f16_t", "matmul_f32",
+                 "attention_f32", "prefill_bf16", "decode_bf16", "swiglu_mask"):
+        lau.load(_build.example_path(stem), th.KernelMode.GENERAL)
+    return lau
+
+
+def up(dev, s, a, dt):
+    b = dev.alloc(a.size, dt)
+    b.copy_from_host(np.ascontiguousarray(a).reshape(-1), s)
+    return b
+
+
+def ptr(b):
+    return C.c_void_p(b.as_raw_ptr())
+
+
+def test_softmax_rows_f32(dev, stream, launcher):
+    tiles = 300  # 1 x 1024 tiles, grid = tiles (the #[tile_kernel] launch shape)
+    rng = np.random.default_rng(1)
+    x = (rng.standard_normal((tiles, 1024)) * 2).astype(np.float32)
+    xb, yb = up(dev, stream, x, D.F32), dev.alloc(x.size, D.F32)
+    launcher.launch("softmax_rows_f32", th.LaunchGrid.cuda(tiles, 1024), [ptr(xb), ptr(yb)], stream)
+    assert_softmax_close(yb.copy_to_host(stream).reshape(tiles, 1024), orc.softmax(x, tiles, 1024))
+
+
+def test_softmax_generic_form_bf16(dev, stream, launcher):
+    tiles = 3  # 4 x 2048 tiles
+    rng = np.random.default_rng(2)
+    x = orc.narrow((rng.standard_normal(tiles * 4 * 2048) * 2).astype(np.float32), orc.BF16)
+    xb, yb = up(dev, stream, x, D.BF16), dev.alloc(x.size, D.BF16)
+    launcher.launch("softmax_bf16_generic", th.LaunchGrid.blocks_only(tiles), [ptr(xb), ptr(yb)], stream)
+    got = orc.widen(yb.copy_to_host(stream), orc.BF16)
+    ref = orc.softmax(orc.widen(x, orc.BF16), tiles * 4, 2048)
+    assert_within_ulp16(got, ref.reshape(-1), orc.BF16)
+
+
+def test_matmul_bf16_acc_f32_two_tiles(dev, stream, launcher):
+    tiles, M, K, N = 2, 512, 256, 384
+    rng = np.random.default_rng(3)
+    a = orc.narrow(rng.uniform(-1, 1, tiles * M * K).astype(np.float32), orc.BF16)
+    b = orc.narrow(rng.uniform(-1, 1, tiles * K * N).astype(np.float32), orc.BF16)
+    ab, bb, cb = up(dev, stream, a, D.BF16), up(dev, stream, b, D.BF16), dev.alloc(tiles * M * N, D.F32)
+    launcher.launch("matmul_bf16_acc_f32", th.LaunchGrid.blocks_only(tiles), [ptr(ab), ptr(bb), ptr(cb)],
+                    stream)
+    got = cb.copy_to_host(stream).reshape(tiles, M, N)
+    for t in range(tiles):
+        ref = orc.matmul(a[t * M * K:(t + 1) * M * K], b[t * K * N:(t + 1) * K * N], M, K, N, orc.BF16)
+        assert_gemm_close(got[t], ref, f"tile {t}")
+
+
+def test_matmul_transposed_f16_out(dev, stream, launcher):
+    M, K, N = 128, 320, 264
+    rng = np.random.default_rng(4)
+    a = orc.narrow(rng.standard_normal(M * K).astype(np.float32), orc.F16)
+    b = orc.narrow((rng.standard_normal(N * K) * 0.02).astype(np.float32), orc.F16)
+    ab, bb, cb = up(dev, stream, a, D.F16), up(dev, stream, b, D.F16), dev.alloc(M * N, D.F16)
+    launcher.launch("matmul_t_f16", th.LaunchGrid.blocks_only(1), [ptr(ab), ptr(bb), ptr(cb)], stream)
+    got = orc.widen(cb.copy_to_host(stream), orc.F16).reshape(M, N)
+    ref = orc.matmul(a, b, M, K, N, orc.F16, orc.F32, b_trans=True)
+    assert_gemm_close(got, orc.widen(orc.narrow(ref, orc.F16), orc.F16), "matmul_t_f16", u16_dtype=orc.F16)
+
+
+def test_matmul_f32_fma_integer_exact(dev, stream, launcher):
+    M, K, N = 96, 72, 80
+    rng = np.random.default_rng(5)
+    a = rng.integers(-5, 6, (M, K)).astype(np.float32)
+    b = rng.integers(-5, 6, (K, N)).astype(np.float32)
+    ab, bb, cb = up(dev, stream, a, D.F32), up(dev, stream, b, D.F32), dev.alloc(M * N, D.F32)
+    launcher.launch("matmul_f32", th.LaunchGrid.blocks_only(1), [ptr(ab), ptr(bb), ptr(cb)], stream)
+    assert np.array_equal(cb.copy_to_host(stream).reshape(M, N), (a.astype(np.int64) @ b).astype(np.float32))
+
+
+def test_attention_f32_tiles(dev, stream, launcher, golden):
+    g = golden("attention_f32.npz")
+    s, d = (int(t) for t in g["sd"])
+    tiles = 2
+    rng = np.random.default_rng(6)
+    q = np.concatenate([g["q"].reshape(-1), rng.standard_normal(s * d).astype(np.float32)])
+    k = np.concatenate([g["k"].reshape(-1), rng.standard_normal(s * d).astype(np.float32)])
+    v = np.concatenate([g["v"].reshape(-1), rng.standard_normal(s * d).astype(np.float32)])
+    bufs = [up(dev, stream, t, D.F32) for t in (q, k, v)]
+    ob = dev.alloc(tiles * s * d, D.F32)
+    launcher.launch("attention_f32", th.LaunchGrid.blocks_only(tiles), [ptr(b) for b in bufs] + [ptr(ob)],
+                    stream)
+    got = ob.copy_to_host(stream).reshape(tiles, s, d)
+    assert np.abs(got[0] - g["o"]).max() < 1e-4
+    ref1 = orc.attention_f32(q[s * d:], k[s * d:], v[s * d:], s, d)
+    assert np.abs(got[1] - ref1).max() < 1e-5
+
+
+@pytest.mark.parametrize("S,start,NH,NKV,Dh", [(200, 0, 4, 2, 128), (70, 9, 2, 1, 64)])
+def test_prefill_bf16(dev, stream, launcher, S, start, NH, NKV, Dh):
+    B, max_seq = 2, start + S + 3
+    rng = np.random.default_rng(S)
+    q = orc.narrow(rng.standard_normal(B * S * NH * Dh).astype(np.float32), orc.BF16)
+    k = orc.narrow(rng.standard_normal(B * NKV * max_seq * Dh).astype(np.float32), orc.BF16)
+    v = orc.narrow(rng.standard_normal(B * NKV * max_seq * Dh).astype(np.float32), orc.BF16)
+    bufs = [up(dev, stream, t, D.BF16) for t in (q, k, v)]
+    ob = dev.alloc(q.size, D.BF16)
+    scal = [C.c_uint32(x) for x in (S, start, max_seq, Dh, NH, NKV)]
+    launcher.launch("prefill_bf16", th.LaunchGrid.blocks_only(B), [ptr(b) for b in bufs] + [ptr(ob)] + scal,
+                    stream)
+    got = orc.widen(ob.copy_to_host(stream), orc.BF16)
+    ref = orc.attention_prefill(q, k, v, orc.BF16, B, S, start, max_seq, Dh, NH, NKV)
+    assert_attn_close(got, ref, "emitted prefill")
+
+
+@pytest.mark.parametrize("L,NH,NKV,Dh", [(700, 8, 2, 128), (1100, 16, 16, 128), (300, 6, 2, 128),
+                                         (257, 4, 1, 64)])
+def test_decode_bf16(dev, stream, launcher, L, NH, NKV, Dh):
+    B, max_seq = 3, L + 5
+    rng = np.random.default_rng(L + NH)
+    q = orc.narrow(rng.standard_normal(B * NH * Dh).astype(np.float32), orc.BF16)
+    k = orc.narrow(rng.standard_normal(B * NKV * max_seq * Dh).astype(np.float32), orc.BF16)
+    v = orc.narrow(rng.standard_normal(B * NKV * max_seq * Dh).astype(np.float32), orc.BF16)
+    bufs = [up(dev, stream, t, D.BF16) for t in (q, k, v)]
+    ob = dev.alloc(q.size, D.BF16)
+    scal = [C.c_uint32(x) for x in (L, max_seq, Dh, NH, NKV)]
+    launcher.launch("decode_bf16", th.LaunchGrid.blocks_only(B), [ptr(b) for b in bufs] + [ptr(ob)] + scal,
+                    stream)
+    got = orc.widen(ob.copy_to_host(stream), orc.BF16)
+    ref = orc.attention_decode(q, k, v, orc.BF16, B, L, max_seq, Dh, NH, NKV)
+    assert_attn_close(got, ref, "emitted decode")
+
+
+def test_elementwise_swiglu_and_scaled_causal(dev, stream, launcher):
+    rng = np.random.default_rng(7)
+    tiles = 5
+    gate = rng.standard_normal(tiles * 2 * 64).astype(np.float32)
+    upv = rng.standard_normal(tiles * 2 * 64).astype(np.float32)
+    gb, ub, ob = up(dev, stream, gate, D.F32), up(dev, stream, upv, D.F32), dev.alloc(gate.size, D.F32)
+    launcher.launch("swiglu", th.LaunchGrid.blocks_only(tiles), [ptr(gb), ptr(ub), ptr(ob)], stream)
+    g64 = gate.astype(np.float64)
+    ref = g64 / (1 + np.exp(-g64)) * upv
+    assert np.allclose(ob.copy_to_host(stream), ref, rtol=1e-5, atol=1e-6)
+
+    x = (rng.standard_normal((3, 16, 16)) * 60).astype(np.float32)
+    xb, yb = up(dev, stream, x, D.F32), dev.alloc(x.size, D.F32)
+    launcher.launch("scaled_causal", th.LaunchGrid.blocks_only(3), [ptr(xb), ptr(yb)], stream)
+    got = yb.copy_to_host(stream).reshape(3, 16, 16)
+    want = np.clip(x * np.float32(0.125), -4, 4)
+    for t in range(3):
+        assert np.array_equal(got[t].view(np.uint32),
+                              orc.causal_mask_f32(want[t], 16, 16).view(np.uint32))
+
+
+def test_unknown_kernel_name_is_a_kernel_error(dev, stream, launcher):
+    with pytest.raises(th.HalError) as e:
+        launcher.launch("no_such_kernel", th.LaunchGrid.blocks_only(1), [], stream)
+    assert e.value.kind == "KernelError" and "no_such_kernel" in str(e.value)

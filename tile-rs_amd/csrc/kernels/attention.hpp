@@ -61,36 +61,35 @@ constexpr int BQ = 256;   // query rows per workgroup
 constexpr int BKV = 64;   // KV positions per LDS stage
 constexpr int NT = 512;   // threads per workgroup (8 waves)
 constexpr float kRescaleThreshold = 8.0f;  // log2 units; see the rescale below
+// A KV block whose probability mass exceeds 1/ratio of the query's running sum
+// gets its P residual as well (bf16 keeps 8 significant bits, f16 keeps 11).
+template <int DT> constexpr float kSplitRatio = (DT == kBF16) ? 16.0f : 2.0f;
 
 __device__ __forceinline__ int k_swz(int row, int chunk) { return chunk ^ (row & 7); }
 __device__ __forceinline__ int v_swz(int row, int chunk) { return chunk ^ ((row ^ (row >> 3)) & 7); }
 }  // namespace fa
 
+// Widen a packed pair of 16-bit values.
 template <int DT>
-__global__ void __launch_bounds__(fa::NT, 1)
-attn_prefill_fa128(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
-                   const uint16_t* __restrict__ V, uint16_t* __restrict__ O, uint32_t batch,
-                   uint32_t seq_len, uint32_t start_pos, uint32_t max_seq, uint32_t nh,
-                   uint32_t nkv, float scale_log2) {
+__device__ __forceinline__ void unpack_pair(uint32_t d, float& lo, float& hi) {
+  lo = u16_to_f32<DT>(static_cast<uint16_t>(d & 0xffffu));
+  hi = u16_to_f32<DT>(static_cast<uint16_t>(d >> 16));
+}
+
+// One work item: query block `qb` (BQ rows) of flattened head `bh` = b*NH + h.
+// Called by all NT threads of a workgroup; uses the workgroup's LDS.
+template <int DT>
+__device__ __forceinline__ void prefill_tile(const uint16_t* __restrict__ Q,
+                                             const uint16_t* __restrict__ K,
+                                             const uint16_t* __restrict__ V,
+                                             uint16_t* __restrict__ O, uint32_t seq_len,
+                                             uint32_t start_pos, uint32_t max_seq, uint32_t nh,
+                                             uint32_t nkv, float scale_log2, uint32_t bh,
+                                             uint32_t qb) {
   using namespace fa;
   __shared__ u32x4 ks[2][BKV * D / 8];  // 16 KB per stage
   __shared__ u32x4 vs[2][D * BKV / 8];  // 16 KB per stage
 
-  // ---- work decode: heavy (late) query blocks first, heads dealt to XCDs ----
-  const uint32_t nqb = (seq_len + BQ - 1) / BQ;
-  const uint32_t nbh = batch * nh;
-  uint32_t bh, qb;
-  {
-    const uint32_t bid = blockIdx.x;
-    if (nbh % 8 == 0) {
-      const uint32_t xcd = bid % 8, r = bid / 8, per = nbh / 8;
-      bh = xcd + 8 * (r % per);
-      qb = nqb - 1 - r / per;
-    } else {
-      bh = bid % nbh;
-      qb = nqb - 1 - bid / nbh;
-    }
-  }
   const uint32_t b = bh / nh, h = bh % nh;
   const uint32_t kvh = h / (nh / nkv);
   const uint32_t q0 = qb * BQ;
@@ -198,19 +197,26 @@ attn_prefill_fa128(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ 
     // the end of the sequence for all of its rows.
     const bool active = (kv0 <= qa_hi) && (qw0 < seq_len);
     if (active) {
-      f32x16 s[2];
+      float s[2][16];
+      {
+        f32x16 acc[2];
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+        for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) s[i][r] = 0.0f;
+          for (int r = 0; r < 16; ++r) acc[i][r] = 0.0f;
 #pragma unroll
-      for (int ds = 0; ds < 8; ++ds) {
+        for (int ds = 0; ds < 8; ++ds) {
 #pragma unroll
-        for (int kt = 0; kt < 2; ++kt) {
-          const int row = 32 * kt + l32;
-          const u32x4 kf = ks[cur][row * 16 + k_swz(row, 2 * ds + g)];
-          s[kt] = mfma32x32x16<DT>(kf, qf[ds], s[kt]);
+          for (int kt = 0; kt < 2; ++kt) {
+            const int row = 32 * kt + l32;
+            const u32x4 kf = ks[cur][row * 16 + k_swz(row, 2 * ds + g)];
+            acc[kt] = mfma32x32x16<DT>(kf, qf[ds], acc[kt]);
+          }
         }
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) s[kt][r] = acc[kt][r];
       }
       // Causal mask only where the block crosses the diagonal.
       if (kv0 + BKV - 1 > qa_lo) {
@@ -244,30 +250,47 @@ attn_prefill_fa128(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ 
         m_run = m_new;
         m_use = m_new;
       }
-      u32x4 pf[4];
       float ls = 0.0f;
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt) {
-        float p[16];
+      for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          p[r] = exp2_fast(__builtin_fmaf(s[kt][r], scale_log2, -m_use));
-          ls += p[r];
+          s[kt][r] = exp2_fast(__builtin_fmaf(s[kt][r], scale_log2, -m_use));
+          ls += s[kt][r];
         }
-#pragma unroll
-        for (int hh = 0; hh < 2; ++hh)
-#pragma unroll
-          for (int pp = 0; pp < 4; ++pp)
-            pf[2 * kt + hh][pp] = cvt_pk<DT>(p[8 * hh + 2 * pp], p[8 * hh + 2 * pp + 1]);
-      }
       l_run += ls;
+      // P enters the MFMA as 16-bit values.  A block that carries a large share
+      // of a query's weight so far (few keys dominate: early rows, peaked
+      // scores) also gets the rounding residual P - hi(P) as a second 16-bit
+      // operand, so its products are exact to ~2^-16 instead of 2^-9 (bf16).
+      const float blk = ls + __shfl_xor(ls, 32);
+      const float tot = l_run + __shfl_xor(l_run, 32);
+      const bool heavy = blk * kSplitRatio<DT> > tot;
+      const bool split = __builtin_amdgcn_ballot_w64(heavy) != 0;
 #pragma unroll
       for (int st = 0; st < 4; ++st) {
+        const int kt = st >> 1, hh = st & 1;
+        u32x4 hi;
+#pragma unroll
+        for (int pp = 0; pp < 4; ++pp)
+          hi[pp] = cvt_pk<DT>(s[kt][8 * hh + 2 * pp], s[kt][8 * hh + 2 * pp + 1]);
+        u32x4 vf[4];
 #pragma unroll
         for (int dt = 0; dt < 4; ++dt) {
           const int row = 32 * dt + l32;
-          const u32x4 vf = vs[cur][row * 8 + v_swz(row, 2 * st + g)];
-          o_acc[dt] = mfma32x32x16<DT>(vf, pf[st], o_acc[dt]);
+          vf[dt] = vs[cur][row * 8 + v_swz(row, 2 * st + g)];
+          o_acc[dt] = mfma32x32x16<DT>(vf[dt], hi, o_acc[dt]);
+        }
+        if (split) {
+          u32x4 lo;
+#pragma unroll
+          for (int pp = 0; pp < 4; ++pp) {
+            float a, c;
+            unpack_pair<DT>(hi[pp], a, c);
+            lo[pp] = cvt_pk<DT>(s[kt][8 * hh + 2 * pp] - a, s[kt][8 * hh + 2 * pp + 1] - c);
+          }
+#pragma unroll
+          for (int dt = 0; dt < 4; ++dt) o_acc[dt] = mfma32x32x16<DT>(vf[dt], lo, o_acc[dt]);
         }
       }
     }
@@ -293,6 +316,32 @@ attn_prefill_fa128(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ 
   }
 }
 
+// Map a work index to (bh, qb): heavy (late) query blocks first; when the head
+// count allows, heads are dealt to XCDs so one head's query blocks share an L2.
+__device__ __forceinline__ void prefill_work(uint32_t w, uint32_t nbh, uint32_t nqb,
+                                             uint32_t& bh, uint32_t& qb) {
+  if (nbh % 8 == 0) {
+    const uint32_t xcd = w % 8, r = w / 8, per = nbh / 8;
+    bh = xcd + 8 * (r % per);
+    qb = nqb - 1 - r / per;
+  } else {
+    bh = w % nbh;
+    qb = nqb - 1 - w / nbh;
+  }
+}
+
+template <int DT>
+__global__ void __launch_bounds__(fa::NT, 1)
+attn_prefill_fa128(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
+                   const uint16_t* __restrict__ V, uint16_t* __restrict__ O, uint32_t batch,
+                   uint32_t seq_len, uint32_t start_pos, uint32_t max_seq, uint32_t nh,
+                   uint32_t nkv, float scale_log2) {
+  const uint32_t nqb = (seq_len + fa::BQ - 1) / fa::BQ;
+  uint32_t bh, qb;
+  prefill_work(blockIdx.x, batch * nh, nqb, bh, qb);
+  prefill_tile<DT>(Q, K, V, O, seq_len, start_pos, max_seq, nh, nkv, scale_log2, bh, qb);
+}
+
 // ============================================================================
 // Decode: one query token per head, GQA group G = NH/NKV query heads share each
 // K/V load.  Grid = B * NKV * n_split workgroups of 256 threads; each handles a
@@ -309,150 +358,196 @@ constexpr int CHUNK = 512;
 constexpr int NT = 256;
 }  // namespace dec
 
+// One work item: chunks [c_begin, c_end) of (batch, kv_head) `bk` = b*NKV + kvh.
+// With `ws` non-null the chunk range's partial (m, l, O) goes to
+// ws[((bk*G + q)*n_split + split)*(D+2)]; otherwise O = acc / l is written to
+// `O` directly (the range must then cover the whole sequence).
+template <int DT, int G>
+__device__ __forceinline__ void decode_tile(const uint16_t* __restrict__ Q,
+                                            const uint16_t* __restrict__ K,
+                                            const uint16_t* __restrict__ V,
+                                            uint16_t* __restrict__ O, float* __restrict__ ws,
+                                            uint32_t seq_len, uint32_t max_seq, uint32_t nh,
+                                            uint32_t nkv, uint32_t n_split, float scale_log2,
+                                            uint32_t bk, uint32_t split, uint32_t c_begin,
+                                            uint32_t c_end) {
+  using namespace dec;
+  __shared__ float sc[G][CHUNK];       // scores, then probabilities
+  __shared__ float red[4][G][D];       // per-wave partial O
+  __shared__ float stat_m[G], stat_l[G], stat_a[G];
+
+  const uint32_t b = bk / nkv, kvh = bk % nkv;
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int l16 = lane & 15, g4 = lane >> 4;
+
+  u32x4 qf[4];
+  {
+    const uint32_t hq = kvh * G + l16;
+    const uint16_t* qp = Q + (static_cast<size_t>(b) * nh + hq) * D;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) qf[s] = (l16 < G) ? ldg128(qp + 32 * s + 8 * g4) : u32x4{0, 0, 0, 0};
+  }
+  if (t < G) {
+    stat_m[t] = -INFINITY;
+    stat_l[t] = 0.0f;
+  }
+
+  float acc[G][8];
+#pragma unroll
+  for (int q = 0; q < G; ++q)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[q][e] = 0.0f;
+  const int dc = l16;  // this lane's d range in phase C: 8*dc .. 8*dc+7
+
+  for (uint32_t ch = c_begin; ch < c_end; ++ch) {
+    const uint32_t c0 = ch * CHUNK;
+    const uint32_t n_here = (c0 < seq_len) ? min(static_cast<uint32_t>(CHUNK), seq_len - c0) : 0u;
+    const uint16_t* kb = K + (static_cast<size_t>(bk) * max_seq + c0) * D;
+    const uint16_t* vb = V + (static_cast<size_t>(bk) * max_seq + c0) * D;
+
+    // ---- phase A: scores S^T = K . Q^T, 16 rows per MFMA tile ----
+    {
+      constexpr int TILES = CHUNK / 4 / 16;  // per wave
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        u32x4 kf[TILES / 2][4];
+#pragma unroll
+        for (int tt = 0; tt < TILES / 2; ++tt) {
+          const uint32_t row = wave * (CHUNK / 4) + (half * (TILES / 2) + tt) * 16 + l16;
+#pragma unroll
+          for (int s = 0; s < 4; ++s)
+            kf[tt][s] = (row < n_here) ? ldg128(kb + static_cast<size_t>(row) * D + 32 * s + 8 * g4)
+                                       : u32x4{0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int tt = 0; tt < TILES / 2; ++tt) {
+          f32x4 a4 = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+          for (int s = 0; s < 4; ++s) a4 = mfma16x16x32<DT>(kf[tt][s], qf[s], a4);
+          const uint32_t row0 = wave * (CHUNK / 4) + (half * (TILES / 2) + tt) * 16 + 4 * g4;
+          if (l16 < G) {
+            f32x4 w;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) w[i] = (row0 + i < n_here) ? a4[i] * scale_log2 : -INFINITY;
+            *reinterpret_cast<f32x4*>(&sc[l16][row0]) = w;
+          }
+        }
+      }
+    }
+    __syncthreads();
+
+    // ---- phase B: per-query max, exp, sum; merge with the running (m, l) ----
+    for (int q = wave; q < G; q += 4) {
+      float mx = -INFINITY;
+      for (int i = lane; i < CHUNK; i += 64) mx = fmaxf(mx, sc[q][i]);
+      mx = wave_max(mx);
+      const float m_old = stat_m[q];
+      const float m_new = fmaxf(m_old, mx);
+      float sum = 0.0f;
+      for (int i = lane; i < CHUNK; i += 64) {
+        const float p = (m_new == -INFINITY) ? 0.0f : exp2_fast(sc[q][i] - m_new);
+        sc[q][i] = p;
+        sum += p;
+      }
+      sum = wave_sum(sum);
+      if (lane == 0) {
+        const float alpha = (m_old == -INFINITY) ? 0.0f : exp2_fast(m_old - m_new);
+        stat_a[q] = alpha;
+        stat_l[q] = stat_l[q] * alpha + sum;
+        stat_m[q] = m_new;
+      }
+    }
+    __syncthreads();
+
+    // ---- phase C: acc = acc * alpha + sum_pos p[q][pos] * V[pos][d] ----
+    {
+#pragma unroll
+      for (int q = 0; q < G; ++q) {
+        const float a = stat_a[q];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[q][e] *= a;
+      }
+      constexpr int ROWS_PER_WAVE = CHUNK / 4;
+      constexpr int UNROLL = 8;
+#pragma unroll 1
+      for (int it = 0; it < ROWS_PER_WAVE / 4; it += UNROLL) {
+        u32x4 vv[UNROLL];
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u) {
+          const uint32_t row = wave * ROWS_PER_WAVE + 4 * (it + u) + g4;
+          vv[u] = (row < n_here) ? ldg128(vb + static_cast<size_t>(row) * D + 8 * dc)
+                                 : u32x4{0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u) {
+          const int row = wave * ROWS_PER_WAVE + 4 * (it + u) + g4;
+          float vf[8];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            vf[2 * e] = u16_to_f32<DT>(static_cast<uint16_t>(vv[u][e] & 0xffffu));
+            vf[2 * e + 1] = u16_to_f32<DT>(static_cast<uint16_t>(vv[u][e] >> 16));
+          }
+#pragma unroll
+          for (int q = 0; q < G; ++q) {
+            const float p = sc[q][row];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) acc[q][e] = __builtin_fmaf(p, vf[e], acc[q][e]);
+          }
+        }
+      }
+    }
+    __syncthreads();  // sc and stat_a are rewritten by the next chunk
+  }
+
+  // reduce the 4 row groups of each wave (lanes l, l^16, l^32, l^48), then the waves
+#pragma unroll
+  for (int q = 0; q < G; ++q)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float v = acc[q][e];
+      v += __shfl_xor(v, 16);
+      v += __shfl_xor(v, 32);
+      acc[q][e] = v;
+    }
+  if (g4 == 0) {
+#pragma unroll
+    for (int q = 0; q < G; ++q)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) red[wave][q][8 * dc + e] = acc[q][e];
+  }
+  __syncthreads();
+
+  for (int i = t; i < G * D; i += NT) {
+    const int q = i / D, d = i % D;
+    const float o = red[0][q][d] + red[1][q][d] + red[2][q][d] + red[3][q][d];
+    if (ws) {
+      float* rec = ws + ((static_cast<size_t>(bk) * G + q) * n_split + split) * (D + 2);
+      rec[2 + d] = o;
+      if (d == 0) {
+        rec[0] = stat_m[q];
+        rec[1] = stat_l[q];
+      }
+    } else {
+      const float l = stat_l[q];
+      const float v = (l > 0.0f) ? o / l : 0.0f;
+      O[(static_cast<size_t>(b) * nh + kvh * G + q) * D + d] = f32_to_u16<DT>(v);
+    }
+  }
+  __syncthreads();  // red and stat_* are reused by the next work item
+}
+
+// Library path: one chunk per workgroup, partials to the workspace.
 template <int DT, int G>
 __global__ void __launch_bounds__(dec::NT)
 attn_decode_split(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
                   const uint16_t* __restrict__ V, float* __restrict__ ws, uint32_t batch,
                   uint32_t seq_len, uint32_t max_seq, uint32_t nh, uint32_t nkv, uint32_t n_split,
                   float scale_log2) {
-  using namespace dec;
-  __shared__ float sc[G][CHUNK];       // scores, then probabilities
-  __shared__ float red[4][G][D];       // per-wave partial O
-  __shared__ float stat_m[G], stat_l[G];
-
+  (void)batch;
   const uint32_t split = blockIdx.x % n_split;
-  const uint32_t bk = blockIdx.x / n_split;  // b * nkv + kvh
-  const uint32_t b = bk / nkv, kvh = bk % nkv;
-  const uint32_t c0 = split * CHUNK;
-  const uint32_t n_here = (c0 < seq_len) ? min(static_cast<uint32_t>(CHUNK), seq_len - c0) : 0u;
-
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const int l16 = lane & 15, g4 = lane >> 4;
-  const uint16_t* kb = K + (static_cast<size_t>(bk) * max_seq + c0) * D;
-  const uint16_t* vb = V + (static_cast<size_t>(bk) * max_seq + c0) * D;
-
-  // ---- phase A: scores ----
-  {
-    u32x4 qf[4];
-    const uint32_t hq = kvh * G + l16;
-    const uint16_t* qp = Q + (static_cast<size_t>(b) * nh + hq) * D;
-#pragma unroll
-    for (int s = 0; s < 4; ++s) qf[s] = (l16 < G) ? ldg128(qp + 32 * s + 8 * g4) : u32x4{0, 0, 0, 0};
-    // wave w: rows [w*128, w*128+128) of the chunk, 8 tiles of 16 rows
-    constexpr int TILES = CHUNK / 4 / 16;
-#pragma unroll
-    for (int half = 0; half < 2; ++half) {
-      u32x4 kf[TILES / 2][4];
-#pragma unroll
-      for (int tt = 0; tt < TILES / 2; ++tt) {
-        const uint32_t row = wave * (CHUNK / 4) + (half * (TILES / 2) + tt) * 16 + l16;
-#pragma unroll
-        for (int s = 0; s < 4; ++s)
-          kf[tt][s] = (row < n_here) ? ldg128(kb + static_cast<size_t>(row) * D + 32 * s + 8 * g4)
-                                     : u32x4{0, 0, 0, 0};
-      }
-#pragma unroll
-      for (int tt = 0; tt < TILES / 2; ++tt) {
-        f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-#pragma unroll
-        for (int s = 0; s < 4; ++s) acc = mfma16x16x32<DT>(kf[tt][s], qf[s], acc);
-        const uint32_t row0 = wave * (CHUNK / 4) + (half * (TILES / 2) + tt) * 16 + 4 * g4;
-        if (l16 < G) {
-          f32x4 w;
-#pragma unroll
-          for (int i = 0; i < 4; ++i) w[i] = (row0 + i < n_here) ? acc[i] * scale_log2 : -INFINITY;
-          *reinterpret_cast<f32x4*>(&sc[l16][row0]) = w;
-        }
-      }
-    }
-  }
-  __syncthreads();
-
-  // ---- phase B: per-query max, exp, sum ----
-  for (int q = wave; q < G; q += 4) {
-    float mx = -INFINITY;
-    for (int i = lane; i < CHUNK; i += 64) mx = fmaxf(mx, sc[q][i]);
-    mx = wave_max(mx);
-    float sum = 0.0f;
-    for (int i = lane; i < CHUNK; i += 64) {
-      const float p = (mx == -INFINITY) ? 0.0f : exp2_fast(sc[q][i] - mx);
-      sc[q][i] = p;
-      sum += p;
-    }
-    sum = wave_sum(sum);
-    if (lane == 0) {
-      stat_m[q] = mx;
-      stat_l[q] = sum;
-    }
-  }
-  __syncthreads();
-
-  // ---- phase C: O_partial[q][d] = sum_pos p[q][pos] * V[pos][d] ----
-  {
-    float acc[G][8];
-#pragma unroll
-    for (int q = 0; q < G; ++q)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) acc[q][e] = 0.0f;
-    const int dc = l16;  // d = 8*dc .. 8*dc+7
-    constexpr int ROWS_PER_WAVE = CHUNK / 4;
-    constexpr int UNROLL = 8;
-#pragma unroll 1
-    for (int it = 0; it < ROWS_PER_WAVE / 4; it += UNROLL) {
-      u32x4 vv[UNROLL];
-#pragma unroll
-      for (int u = 0; u < UNROLL; ++u) {
-        const uint32_t row = wave * ROWS_PER_WAVE + 4 * (it + u) + g4;
-        vv[u] = (row < n_here) ? ldg128(vb + static_cast<size_t>(row) * D + 8 * dc)
-                               : u32x4{0, 0, 0, 0};
-      }
-#pragma unroll
-      for (int u = 0; u < UNROLL; ++u) {
-        const int row = wave * ROWS_PER_WAVE + 4 * (it + u) + g4;
-        float vf[8];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          vf[2 * e] = u16_to_f32<DT>(static_cast<uint16_t>(vv[u][e] & 0xffffu));
-          vf[2 * e + 1] = u16_to_f32<DT>(static_cast<uint16_t>(vv[u][e] >> 16));
-        }
-#pragma unroll
-        for (int q = 0; q < G; ++q) {
-          const float p = sc[q][row];
-#pragma unroll
-          for (int e = 0; e < 8; ++e) acc[q][e] = __builtin_fmaf(p, vf[e], acc[q][e]);
-        }
-      }
-    }
-    // reduce the 4 row groups of the wave (lanes l, l^16, l^32, l^48)
-#pragma unroll
-    for (int q = 0; q < G; ++q)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        float v = acc[q][e];
-        v += __shfl_xor(v, 16);
-        v += __shfl_xor(v, 32);
-        acc[q][e] = v;
-      }
-    if (g4 == 0) {
-#pragma unroll
-      for (int q = 0; q < G; ++q)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) red[wave][q][8 * dc + e] = acc[q][e];
-    }
-  }
-  __syncthreads();
-
-  // ---- write the partial result: ws[(bk*G + q)*n_split + split] = {m, l, O[D]} ----
-  for (int i = t; i < G * D; i += NT) {
-    const int q = i / D, d = i % D;
-    const float o = red[0][q][d] + red[1][q][d] + red[2][q][d] + red[3][q][d];
-    float* rec = ws + ((static_cast<size_t>(bk) * G + q) * n_split + split) * (D + 2);
-    rec[2 + d] = o;
-    if (d == 0) {
-      rec[0] = stat_m[q];
-      rec[1] = stat_l[q];
-    }
-  }
+  const uint32_t bk = blockIdx.x / n_split;
+  decode_tile<DT, G>(Q, K, V, nullptr, ws, seq_len, max_seq, nh, nkv, n_split, scale_log2, bk,
+                     split, split, split + 1);
 }
 
 // Merge the per-chunk partials: O = sum_s 2^(m_s - M) O_s / sum_s 2^(m_s - M) l_s.
@@ -489,19 +584,21 @@ attn_decode_combine(const float* __restrict__ ws, uint16_t* __restrict__ O, uint
 // q_pos_stride is the element stride between consecutive query rows of one head
 // (NH*D for [S][NH][D]); kv tensors are [B][NKV][max_seq][D].
 // ============================================================================
-template <int DT>
-__global__ void __launch_bounds__(256)
-attn_general(const void* __restrict__ Q, const void* __restrict__ K, const void* __restrict__ V,
-             void* __restrict__ O, uint32_t batch, uint32_t seq_len, uint32_t start_pos,
-             uint32_t max_seq, uint32_t kv_len, uint32_t head_dim, uint32_t nh, uint32_t nkv,
-             int causal, float scale) {
+template <int DT, int NT = 256>
+__device__ __forceinline__ void attn_general_item(
+    const void* __restrict__ Q, const void* __restrict__ K, const void* __restrict__ V,
+    void* __restrict__ O, uint32_t seq_len, uint32_t start_pos, uint32_t max_seq,
+    uint32_t kv_len, uint32_t head_dim, uint32_t nh, uint32_t nkv, int causal, float scale,
+    uint32_t item) {
   constexpr int CH = 1024;
+  constexpr int NW = NT / 64;
+  static_assert(NT >= 256 && NT % 64 == 0, "head_dim up to 256 needs >= 256 threads");
   __shared__ float qs[256];
   __shared__ float sc[CH];
-  __shared__ float red[4];
-  const uint32_t h = blockIdx.x % nh;
-  const uint32_t qi = (blockIdx.x / nh) % seq_len;
-  const uint32_t b = blockIdx.x / (nh * seq_len);
+  __shared__ float red[NW];
+  const uint32_t h = item % nh;
+  const uint32_t qi = (item / nh) % seq_len;
+  const uint32_t b = item / (nh * seq_len);
   const uint32_t kvh = h / (nh / nkv);
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
   auto ld = [&](const void* p, size_t i) -> float {
@@ -510,13 +607,13 @@ attn_general(const void* __restrict__ Q, const void* __restrict__ K, const void*
   };
   const size_t q_off = ((static_cast<size_t>(b) * seq_len + qi) * nh + h) * head_dim;
   const size_t kv_off = (static_cast<size_t>(b) * nkv + kvh) * max_seq * head_dim;
-  for (uint32_t d = t; d < head_dim; d += 256) qs[d] = ld(Q, q_off + d);
+  for (uint32_t d = t; d < head_dim; d += NT) qs[d] = ld(Q, q_off + d);
   __syncthreads();
   const uint32_t visible = causal ? min(start_pos + qi + 1, kv_len) : kv_len;
   float m_run = -INFINITY, l_run = 0.0f, acc = 0.0f;  // acc: d = t
   for (uint32_t c0 = 0; c0 < visible; c0 += CH) {
     const uint32_t n = min(static_cast<uint32_t>(CH), visible - c0);
-    for (uint32_t p = t; p < n; p += 256) {
+    for (uint32_t p = t; p < n; p += NT) {
       const size_t kr = kv_off + static_cast<size_t>(c0 + p) * head_dim;
       float dot = 0.0f;
       for (uint32_t d = 0; d < head_dim; ++d) dot = __builtin_fmaf(qs[d], ld(K, kr + d), dot);
@@ -524,16 +621,18 @@ attn_general(const void* __restrict__ Q, const void* __restrict__ K, const void*
     }
     __syncthreads();
     float mx = -INFINITY;
-    for (uint32_t p = t; p < n; p += 256) mx = fmaxf(mx, sc[p]);
+    for (uint32_t p = t; p < n; p += NT) mx = fmaxf(mx, sc[p]);
     mx = wave_max(mx);
     if (lane == 0) red[wave] = mx;
     __syncthreads();
-    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    mx = red[0];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) mx = fmaxf(mx, red[w]);
     __syncthreads();
     const float m_new = fmaxf(m_run, mx);
     const float alpha = expf(m_run - m_new);
     float sum = 0.0f;
-    for (uint32_t p = t; p < n; p += 256) {
+    for (uint32_t p = t; p < n; p += NT) {
       const float e = expf(sc[p] - m_new);
       sc[p] = e;
       sum += e;
@@ -541,7 +640,9 @@ attn_general(const void* __restrict__ Q, const void* __restrict__ K, const void*
     sum = wave_sum(sum);
     if (lane == 0) red[wave] = sum;
     __syncthreads();
-    sum = (red[0] + red[1]) + (red[2] + red[3]);
+    sum = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) sum += red[w];
     l_run = l_run * alpha + sum;
     if (static_cast<uint32_t>(t) < head_dim) {
       float a = acc * alpha;
@@ -557,6 +658,17 @@ attn_general(const void* __restrict__ Q, const void* __restrict__ K, const void*
     if constexpr (DT == kF32) static_cast<float*>(O)[q_off + t] = o;
     else static_cast<uint16_t*>(O)[q_off + t] = f32_to_u16<DT>(o);
   }
+}
+
+template <int DT>
+__global__ void __launch_bounds__(256)
+attn_general(const void* __restrict__ Q, const void* __restrict__ K, const void* __restrict__ V,
+             void* __restrict__ O, uint32_t batch, uint32_t seq_len, uint32_t start_pos,
+             uint32_t max_seq, uint32_t kv_len, uint32_t head_dim, uint32_t nh, uint32_t nkv,
+             int causal, float scale) {
+  (void)batch;
+  attn_general_item<DT>(Q, K, V, O, seq_len, start_pos, max_seq, kv_len, head_dim, nh, nkv,
+                        causal, scale, blockIdx.x);
 }
 
 // Causal mask on an f32 tile (mlir_to_linalg.rs:1191-1247): y = x where col <= row,

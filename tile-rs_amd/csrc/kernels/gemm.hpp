@@ -55,24 +55,16 @@ __device__ __forceinline__ void tile_coords(uint32_t bid, uint32_t tiles_m, uint
 
 }  // namespace gemm
 
-// A: M x K (K contiguous).  B: K x N (N contiguous) or, with B_TRANS, N x K.
-// Requires K % 8 == 0 and, for row-major B, N % 8 == 0; M, N, K tails are handled
-// by zero-filled loads and predicated stores.  Batch index = blockIdx.y with
-// element strides sa, sb, sc.
+// One 256x256 output tile (tm, tn) of C = A*B by a whole workgroup.
 template <int DT, int DT_OUT, bool B_TRANS>
-__global__ void __launch_bounds__(gemm::NT, 1)
-gemm_mfma_256(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, void* __restrict__ C,
-              uint32_t M, uint32_t N, uint32_t K, uint64_t sa, uint64_t sb, uint64_t sc) {
+__device__ __forceinline__ void gemm_tile_256(const uint16_t* __restrict__ A,
+                                              const uint16_t* __restrict__ B,
+                                              void* __restrict__ C, uint32_t M, uint32_t N,
+                                              uint32_t K, uint32_t tm, uint32_t tn) {
   using namespace gemm;
   __shared__ u32x4 lds_a[2][BM * BK / 8];
   __shared__ u32x4 lds_b[2][BN * BK / 8];
-
-  const uint32_t tiles_m = (M + BM - 1) / BM, tiles_n = (N + BN - 1) / BN;
-  uint32_t tm, tn;
-  tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
   const uint32_t m0 = tm * BM, n0 = tn * BN;
-  A += blockIdx.y * sa;
-  B += blockIdx.y * sb;
 
   const int t = threadIdx.x;
   const int lane = t & 63, wave = t >> 6;
@@ -184,7 +176,7 @@ gemm_mfma_256(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, vo
       for (int r = 0; r < 16; ++r) {
         const uint32_t row = m0 + wm * 128 + mi * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
         if (row < M && col < N) {
-          const size_t off = blockIdx.y * sc + static_cast<size_t>(row) * N + col;
+          const size_t off = static_cast<size_t>(row) * N + col;
           if constexpr (DT_OUT == kF32) {
             static_cast<float*>(C)[off] = acc[mi][ni][r];
           } else {
@@ -195,17 +187,33 @@ gemm_mfma_256(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, vo
     }
 }
 
+// A: M x K (K contiguous).  B: K x N (N contiguous) or, with B_TRANS, N x K.
+// Requires K % 8 == 0 and, for row-major B, N % 8 == 0; M, N, K tails are handled
+// by zero-filled loads and predicated stores.  Batch index = blockIdx.y with
+// element strides sa, sb, sc.
+template <int DT, int DT_OUT, bool B_TRANS>
+__global__ void __launch_bounds__(gemm::NT, 1)
+gemm_mfma_256(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, void* __restrict__ C,
+              uint32_t M, uint32_t N, uint32_t K, uint64_t sa, uint64_t sb, uint64_t sc) {
+  const uint32_t tiles_m = (M + gemm::BM - 1) / gemm::BM, tiles_n = (N + gemm::BN - 1) / gemm::BN;
+  uint32_t tm, tn;
+  gemm::tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  constexpr int OSZ = (DT_OUT == kF32) ? 4 : 2;
+  gemm_tile_256<DT, DT_OUT, B_TRANS>(A + blockIdx.y * sa, B + blockIdx.y * sb,
+                                     static_cast<char*>(C) + blockIdx.y * sc * OSZ, M, N, K, tm, tn);
+}
+
 // Fallback for shapes the MFMA path does not take (K % 8 != 0, row-major B with
 // N % 8 != 0) and for f32 operands: 64x64 tile per 256-thread workgroup, each
 // thread a 4x4 block, K staged 16 at a time through LDS, f32 FMA.
 template <int DT, int DT_OUT, bool B_TRANS>
-__global__ void __launch_bounds__(256)
-gemm_fma_64(const void* __restrict__ A, const void* __restrict__ B, void* __restrict__ C,
-            uint32_t M, uint32_t N, uint32_t K, uint64_t sa, uint64_t sb, uint64_t sc) {
+__device__ __forceinline__ void gemm_fma_tile_64(const void* __restrict__ A,
+                                                 const void* __restrict__ B, void* __restrict__ C,
+                                                 uint32_t M, uint32_t N, uint32_t K, uint32_t tile) {
   __shared__ float as[16][64 + 4];
   __shared__ float bs[16][64 + 4];
-  const uint32_t m0 = blockIdx.x / ((N + 63) / 64) * 64;
-  const uint32_t n0 = blockIdx.x % ((N + 63) / 64) * 64;
+  const uint32_t m0 = tile / ((N + 63) / 64) * 64;
+  const uint32_t n0 = tile % ((N + 63) / 64) * 64;
   const int t = threadIdx.x;
   const int tr = t / 16, tc = t % 16;
   float acc[4][4] = {};
@@ -213,7 +221,7 @@ gemm_fma_64(const void* __restrict__ A, const void* __restrict__ B, void* __rest
     if constexpr (DT == kF32) return static_cast<const float*>(p)[i];
     else return u16_to_f32<DT>(static_cast<const uint16_t*>(p)[i]);
   };
-  const size_t boffA = blockIdx.y * sa, boffB = blockIdx.y * sb;
+  const size_t boffA = 0, boffB = 0;
   for (uint32_t k0 = 0; k0 < K; k0 += 16) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -250,11 +258,23 @@ gemm_fma_64(const void* __restrict__ A, const void* __restrict__ B, void* __rest
     for (int j = 0; j < 4; ++j) {
       const uint32_t row = m0 + tr * 4 + i, col = n0 + tc * 4 + j;
       if (row < M && col < N) {
-        const size_t off = blockIdx.y * sc + static_cast<size_t>(row) * N + col;
+        const size_t off = static_cast<size_t>(row) * N + col;
         if constexpr (DT_OUT == kF32) static_cast<float*>(C)[off] = acc[i][j];
         else static_cast<uint16_t*>(C)[off] = f32_to_u16<DT_OUT>(acc[i][j]);
       }
     }
+}
+
+template <int DT, int DT_OUT, bool B_TRANS>
+__global__ void __launch_bounds__(256)
+gemm_fma_64(const void* __restrict__ A, const void* __restrict__ B, void* __restrict__ C,
+            uint32_t M, uint32_t N, uint32_t K, uint64_t sa, uint64_t sb, uint64_t sc) {
+  constexpr int ISZ = (DT == kF32) ? 4 : 2;
+  constexpr int OSZ = (DT_OUT == kF32) ? 4 : 2;
+  gemm_fma_tile_64<DT, DT_OUT, B_TRANS>(static_cast<const char*>(A) + blockIdx.y * sa * ISZ,
+                                        static_cast<const char*>(B) + blockIdx.y * sb * ISZ,
+                                        static_cast<char*>(C) + blockIdx.y * sc * OSZ, M, N, K,
+                                        blockIdx.x);
 }
 
 }  // namespace th

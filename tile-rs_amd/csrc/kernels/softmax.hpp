@@ -48,20 +48,16 @@ __device__ __forceinline__ u32x4 pack16(const float (&f)[SoftmaxVec<DT>::kElems]
   return v;
 }
 
-// Register path: NV 16-byte vectors per lane, so a row holds up to
-// 64 * NV * kElems elements.  Requires cols % kElems == 0 and 16-byte aligned rows.
-// Rows per workgroup = blockDim.x / 64.
+// Register path: one wavefront owns one row; NV 16-byte vectors per lane, so a
+// row holds up to 64 * NV * kElems elements.  Requires cols % kElems == 0 and
+// 16-byte aligned rows.  xr / yr point at the row.
 template <int DT, int NV>
-__global__ void __launch_bounds__(256)
-softmax_rows_reg(const void* __restrict__ x, void* __restrict__ y, uint32_t rows, uint32_t cols) {
+__device__ __forceinline__ void softmax_row_wave(const void* __restrict__ xr_,
+                                                 void* __restrict__ yr_, uint32_t cols, int lane) {
   constexpr int E = SoftmaxVec<DT>::kElems;
-  constexpr int ESZ = (DT == kF32) ? 4 : 2;
-  const int lane = threadIdx.x & 63;
-  const uint32_t row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
-  if (row >= rows) return;
   const uint32_t nvec = cols / E;  // 16-byte vectors in this row
-  const char* xr = static_cast<const char*>(x) + static_cast<size_t>(row) * cols * ESZ;
-  char* yr = static_cast<char*>(y) + static_cast<size_t>(row) * cols * ESZ;
+  const char* xr = static_cast<const char*>(xr_);
+  char* yr = static_cast<char*>(yr_);
 
   float v[NV][E];
   float m = -INFINITY;
@@ -102,6 +98,41 @@ softmax_rows_reg(const void* __restrict__ x, void* __restrict__ y, uint32_t rows
       stg128_nt(yr + static_cast<size_t>(vi) * 16, pack16<DT>(v[i]));
     }
   }
+}
+
+// Rows per workgroup = blockDim.x / 64.
+template <int DT, int NV>
+__global__ void __launch_bounds__(256)
+softmax_rows_reg(const void* __restrict__ x, void* __restrict__ y, uint32_t rows, uint32_t cols) {
+  constexpr int ESZ = (DT == kF32) ? 4 : 2;
+  const uint32_t row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const size_t off = static_cast<size_t>(row) * cols * ESZ;
+  softmax_row_wave<DT, NV>(static_cast<const char*>(x) + off, static_cast<char*>(y) + off, cols,
+                           threadIdx.x & 63);
+}
+
+// Any cols, one wavefront per row, three passes over the row (no LDS).
+template <int DT>
+__device__ __forceinline__ float ld_elem(const void* p, size_t i);
+template <int DT>
+__device__ __forceinline__ void st_elem(void* p, size_t i, float v);
+
+template <int DT>
+__device__ __forceinline__ void softmax_row_wave_any(const void* __restrict__ xr,
+                                                     void* __restrict__ yr, uint32_t cols,
+                                                     int lane) {
+  float m = -INFINITY;
+  for (uint32_t c = lane; c < cols; c += 64) m = fmaxf(m, ld_elem<DT>(xr, c));
+  m = wave_max(m);
+  const float mb = m * kLog2e;
+  float s = 0.0f;
+  for (uint32_t c = lane; c < cols; c += 64)
+    s += exp2_fast(__builtin_fmaf(ld_elem<DT>(xr, c), kLog2e, -mb));
+  s = wave_sum(s);
+  const float inv = 1.0f / s;
+  for (uint32_t c = lane; c < cols; c += 64)
+    st_elem<DT>(yr, c, exp2_fast(__builtin_fmaf(ld_elem<DT>(xr, c), kLog2e, -mb)) * inv);
 }
 
 // Generic path for any cols (ragged, unaligned or longer than the register path

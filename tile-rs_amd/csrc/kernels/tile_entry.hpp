@@ -1,0 +1,147 @@
+// Device-side entry points for kernels emitted by the `hip` codegen target.
+//
+// An emitted tile kernel is a thin extern "C" __global__ wrapper around one of
+// these.  Each loops over its work items grid-stride (item w is handled by
+// workgroup w mod gridDim.x), so results never depend on the hardware grid the
+// launcher picks from the kernel's launch descriptor; the descriptor only sizes
+// the grid.  Per-tile pointer offsets follow the #[tile_kernel] prelude: logical
+// tile t sees every view offset by t * rows * cols of that view
+// (crates/tile_std_macros/src/lib.rs:217-266).
+#pragma once
+
+#include "../launch_desc.hpp"
+#include "attention.hpp"
+#include "common.hpp"
+#include "gemm.hpp"
+#include "softmax.hpp"
+
+namespace th {
+namespace entry {
+
+// ---- row softmax over `rows` contiguous rows of `cols` (one wavefront per row) ----
+template <int DT, int NV>
+__device__ __forceinline__ void softmax_rows(const void* x, void* y, uint32_t rows, uint32_t cols) {
+  constexpr int ESZ = (DT == kF32) ? 4 : 2;
+  const uint32_t wpg = blockDim.x >> 6;
+  const int lane = threadIdx.x & 63;
+  for (uint32_t r = blockIdx.x * wpg + (threadIdx.x >> 6); r < rows; r += gridDim.x * wpg) {
+    const size_t off = static_cast<size_t>(r) * cols * ESZ;
+    const char* xr = static_cast<const char*>(x) + off;
+    char* yr = static_cast<char*>(y) + off;
+    if constexpr (NV > 0) softmax_row_wave<DT, NV>(xr, yr, cols, lane);
+    else softmax_row_wave_any<DT>(xr, yr, cols, lane);
+  }
+}
+
+// ---- batched GEMM: `batch` stacked problems, dense strides ----
+template <int DT, int DTO, bool BT>
+__device__ __forceinline__ void gemm(const uint16_t* A, const uint16_t* B, void* C, uint32_t M,
+                                     uint32_t N, uint32_t K, uint32_t batch) {
+  constexpr int OSZ = (DTO == kF32) ? 4 : 2;
+  const uint32_t tiles_m = (M + gemm::BM - 1) / gemm::BM, tiles_n = (N + gemm::BN - 1) / gemm::BN;
+  const uint32_t per = tiles_m * tiles_n;
+  for (uint32_t w = blockIdx.x; w < per * batch; w += gridDim.x) {
+    const uint32_t bi = w / per;
+    uint32_t tm, tn;
+    gemm::tile_coords(w % per, tiles_m, tiles_n, tm, tn);
+    gemm_tile_256<DT, DTO, BT>(A + static_cast<size_t>(bi) * M * K,
+                               B + static_cast<size_t>(bi) * K * N,
+                               static_cast<char*>(C) + static_cast<size_t>(bi) * M * N * OSZ, M, N,
+                               K, tm, tn);
+  }
+}
+
+template <int DT, int DTO, bool BT>
+__device__ __forceinline__ void gemm_fma(const void* A, const void* B, void* C, uint32_t M,
+                                         uint32_t N, uint32_t K, uint32_t batch) {
+  constexpr int ISZ = (DT == kF32) ? 4 : 2;
+  constexpr int OSZ = (DTO == kF32) ? 4 : 2;
+  const uint32_t per = ((M + 63) / 64) * ((N + 63) / 64);
+  for (uint32_t w = blockIdx.x; w < per * batch; w += gridDim.x) {
+    const uint32_t bi = w / per;
+    gemm_fma_tile_64<DT, DTO, BT>(static_cast<const char*>(A) + static_cast<size_t>(bi) * M * K * ISZ,
+                                  static_cast<const char*>(B) + static_cast<size_t>(bi) * K * N * ISZ,
+                                  static_cast<char*>(C) + static_cast<size_t>(bi) * M * N * OSZ, M,
+                                  N, K, w % per);
+  }
+}
+
+// ---- single-head non-causal attention on S x D tiles (__tile_attention_f32) ----
+template <int DT, int NT>
+__device__ __forceinline__ void attention_tiles(const void* q, const void* k, const void* v,
+                                                void* o, uint32_t s, uint32_t d, uint32_t tiles) {
+  const float scale = static_cast<float>(1.0 / __builtin_sqrt(static_cast<double>(d)));
+  for (uint32_t w = blockIdx.x; w < tiles * s; w += gridDim.x)
+    attn_general_item<DT, NT>(q, k, v, o, s, 0, s, s, d, 1, 1, 0, scale, w);
+}
+
+// ---- causal GQA prefill; runtime params in the Metal target's order ----
+template <int DT>
+__device__ __forceinline__ void prefill(const void* q, const void* k, const void* v, void* o,
+                                        uint32_t batch, uint32_t seq_len, uint32_t start_pos,
+                                        uint32_t max_seq, uint32_t head_dim, uint32_t nh,
+                                        uint32_t nkv) {
+  if (nkv == 0 || nh % nkv != 0 || start_pos + seq_len > max_seq || head_dim == 0) return;
+  const float scale = 1.0f / __builtin_sqrtf(static_cast<float>(head_dim));
+  if constexpr (DT != kF32) {
+    if (head_dim == fa::D) {
+      const uint32_t nqb = (seq_len + fa::BQ - 1) / fa::BQ;
+      for (uint32_t w = blockIdx.x; w < batch * nh * nqb; w += gridDim.x) {
+        uint32_t bh, qb;
+        prefill_work(w, batch * nh, nqb, bh, qb);
+        prefill_tile<DT>(static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
+                         static_cast<const uint16_t*>(v), static_cast<uint16_t*>(o), seq_len,
+                         start_pos, max_seq, nh, nkv, scale * kLog2e, bh, qb);
+      }
+      return;
+    }
+  }
+  if (head_dim <= 256) {
+    for (uint32_t w = blockIdx.x; w < batch * seq_len * nh; w += gridDim.x)
+      attn_general_item<DT, fa::NT>(q, k, v, o, seq_len, start_pos, max_seq, start_pos + seq_len,
+                                    head_dim, nh, nkv, 1, scale, w);
+  }
+}
+
+// ---- GQA decode, one query token; runtime params in the Metal target's order ----
+template <int DT, int G>
+__device__ __forceinline__ void decode_group(const uint16_t* q, const uint16_t* k,
+                                             const uint16_t* v, uint16_t* o, uint32_t batch,
+                                             uint32_t seq_len, uint32_t max_seq, uint32_t nh,
+                                             uint32_t nkv, float scale_log2) {
+  const uint32_t nchunks = (seq_len + dec::CHUNK - 1) / dec::CHUNK;
+  for (uint32_t w = blockIdx.x; w < batch * nkv; w += gridDim.x)
+    decode_tile<DT, G>(q, k, v, o, nullptr, seq_len, max_seq, nh, nkv, 1, scale_log2, w, 0, 0,
+                       nchunks);
+}
+
+template <int DT>
+__device__ __forceinline__ void decode(const void* q, const void* k, const void* v, void* o,
+                                       uint32_t batch, uint32_t seq_len, uint32_t max_seq,
+                                       uint32_t head_dim, uint32_t nh, uint32_t nkv) {
+  if (nkv == 0 || nh % nkv != 0 || seq_len > max_seq || head_dim == 0 || head_dim > 256) return;
+  const float scale = 1.0f / __builtin_sqrtf(static_cast<float>(head_dim));
+  const uint32_t g = nh / nkv;
+  if constexpr (DT != kF32) {
+    if (head_dim == dec::D && seq_len > 0) {
+      const float sl2 = scale * kLog2e;
+      auto Q = static_cast<const uint16_t*>(q);
+      auto K = static_cast<const uint16_t*>(k);
+      auto V = static_cast<const uint16_t*>(v);
+      auto O = static_cast<uint16_t*>(o);
+      switch (g) {
+        case 1: decode_group<DT, 1>(Q, K, V, O, batch, seq_len, max_seq, nh, nkv, sl2); return;
+        case 2: decode_group<DT, 2>(Q, K, V, O, batch, seq_len, max_seq, nh, nkv, sl2); return;
+        case 4: decode_group<DT, 4>(Q, K, V, O, batch, seq_len, max_seq, nh, nkv, sl2); return;
+        case 8: decode_group<DT, 8>(Q, K, V, O, batch, seq_len, max_seq, nh, nkv, sl2); return;
+        default: break;
+      }
+    }
+  }
+  for (uint32_t w = blockIdx.x; w < batch * nh; w += gridDim.x)
+    attn_general_item<DT, dec::NT>(q, k, v, o, 1, 0, max_seq, seq_len, head_dim, nh, nkv, 0,
+                                   scale, w);
+}
+
+}  // namespace entry
+}  // namespace th

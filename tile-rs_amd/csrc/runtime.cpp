@@ -146,6 +146,12 @@ int th_device_open(uint32_t ordinal, th_device* out) {
   d->ordinal = static_cast<int>(ordinal);
   d->name = p.name;
   d->arch = p.gcnArchName;
+  if (d->name.empty()) {
+    char buf[256] = {0};
+    if (hipDeviceGetName(buf, sizeof(buf), static_cast<int>(ordinal)) == hipSuccess) d->name = buf;
+    (void)hipGetLastError();
+  }
+  if (d->name.empty()) d->name = "AMD Instinct GPU (" + d->arch.substr(0, d->arch.find(':')) + ")";
   d->cus = p.multiProcessorCount;
   *out = d;
   return TH_OK;

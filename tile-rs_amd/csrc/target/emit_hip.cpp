@@ -1,0 +1,650 @@
+// The `hip` codegen target: MLIR text -> HIP C++ for gfx950.
+//
+// Mirrors the emitter contract of the reference (`convert_mlir_to_<t>(&str) ->
+// Result<String, String>` wrapped by EmitterTarget, crates/tile_codegen/src/
+// targets.rs:82-101): pure, deterministic, and an error for a module with no
+// entry kernel (mlir_to_linalg.rs:82-84) or an op it cannot lower
+// (mlir_to_linalg.rs:608-612).
+//
+// Lowering (the "hook" that maps tile ops to hand-written kernels):
+//   load -> __tile_softmax_{f32,f16}            -> store : th::entry::softmax_rows
+//   load, load -> __tile_matmul_{f16,f32}        -> store : th::entry::gemm (MFMA) / gemm_fma
+//   load, load -> __tile_matmul_transposed_*     -> store : same, B stored N x K
+//   load x3 -> __tile_attention_f32              -> store : th::entry::attention_tiles
+//   load x3 -> __tile_attention_prefill_f32      -> store : th::entry::prefill
+//   load x3 -> __tile_attention_decode_f32       -> store : th::entry::decode
+//   any DAG of elementwise tile ops              -> a plain HIP per-element kernel
+// Per-tile pointer offsets follow the #[tile_kernel] prelude: logical tile t
+// offsets each view by t * rows * cols (crates/tile_std_macros/src/lib.rs:242).
+//
+// Side channels the trait cannot carry:
+//   - bf16: tile_std carries f16 and bf16 in one u16 type (tile_std/src/lib.rs:
+//     182).  A u16 load/store is bf16 when its callee says so
+//     (__tile_load_bf16, as mlir_to_pto.rs:5666-5690 reads it) or when the
+//     kernel or pointer-argument name contains "bf16" (the name convention of
+//     infer_dtype_from_name, mlir_to_pto.rs:5648-5654); otherwise f16.
+//   - attention runtime scalars: appended as trailing uint32_t kernel
+//     parameters after the buffers, in the Metal target's order
+//     (mlir_to_msl.rs:1816-1823 decode, :1851-1859 prefill).
+// Every emitted kernel also takes a hidden trailing `uint32_t th_tiles` (the
+// logical tile count) and carries a launch descriptor `__th_desc_<name>`.
+#include <cctype>
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <iomanip>
+#include <map>
+#include <set>
+#include <sstream>
+#include <string>
+#include <vector>
+
+#include "launch_desc.hpp"
+#include "target/emit.hpp"
+#include "target/mlir_parse.hpp"
+
+namespace th {
+namespace target {
+namespace {
+
+enum Dt { F32 = 0, F16 = 1, BF16 = 2 };
+
+const char* dt_name(int d) { return d == F32 ? "f32" : d == F16 ? "f16" : "bf16"; }
+const char* dt_enum(int d) { return d == F32 ? "th::kF32" : d == F16 ? "th::kF16" : "th::kBF16"; }
+const char* dt_ctype(int d) { return d == F32 ? "float" : "uint16_t"; }
+
+struct PtrRef {
+  int arg = -1;         // index into the kernel's GM pointer list
+  long long offset = 0; // element offset from the argument
+};
+
+struct TileVal {
+  std::string op;                  // "load" or the intrinsic name
+  std::vector<std::string> ins;    // operand tiles
+  std::vector<double> scalars;     // scalar operands (scale, clamp bounds, fill value)
+  long long rows = 0, cols = 0;
+  int dtype = F32;
+  PtrRef src;                      // for loads
+};
+
+struct Store {
+  PtrRef dst;
+  std::string value;
+  long long rows = 0, cols = 0;
+  int dtype = F32;
+};
+
+struct Kernel {
+  std::string name;
+  std::vector<mlir::FuncArg> gm;              // pointer args in order
+  std::map<std::string, int> gm_index;        // arg name -> position
+  std::map<std::string, double> consts;       // SSA -> numeric constant
+  std::set<std::string> block_derived;        // SSA values computed from get_block_idx
+  std::map<std::string, PtrRef> ptrs;         // SSA -> pointer (arg, offset)
+  std::map<std::string, TileVal> tiles;       // SSA -> tile
+  std::vector<Store> stores;
+  bool bf16_hint = false;
+};
+
+std::string ssa_token(const std::string& s) {
+  size_t e = 0;
+  while (e < s.size() && (std::isalnum(static_cast<unsigned char>(s[e])) || s[e] == '%' ||
+                          s[e] == '_' || s[e] == '#'))
+    ++e;
+  return s.substr(0, e);
+}
+
+bool parse_number(const std::string& txt, double* v) {
+  const std::string t = mlir::trim(txt);
+  if (t == "true") { *v = 1; return true; }
+  if (t == "false") { *v = 0; return true; }
+  char* end = nullptr;
+  const double d = std::strtod(t.c_str(), &end);
+  if (end == t.c_str()) return false;
+  *v = d;
+  return true;
+}
+
+class Lowerer {
+ public:
+  Lowerer(const mlir::Func& f, std::string* err) : f_(f), err_(err) {}
+
+  bool analyze(Kernel* k) {
+    k->name = f_.name;
+    for (const auto& a : f_.args) {
+      if (a.is_gm) {
+        k->gm_index[a.name] = static_cast<int>(k->gm.size());
+        k->ptrs[a.name] = PtrRef{static_cast<int>(k->gm.size()), 0};
+        k->gm.push_back(a);
+        if (a.name.find("bf16") != std::string::npos) k->bf16_hint = true;
+      }
+    }
+    if (k->name.find("bf16") != std::string::npos) k->bf16_hint = true;
+    for (const std::string& raw : f_.body_lines) {
+      const std::string line = mlir::trim(raw);
+      if (line.empty() || line == "llvm.return" || line.rfind("llvm.return", 0) == 0) continue;
+      if (!line_(k, line)) return false;
+    }
+    return true;
+  }
+
+ private:
+  bool fail(const std::string& m) {
+    *err_ = "mlir_to_hip: " + f_.name + ": " + m;
+    return false;
+  }
+
+  bool resolve(const Kernel* k, const std::string& tok, double* v) const {
+    auto it = k->consts.find(tok);
+    if (it != k->consts.end()) {
+      *v = it->second;
+      return true;
+    }
+    return parse_number(tok, v);
+  }
+
+  int u16_dtype(const Kernel* k, const std::string& callee, const std::string& ptr) const {
+    if (callee.find("bf16") != std::string::npos) return BF16;
+    if (k->bf16_hint || ptr.find("bf16") != std::string::npos) return BF16;
+    return F16;
+  }
+
+  bool line_(Kernel* k, const std::string& line) {
+    const auto res = mlir::result_ssa(line);
+    // ---- constants ----
+    if (line.find("llvm.mlir.constant") != std::string::npos) {
+      const size_t open = line.find('(');
+      const size_t colon = line.find(':', open);
+      double v = 0;
+      if (res && open != std::string::npos && colon != std::string::npos &&
+          parse_number(line.substr(open + 1, colon - open - 1), &v)) {
+        k->consts[*res] = v;
+        return true;
+      }
+      return fail("cannot parse constant: " + line);
+    }
+    // ---- integer casts / arithmetic on constants (GEP offsets) ----
+    static const char* kUnary[] = {"llvm.bitcast ", "llvm.zext ", "llvm.sext ", "llvm.trunc ",
+                                   "llvm.ptrtoint ", "llvm.inttoptr "};
+    for (const char* op : kUnary) {
+      const size_t p = line.find(op);
+      if (p != std::string::npos && res) {
+        const std::string src = ssa_token(mlir::trim(line.substr(p + std::strlen(op))));
+        if (k->consts.count(src)) k->consts[*res] = k->consts[src];
+        if (k->block_derived.count(src)) k->block_derived.insert(*res);
+        if (k->ptrs.count(src)) k->ptrs[*res] = k->ptrs[src];
+        return true;
+      }
+    }
+    static const char* kBinary[] = {"llvm.mul ", "llvm.add ", "llvm.sub ", "llvm.shl "};
+    for (const char* op : kBinary) {
+      const size_t p = line.find(op);
+      if (p != std::string::npos && res) {
+        std::string rest = mlir::trim(line.substr(p + std::strlen(op)));
+        const size_t c = rest.find(" : ");
+        if (c != std::string::npos) rest = rest.substr(0, c);
+        const size_t comma = rest.find(',');
+        if (comma == std::string::npos) return fail("cannot parse: " + line);
+        const std::string a = mlir::trim(rest.substr(0, comma));
+        const std::string b = mlir::trim(rest.substr(comma + 1));
+        if (k->block_derived.count(a) || k->block_derived.count(b)) {
+          k->block_derived.insert(*res);
+          return true;
+        }
+        double x = 0, y = 0;
+        if (resolve(k, a, &x) && resolve(k, b, &y)) {
+          const std::string o = op;
+          k->consts[*res] = o == "llvm.mul " ? x * y
+                            : o == "llvm.add " ? x + y
+                            : o == "llvm.sub " ? x - y
+                                               : std::ldexp(x, static_cast<int>(y));
+          return true;
+        }
+        return fail("non-constant integer arithmetic is not supported: " + line);
+      }
+    }
+    // ---- pointer arithmetic ----
+    if (line.find("llvm.getelementptr") != std::string::npos) {
+      if (!res) return fail("getelementptr without result: " + line);
+      size_t p = line.find("llvm.getelementptr") + std::strlen("llvm.getelementptr");
+      std::string rest = mlir::trim(line.substr(p));
+      if (rest.rfind("inbounds", 0) == 0) rest = mlir::trim(rest.substr(8));
+      const size_t lb = rest.find('['), rb = rest.find(']');
+      if (lb == std::string::npos || rb == std::string::npos) return fail("cannot parse: " + line);
+      const std::string base = mlir::trim(rest.substr(0, lb));
+      const std::string idx = mlir::trim(rest.substr(lb + 1, rb - lb - 1));
+      auto bp = k->ptrs.find(base);
+      if (bp == k->ptrs.end()) return fail("getelementptr on an unknown pointer: " + line);
+      PtrRef r = bp->second;
+      double off = 0;
+      if (k->block_derived.count(idx)) {
+        // the #[tile_kernel] per-tile offset: applied implicitly per logical tile
+      } else if (resolve(k, idx, &off)) {
+        r.offset += static_cast<long long>(off);
+      } else {
+        return fail("non-constant pointer offset: " + line);
+      }
+      k->ptrs[*res] = r;
+      return true;
+    }
+    // ---- calls ----
+    const auto cal = mlir::callee(line);
+    if (!cal) return fail("unsupported operation (control flow and scalar memory ops are not lowered): " + line);
+    const auto args = mlir::call_args(line);
+    if (!args) return fail("cannot parse call arguments: " + line);
+    const std::string& c = *cal;
+    const std::vector<std::string>& a = *args;
+    if (c == "get_block_idx" || c == "get_block_num") {
+      if (res) k->block_derived.insert(*res);
+      return true;
+    }
+    if (c == "__tile_pipelined_for_begin" || c == "__tile_pipelined_for_end") return true;
+    if (c.rfind("__tile_load_", 0) == 0) {
+      if (a.size() < 3 || !res) return fail("load: expected (ptr, rows, cols): " + line);
+      auto p = k->ptrs.find(a[0]);
+      if (p == k->ptrs.end()) return fail("load from an unknown pointer: " + line);
+      TileVal t;
+      t.op = "load";
+      t.src = p->second;
+      double r = 0, cc = 0;
+      if (!resolve(k, a[1], &r) || !resolve(k, a[2], &cc)) return fail("load: shape is not constant");
+      t.rows = static_cast<long long>(r);
+      t.cols = static_cast<long long>(cc);
+      if (c == "__tile_load_f32") t.dtype = F32;
+      else if (c == "__tile_load_f16" || c == "__tile_load_bf16") t.dtype = u16_dtype(k, c, a[0]);
+      else return fail("unsupported load " + c);
+      k->tiles[*res] = t;
+      return true;
+    }
+    if (c.rfind("__tile_store_", 0) == 0) {
+      if (a.size() < 4) return fail("store: expected (ptr, tile, rows, cols): " + line);
+      auto p = k->ptrs.find(a[0]);
+      if (p == k->ptrs.end()) return fail("store to an unknown pointer: " + line);
+      Store s;
+      s.dst = p->second;
+      s.value = a[1];
+      double r = 0, cc = 0;
+      if (!resolve(k, a[2], &r) || !resolve(k, a[3], &cc)) return fail("store: shape is not constant");
+      s.rows = static_cast<long long>(r);
+      s.cols = static_cast<long long>(cc);
+      if (c == "__tile_store_f32" || c == "__tile_store_u32") s.dtype = F32;
+      else if (c == "__tile_store_f16" || c == "__tile_store_bf16") s.dtype = u16_dtype(k, c, a[0]);
+      else return fail("unsupported store " + c);
+      if (!k->tiles.count(s.value)) return fail("store of an unknown tile " + s.value);
+      k->stores.push_back(s);
+      return true;
+    }
+    if (c.rfind("__tile_", 0) == 0) {
+      if (!res) return fail("tile op without result: " + line);
+      TileVal t;
+      t.op = c;
+      return op_(k, line, c, a, *res, t);
+    }
+    return fail("unsupported call @" + c);
+  }
+
+  // Operand layouts of the supported tile ops (crates/tile_std/src/tile.rs).
+  bool op_(Kernel* k, const std::string& line, const std::string& c,
+           const std::vector<std::string>& a, const std::string& res, TileVal t) {
+    auto tile = [&](const std::string& s) -> const TileVal* {
+      auto it = k->tiles.find(s);
+      return it == k->tiles.end() ? nullptr : &it->second;
+    };
+    auto num = [&](const std::string& s, double* v) { return resolve(k, s, v); };
+    const std::string base = c.substr(7);  // after "__tile_"
+    auto shape_from = [&](size_t ri, size_t ci) {
+      double r = 0, cc = 0;
+      if (!num(a[ri], &r) || !num(a[ci], &cc)) return false;
+      t.rows = static_cast<long long>(r);
+      t.cols = static_cast<long long>(cc);
+      return true;
+    };
+    static const std::set<std::string> kBin = {"add_f32", "sub_f32", "mul_f32", "div_f32",
+                                               "max_f32", "add_f16", "mul_f16"};
+    static const std::set<std::string> kUn = {"exp_f32", "neg_f32", "silu_f32",
+                                              "causal_mask_f32", "exp_f16", "neg_f16", "silu_f16",
+                                              "cast_f32_f16", "cast_f16_f32", "cast_f32_bf16",
+                                              "cast_bf16_f32"};
+    if (base == "softmax_f32" || base == "softmax_f16") {
+      if (a.size() < 4 || !tile(a[1]) || !shape_from(2, 3)) return fail("softmax arity: " + line);
+      t.ins = {a[1]};
+      t.dtype = tile(a[1])->dtype;
+    } else if (base == "matmul_f32" || base == "matmul_f16" || base == "matmul_transposed_f32" ||
+               base == "matmul_transposed_f16") {
+      if (a.size() < 6 || !tile(a[1]) || !tile(a[2])) return fail("matmul arity: " + line);
+      double m = 0, kk = 0, n = 0;
+      if (!num(a[3], &m) || !num(a[4], &kk) || !num(a[5], &n)) return fail("matmul shape: " + line);
+      t.ins = {a[1], a[2]};
+      t.rows = static_cast<long long>(m);
+      t.cols = static_cast<long long>(n);
+      t.scalars = {kk};
+      t.dtype = tile(a[1])->dtype;
+    } else if (base == "attention_f32") {
+      if (a.size() < 6 || !tile(a[1]) || !tile(a[2]) || !tile(a[3]) || !shape_from(4, 5))
+        return fail("attention arity: " + line);
+      t.ins = {a[1], a[2], a[3]};
+      t.dtype = tile(a[1])->dtype;
+    } else if (base == "attention_prefill_f32" || base == "attention_decode_f32") {
+      if (a.size() < 6 || !tile(a[1]) || !tile(a[2]) || !tile(a[3]) || !shape_from(4, 5))
+        return fail(base + " arity: " + line);
+      t.ins = {a[1], a[2], a[3]};
+      t.dtype = tile(a[1])->dtype;
+    } else if (kBin.count(base)) {
+      if (a.size() < 5 || !tile(a[1]) || !tile(a[2]) || !shape_from(3, 4))
+        return fail(base + " arity: " + line);
+      t.ins = {a[1], a[2]};
+      t.dtype = F32;
+    } else if (kUn.count(base)) {
+      if (a.size() < 4 || !tile(a[1]) || !shape_from(2, 3)) return fail(base + " arity: " + line);
+      t.ins = {a[1]};
+      t.dtype = F32;
+    } else if (base == "scale_f32") {
+      double s = 0;
+      if (a.size() < 5 || !tile(a[1]) || !num(a[2], &s) || !shape_from(3, 4))
+        return fail("scale arity: " + line);
+      t.ins = {a[1]};
+      t.scalars = {s};
+    } else if (base == "clamp_f32") {
+      double lo = 0, hi = 0;
+      if (a.size() < 6 || !tile(a[1]) || !num(a[2], &lo) || !num(a[3], &hi) || !shape_from(4, 5))
+        return fail("clamp arity: " + line);
+      t.ins = {a[1]};
+      t.scalars = {lo, hi};
+    } else if (base == "fill_f32") {
+      double v = 0;
+      if (a.size() < 4 || !num(a[1], &v) || !shape_from(2, 3)) return fail("fill arity: " + line);
+      t.scalars = {v};
+    } else {
+      return fail("unsupported intrinsic " + c);
+    }
+    k->tiles[res] = t;
+    return true;
+  }
+
+  const mlir::Func& f_;
+  std::string* err_;
+};
+
+// ---------------------------------------------------------------------------
+// Code generation
+// ---------------------------------------------------------------------------
+
+std::string u(long long v) { return std::to_string(v) + "u"; }
+
+// Exact C++ spelling of an f32 constant.
+std::string fconst(double v) {
+  std::ostringstream os;
+  os << std::hexfloat << static_cast<float>(v) << "f";
+  return os.str();
+}
+
+void desc(std::ostringstream& os, const std::string& name, unsigned threads, unsigned wg_per_tile,
+          unsigned tiles_per_wg) {
+  os << "extern \"C\" __device__ th::LaunchDesc __th_desc_" << name << " = {th::kLaunchDescMagic, "
+     << threads << "u, " << (wg_per_tile ? wg_per_tile : 1) << "u, "
+     << (tiles_per_wg ? tiles_per_wg : 1) << "u, 0u, {0u, 0u, 0u}};\n\n";
+}
+
+void signature(std::ostringstream& os, const Kernel& k, unsigned threads,
+               const std::vector<std::string>& extra) {
+  os << "extern \"C\" __global__ void __launch_bounds__(" << threads << ") " << k.name << "(";
+  for (size_t i = 0; i < k.gm.size(); ++i) os << (i ? ", " : "") << "void* __restrict__ p" << i;
+  for (const std::string& e : extra) os << ", uint32_t " << e;
+  os << (k.gm.empty() && extra.empty() ? "" : ", ") << "uint32_t th_tiles) {\n";
+}
+
+bool is_elementwise(const std::string& op) {
+  return op != "load" && op.find("softmax") == std::string::npos &&
+         op.find("matmul") == std::string::npos && op.find("attention") == std::string::npos;
+}
+
+// Emits kernels for one function; returns false with *err on unsupported shapes.
+bool emit_kernel(const Kernel& k, std::ostringstream& os, std::string* err) {
+  // Identify a hot-op chain: one store whose value is a hot op fed by loads.
+  const TileVal* hot = nullptr;
+  const Store* st = nullptr;
+  if (k.stores.size() == 1) {
+    const TileVal& v = k.tiles.at(k.stores[0].value);
+    if (v.op != "load" && !is_elementwise(v.op)) {
+      bool direct = true;
+      for (const std::string& in : v.ins) direct = direct && k.tiles.at(in).op == "load";
+      if (!direct) {
+        *err = "mlir_to_hip: " + k.name + ": " + v.op + " operands must come straight from loads";
+        return false;
+      }
+      hot = &v;
+      st = &k.stores[0];
+    }
+  }
+  for (const auto& kv : k.tiles) {
+    if (&kv.second != hot && kv.second.op != "load" && !is_elementwise(kv.second.op)) {
+      *err = "mlir_to_hip: " + k.name + ": " + kv.second.op +
+             " must be the only op between loads and a single store";
+      return false;
+    }
+  }
+  os << "// kernel " << k.name << ": ";
+  if (!hot) {
+    // ---------------- elementwise fallback ----------------
+    if (k.stores.empty()) {
+      *err = "mlir_to_hip: " + k.name + ": kernel has no store";
+      return false;
+    }
+    const long long R = k.stores[0].rows, C = k.stores[0].cols;
+    for (const auto& kv : k.tiles)
+      if (kv.second.rows * kv.second.cols != R * C) {
+        *err = "mlir_to_hip: " + k.name + ": elementwise tiles must share one shape";
+        return false;
+      }
+    for (const Store& s : k.stores)
+      if (s.rows * s.cols != R * C) {
+        *err = "mlir_to_hip: " + k.name + ": elementwise tiles must share one shape";
+        return false;
+      }
+    os << "elementwise over " << R << "x" << C << " tiles (plain HIP)\n";
+    signature(os, k, 256, {});
+    os << "  const uint64_t th_n = static_cast<uint64_t>(th_tiles) * " << R * C << "ull;\n";
+    os << "  for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * 256u + threadIdx.x; i < th_n;"
+          " i += static_cast<uint64_t>(gridDim.x) * 256u) {\n";
+    os << "    const uint32_t row = static_cast<uint32_t>((i / " << C << "ull) % " << R
+       << "ull), col = static_cast<uint32_t>(i % " << C << "ull);\n";
+    os << "    (void)row; (void)col;\n";
+    // topological emission: repeat until every tile value is defined
+    std::map<std::string, std::string> var;
+    int n = 0;
+    bool progress = true;
+    while (progress && var.size() < k.tiles.size()) {
+      progress = false;
+      for (const auto& kv : k.tiles) {
+        if (var.count(kv.first)) continue;
+        bool ready = true;
+        for (const std::string& in : kv.second.ins) ready = ready && var.count(in);
+        if (!ready) continue;
+        const TileVal& t = kv.second;
+        const std::string v = "v" + std::to_string(n++);
+        const std::string o = t.op.size() > 7 ? t.op.substr(7) : t.op;
+        auto in = [&](int i) { return var.at(t.ins[i]); };
+        std::ostringstream e;
+        if (t.op == "load") {
+          const std::string p = "reinterpret_cast<const " + std::string(dt_ctype(t.dtype)) + "*>(p" +
+                                std::to_string(t.src.arg) + ")";
+          const std::string idx = std::to_string(t.src.offset) + "ll + static_cast<int64_t>(i)";
+          if (t.dtype == F32) e << p << "[" << idx << "]";
+          else e << "th::u16_to_f32<" << dt_enum(t.dtype) << ">(" << p << "[" << idx << "])";
+        } else if (o == "add_f32" || o == "add_f16") e << in(0) << " + " << in(1);
+        else if (o == "sub_f32") e << in(0) << " - " << in(1);
+        else if (o == "mul_f32" || o == "mul_f16") e << in(0) << " * " << in(1);
+        else if (o == "div_f32") e << in(0) << " / " << in(1);
+        else if (o == "max_f32") e << "fmaxf(" << in(0) << ", " << in(1) << ")";
+        else if (o == "exp_f32" || o == "exp_f16") e << "expf(" << in(0) << ")";
+        else if (o == "neg_f32" || o == "neg_f16") e << "-" << in(0);
+        else if (o == "silu_f32" || o == "silu_f16") e << in(0) << " / (1.0f + expf(-" << in(0) << "))";
+        else if (o == "scale_f32") e << in(0) << " * " << fconst(t.scalars[0]);
+        else if (o == "clamp_f32")
+          e << "fminf(fmaxf(" << in(0) << ", " << fconst(t.scalars[0]) << "), " << fconst(t.scalars[1]) << ")";
+        else if (o == "fill_f32") e << fconst(t.scalars[0]);
+        else if (o == "causal_mask_f32") e << "(col <= row ? " << in(0) << " : -INFINITY)";
+        else if (o == "cast_f32_f16") e << "th::f16_to_f32(th::f32_to_f16(" << in(0) << "))";
+        else if (o == "cast_f32_bf16") e << "th::bf16_to_f32(th::f32_to_bf16(" << in(0) << "))";
+        else if (o == "cast_f16_f32" || o == "cast_bf16_f32") e << in(0);
+        else {
+          *err = "mlir_to_hip: " + k.name + ": unsupported elementwise op " + t.op;
+          return false;
+        }
+        os << "    const float " << v << " = " << e.str() << ";\n";
+        var[kv.first] = v;
+        progress = true;
+      }
+    }
+    for (const Store& s : k.stores) {
+      const std::string p = "reinterpret_cast<" + std::string(dt_ctype(s.dtype)) + "*>(p" +
+                            std::to_string(s.dst.arg) + ")";
+      const std::string idx = std::to_string(s.dst.offset) + "ll + static_cast<int64_t>(i)";
+      if (s.dtype == F32) os << "    " << p << "[" << idx << "] = " << var.at(s.value) << ";\n";
+      else
+        os << "    " << p << "[" << idx << "] = th::f32_to_u16<" << dt_enum(s.dtype) << ">("
+           << var.at(s.value) << ");\n";
+    }
+    os << "  }\n}\n";
+    const long long per = (R * C + 255) / 256;
+    desc(os, k.name, 256, static_cast<unsigned>(per > 1024 ? 1024 : per), 1);
+    return true;
+  }
+
+  auto in_ptr = [&](int i, const char* ctype) {
+    const TileVal& t = k.tiles.at(hot->ins[i]);
+    return "(reinterpret_cast<const " + std::string(ctype) + "*>(p" + std::to_string(t.src.arg) +
+           ")" + (t.src.offset ? " + " + std::to_string(t.src.offset) + "ll" : "") + ")";
+  };
+  auto out_ptr = [&](const char* ctype) {
+    return "(reinterpret_cast<" + std::string(ctype) + "*>(p" + std::to_string(st->dst.arg) + ")" +
+           (st->dst.offset ? " + " + std::to_string(st->dst.offset) + "ll" : "") + ")";
+  };
+  const std::string o = hot->op.substr(7);
+  if (o == "softmax_f32" || o == "softmax_f16") {
+    const TileVal& x = k.tiles.at(hot->ins[0]);
+    const long long R = hot->rows, C = hot->cols;
+    if (x.rows * x.cols != R * C || st->rows * st->cols != R * C || st->dtype != x.dtype) {
+      *err = "mlir_to_hip: " + k.name + ": softmax shape/dtype mismatch between load and store";
+      return false;
+    }
+    const int E = x.dtype == F32 ? 4 : 8;
+    const long long nvec = C / E;
+    int nv = 0;  // 0 = any-cols path
+    const bool aligned = (C % E == 0) && (x.src.offset % E == 0) && (st->dst.offset % E == 0);
+    if (aligned && nvec <= 64 * 16) nv = nvec <= 64 ? 1 : nvec <= 128 ? 2 : nvec <= 256 ? 4 : nvec <= 512 ? 8 : 16;
+    os << "row softmax " << R << "x" << C << " " << dt_name(x.dtype) << " per tile -> th::entry::softmax_rows\n";
+    signature(os, k, 256, {});
+    os << "  th::entry::softmax_rows<" << dt_enum(x.dtype) << ", " << nv << ">(" << in_ptr(0, dt_ctype(x.dtype))
+       << ", " << out_ptr(dt_ctype(x.dtype)) << ", th_tiles * " << u(R) << ", " << u(C) << ");\n}\n";
+    const unsigned tpw = R >= 4 ? 1 : static_cast<unsigned>(4 / R);
+    const unsigned wpt = R >= 4 ? static_cast<unsigned>((R + 3) / 4) : 1;
+    desc(os, k.name, 256, wpt, tpw);
+    return true;
+  }
+  if (o.rfind("matmul", 0) == 0) {
+    const bool bt = o.find("transposed") != std::string::npos;
+    const TileVal& a = k.tiles.at(hot->ins[0]);
+    const TileVal& b = k.tiles.at(hot->ins[1]);
+    const long long M = hot->rows, N = hot->cols, K = static_cast<long long>(hot->scalars[0]);
+    if (a.rows * a.cols != M * K || b.rows * b.cols != K * N || st->rows * st->cols != M * N) {
+      *err = "mlir_to_hip: " + k.name + ": matmul operand shapes do not match m/k/n";
+      return false;
+    }
+    if (a.dtype != b.dtype) {
+      *err = "mlir_to_hip: " + k.name + ": matmul operands have different dtypes";
+      return false;
+    }
+    const int in = a.dtype, out = st->dtype;
+    const bool mfma = in != F32 && K % 8 == 0 && (bt || N % 8 == 0) && a.src.offset % 8 == 0 &&
+                      b.src.offset % 8 == 0;
+    os << "matmul " << M << "x" << K << "x" << N << (bt ? " (B transposed)" : "") << " " << dt_name(in)
+       << " -> " << dt_name(out) << (mfma ? " -> th::entry::gemm (MFMA)" : " -> th::entry::gemm_fma") << "\n";
+    signature(os, k, 256, {});
+    const std::string tmpl = std::string(dt_enum(in)) + ", " + dt_enum(out) + ", " + (bt ? "true" : "false");
+    if (mfma) {
+      os << "  th::entry::gemm<" << tmpl << ">(" << in_ptr(0, "uint16_t") << ", " << in_ptr(1, "uint16_t")
+         << ", " << out_ptr(dt_ctype(out)) << ", " << u(M) << ", " << u(N) << ", " << u(K) << ", th_tiles);\n}\n";
+      desc(os, k.name, 256, static_cast<unsigned>(((M + 255) / 256) * ((N + 255) / 256)), 1);
+    } else {
+      os << "  th::entry::gemm_fma<" << tmpl << ">(" << in_ptr(0, dt_ctype(in)) << ", " << in_ptr(1, dt_ctype(in))
+         << ", " << out_ptr(dt_ctype(out)) << ", " << u(M) << ", " << u(N) << ", " << u(K) << ", th_tiles);\n}\n";
+      desc(os, k.name, 256, static_cast<unsigned>(((M + 63) / 64) * ((N + 63) / 64)), 1);
+    }
+    return true;
+  }
+  if (o == "attention_f32") {
+    const TileVal& q = k.tiles.at(hot->ins[0]);
+    const long long S = hot->rows, D = hot->cols;
+    if (D > 256) {
+      *err = "mlir_to_hip: " + k.name + ": attention head_dim > 256";
+      return false;
+    }
+    os << "single-head attention S=" << S << " D=" << D << " " << dt_name(q.dtype)
+       << " -> th::entry::attention_tiles\n";
+    signature(os, k, 256, {});
+    os << "  th::entry::attention_tiles<" << dt_enum(q.dtype) << ", 256>(" << in_ptr(0, dt_ctype(q.dtype))
+       << ", " << in_ptr(1, dt_ctype(q.dtype)) << ", " << in_ptr(2, dt_ctype(q.dtype)) << ", "
+       << out_ptr(dt_ctype(st->dtype)) << ", " << u(S) << ", " << u(D) << ", th_tiles);\n}\n";
+    desc(os, k.name, 256, static_cast<unsigned>(S), 1);
+    return true;
+  }
+  if (o == "attention_prefill_f32") {
+    const TileVal& q = k.tiles.at(hot->ins[0]);
+    os << "causal GQA prefill " << dt_name(q.dtype) << " (runtime seq_len, start_pos, max_seq, head_dim, "
+       << "num_heads, num_kv_heads) -> th::entry::prefill\n";
+    signature(os, k, 512, {"seq_len", "start_pos", "max_seq", "head_dim", "num_heads", "num_kv_heads"});
+    const char* ct = dt_ctype(q.dtype);
+    os << "  th::entry::prefill<" << dt_enum(q.dtype) << ">(" << in_ptr(0, ct) << ", " << in_ptr(1, ct)
+       << ", " << in_ptr(2, ct) << ", " << out_ptr(ct)
+       << ", th_tiles, seq_len, start_pos, max_seq, head_dim, num_heads, num_kv_heads);\n}\n";
+    desc(os, k.name, 512, 256, 1);
+    return true;
+  }
+  if (o == "attention_decode_f32") {
+    const TileVal& q = k.tiles.at(hot->ins[0]);
+    os << "GQA decode " << dt_name(q.dtype) << " (runtime seq_len, max_seq, head_dim, num_heads, "
+       << "num_kv_heads) -> th::entry::decode\n";
+    signature(os, k, 256, {"seq_len", "max_seq", "head_dim", "num_heads", "num_kv_heads"});
+    const char* ct = dt_ctype(q.dtype);
+    os << "  th::entry::decode<" << dt_enum(q.dtype) << ">(" << in_ptr(0, ct) << ", " << in_ptr(1, ct)
+       << ", " << in_ptr(2, ct) << ", " << out_ptr(ct)
+       << ", th_tiles, seq_len, max_seq, head_dim, num_heads, num_kv_heads);\n}\n";
+    desc(os, k.name, 256, 64, 1);
+    return true;
+  }
+  *err = "mlir_to_hip: " + k.name + ": unsupported intrinsic " + hot->op;
+  return false;
+}
+
+}  // namespace
+
+bool convert_mlir_to_hip(const std::string& mlir_text, std::string* out,
+                         std::vector<std::string>* kernel_names, std::string* err) {
+  mlir::Module mod;
+  if (!mlir::parse_module(mlir_text, &mod, err)) return false;
+  std::ostringstream os;
+  os << "// Generated by tilers_hip `hip` target (gfx950) — DO NOT EDIT\n";
+  os << "// Build: hipcc --genco --offload-arch=gfx950 -O3 -I <tile-rs_amd/csrc>\n";
+  os << "#include \"kernels/tile_entry.hpp\"\n\n";
+  int count = 0;
+  for (const mlir::Func& f : mod.functions) {
+    if (!f.is_entry || f.body_lines.empty() || mlir::is_builtin_helper(f.name)) continue;
+    Kernel k;
+    Lowerer low(f, err);
+    if (!low.analyze(&k)) return false;
+    if (!emit_kernel(k, os, err)) return false;
+    if (kernel_names) kernel_names->push_back(k.name);
+    ++count;
+  }
+  if (count == 0) {
+    *err = "No entry-point kernel functions found in MLIR module";
+    return false;
+  }
+  *out = os.str();
+  return true;
+}
+
+}  // namespace target
+}  // namespace th

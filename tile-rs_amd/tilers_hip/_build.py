@@ -57,8 +57,44 @@ def _compile_cpp(src: Path, obj: Path) -> None:
           "-o", str(obj)])
 
 
+EXAMPLES_DIR = PKG_DIR / "examples"
+EXAMPLES_OUT = LIB_DIR / "examples"
+
+
 def library_path() -> Path:
     return LIB_DIR / LIB_NAME
+
+
+def example_path(stem: str) -> Path:
+    return EXAMPLES_OUT / f"{stem}.hsaco"
+
+
+def build_examples(verbose: bool = False) -> list:
+    """Emit every tilers_hip/examples/*.mlir through the hip target and compile the
+    HIP source into lib/examples/<stem>.hsaco (the code objects the launcher loads)."""
+    import ctypes as C
+    import importlib
+
+    lib = importlib.import_module("tilers_hip")
+    EXAMPLES_OUT.mkdir(parents=True, exist_ok=True)
+    srcs = []
+    for mlir in sorted(EXAMPLES_DIR.glob("*.mlir")):
+        out = lib.emit(mlir.read_text())
+        hip = EXAMPLES_OUT / f"{mlir.stem}.hip"
+        hip.write_text(out.source)
+        srcs.append((hip, example_path(mlir.stem)))
+
+    def one(pair):
+        hip, hsaco = pair
+        _run([HIPCC, "--genco", *DEVICE_FLAGS, "-I", str(CSRC), str(hip), "-o", str(hsaco)])
+        return hsaco
+
+    workers = max(1, min(len(srcs), os.cpu_count() or 1, 16))
+    with cf.ThreadPoolExecutor(max_workers=workers) as ex:
+        built = list(ex.map(one, srcs))
+    if verbose:
+        print(f"built {len(built)} example code objects in {EXAMPLES_OUT}")
+    return built
 
 
 def build(verbose: bool = False) -> Path:
@@ -87,12 +123,15 @@ def build(verbose: bool = False) -> Path:
     out = library_path()
     tmp = out.with_suffix(".so.tmp")
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp),
-          "-Wl,-soname," + LIB_NAME])
+          "-Wl,-soname," + LIB_NAME, "-ldl"])
     os.replace(tmp, out)
     if verbose:
         print(f"built {out}")
+    build_examples(verbose)
     return out
 
 
 if __name__ == "__main__":
+    import sys
+    sys.path.insert(0, str(ROOT))
     build(verbose=True)
