@@ -253,7 +253,44 @@ class Decode(Workload):
         return kv_bytes / el / 1e9, f"{bh} query heads ({bh // 4} kv heads x 8192 positions)"
 
 
-WORKLOADS = {w.name: w for w in (Softmax, Gemm, Mlp, Attn, Decode)}
+class Copy(Workload):
+    """Calibration only: a 1 GiB device-to-device copy of known size, whose HBM
+    counters (FETCH_SIZE / WRITE_SIZE) scale the counters of the tile kernels."""
+    name, index, bound, dtype, unit = "copy", 0, "hbm", "u8", "GB/s"
+    nbytes = 1 << 30
+
+    def work(self):
+        return 2.0 * self.nbytes
+
+    def config(self):
+        return {"workload": "device-to-device copy, 1 GiB (counter calibration)"}
+
+    def setup(self, th, dev, s):
+        self.src = dev.alloc(self.nbytes // 4, th.TileDtype.F32)
+        self.dst = dev.alloc(self.nbytes // 4, th.TileDtype.F32)
+        th.lib().th_memset_async(self.src.as_raw_ptr(), 1, self.nbytes, s.handle)
+
+    def step(self, th, s, i):
+        from tilers_hip._lib import check
+        check(th.lib().th_memcpy_dtod_async(self.dst.as_raw_ptr(), self.src.as_raw_ptr(),
+                                            self.nbytes, s.handle))
+
+    def cpu_sample(self, th, s, seconds):
+        return 0.0, "none"
+
+
+WORKLOADS = {w.name: w for w in (Softmax, Gemm, Mlp, Attn, Decode, Copy)}
+BENCH_LINES = ("attn", "decode", "gemm", "mlp", "softmax")
+
+
+def measured_traffic(name: str):
+    """HBM bytes per launch of the dominant kernel, from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE passes (profiles/hbm_traffic.json), or None."""
+    try:
+        t = json.loads((ROOT / "profiles" / "hbm_traffic.json").read_text())
+        return round(t[name]["traffic_bytes"])
+    except (OSError, KeyError, ValueError):
+        return None
 
 
 def run(name: str, steps: int, warmup: int, cpu_seconds: float) -> dict:
@@ -303,7 +340,7 @@ def run(name: str, steps: int, warmup: int, cpu_seconds: float) -> dict:
         "data": "synthetic (seeded on-device PRNG, inputs resident in HBM)",
         "config": w.config(),
         "roofline": {"bound": w.bound, "achieved": round(value, 3), "peak": peak, "unit": w.unit,
-                     "frac": round(value / peak, 4), "traffic": None},
+                     "frac": round(value / peak, 4), "traffic": measured_traffic(name)},
         "cpu_baseline": cpu,
     }
 
@@ -322,7 +359,7 @@ def main() -> int:
               "(rows / tiles / heads per GPU), and this build runs on a single GPU only; "
               "use --gpus 1.", file=sys.stderr)
         return 2
-    names = sorted(WORKLOADS) if args.config == "all" else [args.config]
+    names = list(BENCH_LINES) if args.config == "all" else [args.config]
     for n in names:
         print(json.dumps(run(n, args.steps, args.warmup, args.cpu_seconds)), flush=True)
     return 0
