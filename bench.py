@@ -348,8 +348,9 @@ def run(name: str, steps: int, warmup: int, cpu_seconds: float) -> dict:
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--steps", type=int, default=100)
+    # enough untimed steps for the GPU clock to settle (tens of ms of MFMA work)
+    ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--config", default="gemm", choices=sorted(WORKLOADS) + ["all"])
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     args = ap.parse_args()

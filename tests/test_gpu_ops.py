@@ -151,7 +151,7 @@ def test_matmul_golden_vectors(dev, stream, golden):
 @pytest.mark.parametrize("in_dt", [D.BF16, D.F16, D.F32])
 @pytest.mark.parametrize("trans", [False, True])
 @pytest.mark.parametrize("m,k,n", [(256, 256, 256), (300, 72, 136), (1, 8, 8), (513, 1024, 264),
-                                   (64, 33, 40)])
+                                   (64, 33, 40), (512, 96, 768), (768, 1024, 512)])
 def test_matmul_integer_bit_exact(dev, stream, in_dt, trans, m, k, n):
     """Integer-valued inputs make every partial sum exact: any layout/index slip shows."""
     rng = np.random.default_rng(m + 7 * k + 13 * n)

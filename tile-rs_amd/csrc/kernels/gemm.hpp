@@ -23,6 +23,8 @@
 // tall; tiles that share A rows or B columns then share one XCD's L2.
 #pragma once
 
+#include <type_traits>
+
 #include "common.hpp"
 
 namespace th {
@@ -53,129 +55,209 @@ __device__ __forceinline__ void tile_coords(uint32_t bid, uint32_t tiles_m, uint
   tn = in_group / gm;
 }
 
+// The workgroup's LDS for the MFMA GEMM: one allocation shared by every
+// instantiation that is inlined into a kernel (2 stages of A and B, 128 KB).
+struct GemmLds {
+  u32x4 a[2][BM * BK / 8];
+  u32x4 b[2][BN * BK / 8];
+};
+__device__ __forceinline__ GemmLds& gemm_lds() {
+  __shared__ GemmLds lds;
+  return lds;
+}
+
 }  // namespace gemm
 
 // One 256x256 output tile (tm, tn) of C = A*B by a whole workgroup.
-template <int DT, int DT_OUT, bool B_TRANS>
+//
+// Schedule per K-step of 64 (two LDS buffers, `cur` and `nxt`):
+//   - MFMA fragments of sub-step ks+1 are read from LDS while the 16 MFMAs of
+//     sub-step ks run (two register sets);
+//   - the A and B tiles of step k+1, already in registers, are written to the
+//     `nxt` buffer between sub-steps (nobody reads `nxt` in this step);
+//   - after the step's barrier the global loads of step k+2 are issued, so they
+//     have a whole step to land.
+// FULL = M, N multiples of 256 and K of 64: no bounds checks in the loop.
+template <int DT, int DT_OUT, bool B_TRANS, bool FULL, int WM = 2, int WN = 2>
 __device__ __forceinline__ void gemm_tile_256(const uint16_t* __restrict__ A,
                                               const uint16_t* __restrict__ B,
                                               void* __restrict__ C, uint32_t M, uint32_t N,
                                               uint32_t K, uint32_t tm, uint32_t tn) {
   using namespace gemm;
-  __shared__ u32x4 lds_a[2][BM * BK / 8];
-  __shared__ u32x4 lds_b[2][BN * BK / 8];
+  constexpr int NTH = 64 * WM * WN;     // threads in the workgroup
+  constexpr int TM = BM / WM / 32;      // 32x32 accumulator blocks per wave, M
+  constexpr int TN = BN / WN / 32;      // and N
+  constexpr int LA = BM * BK / 8 / NTH; // 16-byte A chunks per thread per K-step
+  GemmLds& lds = gemm_lds();
+  auto& lds_a = lds.a;
+  auto& lds_b = lds.b;
   const uint32_t m0 = tm * BM, n0 = tn * BN;
 
   const int t = threadIdx.x;
   const int lane = t & 63, wave = t >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave / WN, wn = wave % WN;
   const int l32 = lane & 31, g = lane >> 5;
 
-  u32x4 ra[8], rb[8];
+  // Staging.  With 256 threads every thread loads LA chunks of A and one 8x8
+  // block (or 8 chunks) of B.  With 512 threads waves 0-3 load B and waves 4-7
+  // load A, 8 chunks each, into one shared register array.
+  constexpr bool SPLIT = NTH == 512;
+  constexpr int NA = SPLIT ? 8 : LA;
+  u32x4 ra[NA], rb_own[SPLIT ? 1 : 8];
+  u32x4* rb = SPLIT ? ra : rb_own;
+  const int ta = SPLIT ? t - 256 : t;   // index among the A loaders
+  const int tb = t;                      // index among the B loaders (t < 256)
+  const bool is_a = !SPLIT || t >= 256;
+  const bool is_b = !SPLIT || t < 256;
 
-  auto load_tile = [&](uint32_t k0) {
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int c = t + NT * i;
-      const int row = c >> 3, kc = c & 7;
-      const uint32_t gm_ = m0 + row, gk = k0 + kc * 8;
-      ra[i] = (gm_ < M && gk < K) ? ldg128(A + static_cast<size_t>(gm_) * K + gk) : u32x4{0, 0, 0, 0};
-    }
+  auto load_b = [&](uint32_t k0) {
     if constexpr (B_TRANS) {
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        const int c = t + NT * i;
+        const int c = tb + 256 * i;
         const int row = c >> 3, kc = c & 7;
         const uint32_t gn = n0 + row, gk = k0 + kc * 8;
-        rb[i] = (gn < N && gk < K) ? ldg128(B + static_cast<size_t>(gn) * K + gk) : u32x4{0, 0, 0, 0};
+        const uint16_t* p = B + static_cast<size_t>(gn) * K + gk;
+        rb[i] = (FULL || (gn < N && gk < K)) ? ldg128(p) : u32x4{0, 0, 0, 0};
       }
     } else {
-      const int kb = t >> 5, nb = t & 31;
+      const int kb = tb >> 5, nb = tb & 31;
       const uint32_t gn = n0 + nb * 8;
 #pragma unroll
       for (int r = 0; r < 8; ++r) {
         const uint32_t gk = k0 + kb * 8 + r;
-        rb[r] = (gn < N && gk < K) ? ldg128(B + static_cast<size_t>(gk) * N + gn) : u32x4{0, 0, 0, 0};
+        const uint16_t* p = B + static_cast<size_t>(gk) * N + gn;
+        rb[r] = (FULL || (gn < N && gk < K)) ? ldg128(p) : u32x4{0, 0, 0, 0};
       }
     }
   };
-
-  auto store_tile = [&](int buf) {
+  auto load_a = [&](uint32_t k0) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int c = t + NT * i;
+    for (int i = 0; i < NA; ++i) {
+      const int c = ta + 256 * i;
       const int row = c >> 3, kc = c & 7;
-      lds_a[buf][row * 8 + swz(row, kc)] = ra[i];
+      const uint32_t gm_ = m0 + row, gk = k0 + kc * 8;
+      const uint16_t* p = A + static_cast<size_t>(gm_) * K + gk;
+      ra[i] = (FULL || (gm_ < M && gk < K)) ? ldg128(p) : u32x4{0, 0, 0, 0};
     }
-    if constexpr (B_TRANS) {
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        const int c = t + NT * i;
-        const int row = c >> 3, kc = c & 7;
-        lds_b[buf][row * 8 + swz(row, kc)] = rb[i];
-      }
+  };
+  auto load_tile = [&](uint32_t k0) {
+    if constexpr (SPLIT) {
+      if (is_a) load_a(k0);
+      else load_b(k0);
     } else {
-      const int kb = t >> 5, nb = t & 31;
-      u32x4 tr[8];
-      transpose8x8_b16(rb, tr);
+      load_a(k0);
+      load_b(k0);
+    }
+  };
+
+  auto store_a = [&](int buf) {
+    if (is_a) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int row = nb * 8 + j;
-        lds_b[buf][row * 8 + swz(row, kb)] = tr[j];
+      for (int i = 0; i < NA; ++i) {
+        const int c = ta + 256 * i;
+        const int row = c >> 3, kc = c & 7;
+        lds_a[buf][row * 8 + swz(row, kc)] = ra[i];
+      }
+    }
+  };
+  auto store_b = [&](int buf) {
+    if (is_b) {
+      if constexpr (B_TRANS) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const int c = tb + 256 * i;
+          const int row = c >> 3, kc = c & 7;
+          lds_b[buf][row * 8 + swz(row, kc)] = rb[i];
+        }
+      } else {
+        // 8x8 transpose in registers, one output column (4 dwords) at a time.
+        const int kb = tb >> 5, nb = tb & 31;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const int dw = j >> 1;
+          u32x4 col;
+#pragma unroll
+          for (int p = 0; p < 4; ++p) {
+            const uint32_t lo = rb[2 * p][dw], hi = rb[2 * p + 1][dw];
+            col[p] = (j & 1) ? pack_halves<true>(lo, hi) : pack_halves<false>(lo, hi);
+          }
+          const int row = nb * 8 + j;
+          lds_b[buf][row * 8 + swz(row, kb)] = col;
+        }
       }
     }
   };
 
-  f32x16 acc[4][4];
+  // Fragment register sets: two (read ks+1 during the MFMAs of ks) with one
+  // wave per SIMD; one with two waves per SIMD, where the other wave hides the
+  // LDS latency and the registers are needed for the accumulators.
+  constexpr int FS = SPLIT ? 1 : 2;
+  u32x4 fa[FS][TM], fb[FS][TN];
+  auto load_frags = [&](int buf, int ks, int set) {
+    const int chunk = 2 * ks + g;
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+    for (int mi = 0; mi < TM; ++mi) {
+      const int row = wm * (BM / WM) + mi * 32 + l32;
+      fa[set][mi] = lds_a[buf][row * 8 + swz(row, chunk)];
+    }
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int ni = 0; ni < TN; ++ni) {
+      const int row = wn * (BN / WN) + ni * 32 + l32;
+      fb[set][ni] = lds_b[buf][row * 8 + swz(row, chunk)];
+    }
+  };
+
+  f32x16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
   const uint32_t nk = (K + BK - 1) / BK;
   load_tile(0);
-  store_tile(0);
+  store_a(0);
+  store_b(0);
   __syncthreads();
+  if (nk > 1) load_tile(BK);
+  load_frags(0, 0, 0);
 
   for (uint32_t kt = 0; kt < nk; ++kt) {
-    const int cur = kt & 1;
-    if (kt + 1 < nk) load_tile((kt + 1) * BK);
+    const int cur = kt & 1, nxt = cur ^ 1;
+    const bool more = kt + 1 < nk;
 #pragma unroll
     for (int ks = 0; ks < BK / 16; ++ks) {
-      const int chunk = 2 * ks + g;
-      u32x4 fa[4], fb[4];
+      const int set = (FS == 2) ? (ks & 1) : 0;
+      if (FS == 1 && ks > 0) load_frags(cur, ks, 0);
+      if (FS == 2 && ks + 1 < BK / 16) load_frags(cur, ks + 1, set ^ 1);
 #pragma unroll
-      for (int mi = 0; mi < 4; ++mi) {
-        const int row = wm * 128 + mi * 32 + l32;
-        fa[mi] = lds_a[cur][row * 8 + swz(row, chunk)];
-      }
+      for (int mi = 0; mi < TM; ++mi)
 #pragma unroll
-      for (int ni = 0; ni < 4; ++ni) {
-        const int row = wn * 128 + ni * 32 + l32;
-        fb[ni] = lds_b[cur][row * 8 + swz(row, chunk)];
-      }
-#pragma unroll
-      for (int mi = 0; mi < 4; ++mi)
-#pragma unroll
-        for (int ni = 0; ni < 4; ++ni) acc[mi][ni] = mfma32x32x16<DT>(fa[mi], fb[ni], acc[mi][ni]);
+        for (int ni = 0; ni < TN; ++ni)
+          acc[mi][ni] = mfma32x32x16<DT>(fa[set][mi], fb[set][ni], acc[mi][ni]);
+      if (ks == 1 && more) store_a(nxt);
+      if (ks == 2 && more) store_b(nxt);
     }
-    if (kt + 1 < nk) store_tile(cur ^ 1);
     __syncthreads();
+    if (more) {
+      if (kt + 2 < nk) load_tile((kt + 2) * BK);
+      load_frags(nxt, 0, 0);
+    }
   }
 
   // Epilogue.  Accumulator register r of lane l in a 32x32 block holds
   // row 8*(r/4) + 4*(l/32) + r%4, column l%32.
 #pragma unroll
-  for (int mi = 0; mi < 4; ++mi)
+  for (int mi = 0; mi < TM; ++mi)
 #pragma unroll
-    for (int ni = 0; ni < 4; ++ni) {
-      const uint32_t col = n0 + wn * 128 + ni * 32 + l32;
+    for (int ni = 0; ni < TN; ++ni) {
+      const uint32_t col = n0 + wn * (BN / WN) + ni * 32 + l32;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const uint32_t row = m0 + wm * 128 + mi * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-        if (row < M && col < N) {
+        const uint32_t row = m0 + wm * (BM / WM) + mi * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+        if (FULL || (row < M && col < N)) {
           const size_t off = static_cast<size_t>(row) * N + col;
           if constexpr (DT_OUT == kF32) {
             static_cast<float*>(C)[off] = acc[mi][ni][r];
@@ -189,18 +271,314 @@ __device__ __forceinline__ void gemm_tile_256(const uint16_t* __restrict__ A,
 
 // A: M x K (K contiguous).  B: K x N (N contiguous) or, with B_TRANS, N x K.
 // Requires K % 8 == 0 and, for row-major B, N % 8 == 0; M, N, K tails are handled
-// by zero-filled loads and predicated stores.  Batch index = blockIdx.y with
-// element strides sa, sb, sc.
-template <int DT, int DT_OUT, bool B_TRANS>
-__global__ void __launch_bounds__(gemm::NT, 1)
+// by zero-filled loads and predicated stores (FULL = no tails: M, N multiples of
+// 256 and K of 64).  Batch index = blockIdx.y with element strides sa, sb, sc.
+template <int DT, int DT_OUT, bool B_TRANS, int WM, int WN, bool FULL>
+__global__ void __launch_bounds__(64 * WM * WN, 1)
 gemm_mfma_256(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, void* __restrict__ C,
               uint32_t M, uint32_t N, uint32_t K, uint64_t sa, uint64_t sb, uint64_t sc) {
   const uint32_t tiles_m = (M + gemm::BM - 1) / gemm::BM, tiles_n = (N + gemm::BN - 1) / gemm::BN;
   uint32_t tm, tn;
   gemm::tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
   constexpr int OSZ = (DT_OUT == kF32) ? 4 : 2;
-  gemm_tile_256<DT, DT_OUT, B_TRANS>(A + blockIdx.y * sa, B + blockIdx.y * sb,
-                                     static_cast<char*>(C) + blockIdx.y * sc * OSZ, M, N, K, tm, tn);
+  gemm_tile_256<DT, DT_OUT, B_TRANS, FULL, WM, WN>(A + blockIdx.y * sa, B + blockIdx.y * sb,
+                                                   static_cast<char*>(C) + blockIdx.y * sc * OSZ, M,
+                                                   N, K, tm, tn);
+}
+
+// ---------------------------------------------------------------------------
+// Direct-to-LDS pipeline (the path for M, N multiples of 256 and K of 64).
+//
+// 256x256 tile per workgroup, eight waves (two per SIMD) each owning a 128x64
+// sub-tile of 4x2 v_mfma_f32_32x32x16 accumulators.  K is staged 64 at a time
+// through two LDS buffers (2 x 64 KB) filled by global_load_lds_dwordx4: each
+// lane's 16 bytes go straight from L2/HBM into LDS (no registers, no
+// ds_write).  A stage is complete for a thread when its vmcnt has dropped to
+// the loads issued after it; one barrier per stage then publishes every
+// thread's part, and right after that barrier the freed buffer is refilled
+// with the stage two ahead.
+//   A stage: [256 m][64 k], 128-byte rows; 16-byte chunk c of row r sits at
+//            c ^ ((r ^ (r >> 3)) & 7) -> conflict-free 128-bit MFMA reads
+//            (with 32-k stages: 64-byte rows, c ^ ((r >> 2) & 3)).
+//   B stage: row-major B needs no transpose anywhere: it stays [64 k][256 n]
+//            (512-byte rows, chunk c at c ^ 4*(k & 3), so the four k rows one
+//            half-wave reads land in four different 64-byte bank groups of the
+//            64-bank LDS) and the MFMA B operand is read with
+//            ds_read_b64_tr_b16, which hands each lane of a 16-lane group one
+//            n column of a 4 (k) x 16 (n) block: two reads give the eight
+//            consecutive k values of the 32x32x16 operand.
+//   B_TRANS: B stage is [256 n][64 k] like A.
+// The swizzles are applied on the global side: each lane picks the global
+// chunk whose swizzled LDS slot is its own fixed slot (lane*16 bytes).
+// ---------------------------------------------------------------------------
+namespace gemm {
+constexpr int DBK = 64;       // K per stage (default shape)
+constexpr int NSTAGE = 2;     // stages (default shape)
+constexpr int DWAVES = 8;     // 2 x 4 waves of 128 x 64 (2 waves per SIMD)
+// One LDS arena for every DMA-pipeline instantiation: 128 KB for the default
+// 2 x 64 KB, up to 160 KB (all of gfx950's LDS) for other stage shapes.
+__device__ __forceinline__ u32x4* dma_lds_arena() {
+  __shared__ u32x4 arena[160 * 1024 / 16];
+  return arena;
+}
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
+
+// Workgroup barrier without a memory fence: LDS DMA completion is handled by
+// explicit vmcnt waits, and a fence would drain every outstanding load.
+__device__ __forceinline__ void bar() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+// s_waitcnt vmcnt(N) (gfx9 encoding: vmcnt bits [3:0] and [15:14]).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+__device__ __forceinline__ void dma16(const void* src, void* lds_dst) {
+  __builtin_amdgcn_global_load_lds(src, (lds_void*)(lds_dst), 16, 0, 0);
+}
+// Wait until at most `later` stages of NL loads each are still in flight.
+template <int NL, int MAXL>
+__device__ __forceinline__ void wait_stages(uint32_t later) {
+  if constexpr (MAXL >= 3) {
+    if (later >= 3) { wait_vm<3 * NL>(); return; }
+  }
+  if constexpr (MAXL >= 2) {
+    if (later >= 2) { wait_vm<2 * NL>(); return; }
+  }
+  if constexpr (MAXL >= 1) {
+    if (later >= 1) { wait_vm<NL>(); return; }
+  }
+  wait_vm<0>();
+}
+}  // namespace gemm
+
+template <int DT, int DT_OUT, bool B_TRANS, int KB = gemm::DBK, int NS = gemm::NSTAGE,
+          int WAVES = gemm::DWAVES>
+__device__ __forceinline__ void gemm_dma_tile_256(const uint16_t* __restrict__ A,
+                                                  const uint16_t* __restrict__ B,
+                                                  void* __restrict__ C, uint32_t M, uint32_t N,
+                                                  uint32_t K, uint32_t tm, uint32_t tn) {
+  using namespace gemm;
+  static_assert(KB == 32 || KB == 64, "stage K");
+  static_assert(WAVES == 4 || WAVES == 8, "2x2 or 2x4 waves");
+  static_assert(NS * (BM + BN) * KB * 2 <= 160 * 1024, "LDS");
+  constexpr int NTH = 64 * WAVES;          // threads
+  constexpr int WN_W = WAVES / 2;          // waves along N
+  constexpr int TWN = BN / WN_W;           // wave tile N (128 or 64)
+  constexpr int NI = TWN / 32;             // 32-wide MFMA blocks per wave along N
+  constexpr int CPR = KB / 8;              // 16-byte chunks per A row
+  constexpr int SA = BM * KB / 8;          // u32x4 per A stage
+  constexpr int SB = BN * KB / 8;          // u32x4 per B stage
+  constexpr int NLA = SA / NTH;            // DMA per thread per stage, A (and B)
+  static_assert(NLA >= 1 && SA % NTH == 0, "stage split");
+  u32x4* arena = dma_lds_arena();
+  auto lds_a = [&](int st) { return arena + st * (SA + SB); };
+  auto lds_b = [&](int st) { return arena + st * (SA + SB) + SA; };
+  // A-like rows (k contiguous, CPR chunks): chunk c of row r at c ^ sw(r)
+  auto swa = [](int row) { return CPR == 4 ? ((row >> 2) & 3) : ((row ^ (row >> 3)) & 7); };
+  const uint32_t m0 = tm * BM, n0 = tn * BN;
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);  // uniform: SGPR LDS addresses
+  const int wm = wave / WN_W, wn = wave % WN_W;
+  const int l32 = lane & 31, g = lane >> 5;
+  (void)M;
+
+  // ---- per-thread DMA sources (NLA A chunks + NLA B chunks per stage) ----
+  // Each wave-level load fills 1 KB of LDS (64 slots of 16 B); load j of wave w
+  // fills slots (NLA*w + j)*64 ... Lane l owns slot l of that block.
+  const uint16_t* srcA[NLA];
+  const uint16_t* srcB[NLA];
+#pragma unroll
+  for (int j = 0; j < NLA; ++j) {
+    const int slot = (NLA * wave + j) * 64 + lane;
+    const int row = slot / CPR, c = (slot % CPR) ^ swa(row);
+    srcA[j] = A + static_cast<size_t>(m0 + row) * K + 8 * c;
+    if constexpr (B_TRANS) {
+      srcB[j] = B + static_cast<size_t>(n0 + row) * K + 8 * c;
+    } else {
+      // [KB k][256 n] rows of 32 chunks; chunk c of k-row r at c ^ 4*(r & 3)
+      const int kr = slot / 32, cb = (slot % 32) ^ (4 * (kr & 3));
+      srcB[j] = B + static_cast<size_t>(kr) * N + n0 + 8 * cb;
+    }
+  }
+  auto issue = [&](uint32_t stage, uint32_t kt) {
+    const size_t ka = static_cast<size_t>(kt) * KB;  // element offset along K
+#pragma unroll
+    for (int j = 0; j < NLA; ++j) dma16(srcA[j] + ka, lds_a(stage) + (NLA * wave + j) * 64);
+#pragma unroll
+    for (int j = 0; j < NLA; ++j) {
+      const uint16_t* p = B_TRANS ? srcB[j] + ka : srcB[j] + ka * N;
+      dma16(p, lds_b(stage) + (NLA * wave + j) * 64);
+    }
+  };
+
+  // ---- fragment reads ----
+  u32x4 fa[2][4], fb[2][NI];
+  auto load_frags = [&](int stage, int ks, int set) {
+    const int chunk = 2 * ks + g;
+    const u32x4* la = lds_a(stage);
+    const u32x4* lb = lds_b(stage);
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi) {
+      const int row = wm * 128 + mi * 32 + l32;
+      fa[set][mi] = la[row * CPR + (chunk ^ swa(row))];
+    }
+    if constexpr (B_TRANS) {
+#pragma unroll
+      for (int ni = 0; ni < NI; ++ni) {
+        const int row = wn * TWN + ni * 32 + l32;
+        fb[set][ni] = lb[row * CPR + (chunk ^ swa(row))];
+      }
+    } else {
+      const int q = lane >> 4, i = lane & 15;
+      const char* base = reinterpret_cast<const char*>(lb);
+#pragma unroll
+      for (int ni = 0; ni < NI; ++ni) {
+        const int n = wn * TWN + ni * 32 + 16 * (q & 1) + 4 * (i & 3);
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+          const int k = ks * 16 + 8 * (q >> 1) + 4 * r + (i >> 2);
+          const int off = k * 512 + (((n >> 3) ^ (4 * (k & 3))) << 4) + (n & 7) * 2;
+          const v4i16 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (lds_v4i16*)(const_cast<char*>(base) + off));
+          const u32x2 w = __builtin_bit_cast(u32x2, v);
+          fb[set][ni][2 * r] = w[0];
+          fb[set][ni][2 * r + 1] = w[1];
+        }
+      }
+    }
+  };
+
+  f32x16 acc[4][NI];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < NI; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  // Pipeline: all NS buffers are filled ahead.  In step kt the barrier sits
+  // before the MFMAs of the last sub-step (whose fragments are already in
+  // registers): every read of buffer kt%NS is then done, so right after the
+  // barrier the DMA for step kt+NS refills that buffer and the first fragments
+  // of step kt+1 are read, both under the last sub-step's MFMAs.
+  // Each sub-step is one scheduling region: the fragment reads it issues feed
+  // the NEXT sub-step, so they overlap this sub-step's MFMAs instead of being
+  // sunk next to their use (which would expose the LDS latency every sub-step).
+  constexpr int KS = KB / 16;
+  static_assert(KS % 2 == 0, "fragment sets alternate per sub-step");
+  constexpr int NM = 4 * NI;                          // MFMAs per sub-step
+  constexpr int NR = 4 + (B_TRANS ? NI : 2 * NI);     // LDS reads per sub-step
+  const uint32_t nk = K / KB;
+  auto mfmas = [&](int set) {
+#pragma unroll
+    for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+      for (int ni = 0; ni < NI; ++ni)
+        acc[mi][ni] = mfma32x32x16<DT>(fa[set][mi], fb[set][ni], acc[mi][ni]);
+  };
+  // Fragment reads go first, two behind each MFMA, so the next sub-step's
+  // wait finds them done; the DMA issues (a whole step of slack) follow.
+  auto interleave = [&](int nvmem) {
+    int r = NR, v = nvmem;
+#pragma unroll
+    for (int i = 0; i < NM; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+      if (r >= 2) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // LDS read
+        r -= 2;
+      } else if (r == 1) {
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        r = 0;
+      } else if (v >= 2) {
+        __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);  // VMEM (LDS DMA)
+        v -= 2;
+      } else if (v == 1) {
+        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
+        v = 0;
+      }
+    }
+  };
+  // One K step.  FILL: step kt+NS exists, so the freed buffer is refilled and
+  // the loop body has no branches.
+  auto step = [&](uint32_t kt, auto fill) {
+    constexpr bool FILL = decltype(fill)::value;
+    const int cur = kt % NS;
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      const int set = ks & 1;
+      __builtin_amdgcn_sched_barrier(0);
+      if (ks + 1 < KS) {
+        load_frags(cur, ks + 1, set ^ 1);
+        mfmas(set);
+        interleave(0);
+      } else {
+        // this thread's reads of `cur` are complete; step kt+1's loads have landed
+        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+        if constexpr (FILL) {
+          wait_vm<(NS - 2) * 2 * NLA>();
+        } else if (kt + 1 < nk) {
+          wait_stages<2 * NLA, NS - 2>(min(nk - 2 - kt, static_cast<uint32_t>(NS - 2)));
+        }
+        bar();
+        __builtin_amdgcn_sched_barrier(0);
+        if constexpr (FILL) {
+          issue(cur, kt + NS);
+          load_frags((kt + 1) % NS, 0, set ^ 1);
+        } else if (kt + 1 < nk) {
+          load_frags((kt + 1) % NS, 0, set ^ 1);
+        }
+        mfmas(set);
+        interleave(FILL ? 2 * NLA : 0);
+      }
+    }
+  };
+
+#pragma unroll
+  for (uint32_t s = 0; s < NS; ++s)
+    if (s < nk) issue(s, s);
+  wait_stages<2 * NLA, NS - 1>(min(nk - 1, static_cast<uint32_t>(NS - 1)));
+  bar();
+  load_frags(0, 0, 0);
+  uint32_t kt = 0;
+  for (; kt + NS < nk; ++kt) step(kt, std::true_type{});
+  for (; kt < nk; ++kt) step(kt, std::false_type{});
+  __builtin_amdgcn_sched_barrier(0);
+
+  // Epilogue.  Accumulator register r of lane l in a 32x32 block holds
+  // row 8*(r/4) + 4*(l/32) + r%4, column l%32.
+#pragma unroll
+  for (int mi = 0; mi < 4; ++mi)
+#pragma unroll
+    for (int ni = 0; ni < NI; ++ni) {
+      const uint32_t col = n0 + wn * TWN + ni * 32 + l32;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const uint32_t row = m0 + wm * 128 + mi * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+        const size_t off = static_cast<size_t>(row) * N + col;
+        if constexpr (DT_OUT == kF32) static_cast<float*>(C)[off] = acc[mi][ni][r];
+        else static_cast<uint16_t*>(C)[off] = f32_to_u16<DT_OUT>(acc[mi][ni][r]);
+      }
+    }
+}
+
+// M, N multiples of 256, K multiple of KB.  Batch index = blockIdx.y.
+template <int DT, int DT_OUT, bool B_TRANS, int KB = gemm::DBK, int NS = gemm::NSTAGE,
+          int WAVES = gemm::DWAVES>
+__global__ void __launch_bounds__(64 * WAVES, 1)
+gemm_dma_256(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, void* __restrict__ C,
+             uint32_t M, uint32_t N, uint32_t K, uint64_t sa, uint64_t sb, uint64_t sc) {
+  uint32_t tm, tn;
+  gemm::tile_coords(blockIdx.x, M / gemm::BM, N / gemm::BN, tm, tn);
+  constexpr int OSZ = (DT_OUT == kF32) ? 4 : 2;
+  gemm_dma_tile_256<DT, DT_OUT, B_TRANS, KB, NS, WAVES>(A + blockIdx.y * sa,
+                                                              B + blockIdx.y * sb,
+                                                 static_cast<char*>(C) + blockIdx.y * sc * OSZ, M,
+                                                 N, K, tm, tn);
 }
 
 // Fallback for shapes the MFMA path does not take (K % 8 != 0, row-major B with

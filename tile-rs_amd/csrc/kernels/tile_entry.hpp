@@ -44,7 +44,7 @@ __device__ __forceinline__ void gemm(const uint16_t* A, const uint16_t* B, void*
     const uint32_t bi = w / per;
     uint32_t tm, tn;
     gemm::tile_coords(w % per, tiles_m, tiles_n, tm, tn);
-    gemm_tile_256<DT, DTO, BT>(A + static_cast<size_t>(bi) * M * K,
+    gemm_tile_256<DT, DTO, BT, false>(A + static_cast<size_t>(bi) * M * K,
                                B + static_cast<size_t>(bi) * K * N,
                                static_cast<char*>(C) + static_cast<size_t>(bi) * M * N * OSZ, M, N,
                                K, tm, tn);

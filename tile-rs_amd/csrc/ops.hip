@@ -7,6 +7,7 @@
 
 #include <cmath>
 #include <cstdint>
+#include <cstdlib>
 #include <string>
 
 #include "kernels/attention.hpp"
@@ -60,20 +61,66 @@ int softmax_launch(const void* x, void* y, uint32_t rows, uint32_t cols, hipStre
 
 // ---- matmul -------------------------------------------------------------------
 
+// Wave layout of the 256x256 MFMA tile: 4 waves of 128x128 (1 wave per SIMD,
+// 256 accumulator registers) or 8 waves of 128x64 (2 waves per SIMD).
+int gemm_waves() {
+  static const int w = [] {
+    const char* e = std::getenv("TILERS_HIP_GEMM_WAVES");
+    return (e && std::atoi(e) == 8) ? 8 : 4;
+  }();
+  return w;
+}
+
+// The LDS-DMA pipeline serves tile-multiple shapes unless TILERS_HIP_GEMM_DMA=0
+// (then the register-staged kernel runs them too).
+bool gemm_dma() {
+  static const bool v = [] {
+    const char* e = std::getenv("TILERS_HIP_GEMM_DMA");
+    return !(e && std::atoi(e) == 0);
+  }();
+  return v;
+}
+
+template <int DT, int DTO, bool BT>
+void gemm_dma_go(const uint16_t* A, const uint16_t* B, void* c, uint32_t m, uint32_t k, uint32_t n,
+                 dim3 grid, uint64_t sa, uint64_t sb, uint64_t sc, hipStream_t s) {
+  hipLaunchKernelGGL((th::gemm_dma_256<DT, DTO, BT>), grid, dim3(64 * th::gemm::DWAVES), 0, s, A, B,
+                     c, m, n, k, sa, sb, sc);
+}
+
+template <int DT, int DTO, bool BT, bool FULL>
+void gemm_mfma_go(const uint16_t* A, const uint16_t* B, void* c, uint32_t m, uint32_t k,
+                  uint32_t n, dim3 grid, uint64_t sa, uint64_t sb, uint64_t sc, hipStream_t s) {
+  if (gemm_waves() == 4)
+    hipLaunchKernelGGL((th::gemm_mfma_256<DT, DTO, BT, 2, 2, FULL>), grid, dim3(256), 0, s, A, B, c,
+                       m, n, k, sa, sb, sc);
+  else
+    hipLaunchKernelGGL((th::gemm_mfma_256<DT, DTO, BT, 2, 4, FULL>), grid, dim3(512), 0, s, A, B, c,
+                       m, n, k, sa, sb, sc);
+}
+
 template <int DT, int DTO>
 int gemm_mfma_launch(const void* a, const void* b, void* c, uint32_t m, uint32_t k, uint32_t n,
                      bool bt, uint32_t batch, uint64_t sa, uint64_t sb, uint64_t sc,
                      hipStream_t s) {
   const uint32_t tiles = ((m + 255) / 256) * ((n + 255) / 256);
-  const dim3 grid(tiles, batch), block(th::gemm::NT);
+  const dim3 grid(tiles, batch);
   auto A = static_cast<const uint16_t*>(a);
   auto B = static_cast<const uint16_t*>(b);
+  if (gemm_dma() && m % th::gemm::BM == 0 && n % th::gemm::BN == 0 && k % th::gemm::DBK == 0) {
+    if (bt)
+      gemm_dma_go<DT, DTO, true>(A, B, c, m, k, n, grid, sa, sb, sc, s);
+    else
+      gemm_dma_go<DT, DTO, false>(A, B, c, m, k, n, grid, sa, sb, sc, s);
+    return launch_status("matmul (MFMA, LDS DMA) launch");
+  }
+  const bool full = m % th::gemm::BM == 0 && n % th::gemm::BN == 0 && k % th::gemm::BK == 0;
   if (bt)
-    hipLaunchKernelGGL((th::gemm_mfma_256<DT, DTO, true>), grid, block, 0, s, A, B, c, m, n, k, sa,
-                       sb, sc);
+    full ? gemm_mfma_go<DT, DTO, true, true>(A, B, c, m, k, n, grid, sa, sb, sc, s)
+         : gemm_mfma_go<DT, DTO, true, false>(A, B, c, m, k, n, grid, sa, sb, sc, s);
   else
-    hipLaunchKernelGGL((th::gemm_mfma_256<DT, DTO, false>), grid, block, 0, s, A, B, c, m, n, k, sa,
-                       sb, sc);
+    full ? gemm_mfma_go<DT, DTO, false, true>(A, B, c, m, k, n, grid, sa, sb, sc, s)
+         : gemm_mfma_go<DT, DTO, false, false>(A, B, c, m, k, n, grid, sa, sb, sc, s);
   return launch_status("matmul (MFMA) launch");
 }
 
@@ -96,6 +143,15 @@ template <int DT>
 int gemm_dispatch_out(const void* a, const void* b, void* c, uint32_t m, uint32_t k, uint32_t n,
                       th_dtype out, bool bt, uint32_t batch, uint64_t sa, uint64_t sb, uint64_t sc,
                       hipStream_t s, bool mfma) {
+  if constexpr (DT == th::kF32) {
+    // f32 operands have no MFMA path here: only the FMA kernels are instantiated
+    (void)mfma;
+    switch (out) {
+      case TH_F32: return gemm_fma_launch<DT, th::kF32>(a, b, c, m, k, n, bt, batch, sa, sb, sc, s);
+      case TH_F16: return gemm_fma_launch<DT, th::kF16>(a, b, c, m, k, n, bt, batch, sa, sb, sc, s);
+      default: return gemm_fma_launch<DT, th::kBF16>(a, b, c, m, k, n, bt, batch, sa, sb, sc, s);
+    }
+  }
   switch (out) {
     case TH_F32:
       return mfma ? gemm_mfma_launch<DT, th::kF32>(a, b, c, m, k, n, bt, batch, sa, sb, sc, s)
