@@ -19,6 +19,7 @@
 #pragma once
 
 #include "common.hpp"
+#include "gemm.hpp"
 
 namespace th {
 
@@ -340,6 +341,296 @@ attn_prefill_fa128(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ 
   uint32_t bh, qb;
   prefill_work(blockIdx.x, batch * nh, nqb, bh, qb);
   prefill_tile<DT>(Q, K, V, O, seq_len, start_pos, max_seq, nh, nkv, scale_log2, bh, qb);
+}
+
+// ============================================================================
+// Prefill, LDS-DMA form (head_dim 128, 16-bit Q/K/V).
+//
+// Same work split and arithmetic as prefill_tile (8 waves x 32 query rows, S^T
+// = K.Q^T, online softmax per query column, O^T += V^T.P^T with P^T taken from
+// the S^T accumulators in place), but K and V reach LDS by
+// global_load_lds_dwordx4 into a ring of NS stages of 64 KV positions, issued
+// NS-1 blocks ahead, with no register staging and no transpose on the way in:
+//   K stage [64 kv][128 d]: 16-byte chunk c of row r at unit c ^ (r & 15), so
+//            the 16 rows one quarter-wave reads with ds_read_b128 cover all 64
+//            banks.
+//   V stage [64 kv][128 d] row-major: chunk c of row r at unit c ^ 4*(r & 3).
+//            The MFMA A operand V^T (d rows, kv slots) is read with
+//            ds_read_b64_tr_b16 (four kv rows per read, so a half-wave touches
+//            four rows whose 64-byte pieces the swizzle puts on different
+//            banks); the kv rows of the two reads are chosen to match the slot
+//            order of P^T: lane half g holds kv {4g..4g+3, 8+4g..8+4g+3} of
+//            each 16-position group.
+// KV rows past the end of the sequence are fetched from the last valid row (in
+// bounds) and removed by the causal mask, which covers every such position.
+// Cross-half exchanges (the two lanes that share a query column) use
+// v_permlane32_swap instead of an LDS permute.
+// ============================================================================
+namespace fa2 {
+constexpr int D = 128;
+constexpr int BQ = 256;
+constexpr int BKV = 64;
+constexpr int NT = 512;
+constexpr int NS = 4;                  // LDS ring stages (4 x 32 KB)
+constexpr int SK = BKV * D / 8;        // u32x4 per K (or V) stage
+constexpr int NL = 4;                  // DMA instructions per thread per stage
+}  // namespace fa2
+
+// Exchange between the wave halves: after the swap, a holds v of lanes
+// 0..31 in both halves and b holds v of lanes 32..63 in both halves.  Written
+// as inline asm because this compiler folds the builtin's two results into one
+// when both inputs are the same value (r[0] + r[1] came out as r[0] + r[0]).
+// The s_nop covers the VALU-write -> permlane-read hazard.
+__device__ __forceinline__ void swap_halves(float& a, float& b) {
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+}
+// max / sum of v over the two lanes l and l^32 (identical result in both).
+__device__ __forceinline__ float xhalf_max(float v) {
+  float a = v, b = v;
+  swap_halves(a, b);
+  return fmaxf(a, b);
+}
+__device__ __forceinline__ float xhalf_sum(float v) {
+  float a = v, b = v;
+  swap_halves(a, b);
+  return a + b;
+}
+
+template <int DT>
+__device__ __forceinline__ void prefill_tile_dma(const uint16_t* __restrict__ Q,
+                                                 const uint16_t* __restrict__ K,
+                                                 const uint16_t* __restrict__ V,
+                                                 uint16_t* __restrict__ O, uint32_t seq_len,
+                                                 uint32_t start_pos, uint32_t max_seq, uint32_t nh,
+                                                 uint32_t nkv, float scale_log2, uint32_t bh,
+                                                 uint32_t qb) {
+  using namespace fa2;
+  using fa::kRescaleThreshold;
+  u32x4* arena = lds::dma_lds_arena<NS * 2 * SK * 16>();
+  auto lds_k = [&](int st) { return arena + st * 2 * SK; };
+  auto lds_v = [&](int st) { return arena + st * 2 * SK + SK; };
+
+  const uint32_t b = bh / nh, h = bh % nh;
+  const uint32_t kvh = h / (nh / nkv);
+  const uint32_t q0 = qb * BQ;
+  const uint32_t kv_len = start_pos + seq_len;
+
+  const int t = threadIdx.x, lane = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int l32 = lane & 31, g = lane >> 5;
+  const uint32_t qw0 = q0 + 32 * wave;
+  const uint32_t my_q = qw0 + l32;
+  const uint32_t qa_lo = start_pos + qw0;
+  const uint32_t qa_hi = start_pos + qw0 + 31;
+  const uint32_t my_qa = start_pos + my_q;
+
+  const size_t q_row_stride = static_cast<size_t>(nh) * D;
+  const uint16_t* kbase = K + (static_cast<size_t>(b) * nkv + kvh) * max_seq * D;
+  const uint16_t* vbase = V + (static_cast<size_t>(b) * nkv + kvh) * max_seq * D;
+
+  u32x4 qf[8];
+  {
+    const uint16_t* qp = Q + (static_cast<size_t>(b) * seq_len + my_q) * q_row_stride + h * D;
+#pragma unroll
+    for (int ds = 0; ds < 8; ++ds)
+      qf[ds] = (my_q < seq_len) ? ldg128(qp + 16 * ds + 8 * g) : u32x4{0, 0, 0, 0};
+  }
+
+  const uint32_t q_hi_wg = min(q0 + BQ, seq_len);
+  const uint32_t kv_need = start_pos + q_hi_wg;
+  const uint32_t nkb = (kv_need + BKV - 1) / BKV;
+
+  // ---- DMA: load j (0,1) of wave w fills 1 KB block 2w+j of the K and of the
+  //      V stage; lane l owns 16-byte slot l of it (row = slot/16). ----
+  int drow[2], kcol[2], vcol[2];
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int slot = (2 * wave + j) * 64 + lane;
+    const int row = slot >> 4, u = slot & 15;
+    drow[j] = row;
+    kcol[j] = 8 * (u ^ (row & 15));
+    vcol[j] = 8 * (u ^ (4 * (row & 3)));
+  }
+  auto issue = [&](int st, uint32_t kb) {
+    const uint32_t kv0 = kb * BKV;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const size_t pos = min(kv0 + drow[j], kv_len - 1);
+      lds::dma16(kbase + pos * D + kcol[j], lds_k(st) + (2 * wave + j) * 64);
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const size_t pos = min(kv0 + drow[j], kv_len - 1);
+      lds::dma16(vbase + pos * D + vcol[j], lds_v(st) + (2 * wave + j) * 64);
+    }
+  };
+
+  // V^T fragment (d tile dt, kv group st of 16) via two transposed reads.
+  const int tq = lane >> 4, ti = lane & 15;
+  auto read_v = [&](int stg, int st, int dt) {
+    const char* vb = reinterpret_cast<const char*>(lds_v(stg));
+    const int d = 32 * dt + 16 * (tq & 1) + 4 * (ti & 3);
+    u32x4 f;
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+      const int kv = 16 * st + 4 * (tq >> 1) + 8 * r + (ti >> 2);
+      const int off = kv * 256 + ((((d >> 3) ^ (4 * (kv & 3)))) << 4) + (d & 7) * 2;
+      const u32x2 w = lds::read_tr16(vb + off);
+      f[2 * r] = w[0];
+      f[2 * r + 1] = w[1];
+    }
+    return f;
+  };
+
+  f32x16 o_acc[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o_acc[i][r] = 0.0f;
+  float m_run = -INFINITY;
+  float l_run = 0.0f;
+
+  // The previous work item of this workgroup (grid-stride callers) may still
+  // be reading the ring.
+  lds::bar();
+#pragma unroll
+  for (int s = 0; s < NS; ++s)
+    if (static_cast<uint32_t>(s) < nkb) issue(s, s);
+  gemm::wait_stages<NL, NS - 1>(min(nkb - 1, static_cast<uint32_t>(NS - 1)));
+  lds::bar();
+
+  for (uint32_t jb = 0; jb < nkb; ++jb) {
+    const int cur = jb % NS;
+    const uint32_t kv0 = jb * BKV;
+    const bool active = (kv0 <= qa_hi) && (qw0 < seq_len);
+    if (active) {
+      float s[2][16];
+      {
+        f32x16 acc[2];
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[i][r] = 0.0f;
+        const u32x4* kb = lds_k(cur);
+#pragma unroll
+        for (int ds = 0; ds < 8; ++ds) {
+#pragma unroll
+          for (int kt = 0; kt < 2; ++kt) {
+            const int row = 32 * kt + l32;
+            const u32x4 kf = kb[row * 16 + ((2 * ds + g) ^ (row & 15))];
+            acc[kt] = mfma32x32x16<DT>(kf, qf[ds], acc[kt]);
+          }
+        }
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) s[kt][r] = acc[kt][r];
+      }
+      if (kv0 + BKV - 1 > qa_lo) {
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const uint32_t pos = kv0 + 32 * kt + 8 * (r >> 2) + 4 * g + (r & 3);
+            if (pos > my_qa) s[kt][r] = -INFINITY;
+          }
+      }
+      float mx = -INFINITY;
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kt][r]);
+      mx = xhalf_max(mx);
+      const float m_blk = mx * scale_log2;
+      float m_use = m_run;
+      const bool grow = m_blk > m_run + kRescaleThreshold || m_run == -INFINITY;
+      if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+        const float m_new = fmaxf(m_run, m_blk);
+        const float alpha = exp2_fast(m_run - m_new);
+        l_run *= alpha;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) o_acc[i][r] *= alpha;
+        m_run = m_new;
+        m_use = m_new;
+      }
+      float ls = 0.0f;
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          s[kt][r] = exp2_fast(__builtin_fmaf(s[kt][r], scale_log2, -m_use));
+          ls += s[kt][r];
+        }
+      l_run += ls;
+      const float blk = xhalf_sum(ls);
+      const float tot = xhalf_sum(l_run);
+      const bool heavy = blk * fa::kSplitRatio<DT> > tot;
+      const bool split = __builtin_amdgcn_ballot_w64(heavy) != 0;
+#pragma unroll
+      for (int st = 0; st < 4; ++st) {
+        const int kt = st >> 1, hh = st & 1;
+        u32x4 hi;
+#pragma unroll
+        for (int pp = 0; pp < 4; ++pp)
+          hi[pp] = cvt_pk<DT>(s[kt][8 * hh + 2 * pp], s[kt][8 * hh + 2 * pp + 1]);
+        u32x4 vf[4];
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) {
+          vf[dt] = read_v(cur, st, dt);
+          o_acc[dt] = mfma32x32x16<DT>(vf[dt], hi, o_acc[dt]);
+        }
+        if (split) {
+          u32x4 lo;
+#pragma unroll
+          for (int pp = 0; pp < 4; ++pp) {
+            float a, c;
+            unpack_pair<DT>(hi[pp], a, c);
+            lo[pp] = cvt_pk<DT>(s[kt][8 * hh + 2 * pp] - a, s[kt][8 * hh + 2 * pp + 1] - c);
+          }
+#pragma unroll
+          for (int dt = 0; dt < 4; ++dt) o_acc[dt] = mfma32x32x16<DT>(vf[dt], lo, o_acc[dt]);
+        }
+      }
+    }
+    // Block jb+1 must have landed for every thread before anyone reads it, and
+    // every read of buffer `cur` must be done before it is refilled.
+    if (jb + 1 < nkb) {
+      lds::wait_lgkm0();
+      gemm::wait_stages<NL, NS - 2>(min(nkb - 2 - jb, static_cast<uint32_t>(NS - 2)));
+      lds::bar();
+      if (jb + NS < nkb) issue(cur, jb + NS);
+    }
+  }
+
+  const float l_tot = xhalf_sum(l_run);
+  const float inv = 1.0f / l_tot;
+  if (my_q < seq_len) {
+    uint16_t* op = O + (static_cast<size_t>(b) * seq_len + my_q) * q_row_stride + h * D;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const int d = 32 * dt + 8 * q4 + 4 * g;
+        u32x2 w;
+        w[0] = cvt_pk<DT>(o_acc[dt][4 * q4 + 0] * inv, o_acc[dt][4 * q4 + 1] * inv);
+        w[1] = cvt_pk<DT>(o_acc[dt][4 * q4 + 2] * inv, o_acc[dt][4 * q4 + 3] * inv);
+        *reinterpret_cast<u32x2*>(op + d) = w;
+      }
+  }
+}
+
+template <int DT>
+__global__ void __launch_bounds__(fa2::NT, 1)
+attn_prefill_dma128(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
+                    const uint16_t* __restrict__ V, uint16_t* __restrict__ O, uint32_t batch,
+                    uint32_t seq_len, uint32_t start_pos, uint32_t max_seq, uint32_t nh,
+                    uint32_t nkv, float scale_log2) {
+  const uint32_t nqb = (seq_len + fa2::BQ - 1) / fa2::BQ;
+  uint32_t bh, qb;
+  prefill_work(blockIdx.x, batch * nh, nqb, bh, qb);
+  prefill_tile_dma<DT>(Q, K, V, O, seq_len, start_pos, max_seq, nh, nkv, scale_log2, bh, qb);
 }
 
 // ============================================================================

@@ -159,4 +159,46 @@ __device__ __forceinline__ void stg128_nt(void* p, u32x4 v) {
   __builtin_nontemporal_store(v, reinterpret_cast<u32x4*>(p));
 }
 
+// ---- LDS DMA pipeline helpers (gfx950) ------------------------------------------
+namespace lds {
+// LDS ring of a DMA-pipeline kernel (BYTES of gfx950's 160 KB per CU).
+template <int BYTES>
+__device__ __forceinline__ u32x4* dma_lds_arena() {
+  static_assert(BYTES % 16 == 0 && BYTES <= 160 * 1024, "LDS arena");
+  __shared__ u32x4 arena[BYTES / 16];
+  return arena;
+}
+typedef short v4i16 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
+
+// Workgroup barrier without a memory fence: LDS DMA completion is handled by
+// explicit vmcnt waits, and a fence would drain every outstanding load.
+__device__ __forceinline__ void bar() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+// s_waitcnt vmcnt(N) (gfx9 encoding: vmcnt bits [3:0] and [15:14]).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+// s_waitcnt lgkmcnt(0)
+__device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(0xC07F); }
+// global_load_lds_dwordx4: lane i copies 16 bytes from its own `src` to
+// lds_dst + 16*i (lds_dst is the wave-uniform base).
+__device__ __forceinline__ void dma16(const void* src, void* lds_dst) {
+  __builtin_amdgcn_global_load_lds(src, (lds_void*)(lds_dst), 16, 0, 0);
+}
+// ds_read_b64_tr_b16: within each 16-lane group the lanes address a 4 x 16
+// block of 16-bit values (4 rows, lane s pointing at row s/4, elements
+// 4(s%4)..+3); lane i receives column i, rows 0..3.
+__device__ __forceinline__ u32x2 read_tr16(const void* lds_addr) {
+  const v4i16 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_v4i16*)(const_cast<void*>(lds_addr)));
+  return __builtin_bit_cast(u32x2, v);
+}
+}  // namespace lds
+
 }  // namespace th

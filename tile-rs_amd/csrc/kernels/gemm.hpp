@@ -312,34 +312,15 @@ gemm_mfma_256(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, vo
 // chunk whose swizzled LDS slot is its own fixed slot (lane*16 bytes).
 // ---------------------------------------------------------------------------
 namespace gemm {
+using lds::bar;
+using lds::dma16;
+using lds::dma_lds_arena;
+using lds::lds_v4i16;
+using lds::v4i16;
+using lds::wait_vm;
 constexpr int DBK = 64;       // K per stage (default shape)
 constexpr int NSTAGE = 2;     // stages (default shape)
 constexpr int DWAVES = 8;     // 2 x 4 waves of 128 x 64 (2 waves per SIMD)
-// One LDS arena for every DMA-pipeline instantiation: 128 KB for the default
-// 2 x 64 KB, up to 160 KB (all of gfx950's LDS) for other stage shapes.
-__device__ __forceinline__ u32x4* dma_lds_arena() {
-  __shared__ u32x4 arena[160 * 1024 / 16];
-  return arena;
-}
-typedef short v4i16 __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) void lds_void;
-typedef __attribute__((address_space(3))) v4i16 lds_v4i16;
-
-// Workgroup barrier without a memory fence: LDS DMA completion is handled by
-// explicit vmcnt waits, and a fence would drain every outstanding load.
-__device__ __forceinline__ void bar() {
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-}
-// s_waitcnt vmcnt(N) (gfx9 encoding: vmcnt bits [3:0] and [15:14]).
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
-__device__ __forceinline__ void dma16(const void* src, void* lds_dst) {
-  __builtin_amdgcn_global_load_lds(src, (lds_void*)(lds_dst), 16, 0, 0);
-}
 // Wait until at most `later` stages of NL loads each are still in flight.
 template <int NL, int MAXL>
 __device__ __forceinline__ void wait_stages(uint32_t later) {
@@ -375,7 +356,7 @@ __device__ __forceinline__ void gemm_dma_tile_256(const uint16_t* __restrict__ A
   constexpr int SB = BN * KB / 8;          // u32x4 per B stage
   constexpr int NLA = SA / NTH;            // DMA per thread per stage, A (and B)
   static_assert(NLA >= 1 && SA % NTH == 0, "stage split");
-  u32x4* arena = dma_lds_arena();
+  u32x4* arena = dma_lds_arena<NS * (BM + BN) * KB * 2>();
   auto lds_a = [&](int st) { return arena + st * (SA + SB); };
   auto lds_b = [&](int st) { return arena + st * (SA + SB) + SA; };
   // A-like rows (k contiguous, CPR chunks): chunk c of row r at c ^ sw(r)

@@ -84,14 +84,16 @@ __device__ __forceinline__ void prefill(const void* q, const void* k, const void
   if (nkv == 0 || nh % nkv != 0 || start_pos + seq_len > max_seq || head_dim == 0) return;
   const float scale = 1.0f / __builtin_sqrtf(static_cast<float>(head_dim));
   if constexpr (DT != kF32) {
-    if (head_dim == fa::D) {
+    const uintptr_t align = reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) |
+                            reinterpret_cast<uintptr_t>(v) | reinterpret_cast<uintptr_t>(o);
+    if (head_dim == fa::D && (align & 15) == 0) {
       const uint32_t nqb = (seq_len + fa::BQ - 1) / fa::BQ;
       for (uint32_t w = blockIdx.x; w < batch * nh * nqb; w += gridDim.x) {
         uint32_t bh, qb;
         prefill_work(w, batch * nh, nqb, bh, qb);
-        prefill_tile<DT>(static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
-                         static_cast<const uint16_t*>(v), static_cast<uint16_t*>(o), seq_len,
-                         start_pos, max_seq, nh, nkv, scale * kLog2e, bh, qb);
+        prefill_tile_dma<DT>(static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
+                             static_cast<const uint16_t*>(v), static_cast<uint16_t*>(o), seq_len,
+                             start_pos, max_seq, nh, nkv, scale * kLog2e, bh, qb);
       }
       return;
     }

@@ -317,12 +317,24 @@ int th_attention_prefill(const void* q, const void* k, const void* v, void* o, u
     auto K = static_cast<const uint16_t*>(k);
     auto V = static_cast<const uint16_t*>(v);
     auto O = static_cast<uint16_t*>(o);
-    if (dtype == TH_BF16)
+    static const bool dma = [] {
+      const char* e = std::getenv("TILERS_HIP_ATTN_DMA");
+      return !(e && std::atoi(e) == 0);
+    }();
+    if (dma) {
+      if (dtype == TH_BF16)
+        hipLaunchKernelGGL(th::attn_prefill_dma128<th::kBF16>, grid, block, 0, as_stream(s), Q, K, V,
+                           O, batch, seq_len, start_pos, max_seq, num_heads, num_kv_heads, sl2);
+      else
+        hipLaunchKernelGGL(th::attn_prefill_dma128<th::kF16>, grid, block, 0, as_stream(s), Q, K, V,
+                           O, batch, seq_len, start_pos, max_seq, num_heads, num_kv_heads, sl2);
+    } else if (dtype == TH_BF16) {
       hipLaunchKernelGGL(th::attn_prefill_fa128<th::kBF16>, grid, block, 0, as_stream(s), Q, K, V, O,
                          batch, seq_len, start_pos, max_seq, num_heads, num_kv_heads, sl2);
-    else
+    } else {
       hipLaunchKernelGGL(th::attn_prefill_fa128<th::kF16>, grid, block, 0, as_stream(s), Q, K, V, O,
                          batch, seq_len, start_pos, max_seq, num_heads, num_kv_heads, sl2);
+    }
     return launch_status("attention_prefill launch");
   }
   return attn_general_launch(q, k, v, o, batch, seq_len, start_pos, max_seq, start_pos + seq_len,
