@@ -371,7 +371,7 @@ constexpr int D = 128;
 constexpr int BQ = 256;
 constexpr int BKV = 64;
 constexpr int NT = 512;
-constexpr int NS = 4;                  // LDS ring stages (4 x 32 KB)
+constexpr int NS = 5;                  // LDS ring stages (5 x 32 KB, all of LDS)
 constexpr int SK = BKV * D / 8;        // u32x4 per K (or V) stage
 constexpr int NL = 4;                  // DMA instructions per thread per stage
 }  // namespace fa2
@@ -382,7 +382,7 @@ constexpr int NL = 4;                  // DMA instructions per thread per stage
 // when both inputs are the same value (r[0] + r[1] came out as r[0] + r[0]).
 // The s_nop covers the VALU-write -> permlane-read hazard.
 __device__ __forceinline__ void swap_halves(float& a, float& b) {
-  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+  asm("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
 }
 // max / sum of v over the two lanes l and l^32 (identical result in both).
 __device__ __forceinline__ float xhalf_max(float v) {
@@ -396,7 +396,7 @@ __device__ __forceinline__ float xhalf_sum(float v) {
   return a + b;
 }
 
-template <int DT>
+template <int DT, int NS = fa2::NS>
 __device__ __forceinline__ void prefill_tile_dma(const uint16_t* __restrict__ Q,
                                                  const uint16_t* __restrict__ K,
                                                  const uint16_t* __restrict__ V,
@@ -404,8 +404,13 @@ __device__ __forceinline__ void prefill_tile_dma(const uint16_t* __restrict__ Q,
                                                  uint32_t start_pos, uint32_t max_seq, uint32_t nh,
                                                  uint32_t nkv, float scale_log2, uint32_t bh,
                                                  uint32_t qb) {
-  using namespace fa2;
+  using fa2::BKV;
+  using fa2::BQ;
+  using fa2::D;
+  using fa2::NL;
+  using fa2::SK;
   using fa::kRescaleThreshold;
+  static_assert(NS >= 4 && NS * 2 * SK * 16 <= 160 * 1024, "ring depth");
   u32x4* arena = lds::dma_lds_arena<NS * 2 * SK * 16>();
   auto lds_k = [&](int st) { return arena + st * 2 * SK; };
   auto lds_v = [&](int st) { return arena + st * 2 * SK + SK; };
@@ -482,6 +487,12 @@ __device__ __forceinline__ void prefill_tile_dma(const uint16_t* __restrict__ Q,
     return f;
   };
 
+  // This wave's KV blocks: [0, jd) lie wholly at or below the causal diagonal
+  // of all its rows (and inside the sequence); [jd, ja) need the mask; blocks
+  // from ja on are past every row's diagonal (or the wave has no rows).
+  const uint32_t ja = (qw0 < seq_len) ? min(qa_hi / BKV + 1, nkb) : 0u;
+  const uint32_t jd = min((qa_lo + 1) / BKV, ja);
+
   f32x16 o_acc[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
@@ -490,118 +501,175 @@ __device__ __forceinline__ void prefill_tile_dma(const uint16_t* __restrict__ Q,
   float m_run = -INFINITY;
   float l_run = 0.0f;
 
+  // S^T = K.Q^T for the block in ring slot `stg` (raw scores).
+  auto qk = [&](int stg, f32x16 (&acc)[2]) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][r] = 0.0f;
+    const u32x4* kb = lds_k(stg);
+#pragma unroll
+    for (int ds = 0; ds < 8; ++ds) {
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt) {
+        const int row = 32 * kt + l32;
+        const u32x4 kf = kb[row * 16 + ((2 * ds + g) ^ (row & 15))];
+        acc[kt] = mfma32x32x16<DT>(kf, qf[ds], acc[kt]);
+      }
+    }
+  };
+  auto mask = [&](f32x16 (&sc)[2], uint32_t kv0) {
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const uint32_t pos = kv0 + 32 * kt + 8 * (r >> 2) + 4 * g + (r & 3);
+        if (pos > my_qa) sc[kt][r] = -INFINITY;
+      }
+  };
+  // Online-softmax step on the scores in sc (overwritten by P); branch-free.
+  // The running max moves only when some row's block max exceeds it by more
+  // than the threshold (exponents stay <= 2^threshold until then, which f32
+  // sums and 16-bit P absorb).  hi = P as the 16-bit MFMA operand, per group
+  // of 16 KV positions.  split: some key of this block carries more than
+  // 1/kSplitRatio of its row's probability mass so far, so the rounding of
+  // its P to 16 bits would show in O; then the residual P - hi(P) is
+  // accumulated as well.
+  auto softmax = [&](f32x16 (&sc)[2], u32x4 (&hi)[4], float& alpha, bool& grow, bool& split) {
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, sc[kt][r]);
+    mx = xhalf_max(mx);
+    const float m_blk = mx * scale_log2;
+    const bool growl = m_blk > m_run + kRescaleThreshold || m_run == -INFINITY;
+    grow = __builtin_amdgcn_ballot_w64(growl) != 0;
+    const float m_new = grow ? fmaxf(m_run, m_blk) : m_run;
+    alpha = exp2_fast(m_run - m_new);
+    m_run = m_new;
+    float ls = 0.0f;
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        sc[kt][r] = exp2_fast(__builtin_fmaf(sc[kt][r], scale_log2, -m_new));
+        ls += sc[kt][r];
+      }
+    l_run = __builtin_fmaf(l_run, alpha, ls);
+    const float tot = xhalf_sum(l_run);
+    const float pmax = exp2_fast(m_blk - m_new);
+    split = __builtin_amdgcn_ballot_w64(pmax * fa::kSplitRatio<DT> > tot) != 0;
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+      const int kt = st >> 1, hh = st & 1;
+#pragma unroll
+      for (int pp = 0; pp < 4; ++pp)
+        hi[st][pp] = cvt_pk<DT>(sc[kt][8 * hh + 2 * pp], sc[kt][8 * hh + 2 * pp + 1]);
+    }
+  };
+  // lo = P - hi(P) as 16-bit operands (only for split blocks).
+  auto residual = [&](const f32x16 (&sc)[2], const u32x4 (&hi)[4], u32x4 (&lo)[4]) {
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+      const int kt = st >> 1, hh = st & 1;
+#pragma unroll
+      for (int pp = 0; pp < 4; ++pp) {
+        float a, c;
+        unpack_pair<DT>(hi[st][pp], a, c);
+        lo[st][pp] = cvt_pk<DT>(sc[kt][8 * hh + 2 * pp] - a, sc[kt][8 * hh + 2 * pp + 1] - c);
+      }
+    }
+  };
+  // O^T += V^T.P^T for the block in ring slot `stg`.
+  auto pv = [&](int stg, const u32x4 (&hi)[4], const u32x4 (&lo)[4], bool split) {
+#pragma unroll
+    for (int st = 0; st < 4; ++st)
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt)
+        o_acc[dt] = mfma32x32x16<DT>(read_v(stg, st, dt), hi[st], o_acc[dt]);
+    if (split) {
+#pragma unroll
+      for (int st = 0; st < 4; ++st)
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt)
+          o_acc[dt] = mfma32x32x16<DT>(read_v(stg, st, dt), lo[st], o_acc[dt]);
+    }
+  };
+
+  // Two wave groups share each SIMD (wave w and w+4).  Every wave runs the
+  // same stream RA(0) RB(0) RA(1) RB(1) ..., where RA(j) = softmax of block j
+  // fused with the QK MFMAs of block j+1 and RB(j) = the PV MFMAs of block j;
+  // only the position of the per-block barrier differs: group A (waves 0-3)
+  // meets it after RB(j), group B (waves 4-7) after RA(j).  Between two
+  // barriers A therefore runs RA(j+1) RB(j+1) while B runs RB(j) RA(j+1): one
+  // wave of each SIMD is in its VALU-heavy RA while the other is in its
+  // MFMA-only RB.
+  // Ring: between barriers j-1 and j the waves read K of block j+1 and V of
+  // blocks j-1 (B) and j (A); block j+2 must have landed before barrier j,
+  // and after it the slot of block j-1 is refilled with block j+NS-1.
+  const bool grp_b = wave >= 4;
+  u32x4 hi[4], lo[4];
+  bool split = false;
+  auto RA = [&](uint32_t j, f32x16 (&sc)[2], f32x16 (&sn)[2]) {
+    if (j >= ja) return;
+    const bool nxt = j + 1 < ja;
+    const bool fused = j < jd && nxt;
+    float alpha;
+    bool grow;
+    if (fused) {
+      qk((j + 1) % NS, sn);
+      softmax(sc, hi, alpha, grow, split);
+    } else {
+      if (j >= jd) mask(sc, j * BKV);
+      softmax(sc, hi, alpha, grow, split);
+    }
+    if (grow) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o_acc[i][r] *= alpha;
+    }
+    if (split) residual(sc, hi, lo);
+  };
+  auto RB = [&](uint32_t j, f32x16 (&sn)[2]) {
+    if (j >= ja) return;
+    pv(j % NS, hi, lo, split);
+    if (!(j < jd && j + 1 < ja) && j + 1 < ja) qk((j + 1) % NS, sn);
+  };
+  auto sync = [&](uint32_t j) {
+    if (j + 1 >= nkb) return;
+    lds::wait_lgkm0();
+    if (j + 2 < nkb) {
+      if constexpr (NS >= 5)
+        gemm::wait_stages<NL, NS - 4>(min(nkb - 3 - j, static_cast<uint32_t>(NS - 4)));
+      else
+        lds::wait_vm<0>();
+    }
+    lds::bar();
+    if (j >= 1 && j + NS - 1 < nkb) issue((j - 1) % NS, j + NS - 1);
+  };
+  auto iteration = [&](uint32_t j, f32x16 (&sc)[2], f32x16 (&sn)[2]) {
+    RA(j, sc, sn);
+    if (grp_b) sync(j);
+    RB(j, sn);
+    if (!grp_b) sync(j);
+  };
+
   // The previous work item of this workgroup (grid-stride callers) may still
   // be reading the ring.
   lds::bar();
 #pragma unroll
   for (int s = 0; s < NS; ++s)
     if (static_cast<uint32_t>(s) < nkb) issue(s, s);
-  gemm::wait_stages<NL, NS - 1>(min(nkb - 1, static_cast<uint32_t>(NS - 1)));
+  gemm::wait_stages<NL, NS - 2>(nkb >= 2 ? min(nkb - 2, static_cast<uint32_t>(NS - 2)) : 0u);
   lds::bar();
 
-  for (uint32_t jb = 0; jb < nkb; ++jb) {
-    const int cur = jb % NS;
-    const uint32_t kv0 = jb * BKV;
-    const bool active = (kv0 <= qa_hi) && (qw0 < seq_len);
-    if (active) {
-      float s[2][16];
-      {
-        f32x16 acc[2];
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) acc[i][r] = 0.0f;
-        const u32x4* kb = lds_k(cur);
-#pragma unroll
-        for (int ds = 0; ds < 8; ++ds) {
-#pragma unroll
-          for (int kt = 0; kt < 2; ++kt) {
-            const int row = 32 * kt + l32;
-            const u32x4 kf = kb[row * 16 + ((2 * ds + g) ^ (row & 15))];
-            acc[kt] = mfma32x32x16<DT>(kf, qf[ds], acc[kt]);
-          }
-        }
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) s[kt][r] = acc[kt][r];
-      }
-      if (kv0 + BKV - 1 > qa_lo) {
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const uint32_t pos = kv0 + 32 * kt + 8 * (r >> 2) + 4 * g + (r & 3);
-            if (pos > my_qa) s[kt][r] = -INFINITY;
-          }
-      }
-      float mx = -INFINITY;
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kt][r]);
-      mx = xhalf_max(mx);
-      const float m_blk = mx * scale_log2;
-      float m_use = m_run;
-      const bool grow = m_blk > m_run + kRescaleThreshold || m_run == -INFINITY;
-      if (__builtin_amdgcn_ballot_w64(grow) != 0) {
-        const float m_new = fmaxf(m_run, m_blk);
-        const float alpha = exp2_fast(m_run - m_new);
-        l_run *= alpha;
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) o_acc[i][r] *= alpha;
-        m_run = m_new;
-        m_use = m_new;
-      }
-      float ls = 0.0f;
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          s[kt][r] = exp2_fast(__builtin_fmaf(s[kt][r], scale_log2, -m_use));
-          ls += s[kt][r];
-        }
-      l_run += ls;
-      const float blk = xhalf_sum(ls);
-      const float tot = xhalf_sum(l_run);
-      const bool heavy = blk * fa::kSplitRatio<DT> > tot;
-      const bool split = __builtin_amdgcn_ballot_w64(heavy) != 0;
-#pragma unroll
-      for (int st = 0; st < 4; ++st) {
-        const int kt = st >> 1, hh = st & 1;
-        u32x4 hi;
-#pragma unroll
-        for (int pp = 0; pp < 4; ++pp)
-          hi[pp] = cvt_pk<DT>(s[kt][8 * hh + 2 * pp], s[kt][8 * hh + 2 * pp + 1]);
-        u32x4 vf[4];
-#pragma unroll
-        for (int dt = 0; dt < 4; ++dt) {
-          vf[dt] = read_v(cur, st, dt);
-          o_acc[dt] = mfma32x32x16<DT>(vf[dt], hi, o_acc[dt]);
-        }
-        if (split) {
-          u32x4 lo;
-#pragma unroll
-          for (int pp = 0; pp < 4; ++pp) {
-            float a, c;
-            unpack_pair<DT>(hi[pp], a, c);
-            lo[pp] = cvt_pk<DT>(s[kt][8 * hh + 2 * pp] - a, s[kt][8 * hh + 2 * pp + 1] - c);
-          }
-#pragma unroll
-          for (int dt = 0; dt < 4; ++dt) o_acc[dt] = mfma32x32x16<DT>(vf[dt], lo, o_acc[dt]);
-        }
-      }
-    }
-    // Block jb+1 must have landed for every thread before anyone reads it, and
-    // every read of buffer `cur` must be done before it is refilled.
-    if (jb + 1 < nkb) {
-      lds::wait_lgkm0();
-      gemm::wait_stages<NL, NS - 2>(min(nkb - 2 - jb, static_cast<uint32_t>(NS - 2)));
-      lds::bar();
-      if (jb + NS < nkb) issue(cur, jb + NS);
-    }
+  f32x16 sa[2], sb[2];
+  if (ja > 0) qk(0, sa);
+  for (uint32_t j = 0; j < nkb; j += 2) {
+    iteration(j, sa, sb);
+    if (j + 1 < nkb) iteration(j + 1, sb, sa);
   }
 
   const float l_tot = xhalf_sum(l_run);

@@ -91,7 +91,8 @@ __device__ __forceinline__ void prefill(const void* q, const void* k, const void
       for (uint32_t w = blockIdx.x; w < batch * nh * nqb; w += gridDim.x) {
         uint32_t bh, qb;
         prefill_work(w, batch * nh, nqb, bh, qb);
-        prefill_tile_dma<DT>(static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
+        // 4-stage ring: the general kernel below needs LDS in the same entry
+        prefill_tile_dma<DT, 4>(static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
                              static_cast<const uint16_t*>(v), static_cast<uint16_t*>(o), seq_len,
                              start_pos, max_seq, nh, nkv, scale * kLog2e, bh, qb);
       }
