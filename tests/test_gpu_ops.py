@@ -103,7 +103,9 @@ def test_softmax_config1_full(dev, stream):
 
 
 @pytest.mark.parametrize("rows,cols", [(3, 1000), (5, 77), (7, 1), (2, 5000), (33, 4096),
-                                       (4, 256), (1, 64), (9, 17000)])
+                                       (4, 256), (1, 64), (9, 17000),
+                                       # many rows per wave in the streaming kernel, ragged tail
+                                       (12345, 256), (20001, 128), (9000, 1024), (5000, 60)])
 def test_softmax_f32_shapes(dev, stream, rows, cols):
     rng = np.random.default_rng(rows * 131 + cols)
     x = (rng.standard_normal((rows, cols)) * 2).astype(np.float32)
@@ -115,7 +117,7 @@ def test_softmax_f32_shapes(dev, stream, rows, cols):
 
 
 @pytest.mark.parametrize("dtype", [D.F16, D.BF16])
-@pytest.mark.parametrize("rows,cols", [(64, 2048), (3, 100), (4, 8192)])
+@pytest.mark.parametrize("rows,cols", [(64, 2048), (3, 100), (4, 8192), (17003, 512)])
 def test_softmax_u16(dev, stream, dtype, rows, cols):
     rng = np.random.default_rng(cols)
     x = rand16(rng, rows * cols, dtype, 2.0)

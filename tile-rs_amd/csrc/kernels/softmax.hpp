@@ -112,6 +112,75 @@ softmax_rows_reg(const void* __restrict__ x, void* __restrict__ y, uint32_t rows
                            threadIdx.x & 63);
 }
 
+// Streaming form of the register path: a fixed grid of waves walks the rows
+// (row stride = total waves), and the loads of a wave's next row are issued
+// before the reductions of its current row, so every wave keeps one row of
+// loads in flight.
+template <int DT, int NV>
+__global__ void __launch_bounds__(256)
+softmax_rows_stream(const void* __restrict__ x, void* __restrict__ y, uint32_t rows,
+                    uint32_t cols) {
+  constexpr int ESZ = (DT == kF32) ? 4 : 2;
+  constexpr int E = SoftmaxVec<DT>::kElems;
+  const int lane = threadIdx.x & 63;
+  const uint32_t nvec = cols / E;
+  const uint32_t stride = gridDim.x * (blockDim.x >> 6);
+  uint32_t row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  const size_t rbytes = static_cast<size_t>(cols) * ESZ;
+  u32x4 cur[NV], nxt[NV];
+  auto load = [&](uint32_t r, u32x4 (&v)[NV]) {
+    const char* xr = static_cast<const char*>(x) + static_cast<size_t>(r) * rbytes;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const uint32_t vi = static_cast<uint32_t>(i) * 64u + lane;
+      if (vi < nvec) v[i] = ldg128_nt(xr + static_cast<size_t>(vi) * 16);
+    }
+  };
+  if (row < rows) load(row, cur);
+  for (; row < rows; row += stride) {
+    if (row + stride < rows) load(row + stride, nxt);
+    float v[NV][E];
+    float m = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const uint32_t vi = static_cast<uint32_t>(i) * 64u + lane;
+      if (vi < nvec) {
+        unpack16<DT>(cur[i], v[i]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < E; ++e) v[i][e] = -INFINITY;
+      }
+#pragma unroll
+      for (int e = 0; e < E; ++e) m = fmaxf(m, v[i][e]);
+    }
+    m = wave_max(m);
+    const float mb = m * kLog2e;
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        const float p = exp2_fast(__builtin_fmaf(v[i][e], kLog2e, -mb));
+        v[i][e] = p;
+        s += p;
+      }
+    s = wave_sum(s);
+    const float inv = 1.0f / s;
+    char* yr = static_cast<char*>(y) + static_cast<size_t>(row) * rbytes;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const uint32_t vi = static_cast<uint32_t>(i) * 64u + lane;
+      if (vi < nvec) {
+#pragma unroll
+        for (int e = 0; e < E; ++e) v[i][e] *= inv;
+        stg128_nt(yr + static_cast<size_t>(vi) * 16, pack16<DT>(v[i]));
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < NV; ++i) cur[i] = nxt[i];
+  }
+}
+
 // Any cols, one wavefront per row, three passes over the row (no LDS).
 template <int DT>
 __device__ __forceinline__ float ld_elem(const void* p, size_t i);

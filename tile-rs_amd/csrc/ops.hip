@@ -5,6 +5,8 @@
 // stream.  There is no CPU fallback: a shape no kernel takes is an error.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
+
 #include <cmath>
 #include <cstdint>
 #include <cstdlib>
@@ -34,21 +36,46 @@ bool valid_dtype(th_dtype d) { return d == TH_F32 || d == TH_F16 || d == TH_BF16
 
 // ---- softmax ----------------------------------------------------------------
 
+// Compute units of the calling thread's current device (cached per ordinal).
+uint32_t current_cu_count() {
+  static std::atomic<uint32_t> cache[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  uint32_t n = cache[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        cus <= 0)
+      cus = 256;
+    n = static_cast<uint32_t>(cus);
+    cache[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
+
 template <int DT>
 int softmax_launch(const void* x, void* y, uint32_t rows, uint32_t cols, hipStream_t s) {
   constexpr int E = th::SoftmaxVec<DT>::kElems;
   const bool vec_ok = (cols % E == 0) && aligned16(x) && aligned16(y);
   const uint32_t nvec = cols / E;
+  if (vec_ok && nvec <= 64u * 4u) {
+    // Streaming form: 4 workgroups (16 waves) per CU walk the rows; measured
+    // on MI355X this sustains the copy-kernel bandwidth, while one short-lived
+    // wave per row does not.
+    const uint32_t need = (rows + 3) / 4;
+    const dim3 grid(std::min<uint32_t>(need, 4u * current_cu_count())), block(256);
+    if (nvec <= 64)
+      hipLaunchKernelGGL((th::softmax_rows_stream<DT, 1>), grid, block, 0, s, x, y, rows, cols);
+    else if (nvec <= 128)
+      hipLaunchKernelGGL((th::softmax_rows_stream<DT, 2>), grid, block, 0, s, x, y, rows, cols);
+    else
+      hipLaunchKernelGGL((th::softmax_rows_stream<DT, 4>), grid, block, 0, s, x, y, rows, cols);
+    return launch_status("softmax launch");
+  }
   if (vec_ok && nvec <= 64u * 16u) {
     const uint32_t rows_per_wg = 4;
     const dim3 grid((rows + rows_per_wg - 1) / rows_per_wg), block(256);
-    if (nvec <= 64)
-      hipLaunchKernelGGL((th::softmax_rows_reg<DT, 1>), grid, block, 0, s, x, y, rows, cols);
-    else if (nvec <= 128)
-      hipLaunchKernelGGL((th::softmax_rows_reg<DT, 2>), grid, block, 0, s, x, y, rows, cols);
-    else if (nvec <= 256)
-      hipLaunchKernelGGL((th::softmax_rows_reg<DT, 4>), grid, block, 0, s, x, y, rows, cols);
-    else if (nvec <= 512)
+    if (nvec <= 512)
       hipLaunchKernelGGL((th::softmax_rows_reg<DT, 8>), grid, block, 0, s, x, y, rows, cols);
     else
       hipLaunchKernelGGL((th::softmax_rows_reg<DT, 16>), grid, block, 0, s, x, y, rows, cols);
