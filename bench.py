@@ -166,6 +166,86 @@ class Mlp(Gemm):
         th.fill_random(self.b, self.K * self.N, D.F16, "normal", 0.0, 0.02, SEED0 + 103, s)
 
 
+class Swiglu(Mlp):
+    """Config 3's MLP shape with the gate epilogue fused: C = silu(A.B) * UP (f16)."""
+    name = "swiglu"
+
+    def config(self):
+        return {"workload": "MLP gate GEMM M=8192 K=4096 N=14336 with fused silu*mul "
+                            "epilogue, f16 in, f32 acc, f16 UP and out",
+                "M": self.M, "N": self.N, "K": self.K}
+
+    def setup(self, th, dev, s):
+        super().setup(th, dev, s)
+        D = th.TileDtype
+        self.up = dev.alloc(self.M * self.N, D.F16)
+        th.fill_random(self.up, self.M * self.N, D.F16, "normal", 0.0, 1.0, SEED0 + 203, s)
+
+    def step(self, th, s, i):
+        D = th.TileDtype
+        th.matmul_silu_mul(self.a, self.b, self.up, self.c, self.M, self.K, self.N, D.F16, D.F16,
+                           False, stream=s)
+
+    def cpu_sample(self, th, s, seconds):
+        from oracle import oracle as orc
+        import numpy as np
+        a = self.a.copy_to_host(s).reshape(self.M, self.K)
+        b, up = self.b.copy_to_host(s), self.up.copy_to_host(s).reshape(self.M, self.N)
+        rows, t0, chunk = 0, time.perf_counter(), 32
+        while True:
+            r0 = rows % self.M
+            orc.matmul_silu_mul(np.ascontiguousarray(a[r0:r0 + chunk]), b,
+                                np.ascontiguousarray(up[r0:r0 + chunk]), chunk, self.K, self.N,
+                                orc.F16, orc.F16)
+            rows += chunk
+            el = time.perf_counter() - t0
+            if el >= seconds:
+                break
+        return 2.0 * rows * self.K * self.N / el / 1e12, (
+            f"{rows} rows of the gate GEMM + silu*mul, oracle f32")
+
+
+class RmsNorm(Workload):
+    """Row RMSNorm on an LLM hidden-state shape: 8192 tokens x 4096, bf16."""
+    name, index, bound, dtype, unit = "rmsnorm", 6, "hbm", "bf16", "GB/s"
+    rows, cols, eps = 8192, 4096, 1e-6
+
+    def work(self):
+        return 2.0 * self.rows * self.cols * 2
+
+    def config(self):
+        return {"workload": "row RMSNorm bf16 8192x4096 (f32 math), X~N(0,1), eps 1e-6",
+                "rows": self.rows, "cols": self.cols}
+
+    def setup(self, th, dev, s):
+        D = th.TileDtype
+        n = self.rows * self.cols
+        self.sets = []
+        for r in range(rotation_sets(2 * n * 2)):
+            x = dev.alloc(n, D.BF16)
+            th.fill_random(x, n, D.BF16, "normal", 0.0, 1.0, SEED0 + self.index + 1000 * r, s)
+            self.sets.append((x, dev.alloc(n, D.BF16)))
+
+    def step(self, th, s, i):
+        x, y = self.sets[i % len(self.sets)]
+        th.rms_norm(x, y, self.rows, self.cols, self.eps, th.TileDtype.BF16, s)
+
+    def cpu_sample(self, th, s, seconds):
+        from oracle import oracle as orc
+        import numpy as np
+        x = self.sets[0][0].copy_to_host(s).reshape(self.rows, self.cols)
+        done, t0 = 0, time.perf_counter()
+        while True:
+            r0 = (done * 256) % self.rows
+            orc.rms_norm(np.ascontiguousarray(x[r0:r0 + 256]), 256, self.cols, self.eps, orc.BF16)
+            done += 1
+            el = time.perf_counter() - t0
+            if el >= seconds:
+                break
+        rows = done * 256
+        return rows * self.cols * 4 / el / 1e9, f"{rows} rows of the 8192x4096 RMSNorm"
+
+
 class Attn(Workload):
     name, index, bound, dtype, unit = "attn", 4, "mfma", "bf16", "TFLOP/s"
     B, H, S, Dh = 4, 32, 4096, 128
@@ -279,7 +359,7 @@ class Copy(Workload):
         return 0.0, "none"
 
 
-WORKLOADS = {w.name: w for w in (Softmax, Gemm, Mlp, Attn, Decode, Copy)}
+WORKLOADS = {w.name: w for w in (Softmax, Gemm, Mlp, Attn, Decode, Swiglu, RmsNorm, Copy)}
 BENCH_LINES = ("attn", "decode", "gemm", "mlp", "softmax")
 
 

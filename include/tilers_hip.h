@@ -150,6 +150,24 @@ int th_matmul(const void* a, const void* b, void* c, uint32_t m, uint32_t k, uin
               th_dtype in_dtype, th_dtype out_dtype, int b_transposed, uint32_t batch,
               uint64_t sa, uint64_t sb, uint64_t sc, th_stream s);
 
+/* GEMM with the SiLU*Mul epilogue fused: C = silu(A.B) * UP, elementwise, where
+ * silu(x) = x / (1 + exp(-x)).  Replaces the tile chain matmul -> __tile_silu_*
+ * -> __tile_mul_* (tile.rs:229, :1135; linalg mlir_to_linalg.rs:449-451,
+ * :774-782, :425; the gpu target fuses silu+mul the same way,
+ * mlir_to_gpu.rs:536-634).  UP has out_dtype and C's layout and strides;
+ * arithmetic is f32 with one rounding at the output.  Other arguments as
+ * th_matmul. */
+int th_matmul_silu_mul(const void* a, const void* b, const void* up, void* c, uint32_t m,
+                       uint32_t k, uint32_t n, th_dtype in_dtype, th_dtype out_dtype,
+                       int b_transposed, uint32_t batch, uint64_t sa, uint64_t sb, uint64_t sc,
+                       th_stream s);
+
+/* Row RMSNorm (__tile_rms_norm_f32(dst, src, eps, rows, cols), tile.rs:2063;
+ * linalg mlir_to_linalg.rs:1666-1763): y = x * rsqrt(sum(x^2) / cols + eps) per
+ * row, f32 math for every dtype.  eps must be >= 0. */
+int th_rms_norm(const void* x, void* y, uint32_t rows, uint32_t cols, float eps, th_dtype dtype,
+                th_stream s);
+
 /* Causal mask (__tile_causal_mask_f32, tile.rs:1877, :2435; linalg
  * mlir_to_linalg.rs:1191-1247): y[r][c] = x[r][c] if c <= r else -inf, for
  * `tiles` stacked rows x cols tiles. */

@@ -26,6 +26,12 @@
  *                            with NKV = NH reducing to MHA, row 0 -> V[0].
  *   attention decode      — equals the last row of prefill; one position -> V;
  *                            golden vectors from torch CPU.
+ *   rms_norm              — golden vectors from torch CPU (F.rms_norm); scale
+ *                            invariance at eps = 0; constant and one-hot rows;
+ *                            mean(y^2) = mean / (mean + eps).
+ *   silu_mul, matmul_silu_mul — golden vectors from torch CPU (F.silu);
+ *                            silu(0) = 0, silu(x) - silu(-x) = x, silu(x) -> x
+ *                            for large x; the matmul part as matmul.
  * Nothing here is "parity unpinned".
  */
 #include <math.h>
@@ -175,6 +181,42 @@ ORC_EXPORT void orc_softmax_u16(const uint16_t* x, uint16_t* y, int64_t rows, in
 }
 
 /* ------------------------------------------------------------------------ */
+/* RMSNorm (__tile_rms_norm_f32(dst, src, eps, rows, cols), tile.rs:2063;    */
+/* linalg mlir_to_linalg.rs:1666-1763): sq = x*x; red = sum over dim 1;      */
+/* mean = red / cols; var = mean + eps; rs = rsqrt(var); y = x * rs.  The     */
+/* sum is taken in double here (the f32 reduction order of a linalg lowering */
+/* is unspecified); 16-bit I/O is widened exactly and narrowed RNE.          */
+/* ------------------------------------------------------------------------ */
+
+ORC_EXPORT void orc_rms_norm(const void* x, void* y, int64_t rows, int64_t cols, double eps,
+                             int dtype) {
+    #pragma omp parallel for schedule(static) if (rows * cols > (1 << 15))
+    for (int64_t r = 0; r < rows; ++r) {
+        double ss = 0.0;
+        for (int64_t j = 0; j < cols; ++j) {
+            double v = (double)load_elem(x, r * cols + j, dtype);
+            ss += v * v;
+        }
+        double rs = 1.0 / sqrt(ss / (double)cols + eps);
+        for (int64_t j = 0; j < cols; ++j)
+            store_elem(y, r * cols + j, dtype,
+                       (float)((double)load_elem(x, r * cols + j, dtype) * rs));
+    }
+}
+
+/* SiLU * Mul (linalg mlir_to_linalg.rs:774-782: silu(x) = x / (1 + exp(-x)),  */
+/* then the elementwise linalg.mul of :425): out = silu(gate) * up, double     */
+/* math on exactly widened inputs, one RNE narrowing.                          */
+static float silu_mul1(double g, double u) { return (float)(g / (1.0 + exp(-g)) * u); }
+
+ORC_EXPORT void orc_silu_mul(const void* gate, const void* up, void* out, int64_t n, int dtype) {
+    #pragma omp parallel for schedule(static) if (n > (1 << 15))
+    for (int64_t i = 0; i < n; ++i)
+        store_elem(out, i, dtype,
+                   silu_mul1((double)load_elem(gate, i, dtype), (double)load_elem(up, i, dtype)));
+}
+
+/* ------------------------------------------------------------------------ */
 /* Matmul: `linalg.fill 0` + `linalg.matmul` on f32 tensors                  */
 /* (mlir_to_linalg.rs:1345-1393).  16-bit operands are widened exactly      */
 /* (`arith.extf`) before the contraction, the accumulator is f32, and the    */
@@ -230,6 +272,21 @@ ORC_EXPORT void orc_matmul(const void* a, const void* b, void* c, int64_t m, int
 /* Causal mask (mlir_to_linalg.rs:1191-1247): keep x[r][c] when c <= r,     */
 /* otherwise write -inf (0xFF800000).                                        */
 /* ------------------------------------------------------------------------ */
+
+/* C = silu(A.B) * UP for rows [row0, row0 + nrows): the matmul above with an */
+/* f32 result (no intermediate rounding), then silu*mul with UP (c_dtype,     */
+/* C's layout) and one RNE narrowing to c_dtype.                              */
+ORC_EXPORT void orc_matmul_silu_mul_rows(const void* a, const void* b, const void* up, void* c,
+                                         int64_t m, int64_t k, int64_t n, int ab_dtype,
+                                         int c_dtype, int b_trans, int64_t row0, int64_t nrows) {
+    float* acc = (float*)malloc(sizeof(float) * (size_t)nrows * (size_t)n);
+    orc_matmul_rows(a, b, acc, m, k, n, ab_dtype, ab_dtype, ORC_F32, b_trans, row0, nrows);
+    #pragma omp parallel for schedule(static) if (nrows * n > (1 << 15))
+    for (int64_t i = 0; i < nrows * n; ++i)
+        store_elem(c, i, c_dtype,
+                   silu_mul1((double)acc[i], (double)load_elem(up, row0 * n + i, c_dtype)));
+    free(acc);
+}
 
 ORC_EXPORT void orc_causal_mask_f32(const float* x, float* y, int64_t rows, int64_t cols) {
     const float ninf = bits_f32(0xff800000u);

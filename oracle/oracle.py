@@ -48,6 +48,9 @@ def lib():
         L.orc_matmul_rows.argtypes = [vp, vp, vp, i64, i64, i64, i, i, i, i, i64, i64]
         L.orc_matmul.argtypes = [vp, vp, vp, i64, i64, i64, i, i, i, i]
         L.orc_causal_mask_f32.argtypes = [vp, vp, i64, i64]
+        L.orc_rms_norm.argtypes = [vp, vp, i64, i64, C.c_double, i]
+        L.orc_silu_mul.argtypes = [vp, vp, vp, i64, i]
+        L.orc_matmul_silu_mul_rows.argtypes = [vp, vp, vp, vp, i64, i64, i64, i, i, i, i64, i64]
         L.orc_attention_f32.argtypes = [vp, vp, vp, vp, i64, i64]
         L.orc_attention_prefill.argtypes = [vp, vp, vp, vp, i, i] + [i64] * 11
         L.orc_attention_decode.argtypes = [vp, vp, vp, vp, i, i] + [i64] * 8
@@ -108,6 +111,37 @@ def matmul(a, b, m, k, n, in_dtype, out_dtype=F32, b_trans=False, row0=0, nrows=
     c = np.empty((nrows, n), np.float32 if out_dtype == F32 else np.uint16)
     lib().orc_matmul_rows(_ptr(a), _ptr(b), _ptr(c), m, k, n, in_dtype, in_dtype, out_dtype,
                           int(b_trans), row0, nrows)
+    return c
+
+
+def rms_norm(x: np.ndarray, rows: int, cols: int, eps: float, dtype: int = F32) -> np.ndarray:
+    """y = x * rsqrt(sum(x^2)/cols + eps) per row (mlir_to_linalg.rs:1666-1763)."""
+    x = np.ascontiguousarray(x)
+    y = np.empty_like(x)
+    lib().orc_rms_norm(_ptr(x), _ptr(y), rows, cols, float(eps), dtype)
+    return y
+
+
+def silu_mul(gate: np.ndarray, up: np.ndarray, dtype: int = F32) -> np.ndarray:
+    """silu(gate) * up elementwise (mlir_to_linalg.rs:774-782, :425)."""
+    gate = np.ascontiguousarray(gate)
+    up = np.ascontiguousarray(up)
+    assert gate.shape == up.shape and gate.dtype == up.dtype
+    out = np.empty_like(gate)
+    lib().orc_silu_mul(_ptr(gate), _ptr(up), _ptr(out), gate.size, dtype)
+    return out
+
+
+def matmul_silu_mul(a, b, up, m, k, n, in_dtype, out_dtype=F32, b_trans=False, row0=0,
+                    nrows=None):
+    """Rows [row0, row0+nrows) of silu(A*B) * UP; UP is the full m x n tensor."""
+    a = np.ascontiguousarray(a)
+    b = np.ascontiguousarray(b)
+    up = np.ascontiguousarray(up)
+    nrows = m - row0 if nrows is None else nrows
+    c = np.empty((nrows, n), np.float32 if out_dtype == F32 else np.uint16)
+    lib().orc_matmul_silu_mul_rows(_ptr(a), _ptr(b), _ptr(up), _ptr(c), m, k, n, in_dtype,
+                                   out_dtype, int(b_trans), row0, nrows)
     return c
 
 

@@ -12,10 +12,13 @@ kernels, run in float64 — on small seeded inputs, and they pin the C oracle:
   attention_f32.npz    transpose/matmul/scale/softmax/matmul (mlir_to_linalg.rs:1781-1902)
   prefill_bf16.npz     causal GQA prefill                  (mlir_to_msl.rs:10928-11009)
   decode_bf16.npz      GQA decode                          (mlir_to_msl.rs:10747-10816)
+  rms_norm_f32.npz     RMSNorm, torch.nn.functional.rms_norm (mlir_to_linalg.rs:1666-1763)
+  swiglu_bf16.npz      silu(A.B) * UP, torch.nn.functional.silu (mlir_to_linalg.rs:774-782, :425)
 
 Inputs are stored exactly as the kernels see them (f32, or bf16/f16 bit
 patterns as uint16); expected outputs are float64 results rounded to f32.
-Run: python tests/golden/make_golden.py   (CPU only; torch is not needed anywhere else)
+Run: python tests/golden/make_golden.py [case ...]   (CPU only; torch is not needed
+anywhere else; with no arguments every case is written)
 """
 from __future__ import annotations
 
@@ -101,11 +104,35 @@ def decode_case():
              o=o.numpy(), shape=np.array([B, L, max_seq, D, NH, NKV]))
 
 
+def rms_norm_case():
+    g = torch.Generator().manual_seed(16)
+    x = torch.randn(6, 768, generator=g, dtype=torch.float32) * 3.0
+    x[2] = -0.75                 # constant row -> -0.75 / sqrt(0.5625 + eps)
+    x[4] = 0.0
+    x[4, 17] = 5.0               # one-hot row
+    eps = 1e-5
+    y = torch.nn.functional.rms_norm(x.double(), (768,), eps=eps).float()
+    np.savez(HERE / "rms_norm_f32.npz", x=x.numpy(), y=y.numpy(), eps=np.array([eps]))
+
+
+def swiglu_case():
+    g = torch.Generator().manual_seed(17)
+    m, k, n = 48, 64, 72
+    a = torch.randn(m, k, generator=g).to(torch.bfloat16)
+    b = (torch.randn(k, n, generator=g) * 0.3).to(torch.bfloat16)
+    up = torch.randn(m, n, generator=g, dtype=torch.float32)
+    c = (torch.nn.functional.silu(a.double() @ b.double()) * up.double()).float()
+    np.savez(HERE / "swiglu_bf16.npz", a=bf16_bits(a), b=bf16_bits(b), up=up.numpy(), c=c.numpy(),
+             mkn=np.array([m, k, n]))
+
+
+CASES = {"softmax": softmax_case, "matmul": matmul_case, "attention": attention_case,
+         "prefill": prefill_case, "decode": decode_case, "rms_norm": rms_norm_case,
+         "swiglu": swiglu_case}
+
 if __name__ == "__main__":
-    softmax_case()
-    matmul_case()
-    attention_case()
-    prefill_case()
-    decode_case()
+    import sys
+    for name in (sys.argv[1:] or list(CASES)):
+        CASES[name]()
     for p in sorted(HERE.glob("*.npz")):
         print(p.name, p.stat().st_size)

@@ -108,12 +108,14 @@ def test_registry_hip_matches_direct_emit():
 @pytest.mark.parametrize("example,entry", [
     ("softmax_rows", "th::entry::softmax_rows<th::kF32, 4>"),
     ("softmax_generic", "th::entry::softmax_rows<th::kBF16, 4>"),
-    ("matmul_bf16", "th::entry::gemm<th::kBF16, th::kF32, false>"),
-    ("matmul_f16_t", "th::entry::gemm<th::kF16, th::kF16, true>"),
-    ("matmul_f32", "th::entry::gemm_fma<th::kF32, th::kF32, false>"),
+    ("matmul_bf16", "th::entry::gemm<th::kBF16, th::kF32, false, th::gemm::kEpiStore>"),
+    ("matmul_f16_t", "th::entry::gemm<th::kF16, th::kF16, true, th::gemm::kEpiStore>"),
+    ("matmul_f32", "th::entry::gemm_fma<th::kF32, th::kF32, false, th::gemm::kEpiStore>"),
     ("attention_f32", "th::entry::attention_tiles<th::kF32, 256>"),
     ("prefill_bf16", "th::entry::prefill<th::kBF16>"),
     ("decode_bf16", "th::entry::decode<th::kBF16>"),
+    ("rms_norm_rows", "th::entry::rms_norm_rows<th::kF32>"),
+    ("swiglu_gate_bf16", "th::entry::gemm<th::kBF16, th::kF32, false, th::gemm::kEpiSiluMul>"),
 ])
 def test_hot_ops_lower_to_hand_written_kernels(example, entry):
     out = th.emit((EXAMPLES / f"{example}.mlir").read_text())
@@ -198,3 +200,29 @@ def test_compile_error_is_reported(tmp_path):
     with pytest.raises(th.HalError) as e:
         th.compile_source("this is not C++", tmp_path / "bad.hsaco")
     assert "hipcc failed" in str(e.value)
+
+
+def test_rms_norm_eps_and_shape_are_exact():
+    out = th.emit((EXAMPLES / "rms_norm_rows.mlir").read_text()).source
+    # eps constant 9.99999997E-7 is the f32 nearest 1e-6, printed exactly
+    assert "th_tiles * 4u, 768u, 0x1.0c6f7ap-20f)" in out
+
+
+def test_fused_swiglu_takes_up_from_its_own_view():
+    out = th.emit((EXAMPLES / "swiglu_gate_bf16.mlir").read_text()).source
+    # C = silu(X.W) * U: A = p0, B = p1, C = p3, UP = p2 (f32, the output dtype)
+    assert ("(reinterpret_cast<float*>(p3)), 256u, 256u, 512u, th_tiles, "
+            "(reinterpret_cast<const float*>(p2)));") in out
+    assert "silu*mul epilogue" in out
+
+
+def test_fused_swiglu_rejects_up_in_another_dtype():
+    text = (EXAMPLES / "swiglu_gate_bf16.mlir").read_text().replace(
+        "%u = llvm.call @__tile_load_f32(%arg2", "%u = llvm.call @__tile_load_f16(%arg2")
+    with pytest.raises(th.HalError, match="UP in the output dtype"):
+        th.emit(text)
+
+
+def test_silu_mul_without_matmul_stays_elementwise():
+    out = th.emit((EXAMPLES / "swiglu_mask.mlir").read_text()).source
+    assert "elementwise" in out and "kEpiSiluMul" not in out

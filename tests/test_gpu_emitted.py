@@ -26,7 +26,8 @@ D = th.TileDtype
 def launcher(dev):
     lau = dev.create_launcher()
     for stem in ("softmax_rows", "softmax_generic", "matmul_bf16", "matmul_f16_t", "matmul_f32",
-                 "attention_f32", "prefill_bf16", "decode_bf16", "swiglu_mask"):
+                 "attention_f32", "prefill_bf16", "decode_bf16", "swiglu_mask", "rms_norm_rows",
+                 "swiglu_gate_bf16"):
         lau.load(_build.example_path(stem), th.KernelMode.GENERAL)
     return lau
 
@@ -95,6 +96,34 @@ def test_matmul_f32_fma_integer_exact(dev, stream, launcher):
     ab, bb, cb = up(dev, stream, a, D.F32), up(dev, stream, b, D.F32), dev.alloc(M * N, D.F32)
     launcher.launch("matmul_f32", th.LaunchGrid.blocks_only(1), [ptr(ab), ptr(bb), ptr(cb)], stream)
     assert np.array_equal(cb.copy_to_host(stream).reshape(M, N), (a.astype(np.int64) @ b).astype(np.float32))
+
+
+def test_rms_norm_rows_f32(dev, stream, launcher):
+    tiles = 500  # 4 x 768 tiles
+    rng = np.random.default_rng(11)
+    x = (rng.standard_normal((tiles * 4, 768)) * 1.5).astype(np.float32)
+    xb, yb = up(dev, stream, x, D.F32), dev.alloc(x.size, D.F32)
+    launcher.launch("rms_norm_rows_f32", th.LaunchGrid.blocks_only(tiles), [ptr(xb), ptr(yb)], stream)
+    eps = float(np.float32(9.99999997e-7))
+    assert_softmax_close(yb.copy_to_host(stream).reshape(tiles * 4, 768),
+                         orc.rms_norm(x, tiles * 4, 768, eps), "emitted rms_norm")
+
+
+def test_swiglu_gate_bf16_fused(dev, stream, launcher):
+    tiles, M, K, N = 3, 256, 512, 256
+    rng = np.random.default_rng(12)
+    a = orc.narrow(rng.standard_normal(tiles * M * K).astype(np.float32), orc.BF16)
+    b = orc.narrow((rng.standard_normal(tiles * K * N) * 0.05).astype(np.float32), orc.BF16)
+    u = rng.standard_normal(tiles * M * N).astype(np.float32)
+    ab, bb, ub = up(dev, stream, a, D.BF16), up(dev, stream, b, D.BF16), up(dev, stream, u, D.F32)
+    cb = dev.alloc(tiles * M * N, D.F32)
+    launcher.launch("swiglu_gate_bf16", th.LaunchGrid.blocks_only(tiles),
+                    [ptr(ab), ptr(bb), ptr(ub), ptr(cb)], stream)
+    got = cb.copy_to_host(stream).reshape(tiles, M, N)
+    for t in range(tiles):
+        ref = orc.matmul_silu_mul(a[t * M * K:(t + 1) * M * K], b[t * K * N:(t + 1) * K * N],
+                                  u[t * M * N:(t + 1) * M * N], M, K, N, orc.BF16, orc.F32)
+        assert_gemm_close(got[t], ref, f"emitted swiglu tile {t}")
 
 
 def test_attention_f32_tiles(dev, stream, launcher, golden):

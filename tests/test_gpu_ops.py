@@ -381,3 +381,117 @@ def test_decode_matches_last_prefill_row(dev, stream):
     od = run_decode(dev, stream, q, k, v, D.BF16, B, L, L, Dh, NH, NKV)
     op = run_prefill(dev, stream, q, k, v, D.BF16, B, 1, L - 1, L, Dh, NH, NKV)
     assert_attn_close(od, op, "decode vs prefill last row")
+
+
+# ---- rms_norm (row RMSNorm, tile.rs:2063) ------------------------------------------------
+
+def test_rms_norm_golden_vectors(dev, stream, golden):
+    g = golden("rms_norm_f32.npz")
+    x = g["x"]
+    rows, cols = x.shape
+    xb, yb = upload(dev, stream, x, D.F32), dev.alloc(x.size, D.F32)
+    th.rms_norm(xb, yb, rows, cols, float(g["eps"][0]), D.F32, stream)
+    assert_softmax_close(yb.copy_to_host(stream).reshape(rows, cols), g["y"], "rms_norm golden")
+
+
+@pytest.mark.parametrize("rows,cols,eps", [(8192, 1024, 1e-6), (3, 1000, 1e-5), (7, 1, 1e-5),
+                                           (12345, 256, 1e-6), (5, 5003, 0.0), (20001, 128, 1e-5),
+                                           (33, 4096, 1e-6), (2, 77, 0.5)])
+def test_rms_norm_f32_shapes(dev, stream, rows, cols, eps):
+    rng = np.random.default_rng(rows * 17 + cols)
+    x = (rng.standard_normal((rows, cols)) * 1.5).astype(np.float32)
+    xb, yb = upload(dev, stream, x, D.F32), dev.alloc(x.size, D.F32)
+    th.rms_norm(xb, yb, rows, cols, eps, D.F32, stream)
+    assert_softmax_close(yb.copy_to_host(stream).reshape(rows, cols),
+                         orc.rms_norm(x, rows, cols, eps), f"rms_norm {rows}x{cols}")
+
+
+@pytest.mark.parametrize("dtype", [D.F16, D.BF16])
+@pytest.mark.parametrize("rows,cols", [(64, 2048), (3, 100), (4, 8192), (17003, 512)])
+def test_rms_norm_u16(dev, stream, dtype, rows, cols):
+    rng = np.random.default_rng(cols + 5)
+    x = rand16(rng, rows * cols, dtype, 2.0)
+    xb, yb = upload(dev, stream, x, dtype), dev.alloc(x.size, dtype)
+    th.rms_norm(xb, yb, rows, cols, 1e-6, dtype, stream)
+    y = orc.widen(yb.copy_to_host(stream), ORC[dtype])
+    ref = orc.widen(orc.rms_norm(x, rows, cols, 1e-6, ORC[dtype]), ORC[dtype])
+    assert_within_ulp16(y, ref, ORC[dtype], 1.0, f"rms_norm {dtype.name} {rows}x{cols}")
+
+
+def test_rms_norm_in_place_and_errors(dev, stream):
+    rng = np.random.default_rng(8)
+    x = rng.standard_normal((16, 1024)).astype(np.float32)
+    b = upload(dev, stream, x, D.F32)
+    th.rms_norm(b, b, 16, 1024, 1e-6, D.F32, stream)
+    assert_softmax_close(b.copy_to_host(stream).reshape(16, 1024), orc.rms_norm(x, 16, 1024, 1e-6))
+    with pytest.raises(th.HalError):
+        th.rms_norm(b, b, 16, 1024, -1.0, D.F32, stream)
+
+
+# ---- matmul with the SiLU*Mul epilogue (matmul -> silu -> mul chain) ---------------------
+
+def _swiglu_case(dev, stream, rng, m, k, n, in_dt, out_dt, trans, batch=1):
+    a = rand16(rng, batch * m * k, in_dt) if in_dt != D.F32 else \
+        rng.standard_normal(batch * m * k).astype(np.float32)
+    b = (rand16(rng, batch * k * n, in_dt, 0.1) if in_dt != D.F32 else
+         (rng.standard_normal(batch * k * n) * 0.1).astype(np.float32))
+    u32 = rng.standard_normal(batch * m * n).astype(np.float32)
+    u = u32 if out_dt == D.F32 else orc.narrow(u32, ORC[out_dt])
+    ab, bb, ub = (upload(dev, stream, a, in_dt), upload(dev, stream, b, in_dt),
+                  upload(dev, stream, u, out_dt))
+    cb = dev.alloc(batch * m * n, out_dt)
+    th.matmul_silu_mul(ab, bb, ub, cb, m, k, n, in_dt, out_dt, trans, batch, stream=stream)
+    raw = cb.copy_to_host(stream)
+    got = (raw if out_dt == D.F32 else orc.widen(raw, ORC[out_dt])).reshape(batch, m, n)
+    for i in range(batch):
+        ref = orc.matmul_silu_mul(a[i * m * k:(i + 1) * m * k], b[i * k * n:(i + 1) * k * n],
+                                  u[i * m * n:(i + 1) * m * n], m, k, n, ORC[in_dt], ORC[out_dt],
+                                  b_trans=trans)
+        ref32 = ref if out_dt == D.F32 else orc.widen(ref, ORC[out_dt])
+        assert_gemm_close(got[i], ref32.reshape(m, n), f"swiglu {m}x{k}x{n} batch {i}",
+                          u16_dtype=None if out_dt == D.F32 else ORC[out_dt])
+
+
+def test_matmul_silu_mul_golden_vectors(dev, stream, golden):
+    g = golden("swiglu_bf16.npz")
+    m, k, n = (int(v) for v in g["mkn"])
+    ab, bb = upload(dev, stream, g["a"], D.BF16), upload(dev, stream, g["b"], D.BF16)
+    ub, cb = upload(dev, stream, g["up"], D.F32), dev.alloc(m * n, D.F32)
+    th.matmul_silu_mul(ab, bb, ub, cb, m, k, n, D.BF16, D.F32, False, stream=stream)
+    assert_gemm_close(cb.copy_to_host(stream).reshape(m, n), g["c"], "swiglu golden")
+
+
+@pytest.mark.parametrize("m,k,n,in_dt,out_dt,trans", [
+    (512, 512, 768, D.BF16, D.F32, False),    # LDS-DMA pipeline
+    (256, 1024, 512, D.F16, D.F16, True),     # LDS-DMA pipeline, B stored N x K
+    (512, 96, 256, D.BF16, D.BF16, False),    # register-staged MFMA (K % 64 != 0)
+    (300, 72, 136, D.F16, D.F32, False),      # ragged MFMA tiles
+    (64, 33, 40, D.BF16, D.F32, True),        # FMA fallback (K % 8 != 0)
+    (96, 64, 80, D.F32, D.F32, False),        # f32 operands
+])
+def test_matmul_silu_mul_shapes(dev, stream, m, k, n, in_dt, out_dt, trans):
+    _swiglu_case(dev, stream, np.random.default_rng(m + 3 * k + 5 * n), m, k, n, in_dt, out_dt,
+                 trans)
+
+
+def test_matmul_silu_mul_batched(dev, stream):
+    _swiglu_case(dev, stream, np.random.default_rng(77), 256, 128, 256, D.F16, D.F16, False,
+                 batch=3)
+
+
+def test_matmul_silu_mul_config3_subset(dev, stream):
+    """The MLP shape of BASELINE config 3 with the gate epilogue: 96 rows checked."""
+    m, k, n = 8192, 4096, 14336
+    a = device_random(dev, stream, m * k, D.F16, "normal", 0.0, 1.0, 0x71130000 + 3)
+    b = device_random(dev, stream, k * n, D.F16, "normal", 0.0, 0.02, 0x71130000 + 103)
+    u = device_random(dev, stream, m * n, D.F16, "normal", 0.0, 1.0, 0x71130000 + 203)
+    c = dev.alloc(m * n, D.F16)
+    th.matmul_silu_mul(a, b, u, c, m, k, n, D.F16, D.F16, False, stream=stream)
+    ah = a.copy_to_host(stream).reshape(m, k)
+    bh, uh = b.copy_to_host(stream), u.copy_to_host(stream)
+    got = orc.widen(c.copy_to_host(stream), orc.F16).reshape(m, n)
+    for r0 in (0, 4064, 8160):
+        ref = orc.matmul_silu_mul(np.ascontiguousarray(ah[r0:r0 + 32]), bh,
+                                  uh.reshape(m, n)[r0:r0 + 32], 32, k, n, orc.F16, orc.F16)
+        assert_gemm_close(got[r0:r0 + 32], orc.widen(ref, orc.F16).reshape(32, n),
+                          f"config3 swiglu rows {r0}", u16_dtype=orc.F16)

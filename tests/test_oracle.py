@@ -108,6 +108,87 @@ def test_softmax_u16_is_f32_softmax_rounded():
     assert np.array_equal(y, orc.narrow(ref, BF16))
 
 
+# ---- rms_norm ------------------------------------------------------------------------------
+
+def test_rms_norm_golden(golden):
+    g = golden("rms_norm_f32.npz")
+    x = g["x"]
+    y = orc.rms_norm(x, *x.shape, float(g["eps"][0]))
+    assert np.allclose(y, g["y"], rtol=2e-6, atol=0)
+
+
+def test_rms_norm_closed_forms():
+    eps = 1e-5
+    c = np.full((1, 64), -0.75, np.float32)  # constant row -> c / sqrt(c^2 + eps)
+    assert np.allclose(orc.rms_norm(c, 1, 64, eps), -0.75 / np.sqrt(0.5625 + eps), rtol=1e-7)
+    h = np.zeros((1, 100), np.float32)       # one-hot row: v * rsqrt(v^2/100 + eps)
+    h[0, 7] = 5.0
+    yh = orc.rms_norm(h, 1, 100, eps)
+    assert np.isclose(yh[0, 7], 5.0 / np.sqrt(25.0 / 100 + eps), rtol=1e-7)
+    assert np.all(np.delete(yh[0], 7) == 0.0)
+
+
+def test_rms_norm_invariants():
+    rng = np.random.default_rng(21)
+    x = rng.standard_normal((32, 300)).astype(np.float32)
+    # eps = 0: every row has mean(y^2) = 1, and scaling by a power of two cancels
+    y0 = orc.rms_norm(x, 32, 300, 0.0)
+    assert np.allclose((y0.astype(np.float64) ** 2).mean(axis=1), 1.0, rtol=1e-6)
+    y4 = orc.rms_norm((x * -4.0).astype(np.float32), 32, 300, 0.0)
+    assert np.array_equal(y4, -y0)
+    # eps > 0: mean(y^2) = mean / (mean + eps)
+    eps = 0.25
+    y = orc.rms_norm(x, 32, 300, eps)
+    ms = (x.astype(np.float64) ** 2).mean(axis=1)
+    assert np.allclose((y.astype(np.float64) ** 2).mean(axis=1), ms / (ms + eps), rtol=1e-6)
+
+
+def test_rms_norm_u16_is_f32_rms_norm_rounded():
+    rng = np.random.default_rng(22)
+    x = orc.narrow(rng.standard_normal((8, 192)).astype(np.float32), BF16)
+    y = orc.rms_norm(x, 8, 192, 1e-6, BF16)
+    ref = orc.rms_norm(orc.widen(x, BF16), 8, 192, 1e-6)
+    diff = np.abs(y.astype(np.int32) - orc.narrow(ref, BF16).astype(np.int32))
+    assert diff.max() <= 1  # f64 -> f32 -> bf16 vs f64 -> bf16 may differ by one ulp
+
+
+# ---- silu * mul ----------------------------------------------------------------------------
+
+def test_silu_mul_closed_forms():
+    x = np.array([0.0, 1.0, -1.0, 3.5, -3.5, 40.0, -40.0, 100.0], np.float32)
+    ones = np.ones_like(x)
+    s = orc.silu_mul(x, ones).astype(np.float64)
+    assert s[0] == 0.0
+    assert np.allclose(s[1] - s[2], 1.0, rtol=1e-7) and np.allclose(s[3] - s[4], 3.5, rtol=1e-7)
+    assert s[5] == np.float32(40.0) and abs(s[6]) < 1e-15 and s[7] == 100.0
+    assert np.isclose(s[1], 1.0 / (1.0 + np.exp(-1.0)), rtol=1e-7)
+    up = np.array([2.0, -3.0, 0.5, 1.0, 1.0, 1.0, 1.0, 0.0], np.float32)
+    assert np.allclose(orc.silu_mul(x, up), s * up, rtol=1e-7)
+
+
+def test_matmul_silu_mul_golden(golden):
+    g = golden("swiglu_bf16.npz")
+    m, k, n = g["mkn"]
+    c = orc.matmul_silu_mul(g["a"], g["b"], g["up"], m, k, n, BF16, F32)
+    rms = np.sqrt(np.mean(g["c"].astype(np.float64) ** 2))
+    assert np.abs(c - g["c"]).max() <= 1e-5 * rms
+
+
+def test_matmul_silu_mul_is_silu_mul_of_matmul():
+    rng = np.random.default_rng(23)
+    m, k, n = 40, 24, 56
+    a = orc.narrow(rng.standard_normal((m, k)).astype(np.float32), F16)
+    b = orc.narrow(rng.standard_normal((n, k)).astype(np.float32) * 0.2, F16)
+    up = orc.narrow(rng.standard_normal((m, n)).astype(np.float32), F16)
+    c = orc.matmul_silu_mul(a, b, up, m, k, n, F16, F16, b_trans=True)
+    acc = orc.matmul(a, b, m, k, n, F16, F32, b_trans=True)
+    ref = orc.silu_mul(acc, orc.widen(up, F16).reshape(m, n))
+    diff = np.abs(c.astype(np.int32) - orc.narrow(ref, F16).astype(np.int32))
+    assert diff.max() <= 1
+    rows = orc.matmul_silu_mul(a, b, up, m, k, n, F16, F16, b_trans=True, row0=13, nrows=9)
+    assert np.array_equal(rows, c[13:22])
+
+
 # ---- matmul --------------------------------------------------------------------------------
 
 def test_matmul_golden_bf16(golden):

@@ -30,6 +30,22 @@
 namespace th {
 
 namespace gemm {
+// Output stage shared by the GEMM kernels.  kEpiStore: C = acc.  kEpiSiluMul:
+// C = silu(acc) * UP, UP an M x N tensor of C's dtype and layout, with
+// silu(x) = x / (1 + exp(-x)) (mlir_to_linalg.rs:774-782) and the product an
+// elementwise mul (mlir_to_linalg.rs:425); computed in f32, rounded once.
+enum : int { kEpiStore = 0, kEpiSiluMul = 1 };
+template <int EPI, int DT_OUT>
+__device__ __forceinline__ void store_out(void* __restrict__ C, const void* __restrict__ up,
+                                          size_t off, float v) {
+  if constexpr (EPI == kEpiSiluMul) {
+    const float u = (DT_OUT == kF32) ? static_cast<const float*>(up)[off]
+                                     : u16_to_f32<DT_OUT>(static_cast<const uint16_t*>(up)[off]);
+    v = v / (1.0f + expf(-v)) * u;
+  }
+  if constexpr (DT_OUT == kF32) static_cast<float*>(C)[off] = v;
+  else static_cast<uint16_t*>(C)[off] = f32_to_u16<DT_OUT>(v);
+}
 
 constexpr int BM = 256, BN = 256, BK = 64;
 constexpr int NT = 256;          // threads per workgroup
@@ -78,11 +94,12 @@ __device__ __forceinline__ GemmLds& gemm_lds() {
 //   - after the step's barrier the global loads of step k+2 are issued, so they
 //     have a whole step to land.
 // FULL = M, N multiples of 256 and K of 64: no bounds checks in the loop.
-template <int DT, int DT_OUT, bool B_TRANS, bool FULL, int WM = 2, int WN = 2>
+template <int DT, int DT_OUT, bool B_TRANS, bool FULL, int WM = 2, int WN = 2, int EPI = 0>
 __device__ __forceinline__ void gemm_tile_256(const uint16_t* __restrict__ A,
                                               const uint16_t* __restrict__ B,
                                               void* __restrict__ C, uint32_t M, uint32_t N,
-                                              uint32_t K, uint32_t tm, uint32_t tn) {
+                                              uint32_t K, uint32_t tm, uint32_t tn,
+                                              const void* __restrict__ up = nullptr) {
   using namespace gemm;
   constexpr int NTH = 64 * WM * WN;     // threads in the workgroup
   constexpr int TM = BM / WM / 32;      // 32x32 accumulator blocks per wave, M
@@ -257,14 +274,8 @@ __device__ __forceinline__ void gemm_tile_256(const uint16_t* __restrict__ A,
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const uint32_t row = m0 + wm * (BM / WM) + mi * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-        if (FULL || (row < M && col < N)) {
-          const size_t off = static_cast<size_t>(row) * N + col;
-          if constexpr (DT_OUT == kF32) {
-            static_cast<float*>(C)[off] = acc[mi][ni][r];
-          } else {
-            static_cast<uint16_t*>(C)[off] = f32_to_u16<DT_OUT>(acc[mi][ni][r]);
-          }
-        }
+        if (FULL || (row < M && col < N))
+          store_out<EPI, DT_OUT>(C, up, static_cast<size_t>(row) * N + col, acc[mi][ni][r]);
       }
     }
 }
@@ -273,17 +284,19 @@ __device__ __forceinline__ void gemm_tile_256(const uint16_t* __restrict__ A,
 // Requires K % 8 == 0 and, for row-major B, N % 8 == 0; M, N, K tails are handled
 // by zero-filled loads and predicated stores (FULL = no tails: M, N multiples of
 // 256 and K of 64).  Batch index = blockIdx.y with element strides sa, sb, sc.
-template <int DT, int DT_OUT, bool B_TRANS, int WM, int WN, bool FULL>
+template <int DT, int DT_OUT, bool B_TRANS, int WM, int WN, bool FULL, int EPI = 0>
 __global__ void __launch_bounds__(64 * WM * WN, 1)
 gemm_mfma_256(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, void* __restrict__ C,
-              uint32_t M, uint32_t N, uint32_t K, uint64_t sa, uint64_t sb, uint64_t sc) {
+              uint32_t M, uint32_t N, uint32_t K, uint64_t sa, uint64_t sb, uint64_t sc,
+              const void* __restrict__ up) {
   const uint32_t tiles_m = (M + gemm::BM - 1) / gemm::BM, tiles_n = (N + gemm::BN - 1) / gemm::BN;
   uint32_t tm, tn;
   gemm::tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
   constexpr int OSZ = (DT_OUT == kF32) ? 4 : 2;
-  gemm_tile_256<DT, DT_OUT, B_TRANS, FULL, WM, WN>(A + blockIdx.y * sa, B + blockIdx.y * sb,
-                                                   static_cast<char*>(C) + blockIdx.y * sc * OSZ, M,
-                                                   N, K, tm, tn);
+  const size_t co = static_cast<size_t>(blockIdx.y) * sc * OSZ;
+  gemm_tile_256<DT, DT_OUT, B_TRANS, FULL, WM, WN, EPI>(
+      A + blockIdx.y * sa, B + blockIdx.y * sb, static_cast<char*>(C) + co, M, N, K, tm, tn,
+      up ? static_cast<const char*>(up) + co : nullptr);
 }
 
 // ---------------------------------------------------------------------------
@@ -338,11 +351,12 @@ __device__ __forceinline__ void wait_stages(uint32_t later) {
 }  // namespace gemm
 
 template <int DT, int DT_OUT, bool B_TRANS, int KB = gemm::DBK, int NS = gemm::NSTAGE,
-          int WAVES = gemm::DWAVES>
+          int WAVES = gemm::DWAVES, int EPI = 0>
 __device__ __forceinline__ void gemm_dma_tile_256(const uint16_t* __restrict__ A,
                                                   const uint16_t* __restrict__ B,
                                                   void* __restrict__ C, uint32_t M, uint32_t N,
-                                                  uint32_t K, uint32_t tm, uint32_t tn) {
+                                                  uint32_t K, uint32_t tm, uint32_t tn,
+                                                  const void* __restrict__ up = nullptr) {
   using namespace gemm;
   static_assert(KB == 32 || KB == 64, "stage K");
   static_assert(WAVES == 4 || WAVES == 8, "2x2 or 2x4 waves");
@@ -540,35 +554,35 @@ __device__ __forceinline__ void gemm_dma_tile_256(const uint16_t* __restrict__ A
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const uint32_t row = m0 + wm * 128 + mi * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-        const size_t off = static_cast<size_t>(row) * N + col;
-        if constexpr (DT_OUT == kF32) static_cast<float*>(C)[off] = acc[mi][ni][r];
-        else static_cast<uint16_t*>(C)[off] = f32_to_u16<DT_OUT>(acc[mi][ni][r]);
+        store_out<EPI, DT_OUT>(C, up, static_cast<size_t>(row) * N + col, acc[mi][ni][r]);
       }
     }
 }
 
 // M, N multiples of 256, K multiple of KB.  Batch index = blockIdx.y.
 template <int DT, int DT_OUT, bool B_TRANS, int KB = gemm::DBK, int NS = gemm::NSTAGE,
-          int WAVES = gemm::DWAVES>
+          int WAVES = gemm::DWAVES, int EPI = 0>
 __global__ void __launch_bounds__(64 * WAVES, 1)
 gemm_dma_256(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, void* __restrict__ C,
-             uint32_t M, uint32_t N, uint32_t K, uint64_t sa, uint64_t sb, uint64_t sc) {
+             uint32_t M, uint32_t N, uint32_t K, uint64_t sa, uint64_t sb, uint64_t sc,
+             const void* __restrict__ up) {
   uint32_t tm, tn;
   gemm::tile_coords(blockIdx.x, M / gemm::BM, N / gemm::BN, tm, tn);
   constexpr int OSZ = (DT_OUT == kF32) ? 4 : 2;
-  gemm_dma_tile_256<DT, DT_OUT, B_TRANS, KB, NS, WAVES>(A + blockIdx.y * sa,
-                                                              B + blockIdx.y * sb,
-                                                 static_cast<char*>(C) + blockIdx.y * sc * OSZ, M,
-                                                 N, K, tm, tn);
+  const size_t co = static_cast<size_t>(blockIdx.y) * sc * OSZ;
+  gemm_dma_tile_256<DT, DT_OUT, B_TRANS, KB, NS, WAVES, EPI>(
+      A + blockIdx.y * sa, B + blockIdx.y * sb, static_cast<char*>(C) + co, M, N, K, tm, tn,
+      up ? static_cast<const char*>(up) + co : nullptr);
 }
 
 // Fallback for shapes the MFMA path does not take (K % 8 != 0, row-major B with
 // N % 8 != 0) and for f32 operands: 64x64 tile per 256-thread workgroup, each
 // thread a 4x4 block, K staged 16 at a time through LDS, f32 FMA.
-template <int DT, int DT_OUT, bool B_TRANS>
+template <int DT, int DT_OUT, bool B_TRANS, int EPI = 0>
 __device__ __forceinline__ void gemm_fma_tile_64(const void* __restrict__ A,
                                                  const void* __restrict__ B, void* __restrict__ C,
-                                                 uint32_t M, uint32_t N, uint32_t K, uint32_t tile) {
+                                                 uint32_t M, uint32_t N, uint32_t K, uint32_t tile,
+                                                 const void* __restrict__ up = nullptr) {
   __shared__ float as[16][64 + 4];
   __shared__ float bs[16][64 + 4];
   const uint32_t m0 = tile / ((N + 63) / 64) * 64;
@@ -616,24 +630,23 @@ __device__ __forceinline__ void gemm_fma_tile_64(const void* __restrict__ A,
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const uint32_t row = m0 + tr * 4 + i, col = n0 + tc * 4 + j;
-      if (row < M && col < N) {
-        const size_t off = static_cast<size_t>(row) * N + col;
-        if constexpr (DT_OUT == kF32) static_cast<float*>(C)[off] = acc[i][j];
-        else static_cast<uint16_t*>(C)[off] = f32_to_u16<DT_OUT>(acc[i][j]);
-      }
+      if (row < M && col < N)
+        gemm::store_out<EPI, DT_OUT>(C, up, static_cast<size_t>(row) * N + col, acc[i][j]);
     }
 }
 
-template <int DT, int DT_OUT, bool B_TRANS>
+template <int DT, int DT_OUT, bool B_TRANS, int EPI = 0>
 __global__ void __launch_bounds__(256)
 gemm_fma_64(const void* __restrict__ A, const void* __restrict__ B, void* __restrict__ C,
-            uint32_t M, uint32_t N, uint32_t K, uint64_t sa, uint64_t sb, uint64_t sc) {
+            uint32_t M, uint32_t N, uint32_t K, uint64_t sa, uint64_t sb, uint64_t sc,
+            const void* __restrict__ up) {
   constexpr int ISZ = (DT == kF32) ? 4 : 2;
   constexpr int OSZ = (DT_OUT == kF32) ? 4 : 2;
-  gemm_fma_tile_64<DT, DT_OUT, B_TRANS>(static_cast<const char*>(A) + blockIdx.y * sa * ISZ,
-                                        static_cast<const char*>(B) + blockIdx.y * sb * ISZ,
-                                        static_cast<char*>(C) + blockIdx.y * sc * OSZ, M, N, K,
-                                        blockIdx.x);
+  const size_t co = static_cast<size_t>(blockIdx.y) * sc * OSZ;
+  gemm_fma_tile_64<DT, DT_OUT, B_TRANS, EPI>(static_cast<const char*>(A) + blockIdx.y * sa * ISZ,
+                                             static_cast<const char*>(B) + blockIdx.y * sb * ISZ,
+                                             static_cast<char*>(C) + co, M, N, K, blockIdx.x,
+                                             up ? static_cast<const char*>(up) + co : nullptr);
 }
 
 }  // namespace th

@@ -1,0 +1,103 @@
+// Row RMSNorm: y[r][c] = x[r][c] * rsqrt(sum_c x[r][c]^2 / cols + eps).
+//
+// Semantics: `__tile_rms_norm_f32(dst, src, eps, rows, cols)` (reference:
+// crates/tile_std/src/tile.rs:2063) as lowered by the linalg bridge
+// (crates/rustc_codegen_tile/src/mlir_to_linalg.rs:1666-1763): square, sum
+// over dimension 1, divide by cols, add eps, rsqrt, multiply.  Math is f32 for
+// every I/O dtype (16-bit inputs are widened exactly, outputs rounded RNE).
+//
+// HBM-bound, same structure as the streaming softmax: a fixed grid of waves
+// walks the rows, each row held in registers (128-bit nontemporal loads), the
+// sum of squares a 64-lane reduction, one pass over HBM.  Other shapes use one
+// wave per row with two passes.
+#pragma once
+
+#include "common.hpp"
+#include "softmax.hpp"
+
+namespace th {
+
+template <int DT, int NV>
+__global__ void __launch_bounds__(256)
+rms_norm_rows_stream(const void* __restrict__ x, void* __restrict__ y, uint32_t rows,
+                     uint32_t cols, float eps) {
+  constexpr int ESZ = (DT == kF32) ? 4 : 2;
+  constexpr int E = SoftmaxVec<DT>::kElems;
+  const int lane = threadIdx.x & 63;
+  const uint32_t nvec = cols / E;
+  const uint32_t stride = gridDim.x * (blockDim.x >> 6);
+  uint32_t row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);
+  const size_t rbytes = static_cast<size_t>(cols) * ESZ;
+  const float inv_cols = 1.0f / static_cast<float>(cols);
+  u32x4 cur[NV], nxt[NV];
+  auto load = [&](uint32_t r, u32x4 (&v)[NV]) {
+    const char* xr = static_cast<const char*>(x) + static_cast<size_t>(r) * rbytes;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const uint32_t vi = static_cast<uint32_t>(i) * 64u + lane;
+      v[i] = (vi < nvec) ? ldg128_nt(xr + static_cast<size_t>(vi) * 16) : u32x4{0, 0, 0, 0};
+    }
+  };
+  if (row < rows) load(row, cur);
+  for (; row < rows; row += stride) {
+    if (row + stride < rows) load(row + stride, nxt);
+    // Rows stay packed in registers (16 vectors per lane at most): the sum of
+    // squares and the scaling each unpack on the fly.
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      float v[E];
+      unpack16<DT>(cur[i], v);
+#pragma unroll
+      for (int e = 0; e < E; ++e) ss = __builtin_fmaf(v[e], v[e], ss);
+    }
+    ss = wave_sum(ss);
+    // mean = sum / cols; rsqrt(mean + eps)
+    const float rs = 1.0f / __builtin_sqrtf(ss * inv_cols + eps);
+    char* yr = static_cast<char*>(y) + static_cast<size_t>(row) * rbytes;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const uint32_t vi = static_cast<uint32_t>(i) * 64u + lane;
+      if (vi < nvec) {
+        float v[E];
+        unpack16<DT>(cur[i], v);
+#pragma unroll
+        for (int e = 0; e < E; ++e) v[e] *= rs;
+        stg128_nt(yr + static_cast<size_t>(vi) * 16, pack16<DT>(v));
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < NV; ++i) cur[i] = nxt[i];
+  }
+}
+
+// Any cols / alignment: one wavefront per row, two passes over the row.
+template <int DT>
+__device__ __forceinline__ void rms_norm_row_wave_any(const void* __restrict__ xr,
+                                                      void* __restrict__ yr, uint32_t cols,
+                                                      float eps, int lane) {
+  float ss = 0.0f;
+  for (uint32_t c = lane; c < cols; c += 64) {
+    const float v = ld_elem<DT>(xr, c);
+    ss = __builtin_fmaf(v, v, ss);
+  }
+  ss = wave_sum(ss);
+  const float rs = 1.0f / __builtin_sqrtf(ss * (1.0f / static_cast<float>(cols)) + eps);
+  for (uint32_t c = lane; c < cols; c += 64) st_elem<DT>(yr, c, ld_elem<DT>(xr, c) * rs);
+}
+
+template <int DT>
+__global__ void __launch_bounds__(256)
+rms_norm_rows_any(const void* __restrict__ x, void* __restrict__ y, uint32_t rows, uint32_t cols,
+                  float eps) {
+  constexpr int ESZ = (DT == kF32) ? 4 : 2;
+  const uint32_t stride = gridDim.x * (blockDim.x >> 6);
+  for (uint32_t row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6); row < rows;
+       row += stride) {
+    const size_t off = static_cast<size_t>(row) * cols * ESZ;
+    rms_norm_row_wave_any<DT>(static_cast<const char*>(x) + off, static_cast<char*>(y) + off, cols,
+                              eps, threadIdx.x & 63);
+  }
+}
+
+}  // namespace th

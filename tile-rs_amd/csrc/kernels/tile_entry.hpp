@@ -13,6 +13,7 @@
 #include "attention.hpp"
 #include "common.hpp"
 #include "gemm.hpp"
+#include "norm.hpp"
 #include "softmax.hpp"
 
 namespace th {
@@ -33,10 +34,25 @@ __device__ __forceinline__ void softmax_rows(const void* x, void* y, uint32_t ro
   }
 }
 
-// ---- batched GEMM: `batch` stacked problems, dense strides ----
-template <int DT, int DTO, bool BT>
+// ---- row RMSNorm over `rows` contiguous rows of `cols` (one wavefront per row) ----
+template <int DT>
+__device__ __forceinline__ void rms_norm_rows(const void* x, void* y, uint32_t rows, uint32_t cols,
+                                              float eps) {
+  constexpr int ESZ = (DT == kF32) ? 4 : 2;
+  const uint32_t wpg = blockDim.x >> 6;
+  for (uint32_t r = blockIdx.x * wpg + (threadIdx.x >> 6); r < rows; r += gridDim.x * wpg) {
+    const size_t off = static_cast<size_t>(r) * cols * ESZ;
+    rms_norm_row_wave_any<DT>(static_cast<const char*>(x) + off, static_cast<char*>(y) + off, cols,
+                              eps, threadIdx.x & 63);
+  }
+}
+
+// ---- batched GEMM: `batch` stacked problems, dense strides; EPI = gemm::kEpi* ----
+// (kEpiSiluMul: C = silu(A.B) * UP, UP laid out like C)
+template <int DT, int DTO, bool BT, int EPI = gemm::kEpiStore>
 __device__ __forceinline__ void gemm(const uint16_t* A, const uint16_t* B, void* C, uint32_t M,
-                                     uint32_t N, uint32_t K, uint32_t batch) {
+                                     uint32_t N, uint32_t K, uint32_t batch,
+                                     const void* up = nullptr) {
   constexpr int OSZ = (DTO == kF32) ? 4 : 2;
   const uint32_t tiles_m = (M + gemm::BM - 1) / gemm::BM, tiles_n = (N + gemm::BN - 1) / gemm::BN;
   const uint32_t per = tiles_m * tiles_n;
@@ -44,25 +60,29 @@ __device__ __forceinline__ void gemm(const uint16_t* A, const uint16_t* B, void*
     const uint32_t bi = w / per;
     uint32_t tm, tn;
     gemm::tile_coords(w % per, tiles_m, tiles_n, tm, tn);
-    gemm_tile_256<DT, DTO, BT, false>(A + static_cast<size_t>(bi) * M * K,
-                               B + static_cast<size_t>(bi) * K * N,
-                               static_cast<char*>(C) + static_cast<size_t>(bi) * M * N * OSZ, M, N,
-                               K, tm, tn);
+    const size_t co = static_cast<size_t>(bi) * M * N * OSZ;
+    gemm_tile_256<DT, DTO, BT, false, 2, 2, EPI>(
+        A + static_cast<size_t>(bi) * M * K, B + static_cast<size_t>(bi) * K * N,
+        static_cast<char*>(C) + co, M, N, K, tm, tn,
+        up ? static_cast<const char*>(up) + co : nullptr);
   }
 }
 
-template <int DT, int DTO, bool BT>
+template <int DT, int DTO, bool BT, int EPI = gemm::kEpiStore>
 __device__ __forceinline__ void gemm_fma(const void* A, const void* B, void* C, uint32_t M,
-                                         uint32_t N, uint32_t K, uint32_t batch) {
+                                         uint32_t N, uint32_t K, uint32_t batch,
+                                         const void* up = nullptr) {
   constexpr int ISZ = (DT == kF32) ? 4 : 2;
   constexpr int OSZ = (DTO == kF32) ? 4 : 2;
   const uint32_t per = ((M + 63) / 64) * ((N + 63) / 64);
   for (uint32_t w = blockIdx.x; w < per * batch; w += gridDim.x) {
     const uint32_t bi = w / per;
-    gemm_fma_tile_64<DT, DTO, BT>(static_cast<const char*>(A) + static_cast<size_t>(bi) * M * K * ISZ,
-                                  static_cast<const char*>(B) + static_cast<size_t>(bi) * K * N * ISZ,
-                                  static_cast<char*>(C) + static_cast<size_t>(bi) * M * N * OSZ, M,
-                                  N, K, w % per);
+    const size_t co = static_cast<size_t>(bi) * M * N * OSZ;
+    gemm_fma_tile_64<DT, DTO, BT, EPI>(
+        static_cast<const char*>(A) + static_cast<size_t>(bi) * M * K * ISZ,
+        static_cast<const char*>(B) + static_cast<size_t>(bi) * K * N * ISZ,
+        static_cast<char*>(C) + co, M, N, K, w % per,
+        up ? static_cast<const char*>(up) + co : nullptr);
   }
 }
 

@@ -11,10 +11,12 @@
 #include <cstdint>
 #include <cstdlib>
 #include <string>
+#include <type_traits>
 
 #include "kernels/attention.hpp"
 #include "kernels/common.hpp"
 #include "kernels/gemm.hpp"
+#include "kernels/norm.hpp"
 #include "kernels/softmax.hpp"
 #include "runtime.hpp"
 
@@ -86,17 +88,64 @@ int softmax_launch(const void* x, void* y, uint32_t rows, uint32_t cols, hipStre
   return launch_status("softmax launch");
 }
 
+// Streaming row kernels: as many 256-thread workgroups as fit on every CU at
+// once (at most 4), so the grid is one resident wave of work with no tail.
+template <class K>
+uint32_t resident_grid(K kernel, int* cache, uint32_t rows) {
+  if (*cache == 0) {
+    int n = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, 256, 0) != hipSuccess || n <= 0)
+      n = 1;
+    *cache = std::min(n, 4);
+  }
+  return std::max(1u, std::min<uint32_t>((rows + 3) / 4,
+                                         static_cast<uint32_t>(*cache) * current_cu_count()));
+}
+
+template <int DT, int NV>
+void rms_norm_stream_go(const void* x, void* y, uint32_t rows, uint32_t cols, float eps,
+                        hipStream_t s) {
+  static int per_cu = 0;
+  auto k = th::rms_norm_rows_stream<DT, NV>;
+  hipLaunchKernelGGL(k, dim3(resident_grid(k, &per_cu, rows)), dim3(256), 0, s, x, y, rows, cols,
+                     eps);
+}
+
+template <int DT>
+int rms_norm_launch(const void* x, void* y, uint32_t rows, uint32_t cols, float eps,
+                    hipStream_t s) {
+  constexpr int E = th::SoftmaxVec<DT>::kElems;
+  const bool vec_ok = (cols % E == 0) && aligned16(x) && aligned16(y);
+  const uint32_t nvec = cols / E;
+  if (vec_ok && nvec <= 64) rms_norm_stream_go<DT, 1>(x, y, rows, cols, eps, s);
+  else if (vec_ok && nvec <= 128) rms_norm_stream_go<DT, 2>(x, y, rows, cols, eps, s);
+  else if (vec_ok && nvec <= 256) rms_norm_stream_go<DT, 4>(x, y, rows, cols, eps, s);
+  else if (vec_ok && nvec <= 512) rms_norm_stream_go<DT, 8>(x, y, rows, cols, eps, s);
+  else if (vec_ok && nvec <= 1024) rms_norm_stream_go<DT, 16>(x, y, rows, cols, eps, s);
+  else {
+    static int per_cu = 0;
+    auto k = th::rms_norm_rows_any<DT>;
+    hipLaunchKernelGGL(k, dim3(resident_grid(k, &per_cu, rows)), dim3(256), 0, s, x, y, rows,
+                       cols, eps);
+  }
+  return launch_status("rms_norm launch");
+}
+
 // ---- matmul -------------------------------------------------------------------
 
-// Wave layout of the 256x256 MFMA tile: 4 waves of 128x128 (1 wave per SIMD,
-// 256 accumulator registers) or 8 waves of 128x64 (2 waves per SIMD).
-int gemm_waves() {
-  static const int w = [] {
-    const char* e = std::getenv("TILERS_HIP_GEMM_WAVES");
-    return (e && std::atoi(e) == 8) ? 8 : 4;
-  }();
-  return w;
-}
+// One GEMM launch: C[i] = epilogue(A[i] . B[i]) for i < batch, element strides
+// sa, sb, sc; `up` (epilogue kEpiSiluMul) has C's dtype, layout and strides.
+struct GemmArgs {
+  const void* a;
+  const void* b;
+  void* c;
+  const void* up;
+  uint32_t m, k, n;
+  bool bt;
+  uint32_t batch;
+  uint64_t sa, sb, sc;
+  hipStream_t s;
+};
 
 // The LDS-DMA pipeline serves tile-multiple shapes unless TILERS_HIP_GEMM_DMA=0
 // (then the register-staged kernel runs them too).
@@ -108,87 +157,63 @@ bool gemm_dma() {
   return v;
 }
 
-template <int DT, int DTO, bool BT>
-void gemm_dma_go(const uint16_t* A, const uint16_t* B, void* c, uint32_t m, uint32_t k, uint32_t n,
-                 dim3 grid, uint64_t sa, uint64_t sb, uint64_t sc, hipStream_t s) {
-  hipLaunchKernelGGL((th::gemm_dma_256<DT, DTO, BT>), grid, dim3(64 * th::gemm::DWAVES), 0, s, A, B,
-                     c, m, n, k, sa, sb, sc);
-}
-
-template <int DT, int DTO, bool BT, bool FULL>
-void gemm_mfma_go(const uint16_t* A, const uint16_t* B, void* c, uint32_t m, uint32_t k,
-                  uint32_t n, dim3 grid, uint64_t sa, uint64_t sb, uint64_t sc, hipStream_t s) {
-  if (gemm_waves() == 4)
-    hipLaunchKernelGGL((th::gemm_mfma_256<DT, DTO, BT, 2, 2, FULL>), grid, dim3(256), 0, s, A, B, c,
-                       m, n, k, sa, sb, sc);
-  else
-    hipLaunchKernelGGL((th::gemm_mfma_256<DT, DTO, BT, 2, 4, FULL>), grid, dim3(512), 0, s, A, B, c,
-                       m, n, k, sa, sb, sc);
-}
-
-template <int DT, int DTO>
-int gemm_mfma_launch(const void* a, const void* b, void* c, uint32_t m, uint32_t k, uint32_t n,
-                     bool bt, uint32_t batch, uint64_t sa, uint64_t sb, uint64_t sc,
-                     hipStream_t s) {
-  const uint32_t tiles = ((m + 255) / 256) * ((n + 255) / 256);
-  const dim3 grid(tiles, batch);
-  auto A = static_cast<const uint16_t*>(a);
-  auto B = static_cast<const uint16_t*>(b);
-  if (gemm_dma() && m % th::gemm::BM == 0 && n % th::gemm::BN == 0 && k % th::gemm::DBK == 0) {
-    if (bt)
-      gemm_dma_go<DT, DTO, true>(A, B, c, m, k, n, grid, sa, sb, sc, s);
-    else
-      gemm_dma_go<DT, DTO, false>(A, B, c, m, k, n, grid, sa, sb, sc, s);
-    return launch_status("matmul (MFMA, LDS DMA) launch");
+template <int DT, int DTO, int EPI, bool BT>
+void gemm_mfma_go(const GemmArgs& g, dim3 grid) {
+  auto A = static_cast<const uint16_t*>(g.a);
+  auto B = static_cast<const uint16_t*>(g.b);
+  if (gemm_dma() && g.m % th::gemm::BM == 0 && g.n % th::gemm::BN == 0 && g.k % th::gemm::DBK == 0) {
+    hipLaunchKernelGGL((th::gemm_dma_256<DT, DTO, BT, th::gemm::DBK, th::gemm::NSTAGE,
+                                         th::gemm::DWAVES, EPI>),
+                       grid, dim3(64 * th::gemm::DWAVES), 0, g.s, A, B, g.c, g.m, g.n, g.k, g.sa,
+                       g.sb, g.sc, g.up);
+  } else if (g.m % th::gemm::BM == 0 && g.n % th::gemm::BN == 0 && g.k % th::gemm::BK == 0) {
+    hipLaunchKernelGGL((th::gemm_mfma_256<DT, DTO, BT, 2, 2, true, EPI>), grid, dim3(256), 0, g.s,
+                       A, B, g.c, g.m, g.n, g.k, g.sa, g.sb, g.sc, g.up);
+  } else {
+    hipLaunchKernelGGL((th::gemm_mfma_256<DT, DTO, BT, 2, 2, false, EPI>), grid, dim3(256), 0, g.s,
+                       A, B, g.c, g.m, g.n, g.k, g.sa, g.sb, g.sc, g.up);
   }
-  const bool full = m % th::gemm::BM == 0 && n % th::gemm::BN == 0 && k % th::gemm::BK == 0;
-  if (bt)
-    full ? gemm_mfma_go<DT, DTO, true, true>(A, B, c, m, k, n, grid, sa, sb, sc, s)
-         : gemm_mfma_go<DT, DTO, true, false>(A, B, c, m, k, n, grid, sa, sb, sc, s);
-  else
-    full ? gemm_mfma_go<DT, DTO, false, true>(A, B, c, m, k, n, grid, sa, sb, sc, s)
-         : gemm_mfma_go<DT, DTO, false, false>(A, B, c, m, k, n, grid, sa, sb, sc, s);
-  return launch_status("matmul (MFMA) launch");
 }
 
-template <int DT, int DTO>
-int gemm_fma_launch(const void* a, const void* b, void* c, uint32_t m, uint32_t k, uint32_t n,
-                    bool bt, uint32_t batch, uint64_t sa, uint64_t sb, uint64_t sc,
-                    hipStream_t s) {
-  const uint32_t tiles = ((m + 63) / 64) * ((n + 63) / 64);
-  const dim3 grid(tiles, batch), block(256);
-  if (bt)
-    hipLaunchKernelGGL((th::gemm_fma_64<DT, DTO, true>), grid, block, 0, s, a, b, c, m, n, k, sa,
-                       sb, sc);
+template <int DT, int DTO, int EPI>
+int gemm_launch(const GemmArgs& g, bool mfma) {
+  if constexpr (DT != th::kF32) {
+    if (mfma) {
+      const dim3 grid(((g.m + 255) / 256) * ((g.n + 255) / 256), g.batch);
+      if (g.bt) gemm_mfma_go<DT, DTO, EPI, true>(g, grid);
+      else gemm_mfma_go<DT, DTO, EPI, false>(g, grid);
+      return launch_status("matmul (MFMA) launch");
+    }
+  }
+  (void)mfma;
+  const dim3 grid(((g.m + 63) / 64) * ((g.n + 63) / 64), g.batch), block(256);
+  if (g.bt)
+    hipLaunchKernelGGL((th::gemm_fma_64<DT, DTO, true, EPI>), grid, block, 0, g.s, g.a, g.b, g.c,
+                       g.m, g.n, g.k, g.sa, g.sb, g.sc, g.up);
   else
-    hipLaunchKernelGGL((th::gemm_fma_64<DT, DTO, false>), grid, block, 0, s, a, b, c, m, n, k, sa,
-                       sb, sc);
+    hipLaunchKernelGGL((th::gemm_fma_64<DT, DTO, false, EPI>), grid, block, 0, g.s, g.a, g.b, g.c,
+                       g.m, g.n, g.k, g.sa, g.sb, g.sc, g.up);
   return launch_status("matmul (FMA) launch");
 }
 
-template <int DT>
-int gemm_dispatch_out(const void* a, const void* b, void* c, uint32_t m, uint32_t k, uint32_t n,
-                      th_dtype out, bool bt, uint32_t batch, uint64_t sa, uint64_t sb, uint64_t sc,
-                      hipStream_t s, bool mfma) {
-  if constexpr (DT == th::kF32) {
-    // f32 operands have no MFMA path here: only the FMA kernels are instantiated
-    (void)mfma;
+template <int EPI>
+int gemm_dispatch(const GemmArgs& g, th_dtype in, th_dtype out) {
+  // f32 operands have no MFMA path; 16-bit ones need K % 8 == 0, row-major B
+  // N % 8 == 0 and 16-byte aligned operands and strides.
+  const bool mfma = in != TH_F32 && (g.k % 8 == 0) && (g.bt || g.n % 8 == 0) && aligned16(g.a) &&
+                    aligned16(g.b) && (g.sa % 8 == 0) && (g.sb % 8 == 0);
+  auto by_out = [&](auto dt) {
+    constexpr int DT = decltype(dt)::value;
     switch (out) {
-      case TH_F32: return gemm_fma_launch<DT, th::kF32>(a, b, c, m, k, n, bt, batch, sa, sb, sc, s);
-      case TH_F16: return gemm_fma_launch<DT, th::kF16>(a, b, c, m, k, n, bt, batch, sa, sb, sc, s);
-      default: return gemm_fma_launch<DT, th::kBF16>(a, b, c, m, k, n, bt, batch, sa, sb, sc, s);
+      case TH_F32: return gemm_launch<DT, th::kF32, EPI>(g, mfma);
+      case TH_F16: return gemm_launch<DT, th::kF16, EPI>(g, mfma);
+      default: return gemm_launch<DT, th::kBF16, EPI>(g, mfma);
     }
-  }
-  switch (out) {
-    case TH_F32:
-      return mfma ? gemm_mfma_launch<DT, th::kF32>(a, b, c, m, k, n, bt, batch, sa, sb, sc, s)
-                  : gemm_fma_launch<DT, th::kF32>(a, b, c, m, k, n, bt, batch, sa, sb, sc, s);
-    case TH_F16:
-      return mfma ? gemm_mfma_launch<DT, th::kF16>(a, b, c, m, k, n, bt, batch, sa, sb, sc, s)
-                  : gemm_fma_launch<DT, th::kF16>(a, b, c, m, k, n, bt, batch, sa, sb, sc, s);
-    default:
-      return mfma ? gemm_mfma_launch<DT, th::kBF16>(a, b, c, m, k, n, bt, batch, sa, sb, sc, s)
-                  : gemm_fma_launch<DT, th::kBF16>(a, b, c, m, k, n, bt, batch, sa, sb, sc, s);
+  };
+  switch (in) {
+    case TH_F32: return by_out(std::integral_constant<int, th::kF32>{});
+    case TH_F16: return by_out(std::integral_constant<int, th::kF16>{});
+    default: return by_out(std::integral_constant<int, th::kBF16>{});
   }
 }
 
@@ -255,18 +280,46 @@ int th_matmul(const void* a, const void* b, void* c, uint32_t m, uint32_t k, uin
                            "hipMemsetAsync", TH_MEMORY_ERROR));
     return TH_OK;
   }
-  const bool mfma = in_dtype != TH_F32 && (k % 8 == 0) && (bt || n % 8 == 0) && aligned16(a) &&
-                    aligned16(b) && (sa % 8 == 0) && (sb % 8 == 0);
-  switch (in_dtype) {
-    case TH_F32:
-      return gemm_dispatch_out<th::kF32>(a, b, c, m, k, n, out_dtype, bt, batch, sa, sb, sc,
-                                         as_stream(s), false);
-    case TH_F16:
-      return gemm_dispatch_out<th::kF16>(a, b, c, m, k, n, out_dtype, bt, batch, sa, sb, sc,
-                                         as_stream(s), mfma);
-    default:
-      return gemm_dispatch_out<th::kBF16>(a, b, c, m, k, n, out_dtype, bt, batch, sa, sb, sc,
-                                          as_stream(s), mfma);
+  const GemmArgs g{a, b, c, nullptr, m, k, n, bt, batch, sa, sb, sc, as_stream(s)};
+  return gemm_dispatch<th::gemm::kEpiStore>(g, in_dtype, out_dtype);
+}
+
+int th_matmul_silu_mul(const void* a, const void* b, const void* up, void* c, uint32_t m,
+                       uint32_t k, uint32_t n, th_dtype in_dtype, th_dtype out_dtype,
+                       int b_transposed, uint32_t batch, uint64_t sa, uint64_t sb, uint64_t sc,
+                       th_stream s) {
+  if (!valid_dtype(in_dtype) || !valid_dtype(out_dtype))
+    return fail(TH_KERNEL_ERROR, "matmul_silu_mul: unknown dtype");
+  if (m == 0 || n == 0 || batch == 0) return TH_OK;
+  if (!a || !b || !c || !up) return fail(TH_KERNEL_ERROR, "matmul_silu_mul: null pointer");
+  if (batch > 65535) return fail(TH_KERNEL_ERROR, "matmul_silu_mul: batch > 65535");
+  const bool bt = b_transposed != 0;
+  if (sa == 0) sa = static_cast<uint64_t>(m) * k;
+  if (sb == 0) sb = static_cast<uint64_t>(k) * n;
+  if (sc == 0) sc = static_cast<uint64_t>(m) * n;
+  if (k == 0) {
+    // silu(0) * up = 0 everywhere
+    const size_t esz = dtype_size(out_dtype);
+    for (uint32_t i = 0; i < batch; ++i)
+      TH_TRY(th::check_hip(hipMemsetAsync(static_cast<char*>(c) + i * sc * esz, 0,
+                                          static_cast<size_t>(m) * n * esz, as_stream(s)),
+                           "hipMemsetAsync", TH_MEMORY_ERROR));
+    return TH_OK;
+  }
+  const GemmArgs g{a, b, c, up, m, k, n, bt, batch, sa, sb, sc, as_stream(s)};
+  return gemm_dispatch<th::gemm::kEpiSiluMul>(g, in_dtype, out_dtype);
+}
+
+int th_rms_norm(const void* x, void* y, uint32_t rows, uint32_t cols, float eps, th_dtype dtype,
+                th_stream s) {
+  if (!valid_dtype(dtype)) return fail(TH_KERNEL_ERROR, "rms_norm: unknown dtype");
+  if (rows == 0 || cols == 0) return TH_OK;
+  if (!x || !y) return fail(TH_KERNEL_ERROR, "rms_norm: null pointer");
+  if (!(eps >= 0.0f)) return fail(TH_KERNEL_ERROR, "rms_norm: eps must be >= 0");
+  switch (dtype) {
+    case TH_F32: return rms_norm_launch<th::kF32>(x, y, rows, cols, eps, as_stream(s));
+    case TH_F16: return rms_norm_launch<th::kF16>(x, y, rows, cols, eps, as_stream(s));
+    default: return rms_norm_launch<th::kBF16>(x, y, rows, cols, eps, as_stream(s));
   }
 }
 

@@ -8,6 +8,10 @@
 //
 // Lowering (the "hook" that maps tile ops to hand-written kernels):
 //   load -> __tile_softmax_{f32,f16}            -> store : th::entry::softmax_rows
+//   load -> __tile_rms_norm_f32                  -> store : th::entry::rms_norm_rows
+//   load, load -> matmul -> silu, load -> mul    -> store : th::entry::gemm with the
+//                                                           SiLU*Mul epilogue (the fusion the
+//                                                           gpu target does, mlir_to_gpu.rs:536-634)
 //   load, load -> __tile_matmul_{f16,f32}        -> store : th::entry::gemm (MFMA) / gemm_fma
 //   load, load -> __tile_matmul_transposed_*     -> store : same, B stored N x K
 //   load x3 -> __tile_attention_f32              -> store : th::entry::attention_tiles
@@ -310,6 +314,14 @@ class Lowerer {
       if (a.size() < 4 || !tile(a[1]) || !shape_from(2, 3)) return fail("softmax arity: " + line);
       t.ins = {a[1]};
       t.dtype = tile(a[1])->dtype;
+    } else if (base == "rms_norm_f32") {
+      // (dst, src, eps, rows, cols), tile.rs:2063
+      double eps = 0;
+      if (a.size() < 5 || !tile(a[1]) || !num(a[2], &eps) || !shape_from(3, 4))
+        return fail("rms_norm arity: " + line);
+      t.ins = {a[1]};
+      t.scalars = {eps};
+      t.dtype = tile(a[1])->dtype;
     } else if (base == "matmul_f32" || base == "matmul_f16" || base == "matmul_transposed_f32" ||
                base == "matmul_transposed_f16") {
       if (a.size() < 6 || !tile(a[1]) || !tile(a[2])) return fail("matmul arity: " + line);
@@ -396,11 +408,102 @@ void signature(std::ostringstream& os, const Kernel& k, unsigned threads,
 
 bool is_elementwise(const std::string& op) {
   return op != "load" && op.find("softmax") == std::string::npos &&
-         op.find("matmul") == std::string::npos && op.find("attention") == std::string::npos;
+         op.find("rms_norm") == std::string::npos && op.find("matmul") == std::string::npos &&
+         op.find("attention") == std::string::npos;
+}
+
+// Pointer expressions of a loaded view / the stored view (per-tile offsets are
+// added by the entry from th_tiles).
+std::string view_ptr(const TileVal& t, const char* ctype) {
+  return "(reinterpret_cast<const " + std::string(ctype) + "*>(p" + std::to_string(t.src.arg) +
+         ")" + (t.src.offset ? " + " + std::to_string(t.src.offset) + "ll" : "") + ")";
+}
+std::string store_ptr(const Store& st, const char* ctype) {
+  return "(reinterpret_cast<" + std::string(ctype) + "*>(p" + std::to_string(st.dst.arg) + ")" +
+         (st.dst.offset ? " + " + std::to_string(st.dst.offset) + "ll" : "") + ")";
+}
+
+// GEMM body for the matmul tile `mm` stored by `st`; epi names the epilogue
+// (th::gemm::kEpiStore, or kEpiSiluMul with the UP view `up`).
+bool matmul_entry(const Kernel& k, const TileVal& mm, const Store& st, const char* epi,
+                  const TileVal* up, std::ostringstream& os, std::string* err) {
+  const bool bt = mm.op.find("transposed") != std::string::npos;
+  const TileVal& a = k.tiles.at(mm.ins[0]);
+  const TileVal& b = k.tiles.at(mm.ins[1]);
+  const long long M = mm.rows, N = mm.cols, K = static_cast<long long>(mm.scalars[0]);
+  if (a.rows * a.cols != M * K || b.rows * b.cols != K * N || st.rows * st.cols != M * N) {
+    *err = "mlir_to_hip: " + k.name + ": matmul operand shapes do not match m/k/n";
+    return false;
+  }
+  if (a.dtype != b.dtype) {
+    *err = "mlir_to_hip: " + k.name + ": matmul operands have different dtypes";
+    return false;
+  }
+  const int in = a.dtype, out = st.dtype;
+  const bool mfma = in != F32 && K % 8 == 0 && (bt || N % 8 == 0) && a.src.offset % 8 == 0 &&
+                    b.src.offset % 8 == 0;
+  os << "matmul " << M << "x" << K << "x" << N << (bt ? " (B transposed)" : "") << " " << dt_name(in)
+     << " -> " << dt_name(out) << (up ? " with silu*mul epilogue" : "")
+     << (mfma ? " -> th::entry::gemm (MFMA)" : " -> th::entry::gemm_fma") << "\n";
+  signature(os, k, 256, {});
+  const std::string tmpl = std::string(dt_enum(in)) + ", " + dt_enum(out) + ", " +
+                           (bt ? "true" : "false") + ", " + epi;
+  const std::string tail = up ? ", th_tiles, " + view_ptr(*up, dt_ctype(out)) + ");\n}\n"
+                              : ", th_tiles);\n}\n";
+  if (mfma) {
+    os << "  th::entry::gemm<" << tmpl << ">(" << view_ptr(a, "uint16_t") << ", "
+       << view_ptr(b, "uint16_t") << ", " << store_ptr(st, dt_ctype(out)) << ", " << u(M) << ", "
+       << u(N) << ", " << u(K) << tail;
+    desc(os, k.name, 256, static_cast<unsigned>(((M + 255) / 256) * ((N + 255) / 256)), 1);
+  } else {
+    os << "  th::entry::gemm_fma<" << tmpl << ">(" << view_ptr(a, dt_ctype(in)) << ", "
+       << view_ptr(b, dt_ctype(in)) << ", " << store_ptr(st, dt_ctype(out)) << ", " << u(M)
+       << ", " << u(N) << ", " << u(K) << tail;
+    desc(os, k.name, 256, static_cast<unsigned>(((M + 63) / 64) * ((N + 63) / 64)), 1);
+  }
+  return true;
+}
+
+// store(mul(silu(matmul(load, load)), load)) with nothing else in the kernel: the
+// GEMM with the SiLU*Mul epilogue.  Returns false when the kernel is not of that
+// shape (and leaves *err empty); true when emitted, or on error with *err set.
+bool emit_fused_swiglu(const Kernel& k, std::ostringstream& os, std::string* err) {
+  if (k.stores.size() != 1) return false;
+  const Store& st = k.stores[0];
+  const TileVal& mul = k.tiles.at(st.value);
+  if (mul.op != "__tile_mul_f32" && mul.op != "__tile_mul_f16") return false;
+  const TileVal* silu = nullptr;
+  const TileVal* up = nullptr;
+  for (const std::string& in : mul.ins) {
+    const TileVal& t = k.tiles.at(in);
+    if (t.op == "__tile_silu_f32" || t.op == "__tile_silu_f16") silu = &t;
+    else if (t.op == "load") up = &t;
+  }
+  if (!silu || !up) return false;
+  const TileVal& mm = k.tiles.at(silu->ins[0]);
+  if (mm.op.find("matmul") == std::string::npos) return false;
+  for (const std::string& in : mm.ins)
+    if (k.tiles.at(in).op != "load") return false;
+  size_t others = 0;
+  for (const auto& kv : k.tiles)
+    if (kv.second.op != "load") ++others;
+  if (others != 3) return false;  // exactly matmul, silu, mul
+  if (up->dtype != st.dtype) {
+    *err = "mlir_to_hip: " + k.name + ": fused silu*mul needs UP in the output dtype";
+    return true;
+  }
+  if (up->rows * up->cols != mm.rows * mm.cols || st.rows * st.cols != mm.rows * mm.cols) {
+    *err = "mlir_to_hip: " + k.name + ": fused silu*mul operand shapes do not match the matmul";
+    return true;
+  }
+  os << "// kernel " << k.name << ": ";
+  matmul_entry(k, mm, st, "th::gemm::kEpiSiluMul", up, os, err);
+  return true;
 }
 
 // Emits kernels for one function; returns false with *err on unsupported shapes.
 bool emit_kernel(const Kernel& k, std::ostringstream& os, std::string* err) {
+  if (emit_fused_swiglu(k, os, err)) return err->empty();
   // Identify a hot-op chain: one store whose value is a hot op fed by loads.
   const TileVal* hot = nullptr;
   const Store* st = nullptr;
@@ -544,34 +647,25 @@ bool emit_kernel(const Kernel& k, std::ostringstream& os, std::string* err) {
     return true;
   }
   if (o.rfind("matmul", 0) == 0) {
-    const bool bt = o.find("transposed") != std::string::npos;
-    const TileVal& a = k.tiles.at(hot->ins[0]);
-    const TileVal& b = k.tiles.at(hot->ins[1]);
-    const long long M = hot->rows, N = hot->cols, K = static_cast<long long>(hot->scalars[0]);
-    if (a.rows * a.cols != M * K || b.rows * b.cols != K * N || st->rows * st->cols != M * N) {
-      *err = "mlir_to_hip: " + k.name + ": matmul operand shapes do not match m/k/n";
+    matmul_entry(k, *hot, *st, "th::gemm::kEpiStore", nullptr, os, err);
+    return err->empty();
+  }
+  if (o == "rms_norm_f32") {
+    const TileVal& x = k.tiles.at(hot->ins[0]);
+    const long long R = hot->rows, C = hot->cols;
+    if (x.rows * x.cols != R * C || st->rows * st->cols != R * C || st->dtype != x.dtype) {
+      *err = "mlir_to_hip: " + k.name + ": rms_norm shape/dtype mismatch between load and store";
       return false;
     }
-    if (a.dtype != b.dtype) {
-      *err = "mlir_to_hip: " + k.name + ": matmul operands have different dtypes";
-      return false;
-    }
-    const int in = a.dtype, out = st->dtype;
-    const bool mfma = in != F32 && K % 8 == 0 && (bt || N % 8 == 0) && a.src.offset % 8 == 0 &&
-                      b.src.offset % 8 == 0;
-    os << "matmul " << M << "x" << K << "x" << N << (bt ? " (B transposed)" : "") << " " << dt_name(in)
-       << " -> " << dt_name(out) << (mfma ? " -> th::entry::gemm (MFMA)" : " -> th::entry::gemm_fma") << "\n";
+    os << "row rms_norm " << R << "x" << C << " " << dt_name(x.dtype) << " eps "
+       << hot->scalars[0] << " per tile -> th::entry::rms_norm_rows\n";
     signature(os, k, 256, {});
-    const std::string tmpl = std::string(dt_enum(in)) + ", " + dt_enum(out) + ", " + (bt ? "true" : "false");
-    if (mfma) {
-      os << "  th::entry::gemm<" << tmpl << ">(" << in_ptr(0, "uint16_t") << ", " << in_ptr(1, "uint16_t")
-         << ", " << out_ptr(dt_ctype(out)) << ", " << u(M) << ", " << u(N) << ", " << u(K) << ", th_tiles);\n}\n";
-      desc(os, k.name, 256, static_cast<unsigned>(((M + 255) / 256) * ((N + 255) / 256)), 1);
-    } else {
-      os << "  th::entry::gemm_fma<" << tmpl << ">(" << in_ptr(0, dt_ctype(in)) << ", " << in_ptr(1, dt_ctype(in))
-         << ", " << out_ptr(dt_ctype(out)) << ", " << u(M) << ", " << u(N) << ", " << u(K) << ", th_tiles);\n}\n";
-      desc(os, k.name, 256, static_cast<unsigned>(((M + 63) / 64) * ((N + 63) / 64)), 1);
-    }
+    os << "  th::entry::rms_norm_rows<" << dt_enum(x.dtype) << ">(" << in_ptr(0, dt_ctype(x.dtype))
+       << ", " << out_ptr(dt_ctype(x.dtype)) << ", th_tiles * " << u(R) << ", " << u(C) << ", "
+       << fconst(hot->scalars[0]) << ");\n}\n";
+    const unsigned tpw = R >= 4 ? 1 : static_cast<unsigned>(4 / R);
+    const unsigned wpt = R >= 4 ? static_cast<unsigned>((R + 3) / 4) : 1;
+    desc(os, k.name, 256, wpt, tpw);
     return true;
   }
   if (o == "attention_f32") {

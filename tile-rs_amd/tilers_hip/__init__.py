@@ -35,7 +35,7 @@ __all__ = [
     "HalError", "TileDtype", "KernelMode", "LaunchGrid", "MemInfo", "HipDevice", "HipStream",
     "HipBuffer", "HipLauncher", "HipEvent", "BackendSelector", "BackendKind", "EmitOut",
     "TargetMeta", "CodegenTarget", "EmitterTarget", "TargetRegistry", "softmax", "matmul",
-    "causal_mask_f32", "attention", "attention_prefill", "attention_decode",
+    "matmul_silu_mul", "rms_norm", "causal_mask_f32", "attention", "attention_prefill", "attention_decode",
     "attention_decode_workspace_size", "fill_random", "compile_source", "device_count", "lib",
 ]
 
@@ -336,6 +336,21 @@ def matmul(a, b, c, m: int, k: int, n: int, in_dtype: TileDtype, out_dtype: Tile
            stream: Optional[HipStream] = None) -> None:
     check(lib().th_matmul(_p(a), _p(b), _p(c), m, k, n, int(in_dtype), int(out_dtype),
                           int(bool(b_transposed)), batch, sa, sb, sc, _s(stream)))
+
+
+def matmul_silu_mul(a, b, up, c, m: int, k: int, n: int, in_dtype: TileDtype,
+                    out_dtype: TileDtype, b_transposed: bool = False, batch: int = 1, sa: int = 0,
+                    sb: int = 0, sc: int = 0, stream: Optional[HipStream] = None) -> None:
+    """C = silu(A.B) * UP (the matmul -> silu -> mul tile chain in one kernel)."""
+    check(lib().th_matmul_silu_mul(_p(a), _p(b), _p(up), _p(c), m, k, n, int(in_dtype),
+                                   int(out_dtype), int(bool(b_transposed)), batch, sa, sb, sc,
+                                   _s(stream)))
+
+
+def rms_norm(x, y, rows: int, cols: int, eps: float, dtype: TileDtype = TileDtype.F32,
+             stream: Optional[HipStream] = None) -> None:
+    """y = x * rsqrt(mean(x^2, row) + eps) per row (__tile_rms_norm_f32)."""
+    check(lib().th_rms_norm(_p(x), _p(y), rows, cols, float(eps), int(dtype), _s(stream)))
 
 
 def causal_mask_f32(x, y, rows: int, cols: int, tiles: int = 1,

@@ -78,6 +78,9 @@ SIGNATURES: dict[str, tuple] = {
     "th_launcher_launch": (_i, [_vp, _cp, _u32, _u32, _u32, _pp, _sz, _vp]),
     "th_softmax": (_i, [_vp, _vp, _u32, _u32, _i, _vp]),
     "th_matmul": (_i, [_vp, _vp, _vp, _u32, _u32, _u32, _i, _i, _i, _u32, _u64, _u64, _u64, _vp]),
+    "th_matmul_silu_mul": (_i, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _i, _i, _i, _u32, _u64, _u64,
+                                _u64, _vp]),
+    "th_rms_norm": (_i, [_vp, _vp, _u32, _u32, _f, _i, _vp]),
     "th_causal_mask_f32": (_i, [_vp, _vp, _u32, _u32, _u32, _vp]),
     "th_attention": (_i, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _i, _vp]),
     "th_attention_prefill": (_i, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32, _u32,
