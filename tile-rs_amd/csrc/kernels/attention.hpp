@@ -43,18 +43,14 @@ __device__ __forceinline__ uint32_t cvt_pk(float lo, float hi) {
 // Prefill: flash attention forward, causal, GQA, head_dim 128.
 //
 // Workgroup = 8 waves = 256 query rows of one (batch, head); wave w owns rows
-// [32w, 32w+32).  KV is consumed 64 positions at a time, staged in LDS with two
-// buffers: K as [kv][d] (d contiguous), V transposed as [d][kv-slot].
-// Per wave and KV block:
+// [32w, 32w+32).  KV is consumed 64 positions at a time.  Per wave and KV block:
 //   S^T (64 kv x 32 q)  = K . Q^T          2x8 v_mfma_f32_32x32x16, Q^T in registers
 //   online softmax on S^T columns: lane l owns query l%32; its partner lane l^32
 //   holds the other half of that column, so row statistics need one exchange.
 //   O^T (128 d x 32 q) += V^T . P^T        4x4 MFMAs; P^T is the S^T accumulator
 //   converted to 16-bit in place: accumulator j of lane l (half g = l/32) is KV
-//   row 8*(j/4) + 4g + j%4, and the same KV order is used for the V^T slots, so
+//   row 8*(j/4) + 4g + j%4, and the V^T operand is read in the same KV order, so
 //   the B operand needs no data movement.
-// V^T slot order inside each 16-position group: [0-3, 8-11, 4-7, 12-15], which
-// makes each lane's eight MFMA slots one contiguous 16-byte LDS read.
 // ============================================================================
 namespace fa {
 constexpr int D = 128;
@@ -65,9 +61,6 @@ constexpr float kRescaleThreshold = 8.0f;  // log2 units; see the rescale below
 // A KV block whose probability mass exceeds 1/ratio of the query's running sum
 // gets its P residual as well (bf16 keeps 8 significant bits, f16 keeps 11).
 template <int DT> constexpr float kSplitRatio = (DT == kBF16) ? 16.0f : 2.0f;
-
-__device__ __forceinline__ int k_swz(int row, int chunk) { return chunk ^ (row & 7); }
-__device__ __forceinline__ int v_swz(int row, int chunk) { return chunk ^ ((row ^ (row >> 3)) & 7); }
 }  // namespace fa
 
 // Widen a packed pair of 16-bit values.
@@ -75,246 +68,6 @@ template <int DT>
 __device__ __forceinline__ void unpack_pair(uint32_t d, float& lo, float& hi) {
   lo = u16_to_f32<DT>(static_cast<uint16_t>(d & 0xffffu));
   hi = u16_to_f32<DT>(static_cast<uint16_t>(d >> 16));
-}
-
-// One work item: query block `qb` (BQ rows) of flattened head `bh` = b*NH + h.
-// Called by all NT threads of a workgroup; uses the workgroup's LDS.
-template <int DT>
-__device__ __forceinline__ void prefill_tile(const uint16_t* __restrict__ Q,
-                                             const uint16_t* __restrict__ K,
-                                             const uint16_t* __restrict__ V,
-                                             uint16_t* __restrict__ O, uint32_t seq_len,
-                                             uint32_t start_pos, uint32_t max_seq, uint32_t nh,
-                                             uint32_t nkv, float scale_log2, uint32_t bh,
-                                             uint32_t qb) {
-  using namespace fa;
-  __shared__ u32x4 ks[2][BKV * D / 8];  // 16 KB per stage
-  __shared__ u32x4 vs[2][D * BKV / 8];  // 16 KB per stage
-
-  const uint32_t b = bh / nh, h = bh % nh;
-  const uint32_t kvh = h / (nh / nkv);
-  const uint32_t q0 = qb * BQ;
-  const uint32_t kv_len = start_pos + seq_len;
-
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
-  const int l32 = lane & 31, g = lane >> 5;
-  const uint32_t qw0 = q0 + 32 * wave;           // this wave's first query row
-  const uint32_t my_q = qw0 + l32;               // query row owned by this lane
-  const uint32_t qa_lo = start_pos + qw0;        // lowest absolute position in the wave
-  const uint32_t qa_hi = start_pos + qw0 + 31;   // highest
-  const uint32_t my_qa = start_pos + my_q;
-
-  const size_t q_row_stride = static_cast<size_t>(nh) * D;
-  const uint16_t* kbase = K + (static_cast<size_t>(b) * nkv + kvh) * max_seq * D;
-  const uint16_t* vbase = V + (static_cast<size_t>(b) * nkv + kvh) * max_seq * D;
-
-  // Q^T fragments: lane holds query my_q, d = 16*ds + 8*g .. +7.
-  u32x4 qf[8];
-  {
-    const uint16_t* qp = Q + (static_cast<size_t>(b) * seq_len + my_q) * q_row_stride + h * D;
-#pragma unroll
-    for (int ds = 0; ds < 8; ++ds)
-      qf[ds] = (my_q < seq_len) ? ldg128(qp + 16 * ds + 8 * g) : u32x4{0, 0, 0, 0};
-  }
-
-  // KV blocks this workgroup needs: positions [0, start_pos + min(q0 + BQ, S)).
-  const uint32_t q_hi_wg = min(q0 + BQ, seq_len);
-  const uint32_t kv_need = start_pos + q_hi_wg;
-  const uint32_t nkb = (kv_need + BKV - 1) / BKV;
-
-  // ---- staging: waves 0-3 load K (4 x 16 B per thread), waves 4-7 load V as
-  //      8 (kv) x 4 (d) blocks that are transposed on the way into LDS ----
-  u32x4 rk[4];
-  u32x2 rv[8];
-  auto load_kv = [&](uint32_t kv0) {
-    if (t < 256) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int c = t + 256 * i;          // 1024 chunks of 16 B
-        const int row = c >> 4, ch = c & 15;
-        const uint32_t pos = kv0 + row;
-        rk[i] = (pos < kv_len) ? ldg128(kbase + static_cast<size_t>(pos) * D + ch * 8)
-                               : u32x4{0, 0, 0, 0};
-      }
-    } else {
-      const int tt = t - 256;
-      const int db = tt & 31, kvb = tt >> 5;  // d block of 4, kv block of 8
-      const int grp = kvb >> 1, half = kvb & 1;
-#pragma unroll
-      for (int r = 0; r < 8; ++r) {
-        const int kvl = 16 * grp + 4 * half + (r < 4 ? r : 8 + (r - 4));
-        const uint32_t pos = kv0 + kvl;
-        rv[r] = (pos < kv_len)
-                    ? *reinterpret_cast<const u32x2*>(vbase + static_cast<size_t>(pos) * D + 4 * db)
-                    : u32x2{0, 0};
-      }
-    }
-  };
-  auto store_kv = [&](int buf) {
-    if (t < 256) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int c = t + 256 * i;
-        const int row = c >> 4, ch = c & 15;
-        ks[buf][row * 16 + k_swz(row, ch)] = rk[i];
-      }
-    } else {
-      const int tt = t - 256;
-      const int db = tt & 31, kvb = tt >> 5;
-      // rv[r] = 4 d-values of slot r; emit, for each of the 4 d rows, the 8 slots.
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int dw = j >> 1;
-        u32x4 o;
-#pragma unroll
-        for (int p = 0; p < 4; ++p) {
-          const uint32_t lo = rv[2 * p][dw], hi = rv[2 * p + 1][dw];
-          o[p] = (j & 1) ? pack_halves<true>(lo, hi) : pack_halves<false>(lo, hi);
-        }
-        const int row = 4 * db + j;
-        vs[buf][row * 8 + v_swz(row, kvb)] = o;
-      }
-    }
-  };
-
-  f32x16 o_acc[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) o_acc[i][r] = 0.0f;
-  float m_run = -INFINITY;  // running max (log2 units) of this lane's query
-  float l_run = 0.0f;       // this lane's partial sum (partner lane holds the rest)
-
-  load_kv(0);
-  store_kv(0);
-  __syncthreads();
-
-  for (uint32_t jb = 0; jb < nkb; ++jb) {
-    const int cur = jb & 1;
-    const uint32_t kv0 = jb * BKV;
-    if (jb + 1 < nkb) load_kv(kv0 + BKV);
-
-    // Skip blocks that lie entirely above this wave's causal diagonal or past
-    // the end of the sequence for all of its rows.
-    const bool active = (kv0 <= qa_hi) && (qw0 < seq_len);
-    if (active) {
-      float s[2][16];
-      {
-        f32x16 acc[2];
-#pragma unroll
-        for (int i = 0; i < 2; ++i)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) acc[i][r] = 0.0f;
-#pragma unroll
-        for (int ds = 0; ds < 8; ++ds) {
-#pragma unroll
-          for (int kt = 0; kt < 2; ++kt) {
-            const int row = 32 * kt + l32;
-            const u32x4 kf = ks[cur][row * 16 + k_swz(row, 2 * ds + g)];
-            acc[kt] = mfma32x32x16<DT>(kf, qf[ds], acc[kt]);
-          }
-        }
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) s[kt][r] = acc[kt][r];
-      }
-      // Causal mask only where the block crosses the diagonal.
-      if (kv0 + BKV - 1 > qa_lo) {
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const uint32_t pos = kv0 + 32 * kt + 8 * (r >> 2) + 4 * g + (r & 3);
-            if (pos > my_qa) s[kt][r] = -INFINITY;
-          }
-      }
-      float mx = -INFINITY;
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kt][r]);
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
-      const float m_blk = mx * scale_log2;
-      // Rescale only when the running max grows by more than the threshold: until
-      // then exponents stay <= 2^threshold, which f32 sums and 16-bit P absorb.
-      float m_use = m_run;
-      const bool grow = m_blk > m_run + kRescaleThreshold || m_run == -INFINITY;
-      if (__builtin_amdgcn_ballot_w64(grow) != 0) {
-        const float m_new = fmaxf(m_run, m_blk);
-        const float alpha = exp2_fast(m_run - m_new);
-        l_run *= alpha;
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) o_acc[i][r] *= alpha;
-        m_run = m_new;
-        m_use = m_new;
-      }
-      float ls = 0.0f;
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          s[kt][r] = exp2_fast(__builtin_fmaf(s[kt][r], scale_log2, -m_use));
-          ls += s[kt][r];
-        }
-      l_run += ls;
-      // P enters the MFMA as 16-bit values.  A block that carries a large share
-      // of a query's weight so far (few keys dominate: early rows, peaked
-      // scores) also gets the rounding residual P - hi(P) as a second 16-bit
-      // operand, so its products are exact to ~2^-16 instead of 2^-9 (bf16).
-      const float blk = ls + __shfl_xor(ls, 32);
-      const float tot = l_run + __shfl_xor(l_run, 32);
-      const bool heavy = blk * kSplitRatio<DT> > tot;
-      const bool split = __builtin_amdgcn_ballot_w64(heavy) != 0;
-#pragma unroll
-      for (int st = 0; st < 4; ++st) {
-        const int kt = st >> 1, hh = st & 1;
-        u32x4 hi;
-#pragma unroll
-        for (int pp = 0; pp < 4; ++pp)
-          hi[pp] = cvt_pk<DT>(s[kt][8 * hh + 2 * pp], s[kt][8 * hh + 2 * pp + 1]);
-        u32x4 vf[4];
-#pragma unroll
-        for (int dt = 0; dt < 4; ++dt) {
-          const int row = 32 * dt + l32;
-          vf[dt] = vs[cur][row * 8 + v_swz(row, 2 * st + g)];
-          o_acc[dt] = mfma32x32x16<DT>(vf[dt], hi, o_acc[dt]);
-        }
-        if (split) {
-          u32x4 lo;
-#pragma unroll
-          for (int pp = 0; pp < 4; ++pp) {
-            float a, c;
-            unpack_pair<DT>(hi[pp], a, c);
-            lo[pp] = cvt_pk<DT>(s[kt][8 * hh + 2 * pp] - a, s[kt][8 * hh + 2 * pp + 1] - c);
-          }
-#pragma unroll
-          for (int dt = 0; dt < 4; ++dt) o_acc[dt] = mfma32x32x16<DT>(vf[dt], lo, o_acc[dt]);
-        }
-      }
-    }
-    if (jb + 1 < nkb) store_kv(cur ^ 1);
-    __syncthreads();
-  }
-
-  // ---- epilogue: O[q][d] = O^T[d][q] / l ----
-  const float l_tot = l_run + __shfl_xor(l_run, 32);
-  const float inv = 1.0f / l_tot;
-  if (my_q < seq_len) {
-    uint16_t* op = O + (static_cast<size_t>(b) * seq_len + my_q) * q_row_stride + h * D;
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4) {
-        const int d = 32 * dt + 8 * q4 + 4 * g;
-        u32x2 w;
-        w[0] = cvt_pk<DT>(o_acc[dt][4 * q4 + 0] * inv, o_acc[dt][4 * q4 + 1] * inv);
-        w[1] = cvt_pk<DT>(o_acc[dt][4 * q4 + 2] * inv, o_acc[dt][4 * q4 + 3] * inv);
-        *reinterpret_cast<u32x2*>(op + d) = w;
-      }
-  }
 }
 
 // Map a work index to (bh, qb): heavy (late) query blocks first; when the head
@@ -331,26 +84,14 @@ __device__ __forceinline__ void prefill_work(uint32_t w, uint32_t nbh, uint32_t 
   }
 }
 
-template <int DT>
-__global__ void __launch_bounds__(fa::NT, 1)
-attn_prefill_fa128(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
-                   const uint16_t* __restrict__ V, uint16_t* __restrict__ O, uint32_t batch,
-                   uint32_t seq_len, uint32_t start_pos, uint32_t max_seq, uint32_t nh,
-                   uint32_t nkv, float scale_log2) {
-  const uint32_t nqb = (seq_len + fa::BQ - 1) / fa::BQ;
-  uint32_t bh, qb;
-  prefill_work(blockIdx.x, batch * nh, nqb, bh, qb);
-  prefill_tile<DT>(Q, K, V, O, seq_len, start_pos, max_seq, nh, nkv, scale_log2, bh, qb);
-}
-
 // ============================================================================
 // Prefill, LDS-DMA form (head_dim 128, 16-bit Q/K/V).
 //
-// Same work split and arithmetic as prefill_tile (8 waves x 32 query rows, S^T
-// = K.Q^T, online softmax per query column, O^T += V^T.P^T with P^T taken from
-// the S^T accumulators in place), but K and V reach LDS by
-// global_load_lds_dwordx4 into a ring of NS stages of 64 KV positions, issued
-// NS-1 blocks ahead, with no register staging and no transpose on the way in:
+// The work split and arithmetic above (8 waves x 32 query rows, S^T = K.Q^T,
+// online softmax per query column, O^T += V^T.P^T with P^T taken from the S^T
+// accumulators in place).  K and V reach LDS by global_load_lds_dwordx4 into a
+// ring of NS stages of 64 KV positions, issued NS-1 blocks ahead, with no
+// register staging and no transpose on the way in:
 //   K stage [64 kv][128 d]: 16-byte chunk c of row r at unit c ^ (r & 15), so
 //            the 16 rows one quarter-wave reads with ds_read_b128 cover all 64
 //            banks.

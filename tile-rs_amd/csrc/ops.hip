@@ -391,30 +391,19 @@ int th_attention_prefill(const void* q, const void* k, const void* v, void* o, u
     const uint64_t nqb = (seq_len + th::fa::BQ - 1) / th::fa::BQ;
     const uint64_t blocks = nqb * batch * num_heads;
     if (blocks > 0x7fffffffu) return fail(TH_KERNEL_ERROR, "attention_prefill: grid too large");
+    static_assert(th::fa::NT == th::fa2::NT && th::fa::BQ == th::fa2::BQ, "prefill launch shape");
     const dim3 grid(static_cast<uint32_t>(blocks)), block(th::fa::NT);
     const float sl2 = scale * th::kLog2e;
     auto Q = static_cast<const uint16_t*>(q);
     auto K = static_cast<const uint16_t*>(k);
     auto V = static_cast<const uint16_t*>(v);
     auto O = static_cast<uint16_t*>(o);
-    static const bool dma = [] {
-      const char* e = std::getenv("TILERS_HIP_ATTN_DMA");
-      return !(e && std::atoi(e) == 0);
-    }();
-    if (dma) {
-      if (dtype == TH_BF16)
-        hipLaunchKernelGGL(th::attn_prefill_dma128<th::kBF16>, grid, block, 0, as_stream(s), Q, K, V,
-                           O, batch, seq_len, start_pos, max_seq, num_heads, num_kv_heads, sl2);
-      else
-        hipLaunchKernelGGL(th::attn_prefill_dma128<th::kF16>, grid, block, 0, as_stream(s), Q, K, V,
-                           O, batch, seq_len, start_pos, max_seq, num_heads, num_kv_heads, sl2);
-    } else if (dtype == TH_BF16) {
-      hipLaunchKernelGGL(th::attn_prefill_fa128<th::kBF16>, grid, block, 0, as_stream(s), Q, K, V, O,
+    if (dtype == TH_BF16)
+      hipLaunchKernelGGL(th::attn_prefill_dma128<th::kBF16>, grid, block, 0, as_stream(s), Q, K, V, O,
                          batch, seq_len, start_pos, max_seq, num_heads, num_kv_heads, sl2);
-    } else {
-      hipLaunchKernelGGL(th::attn_prefill_fa128<th::kF16>, grid, block, 0, as_stream(s), Q, K, V, O,
+    else
+      hipLaunchKernelGGL(th::attn_prefill_dma128<th::kF16>, grid, block, 0, as_stream(s), Q, K, V, O,
                          batch, seq_len, start_pos, max_seq, num_heads, num_kv_heads, sl2);
-    }
     return launch_status("attention_prefill launch");
   }
   return attn_general_launch(q, k, v, o, batch, seq_len, start_pos, max_seq, start_pos + seq_len,
