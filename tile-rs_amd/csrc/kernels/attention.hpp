@@ -655,11 +655,18 @@ attn_decode_split(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K
 }
 
 // Merge the per-chunk partials: O = sum_s 2^(m_s - M) O_s / sum_s 2^(m_s - M) l_s.
+// One 128-thread block per (batch, head), thread d owns output d.  The chunk
+// statistics come in with one load per thread (128 chunks per pass) and are
+// shared through LDS; the O_s loads are issued eight at a time, so the merge
+// costs a few memory round trips instead of one per chunk.  The sums run over
+// s in ascending order.
 template <int DT>
-__global__ void __launch_bounds__(128)
+__global__ void __launch_bounds__(dec::D)
 attn_decode_combine(const float* __restrict__ ws, uint16_t* __restrict__ O, uint32_t nh,
                     uint32_t nkv, uint32_t n_split) {
   constexpr int D = dec::D;
+  constexpr uint32_t PASS = D;  // chunks whose statistics one pass stages
+  __shared__ float s_w[PASS], s_l[PASS];
   const uint32_t bhq = blockIdx.x;  // b * nh + h
   const uint32_t b = bhq / nh, h = bhq % nh;
   const uint32_t G = nh / nkv;
@@ -667,13 +674,40 @@ attn_decode_combine(const float* __restrict__ ws, uint16_t* __restrict__ O, uint
   const float* rec0 = ws + ((static_cast<size_t>(b) * nkv + kvh) * G + q) * n_split * (D + 2);
   const int d = threadIdx.x;
   float M = -INFINITY;
-  for (uint32_t s = 0; s < n_split; ++s) M = fmaxf(M, rec0[s * (D + 2)]);
+  for (uint32_t s0 = 0; s0 < n_split; s0 += PASS) {
+    const uint32_t cnt = min(PASS, n_split - s0);
+    __syncthreads();
+    if (static_cast<uint32_t>(d) < cnt) s_w[d] = rec0[(s0 + d) * (D + 2)];
+    __syncthreads();
+    for (uint32_t i = 0; i < cnt; ++i) M = fmaxf(M, s_w[i]);
+  }
   float num = 0.0f, den = 0.0f;
-  for (uint32_t s = 0; s < n_split; ++s) {
-    const float* rec = rec0 + s * (D + 2);
-    const float w = (rec[0] == -INFINITY) ? 0.0f : exp2_fast(rec[0] - M);
-    num = __builtin_fmaf(w, rec[2 + d], num);
-    den = __builtin_fmaf(w, rec[1], den);
+  for (uint32_t s0 = 0; s0 < n_split; s0 += PASS) {
+    const uint32_t cnt = min(PASS, n_split - s0);
+    __syncthreads();
+    if (static_cast<uint32_t>(d) < cnt) {
+      const float* rec = rec0 + (s0 + d) * (D + 2);
+      const float m = rec[0];
+      s_w[d] = (m == -INFINITY) ? 0.0f : exp2_fast(m - M);
+      s_l[d] = rec[1];
+    }
+    __syncthreads();
+    const float* od = rec0 + static_cast<size_t>(s0) * (D + 2) + 2 + d;
+    uint32_t i = 0;
+    for (; i + 8 <= cnt; i += 8) {
+      float o[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) o[u] = od[(i + u) * (D + 2)];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        num = __builtin_fmaf(s_w[i + u], o[u], num);
+        den = __builtin_fmaf(s_w[i + u], s_l[i + u], den);
+      }
+    }
+    for (; i < cnt; ++i) {
+      num = __builtin_fmaf(s_w[i], od[i * (D + 2)], num);
+      den = __builtin_fmaf(s_w[i], s_l[i], den);
+    }
   }
   const float o = (den > 0.0f) ? num / den : 0.0f;
   O[static_cast<size_t>(bhq) * D + d] = f32_to_u16<DT>(o);
