@@ -476,6 +476,24 @@ def test_matmul_silu_mul_shapes(dev, stream, m, k, n, in_dt, out_dt, trans):
                  trans)
 
 
+def test_matmul_silu_mul_unaligned_output(dev, stream):
+    """UP and C one element past a 16-byte boundary: the 16-byte epilogue of the DMA
+    pipeline does not apply and the register-staged kernel handles the shape."""
+    rng = np.random.default_rng(91)
+    m = k = n = 256
+    a, b = rand16(rng, m * k, D.BF16), rand16(rng, k * n, D.BF16, 0.1)
+    u = orc.narrow(rng.standard_normal(m * n).astype(np.float32), orc.BF16)
+    ab, bb = upload(dev, stream, a, D.BF16), upload(dev, stream, b, D.BF16)
+    ub = upload(dev, stream, np.concatenate([np.zeros(1, u.dtype), u]), D.BF16)
+    cb = dev.alloc(m * n + 1, D.BF16)
+    th.matmul_silu_mul(ab, bb, ub.as_raw_ptr() + 2, cb.as_raw_ptr() + 2, m, k, n, D.BF16,
+                       D.BF16, False, stream=stream)
+    got = orc.widen(cb.copy_to_host(stream)[1:], orc.BF16).reshape(m, n)
+    ref = orc.matmul_silu_mul(a, b, u, m, k, n, orc.BF16, orc.BF16)
+    assert_gemm_close(got, orc.widen(ref, orc.BF16).reshape(m, n), "swiglu unaligned",
+                      u16_dtype=orc.BF16)
+
+
 def test_matmul_silu_mul_batched(dev, stream):
     _swiglu_case(dev, stream, np.random.default_rng(77), 256, 128, 256, D.F16, D.F16, False,
                  batch=3)

@@ -67,6 +67,40 @@ __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
          (static_cast<uint32_t>(f32_to_u16<DT>(hi)) << 16);
 }
 
+// Elements in one 16-byte vector, and 16-byte vector <-> f32 conversions
+// (exact widening, RNE narrowing).
+template <int DT>
+struct Vec16 {
+  static constexpr int kElems = (DT == kF32) ? 4 : 8;  // elements per 16 B
+};
+
+template <int DT>
+__device__ __forceinline__ void unpack16(u32x4 v, float (&f)[Vec16<DT>::kElems]) {
+  if constexpr (DT == kF32) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) f[i] = __uint_as_float(v[i]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f[2 * i] = u16_to_f32<DT>(static_cast<uint16_t>(v[i] & 0xffffu));
+      f[2 * i + 1] = u16_to_f32<DT>(static_cast<uint16_t>(v[i] >> 16));
+    }
+  }
+}
+
+template <int DT>
+__device__ __forceinline__ u32x4 pack16(const float (&f)[Vec16<DT>::kElems]) {
+  u32x4 v;
+  if constexpr (DT == kF32) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = __float_as_uint(f[i]);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = pack2<DT>(f[2 * i], f[2 * i + 1]);
+  }
+  return v;
+}
+
 // ---- wavefront (64-lane) reductions ---------------------------------------------
 // Lanes within a 16-lane row use DPP; the two cross-row steps use ds_swizzle-free
 // lane shuffles.

@@ -544,19 +544,91 @@ __device__ __forceinline__ void gemm_dma_tile_256(const uint16_t* __restrict__ A
   for (; kt < nk; ++kt) step(kt, std::false_type{});
   __builtin_amdgcn_sched_barrier(0);
 
-  // Epilogue.  Accumulator register r of lane l in a 32x32 block holds
-  // row 8*(r/4) + 4*(l/32) + r%4, column l%32.
+  // Epilogue.  Accumulator register r of lane l in a 32x32 block holds row
+  // 8*(r/4) + 4*(l/32) + r%4, column l%32: a lane has four consecutive rows of
+  // one column, so direct stores are 2- or 4-byte writes (64-128 contiguous
+  // bytes per row and instruction).  For a plain store that is as fast as any
+  // rearrangement (measured): the tile's HBM writes bound it.
+  if constexpr (EPI != kEpiSiluMul) {
 #pragma unroll
-  for (int mi = 0; mi < 4; ++mi)
+    for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
-    for (int ni = 0; ni < NI; ++ni) {
-      const uint32_t col = n0 + wn * TWN + ni * 32 + l32;
+      for (int ni = 0; ni < NI; ++ni) {
+        const uint32_t col = n0 + wn * TWN + ni * 32 + l32;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const uint32_t row = m0 + wm * 128 + mi * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-        store_out<EPI, DT_OUT>(C, up, static_cast<size_t>(row) * N + col, acc[mi][ni][r]);
+        for (int r = 0; r < 16; ++r) {
+          const uint32_t row = m0 + wm * 128 + mi * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+          store_out<EPI, DT_OUT>(C, up, static_cast<size_t>(row) * N + col, acc[mi][ni][r]);
+        }
+      }
+    return;
+  }
+  // With the SiLU*Mul epilogue the UP operand makes scattered 2-byte reads as
+  // well, so the tile goes through LDS: each wave parks 64 rows x 64 columns
+  // of f32 at a time in a private 16 KB region of the idle stage arena and
+  // reads them back as eight consecutive columns per lane.  UP and C then move
+  // in 16-byte pieces (128 contiguous bytes per row and instruction), and UP's
+  // loads are issued before the LDS round trip.
+  // Region layout [64 r][64 c] f32, 4-float chunk q of row r at q ^ s(r) with
+  // s(r) = (r & 1) | 8*((r >> 2) & 1): the scalar writes (rows r, r+4 across
+  // the two lane halves) and the 16-byte reads (two rows per quarter-wave)
+  // both cover all 64 banks.
+  static_assert(TWN == 64 && 8 * 64 * 64 * 4 <= NS * (BM + BN) * KB * 2, "epilogue staging");
+  constexpr int OSZ = (DT_OUT == kF32) ? 4 : 2;
+  constexpr int UPV = 8 * OSZ / 16;  // 16-byte UP vectors per eight columns
+  lds::wait_lgkm0();
+  bar();  // every wave is done with the stage buffers
+  float* wl = reinterpret_cast<float*>(arena) + wave * 64 * 64;
+  auto sw = [](int r) { return (r & 1) | (((r >> 2) & 1) << 3); };
+  const int rl = lane >> 3, cq = lane & 7;  // read-back: row rl + 8*it, columns 8*cq..+7
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const uint32_t row0 = m0 + wm * 128 + 64 * h;
+    const uint32_t col = n0 + wn * TWN + 8 * cq;
+    u32x4 upv[8][UPV];
+#pragma unroll
+    for (int it = 0; it < 8; ++it)
+#pragma unroll
+      for (int u = 0; u < UPV; ++u)
+        upv[it][u] = ldg128(static_cast<const char*>(up) +
+                            ((static_cast<size_t>(row0 + rl + 8 * it) * N + col) * OSZ + 16 * u));
+#pragma unroll
+    for (int m2 = 0; m2 < 2; ++m2)
+#pragma unroll
+      for (int ni = 0; ni < NI; ++ni)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int row = 32 * m2 + 8 * (r >> 2) + 4 * g + (r & 3);
+          const int c = 32 * ni + l32;
+          wl[row * 64 + (((c >> 2) ^ sw(row)) << 2) + (c & 3)] = acc[2 * h + m2][ni][r];
+        }
+#pragma unroll
+    for (int it = 0; it < 8; ++it) {
+      const int row = rl + 8 * it;
+      const f32x4 lo = *reinterpret_cast<const f32x4*>(wl + row * 64 + (((2 * cq) ^ sw(row)) << 2));
+      const f32x4 hi =
+          *reinterpret_cast<const f32x4*>(wl + row * 64 + (((2 * cq + 1) ^ sw(row)) << 2));
+      float v[8] = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      float u[8];
+      if constexpr (DT_OUT == kF32) {
+        // (__builtin_bit_cast straight from a vector element reads element 0 with
+        // this compiler; the element goes through a scalar first)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) u[e] = __uint_as_float(upv[it][e >> 2][e & 3]);
+      } else {
+        unpack16<DT_OUT>(upv[it][0], u);
+      }
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = v[e] / (1.0f + expf(-v[e])) * u[e];
+      char* cp = static_cast<char*>(C) + (static_cast<size_t>(row0 + row) * N + col) * OSZ;
+      if constexpr (DT_OUT == kF32) {
+        stg128(cp, __builtin_bit_cast(u32x4, f32x4{v[0], v[1], v[2], v[3]}));
+        stg128(cp + 16, __builtin_bit_cast(u32x4, f32x4{v[4], v[5], v[6], v[7]}));
+      } else {
+        stg128(cp, pack16<DT_OUT>(v));
       }
     }
+  }
 }
 
 // M, N multiples of 256, K multiple of KB.  Batch index = blockIdx.y.

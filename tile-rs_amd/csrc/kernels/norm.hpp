@@ -22,7 +22,7 @@ __global__ void __launch_bounds__(256)
 rms_norm_rows_stream(const void* __restrict__ x, void* __restrict__ y, uint32_t rows,
                      uint32_t cols, float eps) {
   constexpr int ESZ = (DT == kF32) ? 4 : 2;
-  constexpr int E = SoftmaxVec<DT>::kElems;
+  constexpr int E = Vec16<DT>::kElems;
   const int lane = threadIdx.x & 63;
   const uint32_t nvec = cols / E;
   const uint32_t stride = gridDim.x * (blockDim.x >> 6);

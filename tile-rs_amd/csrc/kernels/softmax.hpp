@@ -15,46 +15,13 @@
 
 namespace th {
 
-// Number of 16-byte vectors each lane holds for one row in the register path.
-template <int DT>
-struct SoftmaxVec {
-  static constexpr int kElems = (DT == kF32) ? 4 : 8;  // elements per 16 B
-};
-
-template <int DT>
-__device__ __forceinline__ void unpack16(u32x4 v, float (&f)[SoftmaxVec<DT>::kElems]) {
-  if constexpr (DT == kF32) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) f[i] = __uint_as_float(v[i]);
-  } else {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      f[2 * i] = u16_to_f32<DT>(static_cast<uint16_t>(v[i] & 0xffffu));
-      f[2 * i + 1] = u16_to_f32<DT>(static_cast<uint16_t>(v[i] >> 16));
-    }
-  }
-}
-
-template <int DT>
-__device__ __forceinline__ u32x4 pack16(const float (&f)[SoftmaxVec<DT>::kElems]) {
-  u32x4 v;
-  if constexpr (DT == kF32) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = __float_as_uint(f[i]);
-  } else {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = pack2<DT>(f[2 * i], f[2 * i + 1]);
-  }
-  return v;
-}
-
 // Register path: one wavefront owns one row; NV 16-byte vectors per lane, so a
 // row holds up to 64 * NV * kElems elements.  Requires cols % kElems == 0 and
 // 16-byte aligned rows.  xr / yr point at the row.
 template <int DT, int NV>
 __device__ __forceinline__ void softmax_row_wave(const void* __restrict__ xr_,
                                                  void* __restrict__ yr_, uint32_t cols, int lane) {
-  constexpr int E = SoftmaxVec<DT>::kElems;
+  constexpr int E = Vec16<DT>::kElems;
   const uint32_t nvec = cols / E;  // 16-byte vectors in this row
   const char* xr = static_cast<const char*>(xr_);
   char* yr = static_cast<char*>(yr_);
@@ -121,7 +88,7 @@ __global__ void __launch_bounds__(256)
 softmax_rows_stream(const void* __restrict__ x, void* __restrict__ y, uint32_t rows,
                     uint32_t cols) {
   constexpr int ESZ = (DT == kF32) ? 4 : 2;
-  constexpr int E = SoftmaxVec<DT>::kElems;
+  constexpr int E = Vec16<DT>::kElems;
   const int lane = threadIdx.x & 63;
   const uint32_t nvec = cols / E;
   const uint32_t stride = gridDim.x * (blockDim.x >> 6);

@@ -57,7 +57,7 @@ uint32_t current_cu_count() {
 
 template <int DT>
 int softmax_launch(const void* x, void* y, uint32_t rows, uint32_t cols, hipStream_t s) {
-  constexpr int E = th::SoftmaxVec<DT>::kElems;
+  constexpr int E = th::Vec16<DT>::kElems;
   const bool vec_ok = (cols % E == 0) && aligned16(x) && aligned16(y);
   const uint32_t nvec = cols / E;
   if (vec_ok && nvec <= 64u * 4u) {
@@ -114,7 +114,7 @@ void rms_norm_stream_go(const void* x, void* y, uint32_t rows, uint32_t cols, fl
 template <int DT>
 int rms_norm_launch(const void* x, void* y, uint32_t rows, uint32_t cols, float eps,
                     hipStream_t s) {
-  constexpr int E = th::SoftmaxVec<DT>::kElems;
+  constexpr int E = th::Vec16<DT>::kElems;
   const bool vec_ok = (cols % E == 0) && aligned16(x) && aligned16(y);
   const uint32_t nvec = cols / E;
   if (vec_ok && nvec <= 64) rms_norm_stream_go<DT, 1>(x, y, rows, cols, eps, s);
@@ -161,7 +161,12 @@ template <int DT, int DTO, int EPI, bool BT>
 void gemm_mfma_go(const GemmArgs& g, dim3 grid) {
   auto A = static_cast<const uint16_t*>(g.a);
   auto B = static_cast<const uint16_t*>(g.b);
-  if (gemm_dma() && g.m % th::gemm::BM == 0 && g.n % th::gemm::BN == 0 && g.k % th::gemm::DBK == 0) {
+  // The DMA kernel's SiLU*Mul epilogue writes C and reads UP in 16-byte pieces.
+  constexpr uint64_t OSZ = (DTO == th::kF32) ? 4 : 2;
+  const bool out_vec = EPI != th::gemm::kEpiSiluMul ||
+                       (aligned16(g.c) && aligned16(g.up) && (g.sc * OSZ) % 16 == 0);
+  if (gemm_dma() && out_vec && g.m % th::gemm::BM == 0 && g.n % th::gemm::BN == 0 &&
+      g.k % th::gemm::DBK == 0) {
     hipLaunchKernelGGL((th::gemm_dma_256<DT, DTO, BT, th::gemm::DBK, th::gemm::NSTAGE,
                                          th::gemm::DWAVES, EPI>),
                        grid, dim3(64 * th::gemm::DWAVES), 0, g.s, A, B, g.c, g.m, g.n, g.k, g.sa,
