@@ -289,15 +289,19 @@ __device__ __forceinline__ void prefill_tile_dma(const uint16_t* __restrict__ Q,
     const float m_new = grow ? fmaxf(m_run, m_blk) : m_run;
     alpha = exp2_fast(m_run - m_new);
     m_run = m_new;
-    float ls = 0.0f;
+    // All exponentials first, then the row sum in two chains: an add that reads
+    // the exp issued just before it waits a cycle (trans -> VALU hazard).
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        sc[kt][r] = exp2_fast(__builtin_fmaf(sc[kt][r], scale_log2, -m_new));
-        ls += sc[kt][r];
-      }
-    l_run = __builtin_fmaf(l_run, alpha, ls);
+      for (int r = 0; r < 16; ++r) sc[kt][r] = exp2_fast(__builtin_fmaf(sc[kt][r], scale_log2, -m_new));
+    float ls0 = 0.0f, ls1 = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      ls0 += sc[0][r];
+      ls1 += sc[1][r];
+    }
+    l_run = __builtin_fmaf(l_run, alpha, ls0 + ls1);
     const float tot = xhalf_sum(l_run);
     const float pmax = exp2_fast(m_blk - m_new);
     split = __builtin_amdgcn_ballot_w64(pmax * fa::kSplitRatio<DT> > tot) != 0;
