@@ -115,11 +115,24 @@ def test_registry_hip_matches_direct_emit():
     ("prefill_bf16", "th::entry::prefill<th::kBF16>"),
     ("decode_bf16", "th::entry::decode<th::kBF16>"),
     ("rms_norm_rows", "th::entry::rms_norm_rows<th::kF32>"),
-    ("swiglu_gate_bf16", "th::entry::gemm<th::kBF16, th::kF32, false, th::gemm::kEpiSiluMul>"),
+    ("swiglu_gate_bf16", "th::entry::gemm_dma<th::kBF16, th::kF32, false, th::gemm::kEpiSiluMul>"),
+    ("matmul_bf16_tiles", "th::entry::gemm_dma<th::kBF16, th::kBF16, false, th::gemm::kEpiStore>"),
 ])
 def test_hot_ops_lower_to_hand_written_kernels(example, entry):
     out = th.emit((EXAMPLES / f"{example}.mlir").read_text())
     assert entry in out.source
+
+
+def test_whole_tile_matmul_takes_the_dma_pipeline_launch_shape():
+    """512x320x768: 256x256 tiles and 64-deep K steps, so the LDS-DMA entry with its
+    512-thread workgroups, 2 x 3 workgroups per logical tile."""
+    src = th.emit((EXAMPLES / "matmul_bf16_tiles.mlir").read_text()).source
+    assert "__launch_bounds__(512) matmul_bf16_tiles(" in src
+    assert "__th_desc_matmul_bf16_tiles = {th::kLaunchDescMagic, 512u, 6u, 1u," in src
+    # N not a multiple of 256: the register-staged entry and its 256-thread groups
+    src = th.emit((EXAMPLES / "matmul_bf16.mlir").read_text()).source
+    assert "__launch_bounds__(256) matmul_bf16_acc_f32(" in src
+    assert "th::entry::gemm_dma" not in src
 
 
 def test_matmul_shape_and_tile_offsets_are_exact():

@@ -27,7 +27,7 @@ def launcher(dev):
     lau = dev.create_launcher()
     for stem in ("softmax_rows", "softmax_generic", "matmul_bf16", "matmul_f16_t", "matmul_f32",
                  "attention_f32", "prefill_bf16", "decode_bf16", "swiglu_mask", "rms_norm_rows",
-                 "swiglu_gate_bf16"):
+                 "swiglu_gate_bf16", "matmul_bf16_tiles"):
         lau.load(_build.example_path(stem), th.KernelMode.GENERAL)
     return lau
 
@@ -74,6 +74,27 @@ def test_matmul_bf16_acc_f32_two_tiles(dev, stream, launcher):
     for t in range(tiles):
         ref = orc.matmul(a[t * M * K:(t + 1) * M * K], b[t * K * N:(t + 1) * K * N], M, K, N, orc.BF16)
         assert_gemm_close(got[t], ref, f"tile {t}")
+
+
+@pytest.mark.parametrize("c_shift", [0, 2])
+def test_matmul_bf16_whole_tiles(dev, stream, launcher, c_shift):
+    """512x320x768 bf16 -> bf16 over two logical tiles: the LDS-DMA entry.  With C two
+    bytes past a 16-byte boundary the entry takes its per-element kernel instead."""
+    tiles, M, K, N = 2, 512, 320, 768
+    rng = np.random.default_rng(5 + c_shift)
+    a = orc.narrow(rng.standard_normal(tiles * M * K).astype(np.float32), orc.BF16)
+    b = orc.narrow((rng.standard_normal(tiles * K * N) * 0.05).astype(np.float32), orc.BF16)
+    ab, bb = up(dev, stream, a, D.BF16), up(dev, stream, b, D.BF16)
+    cb = dev.alloc(tiles * M * N + 8, D.BF16)
+    launcher.launch("matmul_bf16_tiles", th.LaunchGrid.blocks_only(tiles),
+                    [ptr(ab), ptr(bb), C.c_void_p(cb.as_raw_ptr() + c_shift)], stream)
+    raw = cb.copy_to_host(stream)[c_shift // 2:c_shift // 2 + tiles * M * N]
+    got = orc.widen(raw, orc.BF16).reshape(tiles, M, N)
+    for t in range(tiles):
+        ref = orc.matmul(a[t * M * K:(t + 1) * M * K], b[t * K * N:(t + 1) * K * N], M, K, N,
+                         orc.BF16, orc.F32)
+        assert_gemm_close(got[t], orc.widen(orc.narrow(ref, orc.BF16), orc.BF16),
+                          f"matmul_bf16_tiles tile {t} shift {c_shift}", u16_dtype=orc.BF16)
 
 
 def test_matmul_transposed_f16_out(dev, stream, launcher):

@@ -55,7 +55,6 @@ __device__ __forceinline__ uint32_t cvt_pk(float lo, float hi) {
 namespace fa {
 constexpr int D = 128;
 constexpr int BQ = 256;   // query rows per workgroup
-constexpr int BKV = 64;   // KV positions per LDS stage
 constexpr int NT = 512;   // threads per workgroup (8 waves)
 constexpr float kRescaleThreshold = 8.0f;  // log2 units; see the rescale below
 // A KV block whose probability mass exceeds 1/ratio of the query's running sum

@@ -533,6 +533,9 @@ __device__ __forceinline__ void gemm_dma_tile_256(const uint16_t* __restrict__ A
     }
   };
 
+  // A previous work item of this workgroup (grid-stride callers) may still be
+  // reading the arena in its epilogue.
+  bar();
 #pragma unroll
   for (uint32_t s = 0; s < NS; ++s)
     if (s < nk) issue(s, s);
@@ -645,6 +648,30 @@ gemm_dma_256(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, voi
   gemm_dma_tile_256<DT, DT_OUT, B_TRANS, KB, NS, WAVES, EPI>(
       A + blockIdx.y * sa, B + blockIdx.y * sb, static_cast<char*>(C) + co, M, N, K, tm, tn,
       up ? static_cast<const char*>(up) + co : nullptr);
+}
+
+// Per-element GEMM on one 256x256 tile: each thread forms whole dot products
+// with scalar loads, no LDS and no barriers, so it can stand in for any tile
+// kernel whatever its workgroup size or LDS use.  Correctness fallback only (for
+// operands the vector paths cannot take); f32 accumulation in k order.
+template <int DT, int DT_OUT, bool B_TRANS, int EPI = 0>
+__device__ __forceinline__ void gemm_dot_tile_256(const uint16_t* __restrict__ A,
+                                                  const uint16_t* __restrict__ B,
+                                                  void* __restrict__ C, uint32_t M, uint32_t N,
+                                                  uint32_t K, uint32_t tm, uint32_t tn,
+                                                  const void* __restrict__ up = nullptr) {
+  for (uint32_t e = threadIdx.x; e < gemm::BM * gemm::BN; e += blockDim.x) {
+    const uint32_t row = tm * gemm::BM + e / gemm::BN, col = tn * gemm::BN + e % gemm::BN;
+    if (row >= M || col >= N) continue;
+    float acc = 0.0f;
+    for (uint32_t k = 0; k < K; ++k) {
+      const float a = u16_to_f32<DT>(A[static_cast<size_t>(row) * K + k]);
+      const float b = u16_to_f32<DT>(B_TRANS ? B[static_cast<size_t>(col) * K + k]
+                                             : B[static_cast<size_t>(k) * N + col]);
+      acc = __builtin_fmaf(a, b, acc);
+    }
+    gemm::store_out<EPI, DT_OUT>(C, up, static_cast<size_t>(row) * N + col, acc);
+  }
 }
 
 // Fallback for shapes the MFMA path does not take (K % 8 != 0, row-major B with

@@ -68,6 +68,39 @@ __device__ __forceinline__ void gemm(const uint16_t* A, const uint16_t* B, void*
   }
 }
 
+// Same contract on the LDS-DMA pipeline (8 waves: 512 threads per workgroup)
+// for M, N multiples of 256 and K of 64.  Operands that are not 16-byte aligned
+// (checked at run time; the emitter fixes only the view offsets) take the
+// per-element kernel instead, which fits in the same workgroup.
+template <int DT, int DTO, bool BT, int EPI = gemm::kEpiStore>
+__device__ __forceinline__ void gemm_dma(const uint16_t* A, const uint16_t* B, void* C, uint32_t M,
+                                         uint32_t N, uint32_t K, uint32_t batch,
+                                         const void* up = nullptr) {
+  constexpr int OSZ = (DTO == kF32) ? 4 : 2;
+  const uint32_t tiles_m = M / gemm::BM, tiles_n = N / gemm::BN;
+  const uint32_t per = tiles_m * tiles_n;
+  const size_t sa = static_cast<size_t>(M) * K * 2, sb = static_cast<size_t>(K) * N * 2;
+  const size_t sc = static_cast<size_t>(M) * N * OSZ;
+  const uintptr_t bits = reinterpret_cast<uintptr_t>(A) | reinterpret_cast<uintptr_t>(B) |
+                         reinterpret_cast<uintptr_t>(C) | reinterpret_cast<uintptr_t>(up) | sa |
+                         sb | sc;
+  const bool vec = (bits & 15) == 0;
+  for (uint32_t w = blockIdx.x; w < per * batch; w += gridDim.x) {
+    const uint32_t bi = w / per;
+    uint32_t tm, tn;
+    gemm::tile_coords(w % per, tiles_m, tiles_n, tm, tn);
+    const uint16_t* a = A + static_cast<size_t>(bi) * M * K;
+    const uint16_t* b = B + static_cast<size_t>(bi) * K * N;
+    char* c = static_cast<char*>(C) + bi * sc;
+    const void* u = up ? static_cast<const char*>(up) + bi * sc : nullptr;
+    if (vec)
+      gemm_dma_tile_256<DT, DTO, BT, gemm::DBK, gemm::NSTAGE, gemm::DWAVES, EPI>(a, b, c, M, N, K,
+                                                                                tm, tn, u);
+    else
+      gemm_dot_tile_256<DT, DTO, BT, EPI>(a, b, c, M, N, K, tm, tn, u);
+  }
+}
+
 template <int DT, int DTO, bool BT, int EPI = gemm::kEpiStore>
 __device__ __forceinline__ void gemm_fma(const void* A, const void* B, void* C, uint32_t M,
                                          uint32_t N, uint32_t K, uint32_t batch,

@@ -442,15 +442,28 @@ bool matmul_entry(const Kernel& k, const TileVal& mm, const Store& st, const cha
   const int in = a.dtype, out = st.dtype;
   const bool mfma = in != F32 && K % 8 == 0 && (bt || N % 8 == 0) && a.src.offset % 8 == 0 &&
                     b.src.offset % 8 == 0;
+  // Whole 256x256 tiles and 64-deep K steps: the LDS-DMA pipeline (its entry
+  // checks the run-time 16-byte alignment the offsets cannot show).
+  const int osz = out == F32 ? 4 : 2;
+  const bool dma = mfma && M % 256 == 0 && N % 256 == 0 && K % 64 == 0 &&
+                   (st.dst.offset * osz) % 16 == 0 && (!up || (up->src.offset * osz) % 16 == 0);
   os << "matmul " << M << "x" << K << "x" << N << (bt ? " (B transposed)" : "") << " " << dt_name(in)
      << " -> " << dt_name(out) << (up ? " with silu*mul epilogue" : "")
-     << (mfma ? " -> th::entry::gemm (MFMA)" : " -> th::entry::gemm_fma") << "\n";
-  signature(os, k, 256, {});
+     << (dma ? " -> th::entry::gemm_dma (MFMA, LDS-DMA)"
+             : mfma ? " -> th::entry::gemm (MFMA)" : " -> th::entry::gemm_fma")
+     << "\n";
+  const unsigned threads = dma ? 512 : 256;
+  signature(os, k, threads, {});
   const std::string tmpl = std::string(dt_enum(in)) + ", " + dt_enum(out) + ", " +
                            (bt ? "true" : "false") + ", " + epi;
   const std::string tail = up ? ", th_tiles, " + view_ptr(*up, dt_ctype(out)) + ");\n}\n"
                               : ", th_tiles);\n}\n";
-  if (mfma) {
+  if (dma) {
+    os << "  th::entry::gemm_dma<" << tmpl << ">(" << view_ptr(a, "uint16_t") << ", "
+       << view_ptr(b, "uint16_t") << ", " << store_ptr(st, dt_ctype(out)) << ", " << u(M) << ", "
+       << u(N) << ", " << u(K) << tail;
+    desc(os, k.name, threads, static_cast<unsigned>((M / 256) * (N / 256)), 1);
+  } else if (mfma) {
     os << "  th::entry::gemm<" << tmpl << ">(" << view_ptr(a, "uint16_t") << ", "
        << view_ptr(b, "uint16_t") << ", " << store_ptr(st, dt_ctype(out)) << ", " << u(M) << ", "
        << u(N) << ", " << u(K) << tail;
