@@ -348,6 +348,8 @@ def test_decode_golden_vectors(dev, stream, golden):
     (1, 200, 0, 6, 2, 128, False),   # G=3 -> general kernel
     (1, 4500, 3, 4, 2, 128, False),   # 9 chunks: one batch of 8 partials + 1 in the merge
     (1, 66000, 0, 2, 1, 128, True),   # 129 chunks: the merge stages partials in two passes
+    (16, 4196, 0, 16, 8, 128, False),  # 128 items x 9 chunks: splits of several chunks each
+    (64, 1500, 0, 8, 8, 128, True),   # 512 items: one workgroup per item walks all chunks
 ])
 def test_decode_shapes(dev, stream, dtype, B, L, extra, NH, NKV, Dh, ws):
     rng = np.random.default_rng(L * 3 + NH)

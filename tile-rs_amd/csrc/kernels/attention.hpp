@@ -467,7 +467,9 @@ constexpr int NT = 256;
 // With `ws` non-null the chunk range's partial (m, l, O) goes to
 // ws[((bk*G + q)*n_split + split)*(D+2)]; otherwise O = acc / l is written to
 // `O` directly (the range must then cover the whole sequence).
-template <int DT, int G>
+// KP: phase A reads a wave's K rows in KP passes (fewer passes = more loads in
+// flight per wave, more registers); VU: V rows in flight per wave in phase C.
+template <int DT, int G, int KP = 2, int VU = 8>
 __device__ __forceinline__ void decode_tile(const uint16_t* __restrict__ Q,
                                             const uint16_t* __restrict__ K,
                                             const uint16_t* __restrict__ V,
@@ -513,9 +515,10 @@ __device__ __forceinline__ void decode_tile(const uint16_t* __restrict__ Q,
     // ---- phase A: scores S^T = K . Q^T, 16 rows per MFMA tile ----
     {
       constexpr int TILES = CHUNK / 4 / 16;  // per wave
-      constexpr int TP = TILES / 2;           // tiles whose K rows are in flight together
+      constexpr int TP = TILES / KP;          // tiles whose K rows are in flight together
+      static_assert(TILES % KP == 0, "K passes");
 #pragma unroll
-      for (int half = 0; half < 2; ++half) {
+      for (int half = 0; half < KP; ++half) {
         u32x4 kf[TP][4];
 #pragma unroll
         for (int tt = 0; tt < TP; ++tt) {
@@ -575,7 +578,8 @@ __device__ __forceinline__ void decode_tile(const uint16_t* __restrict__ Q,
         for (int e = 0; e < 8; ++e) acc[q][e] *= a;
       }
       constexpr int ROWS_PER_WAVE = CHUNK / 4;
-      constexpr int UNROLL = 8;
+      constexpr int UNROLL = VU;
+      static_assert((ROWS_PER_WAVE / 4) % UNROLL == 0, "V rows per pass");
 #pragma unroll 1
       for (int it = 0; it < ROWS_PER_WAVE / 4; it += UNROLL) {
         u32x4 vv[UNROLL];
@@ -643,18 +647,22 @@ __device__ __forceinline__ void decode_tile(const uint16_t* __restrict__ Q,
   __syncthreads();  // red and stat_* are reused by the next work item
 }
 
-// Library path: one chunk per workgroup, partials to the workspace.
+// Library path: n_split workgroups per (batch, kv_head), each walking `cps`
+// consecutive chunks (the host picks both so that every split has at least one
+// chunk).  With n_split == 1 a workgroup covers the whole sequence and writes O;
+// otherwise its partial goes to the workspace for attn_decode_combine.
 template <int DT, int G>
 __global__ void __launch_bounds__(dec::NT)
 attn_decode_split(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
-                  const uint16_t* __restrict__ V, float* __restrict__ ws, uint32_t batch,
+                  const uint16_t* __restrict__ V, uint16_t* __restrict__ O, float* __restrict__ ws,
                   uint32_t seq_len, uint32_t max_seq, uint32_t nh, uint32_t nkv, uint32_t n_split,
-                  float scale_log2) {
-  (void)batch;
+                  uint32_t cps, float scale_log2) {
+  const uint32_t nchunks = (seq_len + dec::CHUNK - 1) / dec::CHUNK;
   const uint32_t split = blockIdx.x % n_split;
   const uint32_t bk = blockIdx.x / n_split;
-  decode_tile<DT, G>(Q, K, V, nullptr, ws, seq_len, max_seq, nh, nkv, n_split, scale_log2, bk,
-                     split, split, split + 1);
+  const uint32_t c0 = split * cps, c1 = min(nchunks, c0 + cps);
+  decode_tile<DT, G>(Q, K, V, O, n_split > 1 ? ws : nullptr, seq_len, max_seq, nh, nkv, n_split,
+                     scale_log2, bk, split, c0, c1);
 }
 
 // Merge the per-chunk partials: O = sum_s 2^(m_s - M) O_s / sum_s 2^(m_s - M) l_s.

@@ -5,6 +5,7 @@
 // stream.  There is no CPU fallback: a shape no kernel takes is an error.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <atomic>
 
 #include <cmath>
@@ -415,8 +416,20 @@ int th_attention_prefill(const void* q, const void* k, const void* v, void* o, u
                              head_dim, num_heads, num_kv_heads, 1, scale, dtype, as_stream(s));
 }
 
-static uint32_t decode_splits(uint32_t seq_len) {
+static uint32_t decode_chunks(uint32_t seq_len) {
   return (seq_len + th::dec::CHUNK - 1) / th::dec::CHUNK;
+}
+
+// KV split of the decode: about two workgroups per CU in total (measured on
+// MI355X: config 5's 512 (batch, kv_head) items run fastest unsplit, 332 us
+// against 350 us with one workgroup per chunk; a single item at 32K positions
+// wants 64 splits), then chunks spread evenly so that no split is empty.
+static void decode_plan(uint32_t items, uint32_t nchunks, uint32_t* n_split, uint32_t* cps) {
+  const uint32_t target = 2 * current_cu_count();
+  uint32_t n = (target + items - 1) / items;
+  n = std::max(1u, std::min(n, nchunks));
+  *cps = (nchunks + n - 1) / n;
+  *n_split = (nchunks + *cps - 1) / *cps;
 }
 
 static bool decode_fast(uint32_t head_dim, uint32_t nh, uint32_t nkv, th_dtype dtype) {
@@ -429,33 +442,35 @@ size_t th_attention_decode_workspace_size(uint32_t batch, uint32_t seq_len, uint
                                           uint32_t num_heads, uint32_t num_kv_heads) {
   (void)num_kv_heads;
   if (head_dim != th::dec::D) return 0;
-  return static_cast<size_t>(batch) * num_heads * decode_splits(seq_len) * (th::dec::D + 2) *
+  return static_cast<size_t>(batch) * num_heads * decode_chunks(seq_len) * (th::dec::D + 2) *
          sizeof(float);
 }
 
 }  // extern "C"
 
 template <int DT, int G>
-static void decode_split_launch(const void* q, const void* k, const void* v, float* ws,
+static void decode_split_launch(const void* q, const void* k, const void* v, void* o, float* ws,
                                 uint32_t batch, uint32_t seq_len, uint32_t max_seq, uint32_t nh,
-                                uint32_t nkv, uint32_t n_split, float sl2, hipStream_t s) {
+                                uint32_t nkv, uint32_t n_split, uint32_t cps, float sl2,
+                                hipStream_t s) {
   const dim3 grid(batch * nkv * n_split), block(th::dec::NT);
   hipLaunchKernelGGL((th::attn_decode_split<DT, G>), grid, block, 0, s,
                      static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
-                     static_cast<const uint16_t*>(v), ws, batch, seq_len, max_seq, nh, nkv,
-                     n_split, sl2);
+                     static_cast<const uint16_t*>(v), static_cast<uint16_t*>(o), ws, seq_len,
+                     max_seq, nh, nkv, n_split, cps, sl2);
 }
 
 template <int DT>
-static void decode_launch_g(uint32_t g, const void* q, const void* k, const void* v, float* ws,
-                            uint32_t batch, uint32_t seq_len, uint32_t max_seq, uint32_t nh,
-                            uint32_t nkv, uint32_t n_split, float sl2, hipStream_t s) {
+static void decode_launch_g(uint32_t g, const void* q, const void* k, const void* v, void* o,
+                            float* ws, uint32_t batch, uint32_t seq_len, uint32_t max_seq,
+                            uint32_t nh, uint32_t nkv, uint32_t n_split, uint32_t cps, float sl2,
+                            hipStream_t s) {
   switch (g) {
-    case 1: decode_split_launch<DT, 1>(q, k, v, ws, batch, seq_len, max_seq, nh, nkv, n_split, sl2, s); break;
-    case 2: decode_split_launch<DT, 2>(q, k, v, ws, batch, seq_len, max_seq, nh, nkv, n_split, sl2, s); break;
-    case 4: decode_split_launch<DT, 4>(q, k, v, ws, batch, seq_len, max_seq, nh, nkv, n_split, sl2, s); break;
-    case 8: decode_split_launch<DT, 8>(q, k, v, ws, batch, seq_len, max_seq, nh, nkv, n_split, sl2, s); break;
-    default: decode_split_launch<DT, 16>(q, k, v, ws, batch, seq_len, max_seq, nh, nkv, n_split, sl2, s); break;
+    case 1: decode_split_launch<DT, 1>(q, k, v, o, ws, batch, seq_len, max_seq, nh, nkv, n_split, cps, sl2, s); break;
+    case 2: decode_split_launch<DT, 2>(q, k, v, o, ws, batch, seq_len, max_seq, nh, nkv, n_split, cps, sl2, s); break;
+    case 4: decode_split_launch<DT, 4>(q, k, v, o, ws, batch, seq_len, max_seq, nh, nkv, n_split, cps, sl2, s); break;
+    case 8: decode_split_launch<DT, 8>(q, k, v, o, ws, batch, seq_len, max_seq, nh, nkv, n_split, cps, sl2, s); break;
+    default: decode_split_launch<DT, 16>(q, k, v, o, ws, batch, seq_len, max_seq, nh, nkv, n_split, cps, sl2, s); break;
   }
 }
 
@@ -486,7 +501,14 @@ int th_attention_decode(const void* q, const void* k, const void* v, void* o, ui
     return attn_general_launch(q, k, v, o, batch, 1, 0, max_seq, seq_len, head_dim, num_heads,
                                num_kv_heads, 0, scale, dtype, as_stream(s));
   }
-  const uint32_t n_split = decode_splits(seq_len);
+  const uint64_t items = static_cast<uint64_t>(batch) * num_kv_heads;
+  if (items > 0x7fffffffu) return fail(TH_KERNEL_ERROR, "attention_decode: grid too large");
+  uint32_t n_split, cps;
+  decode_plan(static_cast<uint32_t>(items), decode_chunks(seq_len), &n_split, &cps);
+  const uint64_t blocks = items * n_split;
+  if (blocks > 0x7fffffffu) return fail(TH_KERNEL_ERROR, "attention_decode: grid too large");
+  // The workspace contract does not depend on the split chosen here: callers
+  // size it with th_attention_decode_workspace_size (one record per chunk).
   const size_t need = th_attention_decode_workspace_size(batch, seq_len, head_dim, num_heads,
                                                          num_kv_heads);
   void* ws = workspace;
@@ -495,20 +517,20 @@ int th_attention_decode(const void* q, const void* k, const void* v, void* o, ui
       return fail(TH_MEMORY_ERROR, "attention_decode: workspace of " +
                                        std::to_string(workspace_bytes) + " bytes < required " +
                                        std::to_string(need));
-  } else {
+  } else if (n_split > 1) {
     TH_TRY(th::device_scratch(need, &ws));
   }
-  const uint64_t blocks = static_cast<uint64_t>(batch) * num_kv_heads * n_split;
-  if (blocks > 0x7fffffffu) return fail(TH_KERNEL_ERROR, "attention_decode: grid too large");
   const float sl2 = scale * th::kLog2e;
   const uint32_t g = num_heads / num_kv_heads;
+  float* wsf = static_cast<float*>(ws);
   if (dtype == TH_BF16)
-    decode_launch_g<th::kBF16>(g, q, k, v, static_cast<float*>(ws), batch, seq_len, max_seq,
-                               num_heads, num_kv_heads, n_split, sl2, as_stream(s));
+    decode_launch_g<th::kBF16>(g, q, k, v, o, wsf, batch, seq_len, max_seq, num_heads,
+                               num_kv_heads, n_split, cps, sl2, as_stream(s));
   else
-    decode_launch_g<th::kF16>(g, q, k, v, static_cast<float*>(ws), batch, seq_len, max_seq,
-                              num_heads, num_kv_heads, n_split, sl2, as_stream(s));
+    decode_launch_g<th::kF16>(g, q, k, v, o, wsf, batch, seq_len, max_seq, num_heads,
+                              num_kv_heads, n_split, cps, sl2, as_stream(s));
   TH_TRY(launch_status("attention_decode launch"));
+  if (n_split == 1) return TH_OK;  // each workgroup covered its whole sequence and wrote O
   const dim3 cgrid(batch * num_heads), cblock(th::dec::D);
   if (dtype == TH_BF16)
     hipLaunchKernelGGL(th::attn_decode_combine<th::kBF16>, cgrid, cblock, 0, as_stream(s),

@@ -398,9 +398,13 @@ void desc(std::ostringstream& os, const std::string& name, unsigned threads, uns
      << (tiles_per_wg ? tiles_per_wg : 1) << "u, 0u, {0u, 0u, 0u}};\n\n";
 }
 
+// min_groups > 0 asks for that many resident workgroups per CU (it caps the
+// registers per wave accordingly).
 void signature(std::ostringstream& os, const Kernel& k, unsigned threads,
-               const std::vector<std::string>& extra) {
-  os << "extern \"C\" __global__ void __launch_bounds__(" << threads << ") " << k.name << "(";
+               const std::vector<std::string>& extra, unsigned min_groups = 0) {
+  os << "extern \"C\" __global__ void __launch_bounds__(" << threads;
+  if (min_groups) os << ", " << min_groups;
+  os << ") " << k.name << "(";
   for (size_t i = 0; i < k.gm.size(); ++i) os << (i ? ", " : "") << "void* __restrict__ p" << i;
   for (const std::string& e : extra) os << ", uint32_t " << e;
   os << (k.gm.empty() && extra.empty() ? "" : ", ") << "uint32_t th_tiles) {\n";
@@ -713,7 +717,10 @@ bool emit_kernel(const Kernel& k, std::ostringstream& os, std::string* err) {
     const TileVal& q = k.tiles.at(hot->ins[0]);
     os << "GQA decode " << dt_name(q.dtype) << " (runtime seq_len, max_seq, head_dim, num_heads, "
        << "num_kv_heads) -> th::entry::decode\n";
-    signature(os, k, 256, {"seq_len", "max_seq", "head_dim", "num_heads", "num_kv_heads"});
+    // One workgroup per (batch, kv_head) walks all of its chunks, so two resident
+    // workgroups per CU are needed to keep the K/V stream going (the unconstrained
+    // build takes 264 registers per wave: one workgroup per CU).
+    signature(os, k, 256, {"seq_len", "max_seq", "head_dim", "num_heads", "num_kv_heads"}, 2);
     const char* ct = dt_ctype(q.dtype);
     os << "  th::entry::decode<" << dt_enum(q.dtype) << ">(" << in_ptr(0, ct) << ", " << in_ptr(1, ct)
        << ", " << in_ptr(2, ct) << ", " << out_ptr(ct)
