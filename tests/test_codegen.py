@@ -108,8 +108,8 @@ def test_registry_hip_matches_direct_emit():
 @pytest.mark.parametrize("example,entry", [
     ("softmax_rows", "th::entry::softmax_rows<th::kF32, 4>"),
     ("softmax_generic", "th::entry::softmax_rows<th::kBF16, 4>"),
-    ("matmul_bf16", "th::entry::gemm<th::kBF16, th::kF32, false, th::gemm::kEpiStore>"),
-    ("matmul_f16_t", "th::entry::gemm<th::kF16, th::kF16, true, th::gemm::kEpiStore>"),
+    ("matmul_bf16", "th::entry::gemm_dma<th::kBF16, th::kF32, false, th::gemm::kEpiStore>"),
+    ("matmul_f16_t", "th::entry::gemm_dma<th::kF16, th::kF16, true, th::gemm::kEpiStore>"),
     ("matmul_f32", "th::entry::gemm_fma<th::kF32, th::kF32, false, th::gemm::kEpiStore>"),
     ("attention_f32", "th::entry::attention_tiles<th::kF32, 256>"),
     ("prefill_bf16", "th::entry::prefill<th::kBF16>"),
@@ -123,23 +123,28 @@ def test_hot_ops_lower_to_hand_written_kernels(example, entry):
     assert entry in out.source
 
 
-def test_whole_tile_matmul_takes_the_dma_pipeline_launch_shape():
-    """512x320x768: 256x256 tiles and 64-deep K steps, so the LDS-DMA entry with its
-    512-thread workgroups, 2 x 3 workgroups per logical tile."""
+def test_matmul_launch_shapes_follow_the_entry():
+    """K a multiple of 64: the LDS-DMA entry, 512-thread workgroups, one per started
+    256x256 tile (512x320x768: 2 x 3; 512x256x384: 2 x 2).  Other 16-bit K: the
+    register-staged entry with 256 threads."""
     src = th.emit((EXAMPLES / "matmul_bf16_tiles.mlir").read_text()).source
     assert "__launch_bounds__(512) matmul_bf16_tiles(" in src
     assert "__th_desc_matmul_bf16_tiles = {th::kLaunchDescMagic, 512u, 6u, 1u," in src
-    # N not a multiple of 256: the register-staged entry and its 256-thread groups
     src = th.emit((EXAMPLES / "matmul_bf16.mlir").read_text()).source
+    assert "__launch_bounds__(512) matmul_bf16_acc_f32(" in src
+    assert "__th_desc_matmul_bf16_acc_f32 = {th::kLaunchDescMagic, 512u, 4u, 1u," in src
+    k96 = (EXAMPLES / "matmul_bf16.mlir").read_text().replace("constant(256 : i32)",
+                                                                "constant(96 : i32)")
+    src = th.emit(k96).source
+    assert "th::entry::gemm<th::kBF16, th::kF32, false, th::gemm::kEpiStore>" in src
     assert "__launch_bounds__(256) matmul_bf16_acc_f32(" in src
-    assert "th::entry::gemm_dma" not in src
 
 
 def test_matmul_shape_and_tile_offsets_are_exact():
     out = th.emit((EXAMPLES / "matmul_bf16.mlir").read_text())
-    # M=512 K=256 N=384: th::entry::gemm(..., M, N, K, tiles); 2 x 2 workgroups per tile
+    # M=512 K=256 N=384: th::entry::gemm_dma(..., M, N, K, tiles); 2 x 2 workgroups per tile
     assert "512u, 384u, 256u, th_tiles" in out.source
-    assert "__th_desc_matmul_bf16_acc_f32 = {th::kLaunchDescMagic, 256u, 4u, 1u" in out.source
+    assert "__th_desc_matmul_bf16_acc_f32 = {th::kLaunchDescMagic, 512u, 4u, 1u" in out.source
 
 
 def test_attention_runtime_params_follow_metal_order():

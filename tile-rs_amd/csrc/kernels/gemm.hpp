@@ -300,7 +300,7 @@ gemm_mfma_256(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, vo
 }
 
 // ---------------------------------------------------------------------------
-// Direct-to-LDS pipeline (the path for M, N multiples of 256 and K of 64).
+// Direct-to-LDS pipeline (the path for K a multiple of 64; any M, N).
 //
 // 256x256 tile per workgroup, eight waves (two per SIMD) each owning a 128x64
 // sub-tile of 4x2 v_mfma_f32_32x32x16 accumulators.  K is staged 64 at a time
@@ -380,7 +380,9 @@ __device__ __forceinline__ void gemm_dma_tile_256(const uint16_t* __restrict__ A
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);  // uniform: SGPR LDS addresses
   const int wm = wave / WN_W, wn = wave % WN_W;
   const int l32 = lane & 31, g = lane >> 5;
-  (void)M;
+  // A tile that crosses M or N reads a valid row (column chunk) in place of each
+  // missing one; those values reach only outputs past M or N, which are not stored.
+  const bool edge = m0 + BM > M || n0 + BN > N;
 
   // ---- per-thread DMA sources (NLA A chunks + NLA B chunks per stage) ----
   // Each wave-level load fills 1 KB of LDS (64 slots of 16 B); load j of wave w
@@ -391,13 +393,13 @@ __device__ __forceinline__ void gemm_dma_tile_256(const uint16_t* __restrict__ A
   for (int j = 0; j < NLA; ++j) {
     const int slot = (NLA * wave + j) * 64 + lane;
     const int row = slot / CPR, c = (slot % CPR) ^ swa(row);
-    srcA[j] = A + static_cast<size_t>(m0 + row) * K + 8 * c;
+    srcA[j] = A + static_cast<size_t>(min(m0 + row, M - 1)) * K + 8 * c;
     if constexpr (B_TRANS) {
-      srcB[j] = B + static_cast<size_t>(n0 + row) * K + 8 * c;
+      srcB[j] = B + static_cast<size_t>(min(n0 + row, N - 1)) * K + 8 * c;
     } else {
       // [KB k][256 n] rows of 32 chunks; chunk c of k-row r at c ^ 4*(r & 3)
       const int kr = slot / 32, cb = (slot % 32) ^ (4 * (kr & 3));
-      srcB[j] = B + static_cast<size_t>(kr) * N + n0 + 8 * cb;
+      srcB[j] = B + static_cast<size_t>(kr) * N + min(n0 + 8 * cb, N - 8);
     }
   }
   auto issue = [&](uint32_t stage, uint32_t kt) {
@@ -553,17 +555,22 @@ __device__ __forceinline__ void gemm_dma_tile_256(const uint16_t* __restrict__ A
   // bytes per row and instruction).  For a plain store that is as fast as any
   // rearrangement (measured): the tile's HBM writes bound it.
   if constexpr (EPI != kEpiSiluMul) {
+    auto store_all = [&](auto pred) {
 #pragma unroll
-    for (int mi = 0; mi < 4; ++mi)
+      for (int mi = 0; mi < 4; ++mi)
 #pragma unroll
-      for (int ni = 0; ni < NI; ++ni) {
-        const uint32_t col = n0 + wn * TWN + ni * 32 + l32;
+        for (int ni = 0; ni < NI; ++ni) {
+          const uint32_t col = n0 + wn * TWN + ni * 32 + l32;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const uint32_t row = m0 + wm * 128 + mi * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-          store_out<EPI, DT_OUT>(C, up, static_cast<size_t>(row) * N + col, acc[mi][ni][r]);
+          for (int r = 0; r < 16; ++r) {
+            const uint32_t row = m0 + wm * 128 + mi * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+            if (!decltype(pred)::value || (row < M && col < N))
+              store_out<EPI, DT_OUT>(C, up, static_cast<size_t>(row) * N + col, acc[mi][ni][r]);
+          }
         }
-      }
+    };
+    if (edge) store_all(std::true_type{});
+    else store_all(std::false_type{});
     return;
   }
   // With the SiLU*Mul epilogue the UP operand makes scattered 2-byte reads as
@@ -588,13 +595,17 @@ __device__ __forceinline__ void gemm_dma_tile_256(const uint16_t* __restrict__ A
   for (int h = 0; h < 2; ++h) {
     const uint32_t row0 = m0 + wm * 128 + 64 * h;
     const uint32_t col = n0 + wn * TWN + 8 * cq;
+    // (N % 8 == 0 on this path: eight columns are either all inside or all past N)
     u32x4 upv[8][UPV];
 #pragma unroll
     for (int it = 0; it < 8; ++it)
 #pragma unroll
       for (int u = 0; u < UPV; ++u)
-        upv[it][u] = ldg128(static_cast<const char*>(up) +
-                            ((static_cast<size_t>(row0 + rl + 8 * it) * N + col) * OSZ + 16 * u));
+        upv[it][u] = (!edge || (row0 + rl + 8 * it < M && col < N))
+                         ? ldg128(static_cast<const char*>(up) +
+                                  ((static_cast<size_t>(row0 + rl + 8 * it) * N + col) * OSZ +
+                                   16 * u))
+                         : u32x4{0, 0, 0, 0};
 #pragma unroll
     for (int m2 = 0; m2 < 2; ++m2)
 #pragma unroll
@@ -623,6 +634,7 @@ __device__ __forceinline__ void gemm_dma_tile_256(const uint16_t* __restrict__ A
       }
 #pragma unroll
       for (int e = 0; e < 8; ++e) v[e] = v[e] / (1.0f + expf(-v[e])) * u[e];
+      if (edge && !(row0 + row < M && col < N)) continue;
       char* cp = static_cast<char*>(C) + (static_cast<size_t>(row0 + row) * N + col) * OSZ;
       if constexpr (DT_OUT == kF32) {
         stg128(cp, __builtin_bit_cast(u32x4, f32x4{v[0], v[1], v[2], v[3]}));
@@ -634,7 +646,7 @@ __device__ __forceinline__ void gemm_dma_tile_256(const uint16_t* __restrict__ A
   }
 }
 
-// M, N multiples of 256, K multiple of KB.  Batch index = blockIdx.y.
+// K multiple of KB (any M, N).  Batch index = blockIdx.y.
 template <int DT, int DT_OUT, bool B_TRANS, int KB = gemm::DBK, int NS = gemm::NSTAGE,
           int WAVES = gemm::DWAVES, int EPI = 0>
 __global__ void __launch_bounds__(64 * WAVES, 1)
@@ -642,7 +654,8 @@ gemm_dma_256(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, voi
              uint32_t M, uint32_t N, uint32_t K, uint64_t sa, uint64_t sb, uint64_t sc,
              const void* __restrict__ up) {
   uint32_t tm, tn;
-  gemm::tile_coords(blockIdx.x, M / gemm::BM, N / gemm::BN, tm, tn);
+  gemm::tile_coords(blockIdx.x, (M + gemm::BM - 1) / gemm::BM, (N + gemm::BN - 1) / gemm::BN, tm,
+                    tn);
   constexpr int OSZ = (DT_OUT == kF32) ? 4 : 2;
   const size_t co = static_cast<size_t>(blockIdx.y) * sc * OSZ;
   gemm_dma_tile_256<DT, DT_OUT, B_TRANS, KB, NS, WAVES, EPI>(

@@ -69,7 +69,7 @@ __device__ __forceinline__ void gemm(const uint16_t* A, const uint16_t* B, void*
 }
 
 // Same contract on the LDS-DMA pipeline (8 waves: 512 threads per workgroup)
-// for M, N multiples of 256 and K of 64.  Operands that are not 16-byte aligned
+// for K a multiple of 64 (and N of 8).  Operands that are not 16-byte aligned
 // (checked at run time; the emitter fixes only the view offsets) take the
 // per-element kernel instead, which fits in the same workgroup.
 template <int DT, int DTO, bool BT, int EPI = gemm::kEpiStore>
@@ -77,7 +77,7 @@ __device__ __forceinline__ void gemm_dma(const uint16_t* A, const uint16_t* B, v
                                          uint32_t N, uint32_t K, uint32_t batch,
                                          const void* up = nullptr) {
   constexpr int OSZ = (DTO == kF32) ? 4 : 2;
-  const uint32_t tiles_m = M / gemm::BM, tiles_n = N / gemm::BN;
+  const uint32_t tiles_m = (M + gemm::BM - 1) / gemm::BM, tiles_n = (N + gemm::BN - 1) / gemm::BN;
   const uint32_t per = tiles_m * tiles_n;
   const size_t sa = static_cast<size_t>(M) * K * 2, sb = static_cast<size_t>(K) * N * 2;
   const size_t sc = static_cast<size_t>(M) * N * OSZ;

@@ -165,9 +165,8 @@ void gemm_mfma_go(const GemmArgs& g, dim3 grid) {
   // The DMA kernel's SiLU*Mul epilogue writes C and reads UP in 16-byte pieces.
   constexpr uint64_t OSZ = (DTO == th::kF32) ? 4 : 2;
   const bool out_vec = EPI != th::gemm::kEpiSiluMul ||
-                       (aligned16(g.c) && aligned16(g.up) && (g.sc * OSZ) % 16 == 0);
-  if (gemm_dma() && out_vec && g.m % th::gemm::BM == 0 && g.n % th::gemm::BN == 0 &&
-      g.k % th::gemm::DBK == 0) {
+                       (aligned16(g.c) && aligned16(g.up) && (g.sc * OSZ) % 16 == 0 && g.n % 8 == 0);
+  if (gemm_dma() && out_vec && g.k % th::gemm::DBK == 0) {
     hipLaunchKernelGGL((th::gemm_dma_256<DT, DTO, BT, th::gemm::DBK, th::gemm::NSTAGE,
                                          th::gemm::DWAVES, EPI>),
                        grid, dim3(64 * th::gemm::DWAVES), 0, g.s, A, B, g.c, g.m, g.n, g.k, g.sa,

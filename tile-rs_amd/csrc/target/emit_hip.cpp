@@ -446,11 +446,11 @@ bool matmul_entry(const Kernel& k, const TileVal& mm, const Store& st, const cha
   const int in = a.dtype, out = st.dtype;
   const bool mfma = in != F32 && K % 8 == 0 && (bt || N % 8 == 0) && a.src.offset % 8 == 0 &&
                     b.src.offset % 8 == 0;
-  // Whole 256x256 tiles and 64-deep K steps: the LDS-DMA pipeline (its entry
-  // checks the run-time 16-byte alignment the offsets cannot show).
+  // 64-deep K steps (and N % 8 for the 16-byte epilogue): the LDS-DMA pipeline
+  // (its entry checks the run-time 16-byte alignment the offsets cannot show).
   const int osz = out == F32 ? 4 : 2;
-  const bool dma = mfma && M % 256 == 0 && N % 256 == 0 && K % 64 == 0 &&
-                   (st.dst.offset * osz) % 16 == 0 && (!up || (up->src.offset * osz) % 16 == 0);
+  const bool dma = mfma && K % 64 == 0 && N % 8 == 0 && (st.dst.offset * osz) % 16 == 0 &&
+                   (!up || (up->src.offset * osz) % 16 == 0);
   os << "matmul " << M << "x" << K << "x" << N << (bt ? " (B transposed)" : "") << " " << dt_name(in)
      << " -> " << dt_name(out) << (up ? " with silu*mul epilogue" : "")
      << (dma ? " -> th::entry::gemm_dma (MFMA, LDS-DMA)"
@@ -466,7 +466,7 @@ bool matmul_entry(const Kernel& k, const TileVal& mm, const Store& st, const cha
     os << "  th::entry::gemm_dma<" << tmpl << ">(" << view_ptr(a, "uint16_t") << ", "
        << view_ptr(b, "uint16_t") << ", " << store_ptr(st, dt_ctype(out)) << ", " << u(M) << ", "
        << u(N) << ", " << u(K) << tail;
-    desc(os, k.name, threads, static_cast<unsigned>((M / 256) * (N / 256)), 1);
+    desc(os, k.name, threads, static_cast<unsigned>(((M + 255) / 256) * ((N + 255) / 256)), 1);
   } else if (mfma) {
     os << "  th::entry::gemm<" << tmpl << ">(" << view_ptr(a, "uint16_t") << ", "
        << view_ptr(b, "uint16_t") << ", " << store_ptr(st, dt_ctype(out)) << ", " << u(M) << ", "
