@@ -148,8 +148,9 @@ struct GemmArgs {
   hipStream_t s;
 };
 
-// The LDS-DMA pipeline serves tile-multiple shapes unless TILERS_HIP_GEMM_DMA=0
-// (then the register-staged kernel runs them too).
+// The LDS-DMA pipeline serves every shape with K % 64 == 0 unless
+// TILERS_HIP_GEMM_DMA=0 (a debugging switch: the register-staged kernel then
+// runs them too).
 bool gemm_dma() {
   static const bool v = [] {
     const char* e = std::getenv("TILERS_HIP_GEMM_DMA");
