@@ -66,7 +66,8 @@ int softmax_launch(const void* x, void* y, uint32_t rows, uint32_t cols, hipStre
     // on MI355X this sustains the copy-kernel bandwidth, while one short-lived
     // wave per row does not.
     const uint32_t need = (rows + 3) / 4;
-    const dim3 grid(std::min<uint32_t>(need, 4u * current_cu_count())), block(256);
+    // two workgroups per CU: each wave streams several rows, next row in flight
+    const dim3 grid(std::min<uint32_t>(need, 2u * current_cu_count())), block(256);
     if (nvec <= 64)
       hipLaunchKernelGGL((th::softmax_rows_stream<DT, 1>), grid, block, 0, s, x, y, rows, cols);
     else if (nvec <= 128)
