@@ -447,13 +447,15 @@ attn_prefill_dma128(const uint16_t* __restrict__ Q, const uint16_t* __restrict__
 
 // ============================================================================
 // Decode: one query token per head, GQA group G = NH/NKV query heads share each
-// K/V load.  Grid = B * NKV * n_split workgroups of 256 threads; each handles a
-// chunk of up to 512 KV positions of one (batch, kv_head):
+// K/V load.  Grid = B * NKV * n_split workgroups of 256 threads; each walks a
+// run of consecutive 512-position chunks of one (batch, kv_head), per chunk:
 //   A  scores S^T (16 kv x 16 q, G real columns) with v_mfma_f32_16x16x32, K
 //      fragments read straight from HBM (each lane 4 x 16 B of one K row),
-//   B  per-query max / exp / sum over the chunk (in LDS),
+//   B  per-query max / exp / sum over the chunk (in LDS), merged into the
+//      running (m, l) of the workgroup's run,
 //   C  P.V on the vector ALUs in f32: each lane owns 8 d-values of every 4th row.
-// Partial (m, l, O) per chunk go to a workspace; decode_combine merges them.
+// With one split the workgroup writes O itself; otherwise each run's partial
+// (m, l, O) goes to a workspace and attn_decode_combine merges them.
 // K and V are read exactly once, with nontemporal loads (measured on MI355X:
 // ~8% more sustained bandwidth than cached loads for this stream).
 // ============================================================================
