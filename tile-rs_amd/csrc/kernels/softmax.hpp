@@ -82,11 +82,11 @@ softmax_rows_reg(const void* __restrict__ x, void* __restrict__ y, uint32_t rows
 // Streaming form of the register path: a fixed grid of waves walks the rows
 // (row stride = total waves), and the loads of a wave's next row are issued
 // before the reductions of its current row, so every wave keeps one row of
-// loads in flight.
+// loads in flight.  Called by every thread of the workgroup (any grid size).
 template <int DT, int NV>
-__global__ void __launch_bounds__(256)
-softmax_rows_stream(const void* __restrict__ x, void* __restrict__ y, uint32_t rows,
-                    uint32_t cols) {
+__device__ __forceinline__ void softmax_rows_stream_body(const void* __restrict__ x,
+                                                         void* __restrict__ y, uint32_t rows,
+                                                         uint32_t cols) {
   constexpr int ESZ = (DT == kF32) ? 4 : 2;
   constexpr int E = Vec16<DT>::kElems;
   const int lane = threadIdx.x & 63;
@@ -147,6 +147,13 @@ softmax_rows_stream(const void* __restrict__ x, void* __restrict__ y, uint32_t r
 #pragma unroll
     for (int i = 0; i < NV; ++i) cur[i] = nxt[i];
   }
+}
+
+template <int DT, int NV>
+__global__ void __launch_bounds__(256)
+softmax_rows_stream(const void* __restrict__ x, void* __restrict__ y, uint32_t rows,
+                    uint32_t cols) {
+  softmax_rows_stream_body<DT, NV>(x, y, rows, cols);
 }
 
 // Any cols, one wavefront per row, three passes over the row (no LDS).

@@ -19,9 +19,15 @@
 namespace th {
 namespace entry {
 
-// ---- row softmax over `rows` contiguous rows of `cols` (one wavefront per row) ----
+// ---- row softmax over `rows` contiguous rows of `cols` (one wavefront per row;
+//      rows of up to 256 16-byte vectors take the streaming loop of the library
+//      kernel: each wave walks several rows with its next row's loads in flight) ----
 template <int DT, int NV>
 __device__ __forceinline__ void softmax_rows(const void* x, void* y, uint32_t rows, uint32_t cols) {
+  if constexpr (NV > 0 && NV <= 4) {
+    softmax_rows_stream_body<DT, NV>(x, y, rows, cols);
+    return;
+  }
   constexpr int ESZ = (DT == kF32) ? 4 : 2;
   const uint32_t wpg = blockDim.x >> 6;
   const int lane = threadIdx.x & 63;

@@ -658,8 +658,11 @@ bool emit_kernel(const Kernel& k, std::ostringstream& os, std::string* err) {
     signature(os, k, 256, {});
     os << "  th::entry::softmax_rows<" << dt_enum(x.dtype) << ", " << nv << ">(" << in_ptr(0, dt_ctype(x.dtype))
        << ", " << out_ptr(dt_ctype(x.dtype)) << ", th_tiles * " << u(R) << ", " << u(C) << ");\n}\n";
-    const unsigned tpw = R >= 4 ? 1 : static_cast<unsigned>(4 / R);
-    const unsigned wpt = R >= 4 ? static_cast<unsigned>((R + 3) / 4) : 1;
+    // Rows per workgroup: 16 for the streaming loop (nv <= 4: each of the 4 waves
+    // walks about 4 rows, next row in flight), 4 (one per wave) otherwise.
+    const long long per_wg = (nv > 0 && nv <= 4) ? 16 : 4;
+    const unsigned tpw = R >= per_wg ? 1 : static_cast<unsigned>(per_wg / R);
+    const unsigned wpt = R >= per_wg ? static_cast<unsigned>((R + per_wg - 1) / per_wg) : 1;
     desc(os, k.name, 256, wpt, tpw);
     return true;
   }
