@@ -114,7 +114,7 @@ def test_registry_hip_matches_direct_emit():
     ("attention_f32", "th::entry::attention_tiles<th::kF32, 256>"),
     ("prefill_bf16", "th::entry::prefill<th::kBF16>"),
     ("decode_bf16", "th::entry::decode<th::kBF16>"),
-    ("rms_norm_rows", "th::entry::rms_norm_rows<th::kF32>"),
+    ("rms_norm_rows", "th::entry::rms_norm_rows<th::kF32, 4>"),
     ("swiglu_gate_bf16", "th::entry::gemm_dma<th::kBF16, th::kF32, false, th::gemm::kEpiSiluMul>"),
     ("matmul_bf16_tiles", "th::entry::gemm_dma<th::kBF16, th::kBF16, false, th::gemm::kEpiStore>"),
 ])

@@ -17,10 +17,11 @@
 
 namespace th {
 
+// Called by every thread of the workgroup (any grid size).
 template <int DT, int NV>
-__global__ void __launch_bounds__(256)
-rms_norm_rows_stream(const void* __restrict__ x, void* __restrict__ y, uint32_t rows,
-                     uint32_t cols, float eps) {
+__device__ __forceinline__ void rms_norm_rows_stream_body(const void* __restrict__ x,
+                                                          void* __restrict__ y, uint32_t rows,
+                                                          uint32_t cols, float eps) {
   constexpr int ESZ = (DT == kF32) ? 4 : 2;
   constexpr int E = Vec16<DT>::kElems;
   const int lane = threadIdx.x & 63;
@@ -69,6 +70,13 @@ rms_norm_rows_stream(const void* __restrict__ x, void* __restrict__ y, uint32_t 
 #pragma unroll
     for (int i = 0; i < NV; ++i) cur[i] = nxt[i];
   }
+}
+
+template <int DT, int NV>
+__global__ void __launch_bounds__(256)
+rms_norm_rows_stream(const void* __restrict__ x, void* __restrict__ y, uint32_t rows,
+                     uint32_t cols, float eps) {
+  rms_norm_rows_stream_body<DT, NV>(x, y, rows, cols, eps);
 }
 
 // Any cols / alignment: one wavefront per row, two passes over the row.

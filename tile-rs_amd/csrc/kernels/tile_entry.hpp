@@ -40,10 +40,16 @@ __device__ __forceinline__ void softmax_rows(const void* x, void* y, uint32_t ro
   }
 }
 
-// ---- row RMSNorm over `rows` contiguous rows of `cols` (one wavefront per row) ----
-template <int DT>
+// ---- row RMSNorm over `rows` contiguous rows of `cols`: the library's streaming
+//      loop when a row fits NV 16-byte vectors per lane (NV > 0), else one
+//      wavefront per row in two passes ----
+template <int DT, int NV = 0>
 __device__ __forceinline__ void rms_norm_rows(const void* x, void* y, uint32_t rows, uint32_t cols,
                                               float eps) {
+  if constexpr (NV > 0) {
+    rms_norm_rows_stream_body<DT, NV>(x, y, rows, cols, eps);
+    return;
+  }
   constexpr int ESZ = (DT == kF32) ? 4 : 2;
   const uint32_t wpg = blockDim.x >> 6;
   for (uint32_t r = blockIdx.x * wpg + (threadIdx.x >> 6); r < rows; r += gridDim.x * wpg) {
