@@ -723,7 +723,10 @@ bool emit_kernel(const Kernel& k, std::ostringstream& os, std::string* err) {
     os << "  th::entry::prefill<" << dt_enum(q.dtype) << ">(" << in_ptr(0, ct) << ", " << in_ptr(1, ct)
        << ", " << in_ptr(2, ct) << ", " << out_ptr(ct)
        << ", th_tiles, seq_len, start_pos, max_seq, head_dim, num_heads, num_kv_heads);\n}\n";
-    desc(os, k.name, 512, 256, 1);
+    // One workgroup per (head, 256-query block) up to 1024 per tile (e.g. 32 heads x
+    // 8192 queries), so the hardware balances the causal work; workgroups past the
+    // work exit at once (they are dispatched last).
+    desc(os, k.name, 512, 1024, 1);
     return true;
   }
   if (o == "attention_decode_f32") {
