@@ -471,7 +471,7 @@ constexpr int NT = 256;
 // `O` directly (the range must then cover the whole sequence).
 // KP: phase A reads a wave's K rows in KP passes (fewer passes = more loads in
 // flight per wave, more registers); VU: V rows in flight per wave in phase C.
-template <int DT, int G, int KP = 2, int VU = 8>
+template <int DT, int G, int KP = 4, int VU = 8>
 __device__ __forceinline__ void decode_tile(const uint16_t* __restrict__ Q,
                                             const uint16_t* __restrict__ K,
                                             const uint16_t* __restrict__ V,
