@@ -124,7 +124,7 @@ def test_hot_ops_lower_to_hand_written_kernels(example, entry):
 
 
 def test_matmul_launch_shapes_follow_the_entry():
-    """K a multiple of 64: the LDS-DMA entry, 512-thread workgroups, one per started
+    """K a multiple of 32: the LDS-DMA entry, 512-thread workgroups, one per started
     256x256 tile (512x320x768: 2 x 3; 512x256x384: 2 x 2).  Other 16-bit K: the
     register-staged entry with 256 threads."""
     src = th.emit((EXAMPLES / "matmul_bf16_tiles.mlir").read_text()).source
@@ -136,6 +136,10 @@ def test_matmul_launch_shapes_follow_the_entry():
     k96 = (EXAMPLES / "matmul_bf16.mlir").read_text().replace("constant(256 : i32)",
                                                                 "constant(96 : i32)")
     src = th.emit(k96).source
+    assert "__launch_bounds__(512) matmul_bf16_acc_f32(" in src
+    k72 = (EXAMPLES / "matmul_bf16.mlir").read_text().replace("constant(256 : i32)",
+                                                                "constant(72 : i32)")
+    src = th.emit(k72).source
     assert "th::entry::gemm<th::kBF16, th::kF32, false, th::gemm::kEpiStore>" in src
     assert "__launch_bounds__(256) matmul_bf16_acc_f32(" in src
 

@@ -154,7 +154,7 @@ def test_matmul_golden_vectors(dev, stream, golden):
 @pytest.mark.parametrize("trans", [False, True])
 @pytest.mark.parametrize("m,k,n", [(256, 256, 256), (300, 72, 136), (1, 8, 8), (513, 1024, 264),
                                    (64, 33, 40), (512, 96, 768), (768, 1024, 512), (1, 64, 8),
-                                   (40, 64, 36)])
+                                   (40, 64, 36), (40, 32, 36), (300, 160, 264)])
 def test_matmul_integer_bit_exact(dev, stream, in_dt, trans, m, k, n):
     """Integer-valued inputs make every partial sum exact: any layout/index slip shows."""
     rng = np.random.default_rng(m + 7 * k + 13 * n)
@@ -469,7 +469,8 @@ def test_matmul_silu_mul_golden_vectors(dev, stream, golden):
 @pytest.mark.parametrize("m,k,n,in_dt,out_dt,trans", [
     (512, 512, 768, D.BF16, D.F32, False),    # LDS-DMA pipeline
     (256, 1024, 512, D.F16, D.F16, True),     # LDS-DMA pipeline, B stored N x K
-    (512, 96, 256, D.BF16, D.BF16, False),    # register-staged MFMA (K % 64 != 0)
+    (512, 96, 256, D.BF16, D.BF16, False),    # LDS-DMA pipeline, 3 stages of K
+    (512, 80, 256, D.BF16, D.BF16, False),    # register-staged MFMA (K % 32 != 0)
     (300, 72, 136, D.F16, D.F32, False),      # ragged MFMA tiles
     (300, 128, 136, D.F16, D.F16, False),     # LDS-DMA pipeline, tiles cut by M and N
     (200, 256, 328, D.BF16, D.F32, True),     # same, B stored N x K

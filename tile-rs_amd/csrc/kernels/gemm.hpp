@@ -300,19 +300,21 @@ gemm_mfma_256(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, vo
 }
 
 // ---------------------------------------------------------------------------
-// Direct-to-LDS pipeline (the path for K a multiple of 64; any M, N).
+// Direct-to-LDS pipeline (the path for K a multiple of 32; any M, N).
 //
 // 256x256 tile per workgroup, eight waves (two per SIMD) each owning a 128x64
-// sub-tile of 4x2 v_mfma_f32_32x32x16 accumulators.  K is staged 64 at a time
-// through two LDS buffers (2 x 64 KB) filled by global_load_lds_dwordx4: each
-// lane's 16 bytes go straight from L2/HBM into LDS (no registers, no
-// ds_write).  A stage is complete for a thread when its vmcnt has dropped to
-// the loads issued after it; one barrier per stage then publishes every
-// thread's part, and right after that barrier the freed buffer is refilled
-// with the stage two ahead.
-//   A stage: [256 m][64 k], 128-byte rows; 16-byte chunk c of row r sits at
-//            c ^ ((r ^ (r >> 3)) & 7) -> conflict-free 128-bit MFMA reads
-//            (with 32-k stages: 64-byte rows, c ^ ((r >> 2) & 3)).
+// sub-tile of 4x2 v_mfma_f32_32x32x16 accumulators.  K is staged 32 at a time
+// through a ring of four LDS buffers (4 x 32 KB) filled by
+// global_load_lds_dwordx4: each lane's 16 bytes go straight from L2/HBM into
+// LDS (no registers, no ds_write).  A stage is complete for a thread when its
+// vmcnt has dropped to the loads issued after it; one barrier per stage then
+// publishes every thread's part, and right after that barrier the freed buffer
+// is refilled with the stage four ahead, so three stages stay in flight under
+// the MFMAs (measured against two 64-k buffers: 2% faster at 4096^3, 6% for
+// 8192x4096x14336, bit-identical output).
+//   A stage: [256 m][32 k], 64-byte rows; 16-byte chunk c of row r sits at
+//            c ^ ((r >> 2) & 3) -> conflict-free 128-bit MFMA reads
+//            (with 64-k stages: 128-byte rows, c ^ ((r ^ (r >> 3)) & 7)).
 //   B stage: row-major B needs no transpose anywhere: it stays [64 k][256 n]
 //            (512-byte rows, chunk c at c ^ 4*(k & 3), so the four k rows one
 //            half-wave reads land in four different 64-byte bank groups of the
@@ -331,8 +333,8 @@ using lds::dma_lds_arena;
 using lds::lds_v4i16;
 using lds::v4i16;
 using lds::wait_vm;
-constexpr int DBK = 64;       // K per stage (default shape)
-constexpr int NSTAGE = 2;     // stages (default shape)
+constexpr int DBK = 32;       // K per stage (default shape)
+constexpr int NSTAGE = 4;     // stages (default shape)
 constexpr int DWAVES = 8;     // 2 x 4 waves of 128 x 64 (2 waves per SIMD)
 // Wait until at most `later` stages of NL loads each are still in flight.
 template <int NL, int MAXL>

@@ -81,7 +81,7 @@ __device__ __forceinline__ void gemm(const uint16_t* A, const uint16_t* B, void*
 }
 
 // Same contract on the LDS-DMA pipeline (8 waves: 512 threads per workgroup)
-// for K a multiple of 64 (and N of 8).  Operands that are not 16-byte aligned
+// for K a multiple of 32 (and N of 8).  Operands that are not 16-byte aligned
 // (checked at run time; the emitter fixes only the view offsets) take the
 // per-element kernel instead, which fits in the same workgroup.
 template <int DT, int DTO, bool BT, int EPI = gemm::kEpiStore>

@@ -149,7 +149,7 @@ struct GemmArgs {
   hipStream_t s;
 };
 
-// The LDS-DMA pipeline serves every shape with K % 64 == 0 unless
+// The LDS-DMA pipeline serves every shape with K % 32 == 0 unless
 // TILERS_HIP_GEMM_DMA=0 (a debugging switch: the register-staged kernel then
 // runs them too).
 bool gemm_dma() {

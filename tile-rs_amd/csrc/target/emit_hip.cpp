@@ -446,10 +446,10 @@ bool matmul_entry(const Kernel& k, const TileVal& mm, const Store& st, const cha
   const int in = a.dtype, out = st.dtype;
   const bool mfma = in != F32 && K % 8 == 0 && (bt || N % 8 == 0) && a.src.offset % 8 == 0 &&
                     b.src.offset % 8 == 0;
-  // 64-deep K steps (and N % 8 for the 16-byte epilogue): the LDS-DMA pipeline
+  // 32-deep K steps (and N % 8 for the 16-byte epilogue): the LDS-DMA pipeline
   // (its entry checks the run-time 16-byte alignment the offsets cannot show).
   const int osz = out == F32 ? 4 : 2;
-  const bool dma = mfma && K % 64 == 0 && N % 8 == 0 && (st.dst.offset * osz) % 16 == 0 &&
+  const bool dma = mfma && K % 32 == 0 && N % 8 == 0 && (st.dst.offset * osz) % 16 == 0 &&
                    (!up || (up->src.offset * osz) % 16 == 0);
   os << "matmul " << M << "x" << K << "x" << N << (bt ? " (B transposed)" : "") << " " << dt_name(in)
      << " -> " << dt_name(out) << (up ? " with silu*mul epilogue" : "")
