@@ -43,8 +43,10 @@ __device__ __forceinline__ void store_out(void* __restrict__ C, const void* __re
                                      : u16_to_f32<DT_OUT>(static_cast<const uint16_t*>(up)[off]);
     v = v / (1.0f + expf(-v)) * u;
   }
-  if constexpr (DT_OUT == kF32) static_cast<float*>(C)[off] = v;
-  else static_cast<uint16_t*>(C)[off] = f32_to_u16<DT_OUT>(v);
+  // Nontemporal: C is not read again by this kernel (measured 1-4% faster than
+  // ordinary stores for 4096^3 and 8192x4096x14336).
+  if constexpr (DT_OUT == kF32) __builtin_nontemporal_store(v, static_cast<float*>(C) + off);
+  else __builtin_nontemporal_store(f32_to_u16<DT_OUT>(v), static_cast<uint16_t*>(C) + off);
 }
 
 constexpr int BM = 256, BN = 256, BK = 64;
@@ -639,10 +641,10 @@ __device__ __forceinline__ void gemm_dma_tile_256(const uint16_t* __restrict__ A
       if (edge && !(row0 + row < M && col < N)) continue;
       char* cp = static_cast<char*>(C) + (static_cast<size_t>(row0 + row) * N + col) * OSZ;
       if constexpr (DT_OUT == kF32) {
-        stg128(cp, __builtin_bit_cast(u32x4, f32x4{v[0], v[1], v[2], v[3]}));
-        stg128(cp + 16, __builtin_bit_cast(u32x4, f32x4{v[4], v[5], v[6], v[7]}));
+        stg128_nt(cp, __builtin_bit_cast(u32x4, f32x4{v[0], v[1], v[2], v[3]}));
+        stg128_nt(cp + 16, __builtin_bit_cast(u32x4, f32x4{v[4], v[5], v[6], v[7]}));
       } else {
-        stg128(cp, pack16<DT_OUT>(v));
+        stg128_nt(cp, pack16<DT_OUT>(v));
       }
     }
   }
