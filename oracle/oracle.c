@@ -32,6 +32,11 @@
  *   silu_mul, matmul_silu_mul — golden vectors from torch CPU (F.silu);
  *                            silu(0) = 0, silu(x) - silu(-x) = x, silu(x) -> x
  *                            for large x; the matmul part as matmul.
+ *   rope                  — pos = 0 is the identity; each pair keeps its
+ *                            norm; unit pairs (1,0) and (0,1) land on
+ *                            (cos t, sin t) and (-sin t, cos t) with t from a
+ *                            float64 closed form; rope(rope(x, a), b) =
+ *                            rope(x, a + b).
  * Nothing here is "parity unpinned".
  */
 #include <math.h>
@@ -202,6 +207,27 @@ ORC_EXPORT void orc_rms_norm(const void* x, void* y, int64_t rows, int64_t cols,
             store_elem(y, r * cols + j, dtype,
                        (float)((double)load_elem(x, r * cols + j, dtype) * rs));
     }
+}
+
+/* RoPE (__tile_rope_f32(dst, src, pos, rows, cols), tile.rs:232, :2425; gpu  */
+/* lowering mlir_to_gpu.rs:1508-1557, SPIR-V body mlir_to_spirv.rs:1418-1432): */
+/* each row's interleaved pairs (x[2i], x[2i+1]) rotate by the angle           */
+/* pos * freq_i, freq_i = 1 / 10000^(2i / cols).  Both lowerings form freq and */
+/* the angle in f32, so this does too; the rotation is evaluated in double and */
+/* narrowed once.                                                              */
+ORC_EXPORT void orc_rope(const void* x, void* y, int64_t rows, int64_t cols, int64_t pos,
+                         int dtype) {
+    #pragma omp parallel for schedule(static) if (rows * cols > (1 << 15))
+    for (int64_t r = 0; r < rows; ++r)
+        for (int64_t i = 0; i < cols / 2; ++i) {
+            const float freq = 1.0f / powf(10000.0f, 2.0f * (float)i / (float)cols);
+            const float ang = (float)pos * freq;
+            const double c = cos((double)ang), s = sin((double)ang);
+            const double e = (double)load_elem(x, r * cols + 2 * i, dtype);
+            const double o = (double)load_elem(x, r * cols + 2 * i + 1, dtype);
+            store_elem(y, r * cols + 2 * i, dtype, (float)(e * c - o * s));
+            store_elem(y, r * cols + 2 * i + 1, dtype, (float)(e * s + o * c));
+        }
 }
 
 /* SiLU * Mul (linalg mlir_to_linalg.rs:774-782: silu(x) = x / (1 + exp(-x)),  */

@@ -50,6 +50,7 @@ def lib():
         L.orc_causal_mask_f32.argtypes = [vp, vp, i64, i64]
         L.orc_rms_norm.argtypes = [vp, vp, i64, i64, C.c_double, i]
         L.orc_silu_mul.argtypes = [vp, vp, vp, i64, i]
+        L.orc_rope.argtypes = [vp, vp, i64, i64, i64, i]
         L.orc_matmul_silu_mul_rows.argtypes = [vp, vp, vp, vp, i64, i64, i64, i, i, i, i64, i64]
         L.orc_attention_f32.argtypes = [vp, vp, vp, vp, i64, i64]
         L.orc_attention_prefill.argtypes = [vp, vp, vp, vp, i, i] + [i64] * 11
@@ -119,6 +120,15 @@ def rms_norm(x: np.ndarray, rows: int, cols: int, eps: float, dtype: int = F32) 
     x = np.ascontiguousarray(x)
     y = np.empty_like(x)
     lib().orc_rms_norm(_ptr(x), _ptr(y), rows, cols, float(eps), dtype)
+    return y
+
+
+def rope(x: np.ndarray, rows: int, cols: int, pos: int, dtype: int = F32) -> np.ndarray:
+    """Rotary embedding of interleaved pairs at position pos (mlir_to_gpu.rs:1508-1557)."""
+    x = np.ascontiguousarray(x)
+    assert cols % 2 == 0
+    y = np.empty_like(x)
+    lib().orc_rope(_ptr(x), _ptr(y), rows, cols, pos, dtype)
     return y
 
 

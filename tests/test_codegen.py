@@ -169,6 +169,60 @@ def test_elementwise_fallback():
     assert "fminf(fmaxf(" in out.source                  # clamp
 
 
+def test_rope_lowers_to_pair_rotation():
+    out = th.emit((EXAMPLES / "rope.mlir").read_text())
+    assert out.meta.kernel_names == ["rope_f32", "rope_bf16"]
+    src = out.source
+    # freq = 1 / 10000^(2j / cols) in f32, angle = pos * freq (mlir_to_gpu.rs:1536-1545)
+    assert "1.0f / powf(10000.0f, 2.0f * static_cast<float>(col >> 1) / 0x1p+6f)" in src
+    assert "0x1.cp+2f * r" in src                       # pos 7, exact
+    assert "0x1.f4p+9f * r" in src                      # pos 1000, exact
+    assert "static_cast<int64_t>(i ^ 1ull)" in src       # the pair partner
+    assert "th::u16_to_f32<th::kBF16>" in src            # bf16 side channel from the name
+
+
+def test_rope_needs_even_cols_and_a_loaded_input():
+    rope = ("    %p = llvm.mlir.constant(3 : i32) : i32\n"
+            "    %y = llvm.call @__tile_rope_f32(%t0, %t0, %p, %r, %c) : (i32, i32, i32, i32, i32) -> i32")
+    with pytest.raises(th.HalError) as e:
+        th.emit(mlir_one(rope, cols=63))
+    assert "cols must be even" in str(e.value)
+    chained = ("    %e = llvm.call @__tile_exp_f32(%t0, %t0, %r, %c) : (i32, i32, i32, i32) -> i32\n"
+               "    %p = llvm.mlir.constant(3 : i32) : i32\n"
+               "    %y = llvm.call @__tile_rope_f32(%e, %e, %p, %r, %c) : (i32, i32, i32, i32, i32) -> i32")
+    with pytest.raises(th.HalError) as e:
+        th.emit(mlir_one(chained))
+    assert "rope input must come straight from a load" in str(e.value)
+
+
+# The core tile-op set every open backend lowers (tile_spec/features/
+# core_op_lowering.feature:8-41), as rows for the hip target.
+@pytest.mark.parametrize("op,evidence", [
+    ("rms_norm", "th::entry::rms_norm_rows"),
+    ("matmul", "th::entry::gemm"),
+    ("softmax", "th::entry::softmax_rows"),
+    ("rope", "cosf("),
+    ("add", " + "),
+])
+def test_core_op_lowers_to_hip(op, evidence):
+    lines = {
+        "rms_norm": ("    %e = llvm.mlir.constant(0 : i32) : i32\n"
+                     "    %y = llvm.call @__tile_rms_norm_f32(%e, %t0, %e, %r, %c) : (i32, i32, i32, i32, i32) -> i32", 1),
+        "softmax": ("    %y = llvm.call @__tile_softmax_f32(%t0, %t0, %r, %c) : (i32, i32, i32, i32) -> i32", 1),
+        "rope": ("    %p = llvm.mlir.constant(7 : i32) : i32\n"
+                 "    %y = llvm.call @__tile_rope_f32(%t0, %t0, %p, %r, %c) : (i32, i32, i32, i32, i32) -> i32", 1),
+        "add": ("    %y = llvm.call @__tile_add_f32(%t0, %t0, %t1, %r, %c) : (i32, i32, i32, i32, i32) -> i32", 2),
+    }
+    if op == "matmul":
+        text = (EXAMPLES / "matmul_f16_t.mlir").read_text()
+    else:
+        line, loads = lines[op]
+        text = mlir_one(line, loads=loads, rows=4, cols=256, name=f"{op}_k")
+    out = th.emit(text)
+    assert evidence in out.source
+    assert th.emit(text).source == out.source  # pure: byte-identical on re-emit
+
+
 def test_bf16_side_channel_from_names():
     body = "    %y = llvm.call @__tile_softmax_f16(%t0, %t0, %r, %c) : (i32, i32, i32, i32) -> i32"
     f16 = th.emit(mlir_one(body, load="__tile_load_f16", store="__tile_store_f16", name="sm"))

@@ -15,7 +15,7 @@ import pytest
 import tilers_hip as th
 from oracle import oracle as orc
 from tests.tolerances import (assert_attn_close, assert_gemm_close, assert_softmax_close,
-                              assert_within_ulp16)
+                              assert_within_ulp16, ulp16)
 from tilers_hip import _build
 
 pytestmark = pytest.mark.gpu
@@ -27,7 +27,7 @@ def launcher(dev):
     lau = dev.create_launcher()
     for stem in ("softmax_rows", "softmax_generic", "matmul_bf16", "matmul_f16_t", "matmul_f32",
                  "attention_f32", "prefill_bf16", "decode_bf16", "swiglu_mask", "rms_norm_rows",
-                 "swiglu_gate_bf16", "matmul_bf16_tiles"):
+                 "swiglu_gate_bf16", "matmul_bf16_tiles", "rope"):
         lau.load(_build.example_path(stem), th.KernelMode.GENERAL)
     return lau
 
@@ -49,6 +49,37 @@ def test_softmax_rows_f32(dev, stream, launcher):
     xb, yb = up(dev, stream, x, D.F32), dev.alloc(x.size, D.F32)
     launcher.launch("softmax_rows_f32", th.LaunchGrid.cuda(tiles, 1024), [ptr(xb), ptr(yb)], stream)
     assert_softmax_close(yb.copy_to_host(stream).reshape(tiles, 1024), orc.softmax(x, tiles, 1024))
+
+
+def test_rope_f32(dev, stream, launcher):
+    """__tile_rope_f32 on 4 x 64 tiles at pos 7 against the oracle (mlir_to_gpu.rs:1508-1557).
+    Frequency and angle are f32 on both sides; powf/cosf/sinf may differ by an ulp or
+    two, which moves the output by < 1e-6 here."""
+    tiles = 50
+    rng = np.random.default_rng(41)
+    x = rng.standard_normal((tiles * 4, 64)).astype(np.float32)
+    xb, yb = up(dev, stream, x, D.F32), dev.alloc(x.size, D.F32)
+    launcher.launch("rope_f32", th.LaunchGrid.blocks_only(tiles), [ptr(xb), ptr(yb)], stream)
+    got = yb.copy_to_host(stream).reshape(tiles * 4, 64)
+    ref = orc.rope(x, tiles * 4, 64, 7)
+    assert np.allclose(got, ref, rtol=1e-5, atol=1e-5)
+
+
+def test_rope_bf16_large_position(dev, stream, launcher):
+    """__tile_rope_f16 with a bf16 name, 2 x 128 tiles at pos 1000.  At this position a
+    one-ulp difference in the f32 frequency moves the angle by up to 6e-5 rad, so the
+    bound is one bf16 ulp plus 2.5e-4 per unit of the pair's magnitude."""
+    tiles = 20
+    rng = np.random.default_rng(42)
+    x = orc.narrow(rng.standard_normal(tiles * 2 * 128).astype(np.float32), orc.BF16)
+    xb, yb = up(dev, stream, x, D.BF16), dev.alloc(x.size, D.BF16)
+    launcher.launch("rope_bf16", th.LaunchGrid.blocks_only(tiles), [ptr(xb), ptr(yb)], stream)
+    got = orc.widen(yb.copy_to_host(stream), orc.BF16).astype(np.float64)
+    ref = orc.widen(orc.rope(x, tiles * 2, 128, 1000, orc.BF16), orc.BF16).astype(np.float64)
+    xw = orc.widen(x, orc.BF16).astype(np.float64).reshape(-1, 2)
+    mag = np.repeat(np.abs(xw).sum(axis=1), 2)
+    bad = np.abs(got - ref) > ulp16(ref, orc.BF16) + 2.5e-4 * mag
+    assert not bad.any(), (np.flatnonzero(bad)[:8], got[bad][:8], ref[bad][:8])
 
 
 def test_softmax_generic_form_bf16(dev, stream, launcher):

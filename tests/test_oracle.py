@@ -154,6 +154,52 @@ def test_rms_norm_u16_is_f32_rms_norm_rounded():
 
 # ---- silu * mul ----------------------------------------------------------------------------
 
+def _rope_angle(pos, i, cols):
+    """pos * 10000^(-2i/cols) in float64 (the rotation angle of pair i)."""
+    return pos * 10000.0 ** (-2.0 * i / cols)
+
+
+def test_rope_position_zero_is_identity():
+    x = np.random.default_rng(31).standard_normal((5, 48)).astype(np.float32)
+    assert np.array_equal(orc.rope(x, 5, 48, 0), x)
+
+
+def test_rope_unit_pairs_follow_cos_sin():
+    cols, pos = 32, 5
+    e0 = np.zeros((1, cols), np.float32)
+    e0[0, 0::2] = 1.0   # every pair (1, 0)
+    e1 = np.zeros((1, cols), np.float32)
+    e1[0, 1::2] = 1.0   # every pair (0, 1)
+    t = _rope_angle(pos, np.arange(cols // 2), cols)
+    y0, y1 = orc.rope(e0, 1, cols, pos)[0], orc.rope(e1, 1, cols, pos)[0]
+    # (1, 0) -> (cos t, sin t); (0, 1) -> (-sin t, cos t).  The frequency is
+    # formed in f32, so the angle carries ~1e-7 relative error.
+    assert np.allclose(y0[0::2], np.cos(t), atol=4e-6) and np.allclose(y0[1::2], np.sin(t), atol=4e-6)
+    assert np.allclose(y1[0::2], -np.sin(t), atol=4e-6) and np.allclose(y1[1::2], np.cos(t), atol=4e-6)
+
+
+def test_rope_keeps_pair_norms_and_composes():
+    rng = np.random.default_rng(32)
+    x = rng.standard_normal((6, 64)).astype(np.float32)
+    y = orc.rope(x, 6, 64, 37).astype(np.float64)
+    xd = x.astype(np.float64)
+    n_in = xd[:, 0::2] ** 2 + xd[:, 1::2] ** 2
+    n_out = y[:, 0::2] ** 2 + y[:, 1::2] ** 2
+    assert np.allclose(n_out, n_in, rtol=1e-6)
+    # a rotation group: rope(rope(x, a), b) = rope(x, a + b)
+    ab = orc.rope(orc.rope(x, 6, 64, 3), 6, 64, 4)
+    assert np.allclose(ab, orc.rope(x, 6, 64, 7), atol=2e-6)
+
+
+def test_rope_u16_is_f32_rope_rounded():
+    rng = np.random.default_rng(33)
+    for dt in (orc.BF16, orc.F16):
+        x = orc.narrow(rng.standard_normal(2 * 128).astype(np.float32), dt)
+        y = orc.rope(x, 2, 128, 1000, dt)
+        ref = orc.narrow(orc.rope(orc.widen(x, dt), 2, 128, 1000), dt)
+        assert np.array_equal(y, ref)
+
+
 def test_silu_mul_closed_forms():
     x = np.array([0.0, 1.0, -1.0, 3.5, -3.5, 40.0, -40.0, 100.0], np.float32)
     ones = np.ones_like(x)

@@ -351,6 +351,16 @@ class Lowerer {
       if (a.size() < 4 || !tile(a[1]) || !shape_from(2, 3)) return fail(base + " arity: " + line);
       t.ins = {a[1]};
       t.dtype = F32;
+    } else if (base == "rope_f32" || base == "rope_f16") {
+      // (dst, src, pos, rows, cols), tile.rs:232, :2425; pos is a constant as in
+      // the gpu lowering (mlir_to_gpu.rs:1508-1557)
+      double pos = 0;
+      if (a.size() < 5 || !tile(a[1]) || !num(a[2], &pos) || !shape_from(3, 4))
+        return fail(base + " arity: " + line);
+      if (t.cols % 2 != 0) return fail(base + ": cols must be even: " + line);
+      t.ins = {a[1]};
+      t.scalars = {pos};
+      t.dtype = F32;
     } else if (base == "scale_f32") {
       double s = 0;
       if (a.size() < 5 || !tile(a[1]) || !num(a[2], &s) || !shape_from(3, 4))
@@ -586,12 +596,33 @@ bool emit_kernel(const Kernel& k, std::ostringstream& os, std::string* err) {
         const std::string o = t.op.size() > 7 ? t.op.substr(7) : t.op;
         auto in = [&](int i) { return var.at(t.ins[i]); };
         std::ostringstream e;
+        // Element `ix` (an index expression) of a loaded view, widened to f32.
+        auto load_at = [&](const TileVal& l, const std::string& ix) {
+          const std::string p = "reinterpret_cast<const " + std::string(dt_ctype(l.dtype)) + "*>(p" +
+                                std::to_string(l.src.arg) + ")";
+          const std::string idx = std::to_string(l.src.offset) + "ll + static_cast<int64_t>(" + ix + ")";
+          if (l.dtype == F32) return p + "[" + idx + "]";
+          return "th::u16_to_f32<" + std::string(dt_enum(l.dtype)) + ">(" + p + "[" + idx + "])";
+        };
         if (t.op == "load") {
-          const std::string p = "reinterpret_cast<const " + std::string(dt_ctype(t.dtype)) + "*>(p" +
-                                std::to_string(t.src.arg) + ")";
-          const std::string idx = std::to_string(t.src.offset) + "ll + static_cast<int64_t>(i)";
-          if (t.dtype == F32) e << p << "[" << idx << "]";
-          else e << "th::u16_to_f32<" << dt_enum(t.dtype) << ">(" << p << "[" << idx << "])";
+          e << load_at(t, "i");
+        } else if (o == "rope_f32" || o == "rope_f16") {
+          // Interleaved pairs (x[2j], x[2j+1]) of a row rotate by pos * 10000^(-2j/cols);
+          // the partner of element i is element i ^ 1 of the same loaded view (cols
+          // is even, so pairs never straddle rows or tiles).
+          const TileVal& src = k.tiles.at(t.ins[0]);
+          if (src.op != "load") {
+            *err = "mlir_to_hip: " + k.name + ": rope input must come straight from a load";
+            return false;
+          }
+          const std::string r = "r" + std::to_string(n);
+          os << "    const float " << r << "_f = 1.0f / powf(10000.0f, 2.0f * static_cast<float>(col >> 1) / "
+             << fconst(static_cast<double>(C)) << ");\n";
+          os << "    const float " << r << "_a = " << fconst(t.scalars[0]) << " * " << r << "_f;\n";
+          os << "    const float " << r << "_c = cosf(" << r << "_a), " << r << "_s = sinf(" << r << "_a);\n";
+          os << "    const float " << r << "_p = " << load_at(src, "i ^ 1ull") << ";\n";
+          e << "((col & 1u) == 0u ? " << in(0) << " * " << r << "_c - " << r << "_p * " << r << "_s : " << r
+            << "_p * " << r << "_s + " << in(0) << " * " << r << "_c)";
         } else if (o == "add_f32" || o == "add_f16") e << in(0) << " + " << in(1);
         else if (o == "sub_f32") e << in(0) << " - " << in(1);
         else if (o == "mul_f32" || o == "mul_f16") e << in(0) << " * " << in(1);
