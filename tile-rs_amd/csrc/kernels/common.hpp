@@ -164,27 +164,11 @@ __device__ __forceinline__ uint32_t pack_halves(uint32_t lo_src, uint32_t hi_src
   return __builtin_amdgcn_perm(hi_src, lo_src, SEL_HI ? 0x07060302u : 0x05040100u);
 }
 
-// Transpose an 8x8 block of 16-bit values held as 8 rows of 4 dwords:
-// in[r] holds row r (elements c=0..7), out[c] receives column c (elements r=0..7).
-__device__ __forceinline__ void transpose8x8_b16(const u32x4 (&in)[8], u32x4 (&out)[8]) {
-#pragma unroll
-  for (int c = 0; c < 8; ++c) {
-    const int dw = c >> 1;
-#pragma unroll
-    for (int p = 0; p < 4; ++p) {
-      const uint32_t lo = in[2 * p][dw];
-      const uint32_t hi = in[2 * p + 1][dw];
-      out[c][p] = (c & 1) ? pack_halves<true>(lo, hi) : pack_halves<false>(lo, hi);
-    }
-  }
-}
-
 // ---- global memory helpers -----------------------------------------------------
 
 __device__ __forceinline__ u32x4 ldg128(const void* p) {
   return *reinterpret_cast<const u32x4*>(p);
 }
-__device__ __forceinline__ void stg128(void* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
 
 __device__ __forceinline__ u32x4 ldg128_nt(const void* p) {
   return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
