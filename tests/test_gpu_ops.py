@@ -77,6 +77,29 @@ def test_errors_are_hal_errors(dev, stream):
     assert e.value.kind == "KernelError"
 
 
+def test_empty_and_degenerate_sizes(dev, stream):
+    """Zero rows / M / batch / seq_len launch nothing and leave the output untouched;
+    an empty contraction (K = 0) writes C = 0 (linalg.fill 0 with nothing accumulated,
+    mlir_to_linalg.rs:1345-1393); a decode over zero positions writes O = 0."""
+    sentinel = np.full(256, 7.0, np.float32)
+    x = upload(dev, stream, sentinel, D.F32)
+    y = upload(dev, stream, sentinel, D.F32)
+    th.softmax(x, y, 0, 256, D.F32, stream)
+    th.rms_norm(x, y, 0, 256, 1e-6, D.F32, stream)
+    th.matmul(x, x, y, 0, 16, 16, D.F32, D.F32, stream=stream)
+    th.matmul(x, x, y, 16, 16, 16, D.F32, D.F32, batch=0, stream=stream)
+    assert np.array_equal(y.copy_to_host(stream), sentinel)
+    th.matmul(x, x, y, 8, 0, 16, D.F32, D.F32, stream=stream)
+    out = y.copy_to_host(stream)
+    assert np.all(out[:128] == 0.0) and np.array_equal(out[128:], sentinel[128:])
+    q16 = upload(dev, stream, orc.narrow(sentinel, orc.BF16), D.BF16)
+    o16 = upload(dev, stream, orc.narrow(sentinel, orc.BF16), D.BF16)
+    th.attention_prefill(q16, q16, q16, o16, 1, 0, 0, 4, 128, 2, 2, D.BF16, stream)
+    assert np.array_equal(o16.copy_to_host(stream), orc.narrow(sentinel, orc.BF16))
+    th.attention_decode(q16, q16, q16, o16, 1, 0, 4, 128, 2, 2, D.BF16, stream=stream)
+    assert np.all(o16.copy_to_host(stream) == 0)
+
+
 # ---- softmax ------------------------------------------------------------------------
 
 def test_softmax_golden_vectors(dev, stream, golden):
