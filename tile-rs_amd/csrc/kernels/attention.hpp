@@ -463,6 +463,7 @@ namespace dec {
 constexpr int D = 128;
 constexpr int CHUNK = 512;
 constexpr int NT = 256;
+constexpr int CT = 512;  // threads of the combine block
 }  // namespace dec
 
 // One work item: chunks [c_begin, c_end) of (batch, kv_head) `bk` = b*NKV + kvh.
@@ -668,62 +669,95 @@ attn_decode_split(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K
 }
 
 // Merge the per-chunk partials: O = sum_s 2^(m_s - M) O_s / sum_s 2^(m_s - M) l_s.
-// One 128-thread block per (batch, head), thread d owns output d.  The chunk
-// statistics come in with one load per thread (128 chunks per pass) and are
-// shared through LDS; the O_s loads are issued eight at a time, so the merge
-// costs a few memory round trips instead of one per chunk.  The sums run over
-// s in ascending order.
+// One 512-thread block per (batch, head).  The chunk statistics (m_s, l_s) come
+// in with one load per thread per 512 chunks and M is reduced over the block.
+// Then four groups of 128 threads (thread d of a group owns output d) each merge
+// a contiguous quarter of the chunks with sixteen O loads in flight, and the
+// four partial sums are added in group order.  The merge is latency-bound (a
+// few KB per head), so it is built to need few memory round trips: statistics,
+// then ceil(n_split / 64) rounds of O loads.
 template <int DT>
-__global__ void __launch_bounds__(dec::D)
+__global__ void __launch_bounds__(dec::CT)
 attn_decode_combine(const float* __restrict__ ws, uint16_t* __restrict__ O, uint32_t nh,
                     uint32_t nkv, uint32_t n_split) {
-  constexpr int D = dec::D;
-  constexpr uint32_t PASS = D;  // chunks whose statistics one pass stages
-  __shared__ float s_w[PASS], s_l[PASS];
+  constexpr int D = dec::D, CT = dec::CT, NG = CT / D, UNR = 16;
+  __shared__ float s_w[CT], s_l[CT];
+  __shared__ float s_max[CT / 64];
+  __shared__ float s_num[NG][D], s_den[NG][D];
   const uint32_t bhq = blockIdx.x;  // b * nh + h
   const uint32_t b = bhq / nh, h = bhq % nh;
   const uint32_t G = nh / nkv;
   const uint32_t kvh = h / G, q = h % G;
   const float* rec0 = ws + ((static_cast<size_t>(b) * nkv + kvh) * G + q) * n_split * (D + 2);
-  const int d = threadIdx.x;
-  float M = -INFINITY;
-  for (uint32_t s0 = 0; s0 < n_split; s0 += PASS) {
-    const uint32_t cnt = min(PASS, n_split - s0);
-    __syncthreads();
-    if (static_cast<uint32_t>(d) < cnt) s_w[d] = rec0[(s0 + d) * (D + 2)];
-    __syncthreads();
-    for (uint32_t i = 0; i < cnt; ++i) M = fmaxf(M, s_w[i]);
+  const int t = threadIdx.x, d = t % D, grp = t / D;
+
+  // M = max_s m_s; the first pass's (m, l) stay in registers.
+  float m_own = -INFINITY, l_own = 0.0f, mx = -INFINITY;
+  for (uint32_t s0 = 0; s0 < n_split; s0 += CT) {
+    if (s0 + t < n_split) {
+      const float m = rec0[(s0 + t) * (D + 2)];
+      if (s0 == 0) {
+        m_own = m;
+        l_own = rec0[t * (D + 2) + 1];
+      }
+      mx = fmaxf(mx, m);
+    }
   }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+  if ((t & 63) == 0) s_max[t >> 6] = mx;
+  __syncthreads();
+  float M = s_max[0];
+#pragma unroll
+  for (int w = 1; w < CT / 64; ++w) M = fmaxf(M, s_max[w]);
+
   float num = 0.0f, den = 0.0f;
-  for (uint32_t s0 = 0; s0 < n_split; s0 += PASS) {
-    const uint32_t cnt = min(PASS, n_split - s0);
-    __syncthreads();
-    if (static_cast<uint32_t>(d) < cnt) {
-      const float* rec = rec0 + (s0 + d) * (D + 2);
-      const float m = rec[0];
-      s_w[d] = (m == -INFINITY) ? 0.0f : exp2_fast(m - M);
-      s_l[d] = rec[1];
+  for (uint32_t s0 = 0; s0 < n_split; s0 += CT) {
+    const uint32_t cnt = min(static_cast<uint32_t>(CT), n_split - s0);
+    if (s0 > 0) __syncthreads();  // the previous pass is done with s_w / s_l
+    if (static_cast<uint32_t>(t) < cnt) {
+      float m = m_own, l = l_own;
+      if (s0 > 0) {
+        const float* rec = rec0 + (s0 + t) * (D + 2);
+        m = rec[0];
+        l = rec[1];
+      }
+      s_w[t] = (m == -INFINITY) ? 0.0f : exp2_fast(m - M);
+      s_l[t] = l;
     }
     __syncthreads();
+    const uint32_t per = (cnt + NG - 1) / NG;
+    const uint32_t lo = min(cnt, grp * per), hi = min(cnt, lo + per);
     const float* od = rec0 + static_cast<size_t>(s0) * (D + 2) + 2 + d;
-    uint32_t i = 0;
-    for (; i + 8 <= cnt; i += 8) {
-      float o[8];
+    uint32_t i = lo;
+    for (; i + UNR <= hi; i += UNR) {
+      float o[UNR];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) o[u] = od[(i + u) * (D + 2)];
+      for (int u = 0; u < UNR; ++u) o[u] = od[(i + u) * (D + 2)];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) {
+      for (int u = 0; u < UNR; ++u) {
         num = __builtin_fmaf(s_w[i + u], o[u], num);
         den = __builtin_fmaf(s_w[i + u], s_l[i + u], den);
       }
     }
-    for (; i < cnt; ++i) {
+    for (; i < hi; ++i) {
       num = __builtin_fmaf(s_w[i], od[i * (D + 2)], num);
       den = __builtin_fmaf(s_w[i], s_l[i], den);
     }
   }
-  const float o = (den > 0.0f) ? num / den : 0.0f;
-  O[static_cast<size_t>(bhq) * D + d] = f32_to_u16<DT>(o);
+  s_num[grp][d] = num;
+  s_den[grp][d] = den;
+  __syncthreads();
+  if (grp == 0) {
+    float n = s_num[0][d], dd = s_den[0][d];
+#pragma unroll
+    for (int g = 1; g < NG; ++g) {
+      n += s_num[g][d];
+      dd += s_den[g][d];
+    }
+    const float o = (dd > 0.0f) ? n / dd : 0.0f;
+    O[static_cast<size_t>(bhq) * D + d] = f32_to_u16<DT>(o);
+  }
 }
 
 // ============================================================================

@@ -532,7 +532,7 @@ int th_attention_decode(const void* q, const void* k, const void* v, void* o, ui
                               num_kv_heads, n_split, cps, sl2, as_stream(s));
   TH_TRY(launch_status("attention_decode launch"));
   if (n_split == 1) return TH_OK;  // each workgroup covered its whole sequence and wrote O
-  const dim3 cgrid(batch * num_heads), cblock(th::dec::D);
+  const dim3 cgrid(batch * num_heads), cblock(th::dec::CT);
   if (dtype == TH_BF16)
     hipLaunchKernelGGL(th::attn_decode_combine<th::kBF16>, cgrid, cblock, 0, as_stream(s),
                        static_cast<const float*>(ws), static_cast<uint16_t*>(o), num_heads,
