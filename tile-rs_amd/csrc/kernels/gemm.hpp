@@ -7,15 +7,19 @@
 // tile.rs:2666); __tile_matmul_transposed_f16 (tile.rs:2028, :2694);
 // __tile_matmul_f32 (tile.rs:193, :2309) uses the f32 fallback kernel below.
 //
-// MFMA path (gfx950): 256x256 macro-tile per workgroup, K staged 64 at a time
-// through LDS with two buffers, four waves each owning a 128x128 sub-tile of
-// 4x4 v_mfma_f32_32x32x16_{bf16,f16} accumulators (f32).  Global tiles are
-// fetched into registers one K-step ahead, so the HBM/L2 latency of step k+1
-// hides behind the MFMAs of step k.  In LDS both operands are stored with K
-// contiguous (row = 64 elements = 128 B = 8 chunks of 16 B) and the 16-byte chunk
-// index is XOR-swizzled by the row so that 8 consecutive lanes always touch 8
-// different chunks (conflict-free 128-bit reads and writes).  A row-major B is
-// transposed 8x8 in registers on its way into LDS.
+// Two MFMA paths (gfx950), both on 256x256 macro-tiles with
+// v_mfma_f32_32x32x16_{bf16,f16} and f32 accumulators:
+//  - gemm_dma_256 (the direct-to-LDS pipeline further down) for K a multiple
+//    of 32: the path every config shape takes;
+//  - gemm_mfma_256, register-staged, for the other 16-bit shapes (K a multiple
+//    of 8): K staged 64 at a time through LDS with two buffers, four waves each
+//    owning a 128x128 sub-tile.  Global tiles are fetched into registers one
+//    K-step ahead, so the HBM/L2 latency of step k+1 hides behind the MFMAs of
+//    step k.  In LDS both operands are stored with K contiguous (row = 64
+//    elements = 128 B = 8 chunks of 16 B) and the 16-byte chunk index is
+//    XOR-swizzled by the row so that 8 consecutive lanes always touch 8
+//    different chunks (conflict-free 128-bit reads and writes).  A row-major B
+//    is transposed 8x8 in registers on its way into LDS.
 //
 // The 1-D hardware grid is mapped to tiles XCD-first: workgroups are dealt to
 // the 8 XCDs round-robin, so hardware block b is renumbered so that each XCD
