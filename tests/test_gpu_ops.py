@@ -152,6 +152,53 @@ def test_softmax_u16(dev, stream, dtype, rows, cols):
     assert_within_ulp16(y, ref, ORC[dtype], 1.0, f"softmax {dtype.name} {rows}x{cols}")
 
 
+@pytest.mark.parametrize("rows,cols", [(1, 1 << 20), (64, 131072), (3, 100003), (256, 32000),
+                                       (1, 2049), (2, 8 * 4096 + 4),
+                                       # enough rows for one workgroup per row in registers
+                                       (300, 8000), (512, 16384), (300, 8001)])
+def test_softmax_long_rows_f32(dev, stream, rows, cols):
+    """Rows split over several workgroups (chunk statistics merged per row), or one
+    workgroup per row when the rows fill the chip; ragged and unaligned column counts
+    take the scalar form of the split kernels."""
+    rng = np.random.default_rng(rows * 7 + cols)
+    x = (rng.standard_normal((rows, cols)) * 3).astype(np.float32)
+    xb = upload(dev, stream, x, D.F32)
+    yb = dev.alloc(x.size, D.F32)
+    th.softmax(xb, yb, rows, cols, D.F32, stream)
+    y = yb.copy_to_host(stream).reshape(rows, cols)
+    assert_softmax_close(y, orc.softmax(x, rows, cols), f"softmax {rows}x{cols}")
+    assert np.allclose(y.astype(np.float64).sum(axis=1), 1.0, atol=1e-5)
+
+
+@pytest.mark.parametrize("dtype", [D.F16, D.BF16])
+@pytest.mark.parametrize("rows,cols", [(3, 152064), (2048, 32000), (5, 70001)])
+def test_softmax_long_rows_u16(dev, stream, dtype, rows, cols):
+    rng = np.random.default_rng(cols + rows)
+    x = rand16(rng, rows * cols, dtype, 2.0)
+    xb = upload(dev, stream, x, dtype)
+    yb = dev.alloc(x.size, dtype)
+    th.softmax(xb, yb, rows, cols, dtype, stream)
+    y = orc.widen(yb.copy_to_host(stream), ORC[dtype])
+    ref = orc.softmax(orc.widen(x, ORC[dtype]), rows, cols)
+    assert_within_ulp16(y, ref, ORC[dtype], 1.0, f"softmax {dtype.name} {rows}x{cols}")
+
+
+def test_softmax_long_rows_masked_and_in_place(dev, stream):
+    """A long row whose first 60000 entries are -inf (whole chunks with no finite value)
+    next to an unmasked row; computed in place."""
+    rows, cols = 2, 200000
+    rng = np.random.default_rng(5)
+    x = (rng.standard_normal((rows, cols)) * 2).astype(np.float32)
+    x[0, :60000] = -np.inf
+    x[1, 199990:] = -np.inf
+    b = upload(dev, stream, x, D.F32)
+    th.softmax(b, b, rows, cols, D.F32, stream)
+    y = b.copy_to_host(stream).reshape(rows, cols)
+    ref = orc.softmax(x, rows, cols)
+    assert np.all(y[0, :60000] == 0.0) and np.all(y[1, 199990:] == 0.0)
+    assert_softmax_close(y, ref, "softmax masked long rows")
+
+
 def test_softmax_in_place(dev, stream):
     rng = np.random.default_rng(99)
     x = rng.standard_normal((16, 1024)).astype(np.float32)

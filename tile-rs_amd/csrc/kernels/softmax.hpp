@@ -8,7 +8,9 @@
 // HBM-bound.  Each row is owned by one wavefront: the row is read once with
 // 128-bit coalesced loads straight into registers, the max and the sum are
 // 64-lane DPP/shuffle reductions, and the row is written once.  Rows too long
-// for registers use a three-pass workgroup kernel instead.
+// for one wavefront's registers use one workgroup per row (the row still in
+// registers) or, for longer rows or few rows, a two-pass kernel pair over row
+// chunks spread across the chip.
 #pragma once
 
 #include "common.hpp"
@@ -77,6 +79,66 @@ softmax_rows_reg(const void* __restrict__ x, void* __restrict__ y, uint32_t rows
   const size_t off = static_cast<size_t>(row) * cols * ESZ;
   softmax_row_wave<DT, NV>(static_cast<const char*>(x) + off, static_cast<char*>(y) + off, cols,
                            threadIdx.x & 63);
+}
+
+// Workgroup form of the register path: one 256-thread workgroup per row, NV
+// 16-byte vectors per thread (rows up to 4096 vectors: 16384 f32 or 32768
+// 16-bit values), block-wide max and sum.  One read and one write of the row.
+template <int DT, int NV>
+__global__ void __launch_bounds__(256)
+softmax_rows_wg(const void* __restrict__ x, void* __restrict__ y, uint32_t rows, uint32_t cols) {
+  constexpr int ESZ = (DT == kF32) ? 4 : 2;
+  constexpr int E = Vec16<DT>::kElems;
+  __shared__ float red[4];
+  const uint32_t row = blockIdx.x;
+  if (row >= rows) return;
+  const uint32_t nvec = cols / E;
+  const char* xr = static_cast<const char*>(x) + static_cast<size_t>(row) * cols * ESZ;
+  char* yr = static_cast<char*>(y) + static_cast<size_t>(row) * cols * ESZ;
+  const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
+  float v[NV][E];
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const uint32_t vi = static_cast<uint32_t>(i) * 256u + t;
+    if (vi < nvec) {
+      unpack16<DT>(ldg128_nt(xr + static_cast<size_t>(vi) * 16), v[i]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < E; ++e) v[i][e] = -INFINITY;
+    }
+  }
+  float m = -INFINITY;
+#pragma unroll
+  for (int i = 0; i < NV; ++i)
+#pragma unroll
+    for (int e = 0; e < E; ++e) m = fmaxf(m, v[i][e]);
+  m = wave_max(m);
+  if (lane == 0) red[wave] = m;
+  __syncthreads();
+  m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  __syncthreads();
+  const float mb = m * kLog2e;
+  float s = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i)
+#pragma unroll
+    for (int e = 0; e < E; ++e) {
+      v[i][e] = exp2_fast(__builtin_fmaf(v[i][e], kLog2e, -mb));
+      s += v[i][e];
+    }
+  s = wave_sum(s);
+  if (lane == 0) red[wave] = s;
+  __syncthreads();
+  const float inv = 1.0f / ((red[0] + red[1]) + (red[2] + red[3]));
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const uint32_t vi = static_cast<uint32_t>(i) * 256u + t;
+    if (vi < nvec) {
+#pragma unroll
+      for (int e = 0; e < E; ++e) v[i][e] *= inv;
+      stg128_nt(yr + static_cast<size_t>(vi) * 16, pack16<DT>(v[i]));
+    }
+  }
 }
 
 // Streaming form of the register path: a fixed grid of waves walks the rows
@@ -179,8 +241,7 @@ __device__ __forceinline__ void softmax_row_wave_any(const void* __restrict__ xr
     st_elem<DT>(yr, c, exp2_fast(__builtin_fmaf(ld_elem<DT>(xr, c), kLog2e, -mb)) * inv);
 }
 
-// Generic path for any cols (ragged, unaligned or longer than the register path
-// holds): one 256-thread workgroup per row, three passes over the row.
+// Scalar element access for ragged or unaligned rows.
 template <int DT>
 __device__ __forceinline__ float ld_elem(const void* p, size_t i) {
   if constexpr (DT == kF32) return static_cast<const float*>(p)[i];
@@ -192,36 +253,145 @@ __device__ __forceinline__ void st_elem(void* p, size_t i, float v) {
   else static_cast<uint16_t*>(p)[i] = f32_to_u16<DT>(v);
 }
 
-template <int DT>
+// ---- long rows: each row split over `parts` workgroups --------------------------
+// Rows too long for one wavefront's registers are cut into chunks of `chunk`
+// elements so that every CU takes part whatever the row count:
+//   softmax_part_stats: workgroup (row, p) reads chunk p once and writes its
+//     statistics (m_p, s_p), m_p = max x (in log2 units), s_p = sum 2^(x - m_p);
+//   softmax_part_apply: workgroup (row, p) merges its row's statistics,
+//     M = max m_p, S = sum s_p 2^(m_p - M), and writes 2^(x - M) / S over chunk p.
+// Two reads and one write of the row.  A row of -inf only gives NaN, as the
+// single-pass kernels do.  VEC: 16-byte loads and stores (cols a multiple of the
+// vector and 16-byte aligned rows; chunk is then a multiple of 8 elements).
+
+// (m, s) pairs in log2 units: merge b into a.
+__device__ __forceinline__ void stat_merge(float& m, float& s, float mb, float sb) {
+  const float mx = fmaxf(m, mb);
+  if (mx == -INFINITY) return;  // both empty
+  s = s * exp2_fast(m - mx) + sb * exp2_fast(mb - mx);
+  m = mx;
+}
+
+// Block-wide merge of every thread's (m, s); the result is valid in every thread.
+__device__ __forceinline__ void block_stat_merge(float& m, float& s) {
+  __shared__ float red_m[4], red_s[4];
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1)
+    stat_merge(m, s, __shfl_xor(m, off, 64), __shfl_xor(s, off, 64));
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) {
+    red_m[wave] = m;
+    red_s[wave] = s;
+  }
+  __syncthreads();
+  m = red_m[0];
+  s = red_s[0];
+#pragma unroll
+  for (int w = 1; w < 4; ++w) stat_merge(m, s, red_m[w], red_s[w]);
+}
+
+template <int DT, bool VEC>
 __global__ void __launch_bounds__(256)
-softmax_rows_generic(const void* __restrict__ x, void* __restrict__ y, uint32_t rows,
-                     uint32_t cols) {
-  __shared__ float red[4];
-  const uint32_t row = blockIdx.x;
-  if (row >= rows) return;
+softmax_part_stats(const void* __restrict__ x, float2* __restrict__ st, uint32_t cols,
+                   uint32_t parts, uint32_t chunk) {
+  constexpr int E = Vec16<DT>::kElems;
+  const uint32_t row = blockIdx.x / parts, p = blockIdx.x % parts;
+  const uint32_t c0 = p * chunk, c1 = min(cols, c0 + chunk);
   const size_t base = static_cast<size_t>(row) * cols;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  float m = -INFINITY, s = 0.0f;
+  // fold n values (already scaled to log2 units) into (m, s)
+  auto fold = [&](const float* v, int n) {
+    float vm = v[0];
+    for (int i = 1; i < n; ++i) vm = fmaxf(vm, v[i]);
+    if (vm == -INFINITY) return;
+    if (vm > m) {
+      s *= exp2_fast(m - vm);
+      m = vm;
+    }
+    for (int i = 0; i < n; ++i) s += exp2_fast(v[i] - m);
+  };
+  if constexpr (VEC) {
+    const char* xr = static_cast<const char*>(x) + (base + c0) * (DT == kF32 ? 4 : 2);
+    const uint32_t nv = (c1 - c0) / E;
+    constexpr int U = 4;
+    uint32_t v = threadIdx.x;
+    for (; v + 256 * (U - 1) < nv; v += 256 * U) {
+      u32x4 raw[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) raw[u] = ldg128_nt(xr + static_cast<size_t>(v + 256 * u) * 16);
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        float f[E];
+        unpack16<DT>(raw[u], f);
+#pragma unroll
+        for (int e = 0; e < E; ++e) f[e] *= kLog2e;
+        fold(f, E);
+      }
+    }
+    for (; v < nv; v += 256) {
+      float f[E];
+      unpack16<DT>(ldg128_nt(xr + static_cast<size_t>(v) * 16), f);
+#pragma unroll
+      for (int e = 0; e < E; ++e) f[e] *= kLog2e;
+      fold(f, E);
+    }
+  } else {
+    for (uint32_t c = c0 + threadIdx.x; c < c1; c += 256) {
+      const float f = ld_elem<DT>(x, base + c) * kLog2e;
+      fold(&f, 1);
+    }
+  }
+  block_stat_merge(m, s);
+  if (threadIdx.x == 0) st[blockIdx.x] = make_float2(m, s);
+}
 
-  float m = -INFINITY;
-  for (uint32_t c = threadIdx.x; c < cols; c += 256) m = fmaxf(m, ld_elem<DT>(x, base + c));
-  m = wave_max(m);
-  if (lane == 0) red[wave] = m;
-  __syncthreads();
-  m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  __syncthreads();
-
-  const float mb = m * kLog2e;
-  float s = 0.0f;
-  for (uint32_t c = threadIdx.x; c < cols; c += 256)
-    s += exp2_fast(__builtin_fmaf(ld_elem<DT>(x, base + c), kLog2e, -mb));
-  s = wave_sum(s);
-  if (lane == 0) red[wave] = s;
-  __syncthreads();
-  s = (red[0] + red[1]) + (red[2] + red[3]);
+template <int DT, bool VEC>
+__global__ void __launch_bounds__(256)
+softmax_part_apply(const void* x, void* y, const float2* __restrict__ st, uint32_t cols,
+                   uint32_t parts, uint32_t chunk) {
+  constexpr int E = Vec16<DT>::kElems;
+  const uint32_t row = blockIdx.x / parts, p = blockIdx.x % parts;
+  const uint32_t c0 = p * chunk, c1 = min(cols, c0 + chunk);
+  const size_t base = static_cast<size_t>(row) * cols;
+  float m = -INFINITY, s = 0.0f;
+  for (uint32_t q = threadIdx.x; q < parts; q += 256) {
+    const float2 v = st[static_cast<size_t>(row) * parts + q];
+    stat_merge(m, s, v.x, v.y);
+  }
+  block_stat_merge(m, s);
+  if (m == -INFINITY) s = NAN;  // a row of -inf: 0/0 as in the single-pass kernels
   const float inv = 1.0f / s;
-
-  for (uint32_t c = threadIdx.x; c < cols; c += 256)
-    st_elem<DT>(y, base + c, exp2_fast(__builtin_fmaf(ld_elem<DT>(x, base + c), kLog2e, -mb)) * inv);
+  if constexpr (VEC) {
+    constexpr int ESZ = (DT == kF32) ? 4 : 2;
+    const char* xr = static_cast<const char*>(x) + (base + c0) * ESZ;
+    char* yr = static_cast<char*>(y) + (base + c0) * ESZ;
+    const uint32_t nv = (c1 - c0) / E;
+    constexpr int U = 4;
+    uint32_t v = threadIdx.x;
+    for (; v + 256 * (U - 1) < nv; v += 256 * U) {
+      u32x4 raw[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) raw[u] = ldg128(xr + static_cast<size_t>(v + 256 * u) * 16);
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        float f[E];
+        unpack16<DT>(raw[u], f);
+#pragma unroll
+        for (int e = 0; e < E; ++e) f[e] = exp2_fast(__builtin_fmaf(f[e], kLog2e, -m)) * inv;
+        stg128_nt(yr + static_cast<size_t>(v + 256 * u) * 16, pack16<DT>(f));
+      }
+    }
+    for (; v < nv; v += 256) {
+      float f[E];
+      unpack16<DT>(ldg128(xr + static_cast<size_t>(v) * 16), f);
+#pragma unroll
+      for (int e = 0; e < E; ++e) f[e] = exp2_fast(__builtin_fmaf(f[e], kLog2e, -m)) * inv;
+      stg128_nt(yr + static_cast<size_t>(v) * 16, pack16<DT>(f));
+    }
+  } else {
+    for (uint32_t c = c0 + threadIdx.x; c < c1; c += 256)
+      st_elem<DT>(y, base + c, exp2_fast(__builtin_fmaf(ld_elem<DT>(x, base + c), kLog2e, -m)) * inv);
+  }
 }
 
 }  // namespace th

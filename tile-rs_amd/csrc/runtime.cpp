@@ -31,6 +31,17 @@ struct Scratch {
 };
 std::mutex g_scratch_mu;
 std::unordered_map<int, Scratch> g_scratch;
+struct StreamKey {
+  int dev;
+  hipStream_t stream;
+  bool operator==(const StreamKey& o) const { return dev == o.dev && stream == o.stream; }
+};
+struct StreamKeyHash {
+  size_t operator()(const StreamKey& k) const {
+    return std::hash<const void*>()(k.stream) ^ (static_cast<size_t>(k.dev) << 1);
+  }
+};
+std::unordered_map<StreamKey, Scratch, StreamKeyHash> g_stream_scratch;
 }  // namespace
 
 int fail(int code, const std::string& msg) {
@@ -65,6 +76,27 @@ int device_scratch(size_t bytes, void** out) {
       s.bytes = 0;
     }
     size_t want = bytes < (size_t(1) << 20) ? (size_t(1) << 20) : bytes;
+    TH_TRY(check_hip(hipMalloc(&s.ptr, want), "hipMalloc", TH_MEMORY_ERROR));
+    s.bytes = want;
+  }
+  *out = s.ptr;
+  return TH_OK;
+}
+
+int stream_scratch(hipStream_t stream, size_t bytes, void** out) {
+  int dev = 0;
+  TH_TRY(check_hip(hipGetDevice(&dev), "hipGetDevice", TH_DEVICE_ERROR));
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  Scratch& s = g_stream_scratch[StreamKey{dev, stream}];
+  if (s.bytes < bytes) {
+    if (s.ptr) {
+      // earlier work on this stream may still read the old buffer
+      TH_TRY(check_hip(hipStreamSynchronize(stream), "hipStreamSynchronize", TH_STREAM_ERROR));
+      TH_TRY(check_hip(hipFree(s.ptr), "hipFree", TH_MEMORY_ERROR));
+      s.ptr = nullptr;
+      s.bytes = 0;
+    }
+    size_t want = bytes < (size_t(64) << 10) ? (size_t(64) << 10) : bytes;
     TH_TRY(check_hip(hipMalloc(&s.ptr, want), "hipMalloc", TH_MEMORY_ERROR));
     s.bytes = want;
   }

@@ -28,6 +28,12 @@ int use_device(int ordinal);
 // demand, kept until process exit).
 int device_scratch(size_t bytes, void** out);
 
+// Per-(device, stream) scratch for entry points without a workspace argument:
+// work queued on one stream runs in order, so calls never share the buffer
+// concurrently.  At least `bytes` (grown on demand after draining that stream,
+// kept until process exit).
+int stream_scratch(hipStream_t stream, size_t bytes, void** out);
+
 }  // namespace th
 
 #define TH_TRY(expr)                 \
