@@ -493,6 +493,31 @@ def test_rms_norm_u16(dev, stream, dtype, rows, cols):
     assert_within_ulp16(y, ref, ORC[dtype], 1.0, f"rms_norm {dtype.name} {rows}x{cols}")
 
 
+@pytest.mark.parametrize("dtype,rows,cols", [(D.F32, 64, 131072), (D.F32, 2, 70000),
+                                             (D.BF16, 300, 16384), (D.BF16, 260, 32768),
+                                             (D.F16, 5, 100003), (D.BF16, 3, 12289)])
+def test_rms_norm_long_rows(dev, stream, dtype, rows, cols):
+    """Rows beyond one wave's registers: one workgroup per row (enough rows), else chunk
+    sums of squares merged per row; ragged rows take the scalar form."""
+    rng = np.random.default_rng(rows + cols)
+    eps = 1e-6
+    if dtype == D.F32:
+        x = rng.standard_normal((rows, cols)).astype(np.float32)
+        xb = upload(dev, stream, x, D.F32)
+        yb = dev.alloc(x.size, D.F32)
+        th.rms_norm(xb, yb, rows, cols, eps, D.F32, stream)
+        assert_softmax_close(yb.copy_to_host(stream).reshape(rows, cols),
+                             orc.rms_norm(x, rows, cols, eps), f"rms_norm {rows}x{cols}")
+    else:
+        x = rand16(rng, rows * cols, dtype, 1.0)
+        xb = upload(dev, stream, x, dtype)
+        yb = dev.alloc(x.size, dtype)
+        th.rms_norm(xb, yb, rows, cols, eps, dtype, stream)
+        y = orc.widen(yb.copy_to_host(stream), ORC[dtype])
+        ref = orc.rms_norm(orc.widen(x, ORC[dtype]), rows, cols, eps)
+        assert_within_ulp16(y, ref, ORC[dtype], 1.0, f"rms_norm {dtype.name} {rows}x{cols}")
+
+
 def test_rms_norm_in_place_and_errors(dev, stream):
     rng = np.random.default_rng(8)
     x = rng.standard_normal((16, 1024)).astype(np.float32)

@@ -8,8 +8,8 @@
 //
 // HBM-bound, same structure as the streaming softmax: a fixed grid of waves
 // walks the rows, each row held in registers (128-bit nontemporal loads), the
-// sum of squares a 64-lane reduction, one pass over HBM.  Other shapes use one
-// wave per row with two passes.
+// sum of squares a 64-lane reduction, one pass over HBM.  Longer rows use one
+// workgroup per row or a chunked two-kernel pass (below).
 #pragma once
 
 #include "common.hpp"
@@ -94,17 +94,143 @@ __device__ __forceinline__ void rms_norm_row_wave_any(const void* __restrict__ x
   for (uint32_t c = lane; c < cols; c += 64) st_elem<DT>(yr, c, ld_elem<DT>(xr, c) * rs);
 }
 
-template <int DT>
+// Long rows.  With at least one row per CU and up to 4096 16-byte vectors per
+// row: one 256-thread workgroup per row, the row in registers, a block-wide sum
+// of squares (one read, one write).  Otherwise each row is cut into chunks
+// spread over about four workgroups per CU: rms_norm_part_stats writes every
+// chunk's sum of squares, rms_norm_part_apply adds its row's sums and scales
+// the chunk (two reads, one write).  VEC: 16-byte loads and stores.
+__device__ __forceinline__ float block_sum256(float v) {
+  __shared__ float red[4];
+  v = wave_sum(v);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;
+  __syncthreads();
+  return (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+template <int DT, int NV>
 __global__ void __launch_bounds__(256)
-rms_norm_rows_any(const void* __restrict__ x, void* __restrict__ y, uint32_t rows, uint32_t cols,
-                  float eps) {
+rms_norm_rows_wg(const void* __restrict__ x, void* __restrict__ y, uint32_t rows, uint32_t cols,
+                 float eps) {
   constexpr int ESZ = (DT == kF32) ? 4 : 2;
-  const uint32_t stride = gridDim.x * (blockDim.x >> 6);
-  for (uint32_t row = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6); row < rows;
-       row += stride) {
-    const size_t off = static_cast<size_t>(row) * cols * ESZ;
-    rms_norm_row_wave_any<DT>(static_cast<const char*>(x) + off, static_cast<char*>(y) + off, cols,
-                              eps, threadIdx.x & 63);
+  constexpr int E = Vec16<DT>::kElems;
+  const uint32_t row = blockIdx.x;
+  if (row >= rows) return;
+  const uint32_t nvec = cols / E;
+  const char* xr = static_cast<const char*>(x) + static_cast<size_t>(row) * cols * ESZ;
+  char* yr = static_cast<char*>(y) + static_cast<size_t>(row) * cols * ESZ;
+  const int t = threadIdx.x;
+  float v[NV][E];
+  float ss = 0.0f;
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const uint32_t vi = static_cast<uint32_t>(i) * 256u + t;
+    if (vi < nvec) {
+      unpack16<DT>(ldg128_nt(xr + static_cast<size_t>(vi) * 16), v[i]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < E; ++e) v[i][e] = 0.0f;
+    }
+#pragma unroll
+    for (int e = 0; e < E; ++e) ss = __builtin_fmaf(v[i][e], v[i][e], ss);
+  }
+  ss = block_sum256(ss);
+  const float rs = 1.0f / __builtin_sqrtf(ss * (1.0f / static_cast<float>(cols)) + eps);
+#pragma unroll
+  for (int i = 0; i < NV; ++i) {
+    const uint32_t vi = static_cast<uint32_t>(i) * 256u + t;
+    if (vi < nvec) {
+#pragma unroll
+      for (int e = 0; e < E; ++e) v[i][e] *= rs;
+      stg128_nt(yr + static_cast<size_t>(vi) * 16, pack16<DT>(v[i]));
+    }
+  }
+}
+
+template <int DT, bool VEC>
+__global__ void __launch_bounds__(256)
+rms_norm_part_stats(const void* __restrict__ x, float* __restrict__ st, uint32_t cols,
+                    uint32_t parts, uint32_t chunk) {
+  constexpr int E = Vec16<DT>::kElems;
+  const uint32_t row = blockIdx.x / parts, p = blockIdx.x % parts;
+  const uint32_t c0 = p * chunk, c1 = min(cols, c0 + chunk);
+  const size_t base = static_cast<size_t>(row) * cols;
+  float ss = 0.0f;
+  if constexpr (VEC) {
+    const char* xr = static_cast<const char*>(x) + (base + c0) * (DT == kF32 ? 4 : 2);
+    const uint32_t nv = (c1 - c0) / E;
+    constexpr int U = 4;
+    uint32_t v = threadIdx.x;
+    for (; v + 256 * (U - 1) < nv; v += 256 * U) {
+      u32x4 raw[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) raw[u] = ldg128_nt(xr + static_cast<size_t>(v + 256 * u) * 16);
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        float f[E];
+        unpack16<DT>(raw[u], f);
+#pragma unroll
+        for (int e = 0; e < E; ++e) ss = __builtin_fmaf(f[e], f[e], ss);
+      }
+    }
+    for (; v < nv; v += 256) {
+      float f[E];
+      unpack16<DT>(ldg128_nt(xr + static_cast<size_t>(v) * 16), f);
+#pragma unroll
+      for (int e = 0; e < E; ++e) ss = __builtin_fmaf(f[e], f[e], ss);
+    }
+  } else {
+    for (uint32_t c = c0 + threadIdx.x; c < c1; c += 256) {
+      const float f = ld_elem<DT>(x, base + c);
+      ss = __builtin_fmaf(f, f, ss);
+    }
+  }
+  ss = block_sum256(ss);
+  if (threadIdx.x == 0) st[blockIdx.x] = ss;
+}
+
+template <int DT, bool VEC>
+__global__ void __launch_bounds__(256)
+rms_norm_part_apply(const void* x, void* y, const float* __restrict__ st, uint32_t cols,
+                    uint32_t parts, uint32_t chunk, float eps) {
+  constexpr int E = Vec16<DT>::kElems;
+  const uint32_t row = blockIdx.x / parts, p = blockIdx.x % parts;
+  const uint32_t c0 = p * chunk, c1 = min(cols, c0 + chunk);
+  const size_t base = static_cast<size_t>(row) * cols;
+  float ss = 0.0f;
+  for (uint32_t q = threadIdx.x; q < parts; q += 256) ss += st[static_cast<size_t>(row) * parts + q];
+  ss = block_sum256(ss);
+  const float rs = 1.0f / __builtin_sqrtf(ss * (1.0f / static_cast<float>(cols)) + eps);
+  if constexpr (VEC) {
+    constexpr int ESZ = (DT == kF32) ? 4 : 2;
+    const char* xr = static_cast<const char*>(x) + (base + c0) * ESZ;
+    char* yr = static_cast<char*>(y) + (base + c0) * ESZ;
+    const uint32_t nv = (c1 - c0) / E;
+    constexpr int U = 4;
+    uint32_t v = threadIdx.x;
+    for (; v + 256 * (U - 1) < nv; v += 256 * U) {
+      u32x4 raw[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) raw[u] = ldg128(xr + static_cast<size_t>(v + 256 * u) * 16);
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        float f[E];
+        unpack16<DT>(raw[u], f);
+#pragma unroll
+        for (int e = 0; e < E; ++e) f[e] *= rs;
+        stg128_nt(yr + static_cast<size_t>(v + 256 * u) * 16, pack16<DT>(f));
+      }
+    }
+    for (; v < nv; v += 256) {
+      float f[E];
+      unpack16<DT>(ldg128(xr + static_cast<size_t>(v) * 16), f);
+#pragma unroll
+      for (int e = 0; e < E; ++e) f[e] *= rs;
+      stg128_nt(yr + static_cast<size_t>(v) * 16, pack16<DT>(f));
+    }
+  } else {
+    for (uint32_t c = c0 + threadIdx.x; c < c1; c += 256)
+      st_elem<DT>(y, base + c, ld_elem<DT>(x, base + c) * rs);
   }
 }
 

@@ -166,11 +166,39 @@ int rms_norm_launch(const void* x, void* y, uint32_t rows, uint32_t cols, float 
   else if (vec_ok && nvec <= 256) rms_norm_stream_go<DT, 4>(x, y, rows, cols, eps, s);
   else if (vec_ok && nvec <= 512) rms_norm_stream_go<DT, 8>(x, y, rows, cols, eps, s);
   else if (vec_ok && nvec <= 1024) rms_norm_stream_go<DT, 16>(x, y, rows, cols, eps, s);
-  else {
-    static int per_cu = 0;
-    auto k = th::rms_norm_rows_any<DT>;
-    hipLaunchKernelGGL(k, dim3(resident_grid(k, &per_cu, rows)), dim3(256), 0, s, x, y, rows,
-                       cols, eps);
+  else if (vec_ok && nvec <= 256u * 16u && rows >= current_cu_count()) {
+    // enough rows to fill the chip: one workgroup per row, the row in registers
+    if (nvec <= 256u * 8u)
+      hipLaunchKernelGGL((th::rms_norm_rows_wg<DT, 8>), dim3(rows), dim3(256), 0, s, x, y, rows,
+                         cols, eps);
+    else
+      hipLaunchKernelGGL((th::rms_norm_rows_wg<DT, 16>), dim3(rows), dim3(256), 0, s, x, y, rows,
+                         cols, eps);
+  } else {
+    // long, ragged or unaligned rows: chunk sums of squares, then scale (as softmax_long)
+    const uint64_t target = 4ull * current_cu_count();
+    uint64_t parts = std::max<uint64_t>(1, (target + rows - 1) / rows);
+    parts = std::min<uint64_t>(parts, (cols + 2047) / 2048);
+    uint64_t chunk = (cols + parts - 1) / parts;
+    chunk = (chunk + 7) / 8 * 8;
+    parts = (cols + chunk - 1) / chunk;
+    const uint64_t blocks = static_cast<uint64_t>(rows) * parts;
+    if (blocks > 0x7fffffffu) return fail(TH_KERNEL_ERROR, "rms_norm: grid too large");
+    void* stv = nullptr;
+    TH_TRY(th::stream_scratch(s, blocks * sizeof(float), &stv));
+    auto* st = static_cast<float*>(stv);
+    const dim3 grid(static_cast<uint32_t>(blocks)), block(256);
+    const uint32_t P = static_cast<uint32_t>(parts), Cn = static_cast<uint32_t>(chunk);
+    if (vec_ok) {
+      hipLaunchKernelGGL((th::rms_norm_part_stats<DT, true>), grid, block, 0, s, x, st, cols, P, Cn);
+      hipLaunchKernelGGL((th::rms_norm_part_apply<DT, true>), grid, block, 0, s, x, y, st, cols, P,
+                         Cn, eps);
+    } else {
+      hipLaunchKernelGGL((th::rms_norm_part_stats<DT, false>), grid, block, 0, s, x, st, cols, P,
+                         Cn);
+      hipLaunchKernelGGL((th::rms_norm_part_apply<DT, false>), grid, block, 0, s, x, y, st, cols,
+                         P, Cn, eps);
+    }
   }
   return launch_status("rms_norm launch");
 }
