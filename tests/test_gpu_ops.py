@@ -199,6 +199,24 @@ def test_softmax_long_rows_masked_and_in_place(dev, stream):
     assert_softmax_close(y, ref, "softmax masked long rows")
 
 
+@pytest.mark.parametrize("x_off,y_off", [(1, 1), (1, 2), (0, 3)])
+def test_row_ops_offset_pointers(dev, stream, x_off, y_off):
+    """Long ragged rows at element offsets: the same 16-byte phase for x and y (vector
+    middle between scalar head and tail) and different phases (scalar apply)."""
+    rows, cols = 4, 50257
+    rng = np.random.default_rng(x_off * 10 + y_off)
+    x = (rng.standard_normal((rows, cols)) * 2).astype(np.float32)
+    xb = upload(dev, stream, np.concatenate([np.zeros(x_off, np.float32), x.reshape(-1)]), D.F32)
+    yb = dev.alloc(rows * cols + y_off, D.F32)
+    xp, yp = xb.as_raw_ptr() + 4 * x_off, yb.as_raw_ptr() + 4 * y_off
+    th.softmax(xp, yp, rows, cols, D.F32, stream)
+    y = yb.copy_to_host(stream)[y_off:].reshape(rows, cols)
+    assert_softmax_close(y, orc.softmax(x, rows, cols), "softmax offset pointers")
+    th.rms_norm(xp, yp, rows, cols, 1e-6, D.F32, stream)
+    y = yb.copy_to_host(stream)[y_off:].reshape(rows, cols)
+    assert_softmax_close(y, orc.rms_norm(x, rows, cols, 1e-6), "rms_norm offset pointers")
+
+
 def test_softmax_in_place(dev, stream):
     rng = np.random.default_rng(99)
     x = rng.standard_normal((16, 1024)).astype(np.float32)

@@ -99,7 +99,7 @@ __device__ __forceinline__ void rms_norm_row_wave_any(const void* __restrict__ x
 // of squares (one read, one write).  Otherwise each row is cut into chunks
 // spread over about four workgroups per CU: rms_norm_part_stats writes every
 // chunk's sum of squares, rms_norm_part_apply adds its row's sums and scales
-// the chunk (two reads, one write).  VEC: 16-byte loads and stores.
+// the chunk (two reads, one write).
 __device__ __forceinline__ float block_sum256(float v) {
   __shared__ float red[4];
   v = wave_sum(v);
@@ -147,53 +147,39 @@ rms_norm_rows_wg(const void* __restrict__ x, void* __restrict__ y, uint32_t rows
   }
 }
 
-template <int DT, bool VEC>
+template <int DT>
 __global__ void __launch_bounds__(256)
 rms_norm_part_stats(const void* __restrict__ x, float* __restrict__ st, uint32_t cols,
                     uint32_t parts, uint32_t chunk) {
   constexpr int E = Vec16<DT>::kElems;
+  constexpr int ESZ = (DT == kF32) ? 4 : 2;
   const uint32_t row = blockIdx.x / parts, p = blockIdx.x % parts;
   const uint32_t c0 = p * chunk, c1 = min(cols, c0 + chunk);
   const size_t base = static_cast<size_t>(row) * cols;
   float ss = 0.0f;
-  if constexpr (VEC) {
-    const char* xr = static_cast<const char*>(x) + (base + c0) * (DT == kF32 ? 4 : 2);
-    const uint32_t nv = (c1 - c0) / E;
-    constexpr int U = 4;
-    uint32_t v = threadIdx.x;
-    for (; v + 256 * (U - 1) < nv; v += 256 * U) {
-      u32x4 raw[U];
-#pragma unroll
-      for (int u = 0; u < U; ++u) raw[u] = ldg128_nt(xr + static_cast<size_t>(v + 256 * u) * 16);
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
+  chunk_visit<ESZ, true>(
+      static_cast<const char*>(x) + base * ESZ, c0, c1,
+      [&](u32x4 raw, uint32_t) {
         float f[E];
-        unpack16<DT>(raw[u], f);
+        unpack16<DT>(raw, f);
 #pragma unroll
         for (int e = 0; e < E; ++e) ss = __builtin_fmaf(f[e], f[e], ss);
-      }
-    }
-    for (; v < nv; v += 256) {
-      float f[E];
-      unpack16<DT>(ldg128_nt(xr + static_cast<size_t>(v) * 16), f);
-#pragma unroll
-      for (int e = 0; e < E; ++e) ss = __builtin_fmaf(f[e], f[e], ss);
-    }
-  } else {
-    for (uint32_t c = c0 + threadIdx.x; c < c1; c += 256) {
-      const float f = ld_elem<DT>(x, base + c);
-      ss = __builtin_fmaf(f, f, ss);
-    }
-  }
+      },
+      [&](uint32_t c) {
+        const float f = ld_elem<DT>(x, base + c);
+        ss = __builtin_fmaf(f, f, ss);
+      });
   ss = block_sum256(ss);
   if (threadIdx.x == 0) st[blockIdx.x] = ss;
 }
 
+// VEC: x and y have the same 16-byte phase (see softmax_part_apply).
 template <int DT, bool VEC>
 __global__ void __launch_bounds__(256)
 rms_norm_part_apply(const void* x, void* y, const float* __restrict__ st, uint32_t cols,
                     uint32_t parts, uint32_t chunk, float eps) {
   constexpr int E = Vec16<DT>::kElems;
+  constexpr int ESZ = (DT == kF32) ? 4 : 2;
   const uint32_t row = blockIdx.x / parts, p = blockIdx.x % parts;
   const uint32_t c0 = p * chunk, c1 = min(cols, c0 + chunk);
   const size_t base = static_cast<size_t>(row) * cols;
@@ -201,36 +187,21 @@ rms_norm_part_apply(const void* x, void* y, const float* __restrict__ st, uint32
   for (uint32_t q = threadIdx.x; q < parts; q += 256) ss += st[static_cast<size_t>(row) * parts + q];
   ss = block_sum256(ss);
   const float rs = 1.0f / __builtin_sqrtf(ss * (1.0f / static_cast<float>(cols)) + eps);
+  auto one = [&](uint32_t c) { st_elem<DT>(y, base + c, ld_elem<DT>(x, base + c) * rs); };
   if constexpr (VEC) {
-    constexpr int ESZ = (DT == kF32) ? 4 : 2;
-    const char* xr = static_cast<const char*>(x) + (base + c0) * ESZ;
-    char* yr = static_cast<char*>(y) + (base + c0) * ESZ;
-    const uint32_t nv = (c1 - c0) / E;
-    constexpr int U = 4;
-    uint32_t v = threadIdx.x;
-    for (; v + 256 * (U - 1) < nv; v += 256 * U) {
-      u32x4 raw[U];
+    char* yr = static_cast<char*>(y) + base * ESZ;
+    chunk_visit<ESZ, false>(
+        static_cast<const char*>(x) + base * ESZ, c0, c1,
+        [&](u32x4 raw, uint32_t c) {
+          float f[E];
+          unpack16<DT>(raw, f);
 #pragma unroll
-      for (int u = 0; u < U; ++u) raw[u] = ldg128(xr + static_cast<size_t>(v + 256 * u) * 16);
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        float f[E];
-        unpack16<DT>(raw[u], f);
-#pragma unroll
-        for (int e = 0; e < E; ++e) f[e] *= rs;
-        stg128_nt(yr + static_cast<size_t>(v + 256 * u) * 16, pack16<DT>(f));
-      }
-    }
-    for (; v < nv; v += 256) {
-      float f[E];
-      unpack16<DT>(ldg128(xr + static_cast<size_t>(v) * 16), f);
-#pragma unroll
-      for (int e = 0; e < E; ++e) f[e] *= rs;
-      stg128_nt(yr + static_cast<size_t>(v) * 16, pack16<DT>(f));
-    }
+          for (int e = 0; e < E; ++e) f[e] *= rs;
+          stg128_nt(yr + static_cast<size_t>(c) * ESZ, pack16<DT>(f));
+        },
+        one);
   } else {
-    for (uint32_t c = c0 + threadIdx.x; c < c1; c += 256)
-      st_elem<DT>(y, base + c, ld_elem<DT>(x, base + c) * rs);
+    for (uint32_t c = c0 + threadIdx.x; c < c1; c += 256) one(c);
   }
 }
 

@@ -261,8 +261,38 @@ __device__ __forceinline__ void st_elem(void* p, size_t i, float v) {
 //   softmax_part_apply: workgroup (row, p) merges its row's statistics,
 //     M = max m_p, S = sum s_p 2^(m_p - M), and writes 2^(x - M) / S over chunk p.
 // Two reads and one write of the row.  A row of -inf only gives NaN, as the
-// single-pass kernels do.  VEC: 16-byte loads and stores (cols a multiple of the
-// vector and 16-byte aligned rows; chunk is then a multiple of 8 elements).
+// single-pass kernels do.  Chunks are read with 16-byte loads between scalar
+// head and tail columns, so ragged and unaligned rows keep most of the rate.
+
+// Visit columns [c0, c1) of a row (element 0 at `row`), thread-strided over a
+// 256-thread workgroup: scalar columns up to the first 16-byte boundary, then
+// 16-byte vectors (four in flight per thread), then the scalar tail.  vec(raw,
+// c) receives the vector starting at column c, one(c) a single column.
+template <int ESZ, bool NT, class FV, class F1>
+__device__ __forceinline__ void chunk_visit(const char* row, uint32_t c0, uint32_t c1, FV&& vec,
+                                            F1&& one) {
+  constexpr uint32_t E = 16 / ESZ;
+  const char* s0 = row + static_cast<size_t>(c0) * ESZ;
+  const uint32_t head =
+      min(c1 - c0, static_cast<uint32_t>(((16u - (reinterpret_cast<uintptr_t>(s0) & 15u)) & 15u) / ESZ));
+  const uint32_t cv = c0 + head;
+  const uint32_t nv = (c1 - cv) / E;
+  const char* sv = s0 + static_cast<size_t>(head) * ESZ;
+  auto ld = [&](uint32_t v) { return NT ? ldg128_nt(sv + static_cast<size_t>(v) * 16)
+                                        : ldg128(sv + static_cast<size_t>(v) * 16); };
+  for (uint32_t c = c0 + threadIdx.x; c < cv; c += 256) one(c);
+  constexpr int U = 4;
+  uint32_t v = threadIdx.x;
+  for (; v + 256 * (U - 1) < nv; v += 256 * U) {
+    u32x4 raw[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) raw[u] = ld(v + 256 * u);
+#pragma unroll
+    for (int u = 0; u < U; ++u) vec(raw[u], cv + (v + 256 * u) * E);
+  }
+  for (; v < nv; v += 256) vec(ld(v), cv + v * E);
+  for (uint32_t c = cv + nv * E + threadIdx.x; c < c1; c += 256) one(c);
+}
 
 // (m, s) pairs in log2 units: merge b into a.
 __device__ __forceinline__ void stat_merge(float& m, float& s, float mb, float sb) {
@@ -290,11 +320,12 @@ __device__ __forceinline__ void block_stat_merge(float& m, float& s) {
   for (int w = 1; w < 4; ++w) stat_merge(m, s, red_m[w], red_s[w]);
 }
 
-template <int DT, bool VEC>
+template <int DT>
 __global__ void __launch_bounds__(256)
 softmax_part_stats(const void* __restrict__ x, float2* __restrict__ st, uint32_t cols,
                    uint32_t parts, uint32_t chunk) {
   constexpr int E = Vec16<DT>::kElems;
+  constexpr int ESZ = (DT == kF32) ? 4 : 2;
   const uint32_t row = blockIdx.x / parts, p = blockIdx.x % parts;
   const uint32_t c0 = p * chunk, c1 = min(cols, c0 + chunk);
   const size_t base = static_cast<size_t>(row) * cols;
@@ -310,46 +341,31 @@ softmax_part_stats(const void* __restrict__ x, float2* __restrict__ st, uint32_t
     }
     for (int i = 0; i < n; ++i) s += exp2_fast(v[i] - m);
   };
-  if constexpr (VEC) {
-    const char* xr = static_cast<const char*>(x) + (base + c0) * (DT == kF32 ? 4 : 2);
-    const uint32_t nv = (c1 - c0) / E;
-    constexpr int U = 4;
-    uint32_t v = threadIdx.x;
-    for (; v + 256 * (U - 1) < nv; v += 256 * U) {
-      u32x4 raw[U];
-#pragma unroll
-      for (int u = 0; u < U; ++u) raw[u] = ldg128_nt(xr + static_cast<size_t>(v + 256 * u) * 16);
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
+  chunk_visit<ESZ, true>(
+      static_cast<const char*>(x) + base * ESZ, c0, c1,
+      [&](u32x4 raw, uint32_t) {
         float f[E];
-        unpack16<DT>(raw[u], f);
+        unpack16<DT>(raw, f);
 #pragma unroll
         for (int e = 0; e < E; ++e) f[e] *= kLog2e;
         fold(f, E);
-      }
-    }
-    for (; v < nv; v += 256) {
-      float f[E];
-      unpack16<DT>(ldg128_nt(xr + static_cast<size_t>(v) * 16), f);
-#pragma unroll
-      for (int e = 0; e < E; ++e) f[e] *= kLog2e;
-      fold(f, E);
-    }
-  } else {
-    for (uint32_t c = c0 + threadIdx.x; c < c1; c += 256) {
-      const float f = ld_elem<DT>(x, base + c) * kLog2e;
-      fold(&f, 1);
-    }
-  }
+      },
+      [&](uint32_t c) {
+        const float f = ld_elem<DT>(x, base + c) * kLog2e;
+        fold(&f, 1);
+      });
   block_stat_merge(m, s);
   if (threadIdx.x == 0) st[blockIdx.x] = make_float2(m, s);
 }
 
+// VEC: x and y have the same 16-byte phase, so the vector middle of each chunk
+// is aligned for both; otherwise every column is scalar.
 template <int DT, bool VEC>
 __global__ void __launch_bounds__(256)
 softmax_part_apply(const void* x, void* y, const float2* __restrict__ st, uint32_t cols,
                    uint32_t parts, uint32_t chunk) {
   constexpr int E = Vec16<DT>::kElems;
+  constexpr int ESZ = (DT == kF32) ? 4 : 2;
   const uint32_t row = blockIdx.x / parts, p = blockIdx.x % parts;
   const uint32_t c0 = p * chunk, c1 = min(cols, c0 + chunk);
   const size_t base = static_cast<size_t>(row) * cols;
@@ -361,36 +377,23 @@ softmax_part_apply(const void* x, void* y, const float2* __restrict__ st, uint32
   block_stat_merge(m, s);
   if (m == -INFINITY) s = NAN;  // a row of -inf: 0/0 as in the single-pass kernels
   const float inv = 1.0f / s;
+  auto one = [&](uint32_t c) {
+    st_elem<DT>(y, base + c, exp2_fast(__builtin_fmaf(ld_elem<DT>(x, base + c), kLog2e, -m)) * inv);
+  };
   if constexpr (VEC) {
-    constexpr int ESZ = (DT == kF32) ? 4 : 2;
-    const char* xr = static_cast<const char*>(x) + (base + c0) * ESZ;
-    char* yr = static_cast<char*>(y) + (base + c0) * ESZ;
-    const uint32_t nv = (c1 - c0) / E;
-    constexpr int U = 4;
-    uint32_t v = threadIdx.x;
-    for (; v + 256 * (U - 1) < nv; v += 256 * U) {
-      u32x4 raw[U];
+    char* yr = static_cast<char*>(y) + base * ESZ;
+    chunk_visit<ESZ, false>(
+        static_cast<const char*>(x) + base * ESZ, c0, c1,
+        [&](u32x4 raw, uint32_t c) {
+          float f[E];
+          unpack16<DT>(raw, f);
 #pragma unroll
-      for (int u = 0; u < U; ++u) raw[u] = ldg128(xr + static_cast<size_t>(v + 256 * u) * 16);
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        float f[E];
-        unpack16<DT>(raw[u], f);
-#pragma unroll
-        for (int e = 0; e < E; ++e) f[e] = exp2_fast(__builtin_fmaf(f[e], kLog2e, -m)) * inv;
-        stg128_nt(yr + static_cast<size_t>(v + 256 * u) * 16, pack16<DT>(f));
-      }
-    }
-    for (; v < nv; v += 256) {
-      float f[E];
-      unpack16<DT>(ldg128(xr + static_cast<size_t>(v) * 16), f);
-#pragma unroll
-      for (int e = 0; e < E; ++e) f[e] = exp2_fast(__builtin_fmaf(f[e], kLog2e, -m)) * inv;
-      stg128_nt(yr + static_cast<size_t>(v) * 16, pack16<DT>(f));
-    }
+          for (int e = 0; e < E; ++e) f[e] = exp2_fast(__builtin_fmaf(f[e], kLog2e, -m)) * inv;
+          stg128_nt(yr + static_cast<size_t>(c) * ESZ, pack16<DT>(f));
+        },
+        one);
   } else {
-    for (uint32_t c = c0 + threadIdx.x; c < c1; c += 256)
-      st_elem<DT>(y, base + c, exp2_fast(__builtin_fmaf(ld_elem<DT>(x, base + c), kLog2e, -m)) * inv);
+    for (uint32_t c = c0 + threadIdx.x; c < c1; c += 256) one(c);
   }
 }
 

@@ -32,6 +32,10 @@ int launch_status(const char* what) {
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+// x and y sit at the same offset within a 16-byte block (so do their rows).
+bool same_phase16(const void* x, const void* y) {
+  return ((reinterpret_cast<uintptr_t>(x) ^ reinterpret_cast<uintptr_t>(y)) & 15u) == 0;
+}
 
 int dtype_size(th_dtype d) { return d == TH_F32 ? 4 : 2; }
 
@@ -63,8 +67,7 @@ uint32_t current_cu_count() {
 // writes the chunk.  Measured on MI355X against one workgroup per row with
 // scalar loads: 64 x 131072 f32 411 -> 21 us, 1 x 2^20 f32 2708 -> 9 us.
 template <int DT>
-int softmax_long(const void* x, void* y, uint32_t rows, uint32_t cols, bool vec,
-                 hipStream_t s) {
+int softmax_long(const void* x, void* y, uint32_t rows, uint32_t cols, hipStream_t s) {
   const uint64_t target = 4ull * current_cu_count();
   uint64_t parts = std::max<uint64_t>(1, (target + rows - 1) / rows);
   parts = std::min<uint64_t>(parts, (cols + 2047) / 2048);
@@ -78,15 +81,13 @@ int softmax_long(const void* x, void* y, uint32_t rows, uint32_t cols, bool vec,
   auto* st = static_cast<float2*>(stv);
   const dim3 grid(static_cast<uint32_t>(blocks)), block(256);
   const uint32_t P = static_cast<uint32_t>(parts), Cn = static_cast<uint32_t>(chunk);
-  if (vec) {
-    hipLaunchKernelGGL((th::softmax_part_stats<DT, true>), grid, block, 0, s, x, st, cols, P, Cn);
+  hipLaunchKernelGGL((th::softmax_part_stats<DT>), grid, block, 0, s, x, st, cols, P, Cn);
+  if (same_phase16(x, y))
     hipLaunchKernelGGL((th::softmax_part_apply<DT, true>), grid, block, 0, s, x, y, st, cols, P,
                        Cn);
-  } else {
-    hipLaunchKernelGGL((th::softmax_part_stats<DT, false>), grid, block, 0, s, x, st, cols, P, Cn);
+  else
     hipLaunchKernelGGL((th::softmax_part_apply<DT, false>), grid, block, 0, s, x, y, st, cols, P,
                        Cn);
-  }
   return launch_status("softmax launch");
 }
 
@@ -127,7 +128,7 @@ int softmax_launch(const void* x, void* y, uint32_t rows, uint32_t cols, hipStre
     else
       hipLaunchKernelGGL((th::softmax_rows_reg<DT, 16>), grid, block, 0, s, x, y, rows, cols);
   } else {
-    return softmax_long<DT>(x, y, rows, cols, vec_ok, s);
+    return softmax_long<DT>(x, y, rows, cols, s);
   }
   return launch_status("softmax launch");
 }
@@ -189,16 +190,13 @@ int rms_norm_launch(const void* x, void* y, uint32_t rows, uint32_t cols, float 
     auto* st = static_cast<float*>(stv);
     const dim3 grid(static_cast<uint32_t>(blocks)), block(256);
     const uint32_t P = static_cast<uint32_t>(parts), Cn = static_cast<uint32_t>(chunk);
-    if (vec_ok) {
-      hipLaunchKernelGGL((th::rms_norm_part_stats<DT, true>), grid, block, 0, s, x, st, cols, P, Cn);
+    hipLaunchKernelGGL((th::rms_norm_part_stats<DT>), grid, block, 0, s, x, st, cols, P, Cn);
+    if (same_phase16(x, y))
       hipLaunchKernelGGL((th::rms_norm_part_apply<DT, true>), grid, block, 0, s, x, y, st, cols, P,
                          Cn, eps);
-    } else {
-      hipLaunchKernelGGL((th::rms_norm_part_stats<DT, false>), grid, block, 0, s, x, st, cols, P,
-                         Cn);
+    else
       hipLaunchKernelGGL((th::rms_norm_part_apply<DT, false>), grid, block, 0, s, x, y, st, cols,
                          P, Cn, eps);
-    }
   }
   return launch_status("rms_norm launch");
 }
