@@ -272,6 +272,34 @@ def test_matmul_u16_output_rounding(dev, stream, out_dt):
                       u16_dtype=ORC[out_dt])
 
 
+@pytest.mark.parametrize("m,k,n,in_dt,out_dt,trans", [
+    (1, 4096, 14336, D.F16, D.F16, False),     # decode-time projection, split K
+    (8, 14336, 4096, D.BF16, D.BF16, True),    # B stored N x K, 14 slices
+    (16, 4096, 4096, D.BF16, D.F32, False),
+    (3, 1024, 520, D.F16, D.F32, True),        # ragged N
+    (48, 2048, 1024, D.BF16, D.F32, False),    # two live 32-row blocks per wave
+    (100, 1024, 768, D.F16, D.F16, True),      # whole 128-row halves
+])
+def test_matmul_small_m_split_k(dev, stream, m, k, n, in_dt, out_dt, trans):
+    """Few 256 x 256 tiles: K is split over workgroups and the f32 partials merged."""
+    rng = np.random.default_rng(m + k + n)
+    a = rand16(rng, m * k, in_dt)
+    b = rand16(rng, k * n, in_dt, 0.05)
+    ab, bb = upload(dev, stream, a, in_dt), upload(dev, stream, b, in_dt)
+    cb = dev.alloc(m * n, out_dt)
+    th.matmul(ab, bb, cb, m, k, n, in_dt, out_dt, trans, stream=stream)
+    raw = cb.copy_to_host(stream)
+    got = raw if out_dt == D.F32 else orc.widen(raw, ORC[out_dt])
+    ref = orc.matmul(a, b, m, k, n, ORC[in_dt], ORC[out_dt], b_trans=trans)
+    ref32 = ref if out_dt == D.F32 else orc.widen(ref, ORC[out_dt])
+    assert_gemm_close(got.reshape(m, n), ref32.reshape(m, n), f"split-K {m}x{k}x{n}",
+                      u16_dtype=None if out_dt == D.F32 else ORC[out_dt])
+
+
+def test_matmul_silu_mul_small_m_split_k(dev, stream):
+    _swiglu_case(dev, stream, np.random.default_rng(77), 4, 4096, 2048, D.BF16, D.BF16, False)
+
+
 def test_matmul_batched(dev, stream):
     rng = np.random.default_rng(6)
     bsz, m, k, n = 3, 128, 64, 96

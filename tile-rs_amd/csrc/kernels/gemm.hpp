@@ -358,14 +358,21 @@ __device__ __forceinline__ void wait_stages(uint32_t later) {
 }
 }  // namespace gemm
 
+// ldk: row stride along K of A (and of B when B_TRANS), 0 = K; a split-K caller
+// passes the full K with K the slice depth.
+// MI: 32-row blocks each wave computes (4 = its whole 128 rows).  Fewer serve
+// tiles whose rows past 32 * MI (in each wave's half) are never stored: the
+// small-M split-K launches, where most of a 256-row tile is padding.
 template <int DT, int DT_OUT, bool B_TRANS, int KB = gemm::DBK, int NS = gemm::NSTAGE,
-          int WAVES = gemm::DWAVES, int EPI = 0>
+          int WAVES = gemm::DWAVES, int EPI = 0, int MI = 4>
 __device__ __forceinline__ void gemm_dma_tile_256(const uint16_t* __restrict__ A,
                                                   const uint16_t* __restrict__ B,
                                                   void* __restrict__ C, uint32_t M, uint32_t N,
                                                   uint32_t K, uint32_t tm, uint32_t tn,
-                                                  const void* __restrict__ up = nullptr) {
+                                                  const void* __restrict__ up = nullptr,
+                                                  uint32_t ldk = 0) {
   using namespace gemm;
+  const size_t lk = ldk ? ldk : K;
   static_assert(KB == 32 || KB == 64, "stage K");
   static_assert(WAVES == 4 || WAVES == 8, "2x2 or 2x4 waves");
   static_assert(NS * (BM + BN) * KB * 2 <= 160 * 1024, "LDS");
@@ -401,9 +408,9 @@ __device__ __forceinline__ void gemm_dma_tile_256(const uint16_t* __restrict__ A
   for (int j = 0; j < NLA; ++j) {
     const int slot = (NLA * wave + j) * 64 + lane;
     const int row = slot / CPR, c = (slot % CPR) ^ swa(row);
-    srcA[j] = A + static_cast<size_t>(min(m0 + row, M - 1)) * K + 8 * c;
+    srcA[j] = A + static_cast<size_t>(min(m0 + row, M - 1)) * lk + 8 * c;
     if constexpr (B_TRANS) {
-      srcB[j] = B + static_cast<size_t>(min(n0 + row, N - 1)) * K + 8 * c;
+      srcB[j] = B + static_cast<size_t>(min(n0 + row, N - 1)) * lk + 8 * c;
     } else {
       // [KB k][256 n] rows of 32 chunks; chunk c of k-row r at c ^ 4*(r & 3)
       const int kr = slot / 32, cb = (slot % 32) ^ (4 * (kr & 3));
@@ -422,13 +429,15 @@ __device__ __forceinline__ void gemm_dma_tile_256(const uint16_t* __restrict__ A
   };
 
   // ---- fragment reads ----
-  u32x4 fa[2][4], fb[2][NI];
+  static_assert(MI == 1 || MI == 2 || MI == 4, "live row blocks");
+  static_assert(EPI != kEpiSiluMul || MI == 4, "the staged epilogue covers whole tiles");
+  u32x4 fa[2][MI], fb[2][NI];
   auto load_frags = [&](int stage, int ks, int set) {
     const int chunk = 2 * ks + g;
     const u32x4* la = lds_a(stage);
     const u32x4* lb = lds_b(stage);
 #pragma unroll
-    for (int mi = 0; mi < 4; ++mi) {
+    for (int mi = 0; mi < MI; ++mi) {
       const int row = wm * 128 + mi * 32 + l32;
       fa[set][mi] = la[row * CPR + (chunk ^ swa(row))];
     }
@@ -458,9 +467,9 @@ __device__ __forceinline__ void gemm_dma_tile_256(const uint16_t* __restrict__ A
     }
   };
 
-  f32x16 acc[4][NI];
+  f32x16 acc[MI][NI];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < MI; ++i)
 #pragma unroll
     for (int j = 0; j < NI; ++j)
 #pragma unroll
@@ -476,12 +485,12 @@ __device__ __forceinline__ void gemm_dma_tile_256(const uint16_t* __restrict__ A
   // sunk next to their use (which would expose the LDS latency every sub-step).
   constexpr int KS = KB / 16;
   static_assert(KS % 2 == 0, "fragment sets alternate per sub-step");
-  constexpr int NM = 4 * NI;                          // MFMAs per sub-step
-  constexpr int NR = 4 + (B_TRANS ? NI : 2 * NI);     // LDS reads per sub-step
+  constexpr int NM = MI * NI;                         // MFMAs per sub-step
+  constexpr int NR = MI + (B_TRANS ? NI : 2 * NI);    // LDS reads per sub-step
   const uint32_t nk = K / KB;
   auto mfmas = [&](int set) {
 #pragma unroll
-    for (int mi = 0; mi < 4; ++mi)
+    for (int mi = 0; mi < MI; ++mi)
 #pragma unroll
       for (int ni = 0; ni < NI; ++ni)
         acc[mi][ni] = mfma32x32x16<DT>(fa[set][mi], fb[set][ni], acc[mi][ni]);
@@ -565,7 +574,7 @@ __device__ __forceinline__ void gemm_dma_tile_256(const uint16_t* __restrict__ A
   if constexpr (EPI != kEpiSiluMul) {
     auto store_all = [&](auto pred) {
 #pragma unroll
-      for (int mi = 0; mi < 4; ++mi)
+      for (int mi = 0; mi < MI; ++mi)
 #pragma unroll
         for (int ni = 0; ni < NI; ++ni) {
           const uint32_t col = n0 + wn * TWN + ni * 32 + l32;
@@ -656,19 +665,34 @@ __device__ __forceinline__ void gemm_dma_tile_256(const uint16_t* __restrict__ A
 
 // K multiple of KB (any M, N).  Batch index = blockIdx.y.
 template <int DT, int DT_OUT, bool B_TRANS, int KB = gemm::DBK, int NS = gemm::NSTAGE,
-          int WAVES = gemm::DWAVES, int EPI = 0>
+          int WAVES = gemm::DWAVES, int EPI = 0, int MI = 4>
 __global__ void __launch_bounds__(64 * WAVES, 1)
 gemm_dma_256(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, void* __restrict__ C,
              uint32_t M, uint32_t N, uint32_t K, uint64_t sa, uint64_t sb, uint64_t sc,
-             const void* __restrict__ up) {
+             const void* __restrict__ up, uint32_t ldk) {
   uint32_t tm, tn;
   gemm::tile_coords(blockIdx.x, (M + gemm::BM - 1) / gemm::BM, (N + gemm::BN - 1) / gemm::BN, tm,
                     tn);
   constexpr int OSZ = (DT_OUT == kF32) ? 4 : 2;
   const size_t co = static_cast<size_t>(blockIdx.y) * sc * OSZ;
-  gemm_dma_tile_256<DT, DT_OUT, B_TRANS, KB, NS, WAVES, EPI>(
+  gemm_dma_tile_256<DT, DT_OUT, B_TRANS, KB, NS, WAVES, EPI, MI>(
       A + blockIdx.y * sa, B + blockIdx.y * sb, static_cast<char*>(C) + co, M, N, K, tm, tn,
-      up ? static_cast<const char*>(up) + co : nullptr);
+      up ? static_cast<const char*>(up) + co : nullptr, ldk);
+}
+
+// Split-K merge: C = epilogue(sum_s W[s]) for an S x M x N f32 workspace whose
+// slice s holds A[:, s-th K range] . B[s-th K range, :].  Slices are added in
+// ascending order; one rounding to C's dtype.
+template <int DT_OUT, int EPI>
+__global__ void __launch_bounds__(256)
+gemm_splitk_reduce(const float* __restrict__ W, void* __restrict__ C, const void* __restrict__ up,
+                   uint64_t mn, uint32_t S) {
+  for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * 256u + threadIdx.x; i < mn;
+       i += static_cast<uint64_t>(gridDim.x) * 256u) {
+    float v = 0.0f;
+    for (uint32_t s = 0; s < S; ++s) v += W[s * mn + i];
+    gemm::store_out<EPI, DT_OUT>(C, up, i, v);
+  }
 }
 
 // Per-element GEMM on one 256x256 tile: each thread forms whole dot products

@@ -228,8 +228,53 @@ bool gemm_dma() {
   return v;
 }
 
+// Split-K for shapes with too few 256 x 256 tiles to fill the chip (small M:
+// decode-time projections).  S slices of K (each a multiple of 32, at least 256
+// deep, S a divisor of K / 32) run as the batch dimension of the DMA kernel,
+// writing f32 partials to a per-stream workspace; gemm_splitk_reduce adds them
+// and applies the epilogue.  Only for batch 1.  Returns 1 for no split.
+uint32_t splitk_slices(const GemmArgs& g, uint32_t tiles) {
+  const uint32_t cus = current_cu_count();
+  if (g.batch != 1 || 2u * tiles > cus || g.k < 512) return 1;
+  const uint32_t units = g.k / th::gemm::DBK;             // K in 32-deep steps
+  const uint32_t cap = std::min<uint32_t>({cus / tiles, g.k / 256u, 32u});
+  uint32_t best = 1;
+  for (uint32_t s = 2; s <= cap; ++s)
+    if (units % s == 0) best = s;
+  return best;
+}
+
 template <int DT, int DTO, int EPI, bool BT>
-void gemm_mfma_go(const GemmArgs& g, dim3 grid) {
+int gemm_splitk(const GemmArgs& g, uint32_t tiles, uint32_t S) {
+  const uint32_t ks = g.k / S;
+  const uint64_t mn = static_cast<uint64_t>(g.m) * g.n;
+  void* wv = nullptr;
+  TH_TRY(th::stream_scratch(g.s, S * mn * sizeof(float), &wv));
+  auto* W = static_cast<float*>(wv);
+  auto go = [&](auto mi) {
+    constexpr int MI = decltype(mi)::value;
+    hipLaunchKernelGGL((th::gemm_dma_256<DT, th::kF32, BT, th::gemm::DBK, th::gemm::NSTAGE,
+                                         th::gemm::DWAVES, th::gemm::kEpiStore, MI>),
+                       dim3(tiles, S), dim3(64 * th::gemm::DWAVES), 0, g.s,
+                       static_cast<const uint16_t*>(g.a), static_cast<const uint16_t*>(g.b),
+                       static_cast<void*>(W), g.m, g.n, ks, static_cast<uint64_t>(ks),
+                       BT ? static_cast<uint64_t>(ks) : static_cast<uint64_t>(ks) * g.n, mn,
+                       static_cast<const void*>(nullptr), g.k);
+  };
+  // rows past M are padding: compute only the 32-row blocks that hold real rows
+  if (g.m <= 32) go(std::integral_constant<int, 1>{});
+  else if (g.m <= 64) go(std::integral_constant<int, 2>{});
+  else go(std::integral_constant<int, 4>{});
+  TH_TRY(launch_status("matmul (split-K) launch"));
+  const uint32_t blocks = static_cast<uint32_t>(
+      std::min<uint64_t>((mn + 255) / 256, 4ull * current_cu_count()));
+  hipLaunchKernelGGL((th::gemm_splitk_reduce<DTO, EPI>), dim3(blocks), dim3(256), 0, g.s, W, g.c,
+                     g.up, mn, S);
+  return launch_status("matmul (split-K merge) launch");
+}
+
+template <int DT, int DTO, int EPI, bool BT>
+int gemm_mfma_go(const GemmArgs& g, dim3 grid) {
   auto A = static_cast<const uint16_t*>(g.a);
   auto B = static_cast<const uint16_t*>(g.b);
   // The DMA kernel's SiLU*Mul epilogue writes C and reads UP in 16-byte pieces.
@@ -237,10 +282,12 @@ void gemm_mfma_go(const GemmArgs& g, dim3 grid) {
   const bool out_vec = EPI != th::gemm::kEpiSiluMul ||
                        (aligned16(g.c) && aligned16(g.up) && (g.sc * OSZ) % 16 == 0 && g.n % 8 == 0);
   if (gemm_dma() && out_vec && g.k % th::gemm::DBK == 0) {
+    const uint32_t S = splitk_slices(g, grid.x);
+    if (S > 1) return gemm_splitk<DT, DTO, EPI, BT>(g, grid.x, S);
     hipLaunchKernelGGL((th::gemm_dma_256<DT, DTO, BT, th::gemm::DBK, th::gemm::NSTAGE,
                                          th::gemm::DWAVES, EPI>),
                        grid, dim3(64 * th::gemm::DWAVES), 0, g.s, A, B, g.c, g.m, g.n, g.k, g.sa,
-                       g.sb, g.sc, g.up);
+                       g.sb, g.sc, g.up, 0u);
   } else if (g.m % th::gemm::BM == 0 && g.n % th::gemm::BN == 0 && g.k % th::gemm::BK == 0) {
     hipLaunchKernelGGL((th::gemm_mfma_256<DT, DTO, BT, 2, 2, true, EPI>), grid, dim3(256), 0, g.s,
                        A, B, g.c, g.m, g.n, g.k, g.sa, g.sb, g.sc, g.up);
@@ -248,6 +295,7 @@ void gemm_mfma_go(const GemmArgs& g, dim3 grid) {
     hipLaunchKernelGGL((th::gemm_mfma_256<DT, DTO, BT, 2, 2, false, EPI>), grid, dim3(256), 0, g.s,
                        A, B, g.c, g.m, g.n, g.k, g.sa, g.sb, g.sc, g.up);
   }
+  return launch_status("matmul (MFMA) launch");
 }
 
 template <int DT, int DTO, int EPI>
@@ -255,9 +303,8 @@ int gemm_launch(const GemmArgs& g, bool mfma) {
   if constexpr (DT != th::kF32) {
     if (mfma) {
       const dim3 grid(((g.m + 255) / 256) * ((g.n + 255) / 256), g.batch);
-      if (g.bt) gemm_mfma_go<DT, DTO, EPI, true>(g, grid);
-      else gemm_mfma_go<DT, DTO, EPI, false>(g, grid);
-      return launch_status("matmul (MFMA) launch");
+      return g.bt ? gemm_mfma_go<DT, DTO, EPI, true>(g, grid)
+                  : gemm_mfma_go<DT, DTO, EPI, false>(g, grid);
     }
   }
   (void)mfma;
