@@ -169,6 +169,14 @@ def test_elementwise_fallback():
     assert "fminf(fmaxf(" in out.source                  # clamp
 
 
+def test_long_rows_lower_to_one_workgroup_per_row():
+    src = th.emit((EXAMPLES / "rows_long.mlir").read_text()).source
+    assert "th::entry::softmax_rows_wg<th::kF32, 16>(" in src      # 4096 vectors per row
+    assert "__th_desc_softmax_long_f32 = {th::kLaunchDescMagic, 256u, 1u, 1u," in src
+    assert "th::entry::rms_norm_rows_wg<th::kF32, 8>(" in src      # 2048 vectors per row
+    assert "__th_desc_rms_long_f32 = {th::kLaunchDescMagic, 256u, 2u, 1u," in src
+
+
 def test_rope_lowers_to_pair_rotation():
     out = th.emit((EXAMPLES / "rope.mlir").read_text())
     assert out.meta.kernel_names == ["rope_f32", "rope_bf16"]

@@ -27,7 +27,7 @@ def launcher(dev):
     lau = dev.create_launcher()
     for stem in ("softmax_rows", "softmax_generic", "matmul_bf16", "matmul_f16_t", "matmul_f32",
                  "attention_f32", "prefill_bf16", "decode_bf16", "swiglu_mask", "rms_norm_rows",
-                 "swiglu_gate_bf16", "matmul_bf16_tiles", "rope"):
+                 "swiglu_gate_bf16", "matmul_bf16_tiles", "rope", "rows_long"):
         lau.load(_build.example_path(stem), th.KernelMode.GENERAL)
     return lau
 
@@ -49,6 +49,22 @@ def test_softmax_rows_f32(dev, stream, launcher):
     xb, yb = up(dev, stream, x, D.F32), dev.alloc(x.size, D.F32)
     launcher.launch("softmax_rows_f32", th.LaunchGrid.cuda(tiles, 1024), [ptr(xb), ptr(yb)], stream)
     assert_softmax_close(yb.copy_to_host(stream).reshape(tiles, 1024), orc.softmax(x, tiles, 1024))
+
+
+def test_long_rows_one_workgroup_per_row(dev, stream, launcher):
+    """Emitted softmax over 1 x 16384 f32 tiles and RMSNorm over 2 x 8192 f32 tiles: one
+    workgroup per row, the row in registers."""
+    rng = np.random.default_rng(43)
+    tiles = 37
+    x = (rng.standard_normal((tiles, 16384)) * 2).astype(np.float32)
+    xb, yb = up(dev, stream, x, D.F32), dev.alloc(x.size, D.F32)
+    launcher.launch("softmax_long_f32", th.LaunchGrid.blocks_only(tiles), [ptr(xb), ptr(yb)], stream)
+    assert_softmax_close(yb.copy_to_host(stream).reshape(tiles, 16384), orc.softmax(x, tiles, 16384))
+    x2 = rng.standard_normal((tiles * 2, 8192)).astype(np.float32)
+    xb2, yb2 = up(dev, stream, x2, D.F32), dev.alloc(x2.size, D.F32)
+    launcher.launch("rms_long_f32", th.LaunchGrid.blocks_only(tiles), [ptr(xb2), ptr(yb2)], stream)
+    assert_softmax_close(yb2.copy_to_host(stream).reshape(tiles * 2, 8192),
+                         orc.rms_norm(x2, tiles * 2, 8192, 1e-5))
 
 
 def test_rope_f32(dev, stream, launcher):

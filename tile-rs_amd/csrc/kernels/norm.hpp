@@ -108,18 +108,15 @@ __device__ __forceinline__ float block_sum256(float v) {
   return (red[0] + red[1]) + (red[2] + red[3]);
 }
 
+// Body: the calling workgroup normalizes the row at xr into yr (may be called
+// again for another row).
 template <int DT, int NV>
-__global__ void __launch_bounds__(256)
-rms_norm_rows_wg(const void* __restrict__ x, void* __restrict__ y, uint32_t rows, uint32_t cols,
-                 float eps) {
-  constexpr int ESZ = (DT == kF32) ? 4 : 2;
+__device__ __forceinline__ void rms_norm_row_wg(const char* __restrict__ xr, char* __restrict__ yr,
+                                                uint32_t cols, float eps) {
   constexpr int E = Vec16<DT>::kElems;
-  const uint32_t row = blockIdx.x;
-  if (row >= rows) return;
   const uint32_t nvec = cols / E;
-  const char* xr = static_cast<const char*>(x) + static_cast<size_t>(row) * cols * ESZ;
-  char* yr = static_cast<char*>(y) + static_cast<size_t>(row) * cols * ESZ;
   const int t = threadIdx.x;
+  __syncthreads();  // a previous row's readers of the reduction slots are done
   float v[NV][E];
   float ss = 0.0f;
 #pragma unroll
@@ -145,6 +142,18 @@ rms_norm_rows_wg(const void* __restrict__ x, void* __restrict__ y, uint32_t rows
       stg128_nt(yr + static_cast<size_t>(vi) * 16, pack16<DT>(v[i]));
     }
   }
+}
+
+template <int DT, int NV>
+__global__ void __launch_bounds__(256)
+rms_norm_rows_wg(const void* __restrict__ x, void* __restrict__ y, uint32_t rows, uint32_t cols,
+                 float eps) {
+  constexpr int ESZ = (DT == kF32) ? 4 : 2;
+  const uint32_t row = blockIdx.x;
+  if (row >= rows) return;
+  const size_t off = static_cast<size_t>(row) * cols * ESZ;
+  rms_norm_row_wg<DT, NV>(static_cast<const char*>(x) + off, static_cast<char*>(y) + off, cols,
+                          eps);
 }
 
 template <int DT>

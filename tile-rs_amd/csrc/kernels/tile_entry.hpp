@@ -40,6 +40,28 @@ __device__ __forceinline__ void softmax_rows(const void* x, void* y, uint32_t ro
   }
 }
 
+// ---- rows of 1025-4096 16-byte vectors: one 256-thread workgroup per row, the
+//      row in registers (workgroups stride over the rows) ----
+template <int DT, int NV>
+__device__ __forceinline__ void softmax_rows_wg(const void* x, void* y, uint32_t rows,
+                                                uint32_t cols) {
+  constexpr int ESZ = (DT == kF32) ? 4 : 2;
+  for (uint32_t r = blockIdx.x; r < rows; r += gridDim.x) {
+    const size_t off = static_cast<size_t>(r) * cols * ESZ;
+    softmax_row_wg<DT, NV>(static_cast<const char*>(x) + off, static_cast<char*>(y) + off, cols);
+  }
+}
+template <int DT, int NV>
+__device__ __forceinline__ void rms_norm_rows_wg(const void* x, void* y, uint32_t rows,
+                                                 uint32_t cols, float eps) {
+  constexpr int ESZ = (DT == kF32) ? 4 : 2;
+  for (uint32_t r = blockIdx.x; r < rows; r += gridDim.x) {
+    const size_t off = static_cast<size_t>(r) * cols * ESZ;
+    rms_norm_row_wg<DT, NV>(static_cast<const char*>(x) + off, static_cast<char*>(y) + off, cols,
+                            eps);
+  }
+}
+
 // ---- row RMSNorm over `rows` contiguous rows of `cols`: the library's streaming
 //      loop when a row fits NV 16-byte vectors per lane (NV > 0), else one
 //      wavefront per row in two passes ----

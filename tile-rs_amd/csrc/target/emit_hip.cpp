@@ -685,6 +685,18 @@ bool emit_kernel(const Kernel& k, std::ostringstream& os, std::string* err) {
     int nv = 0;  // 0 = any-cols path
     const bool aligned = (C % E == 0) && (x.src.offset % E == 0) && (st->dst.offset % E == 0);
     if (aligned && nvec <= 64 * 16) nv = nvec <= 64 ? 1 : nvec <= 128 ? 2 : nvec <= 256 ? 4 : nvec <= 512 ? 8 : 16;
+    if (aligned && nvec > 64 * 16 && nvec <= 256 * 16) {
+      // one workgroup per row, the row in registers
+      const int wnv = nvec <= 256 * 8 ? 8 : 16;
+      os << "row softmax " << R << "x" << C << " " << dt_name(x.dtype)
+         << " per tile -> th::entry::softmax_rows_wg (one workgroup per row)\n";
+      signature(os, k, 256, {});
+      os << "  th::entry::softmax_rows_wg<" << dt_enum(x.dtype) << ", " << wnv << ">("
+         << in_ptr(0, dt_ctype(x.dtype)) << ", " << out_ptr(dt_ctype(x.dtype)) << ", th_tiles * "
+         << u(R) << ", " << u(C) << ");\n}\n";
+      desc(os, k.name, 256, static_cast<unsigned>(R), 1);
+      return true;
+    }
     os << "row softmax " << R << "x" << C << " " << dt_name(x.dtype) << " per tile -> th::entry::softmax_rows\n";
     signature(os, k, 256, {});
     os << "  th::entry::softmax_rows<" << dt_enum(x.dtype) << ", " << nv << ">(" << in_ptr(0, dt_ctype(x.dtype))
@@ -715,6 +727,18 @@ bool emit_kernel(const Kernel& k, std::ostringstream& os, std::string* err) {
     int nv = 0;
     const bool aligned = (C % E == 0) && (x.src.offset % E == 0) && (st->dst.offset % E == 0);
     if (aligned && nvec <= 64 * 16) nv = nvec <= 64 ? 1 : nvec <= 128 ? 2 : nvec <= 256 ? 4 : nvec <= 512 ? 8 : 16;
+    if (aligned && nvec > 64 * 16 && nvec <= 256 * 16) {
+      // one workgroup per row, the row in registers
+      const int wnv = nvec <= 256 * 8 ? 8 : 16;
+      os << "row rms_norm " << R << "x" << C << " " << dt_name(x.dtype) << " eps "
+         << hot->scalars[0] << " per tile -> th::entry::rms_norm_rows_wg (one workgroup per row)\n";
+      signature(os, k, 256, {});
+      os << "  th::entry::rms_norm_rows_wg<" << dt_enum(x.dtype) << ", " << wnv << ">("
+         << in_ptr(0, dt_ctype(x.dtype)) << ", " << out_ptr(dt_ctype(x.dtype)) << ", th_tiles * "
+         << u(R) << ", " << u(C) << ", " << fconst(hot->scalars[0]) << ");\n}\n";
+      desc(os, k.name, 256, static_cast<unsigned>(R), 1);
+      return true;
+    }
     os << "row rms_norm " << R << "x" << C << " " << dt_name(x.dtype) << " eps "
        << hot->scalars[0] << " per tile -> th::entry::rms_norm_rows\n";
     signature(os, k, 256, {});
