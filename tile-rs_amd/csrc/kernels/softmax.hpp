@@ -149,6 +149,93 @@ softmax_rows_wg(const void* __restrict__ x, void* __restrict__ y, uint32_t rows,
   softmax_row_wg<DT, NV>(static_cast<const char*>(x) + off, static_cast<char*>(y) + off, cols);
 }
 
+// Streaming workgroup form: a fixed grid of NT-thread workgroups walks the rows
+// (NV 16-byte vectors per thread, rows up to NT * NV vectors), and each
+// workgroup's loads of its next row are issued before it reduces the current
+// one, so no row's load latency is exposed.
+template <int DT, int NT, int NV>
+__global__ void __launch_bounds__(NT)
+softmax_rows_wg_stream(const void* __restrict__ x, void* __restrict__ y, uint32_t rows,
+                       uint32_t cols) {
+  constexpr int ESZ = (DT == kF32) ? 4 : 2;
+  constexpr int E = Vec16<DT>::kElems;
+  constexpr int NW = NT / 64;
+  __shared__ float red[NW];
+  const uint32_t nvec = cols / E;
+  const size_t rbytes = static_cast<size_t>(cols) * ESZ;
+  const int t = threadIdx.x, wave = t >> 6, lane = t & 63;
+  u32x4 cur[NV], nxt[NV];
+  auto load = [&](uint32_t r, u32x4 (&v)[NV]) {
+    const char* xr = static_cast<const char*>(x) + static_cast<size_t>(r) * rbytes;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const uint32_t vi = static_cast<uint32_t>(i) * NT + t;
+      if (vi < nvec) v[i] = ldg128_nt(xr + static_cast<size_t>(vi) * 16);
+    }
+  };
+  auto block_max = [&](float v) {
+    v = wave_max(v);
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    float r = red[0];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) r = fmaxf(r, red[w]);
+    __syncthreads();
+    return r;
+  };
+  auto block_sum = [&](float v) {
+    v = wave_sum(v);
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    float r = red[0];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) r += red[w];
+    __syncthreads();
+    return r;
+  };
+  uint32_t row = blockIdx.x;
+  if (row < rows) load(row, cur);
+  for (; row < rows; row += gridDim.x) {
+    if (row + gridDim.x < rows) load(row + gridDim.x, nxt);
+    float v[NV][E];
+    float m = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const uint32_t vi = static_cast<uint32_t>(i) * NT + t;
+      if (vi < nvec) {
+        unpack16<DT>(cur[i], v[i]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < E; ++e) v[i][e] = -INFINITY;
+      }
+#pragma unroll
+      for (int e = 0; e < E; ++e) m = fmaxf(m, v[i][e]);
+    }
+    const float mb = block_max(m) * kLog2e;
+    float sum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+#pragma unroll
+      for (int e = 0; e < E; ++e) {
+        v[i][e] = exp2_fast(__builtin_fmaf(v[i][e], kLog2e, -mb));
+        sum += v[i][e];
+      }
+    const float inv = 1.0f / block_sum(sum);
+    char* yr = static_cast<char*>(y) + static_cast<size_t>(row) * rbytes;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      const uint32_t vi = static_cast<uint32_t>(i) * NT + t;
+      if (vi < nvec) {
+#pragma unroll
+        for (int e = 0; e < E; ++e) v[i][e] *= inv;
+        stg128_nt(yr + static_cast<size_t>(vi) * 16, pack16<DT>(v[i]));
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < NV; ++i) cur[i] = nxt[i];
+  }
+}
+
 // Streaming form of the register path: a fixed grid of waves walks the rows
 // (row stride = total waves), and the loads of a wave's next row are issued
 // before the reductions of its current row, so every wave keeps one row of

@@ -111,13 +111,19 @@ int softmax_launch(const void* x, void* y, uint32_t rows, uint32_t cols, hipStre
       hipLaunchKernelGGL((th::softmax_rows_stream<DT, 4>), grid, block, 0, s, x, y, rows, cols);
     return launch_status("softmax launch");
   }
-  if (vec_ok && nvec > 64u * 16u && nvec <= 256u * 16u && rows >= current_cu_count()) {
-    // enough rows to fill the chip: one workgroup per row, the row in registers
-    const dim3 grid(rows), block(256);
-    if (nvec <= 256u * 8u)
-      hipLaunchKernelGGL((th::softmax_rows_wg<DT, 8>), grid, block, 0, s, x, y, rows, cols);
-    else
-      hipLaunchKernelGGL((th::softmax_rows_wg<DT, 16>), grid, block, 0, s, x, y, rows, cols);
+  if (vec_ok && nvec > 64u * 16u && nvec <= 512u * 8u && rows >= current_cu_count()) {
+    // enough rows to fill the chip: a fixed grid of workgroups walks the rows,
+    // each row in registers and the next row's loads in flight
+    const uint32_t cus = current_cu_count();
+    if (nvec <= 256u * 8u) {
+      const dim3 grid(std::min<uint32_t>(rows, 2u * cus)), block(256);
+      hipLaunchKernelGGL((th::softmax_rows_wg_stream<DT, 256, 8>), grid, block, 0, s, x, y, rows,
+                         cols);
+    } else {
+      const dim3 grid(std::min<uint32_t>(rows, 2u * cus)), block(512);
+      hipLaunchKernelGGL((th::softmax_rows_wg_stream<DT, 512, 8>), grid, block, 0, s, x, y, rows,
+                         cols);
+    }
     return launch_status("softmax launch");
   }
   if (vec_ok && nvec <= 64u * 16u) {
