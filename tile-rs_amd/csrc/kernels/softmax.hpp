@@ -81,11 +81,11 @@ softmax_rows_reg(const void* __restrict__ x, void* __restrict__ y, uint32_t rows
                            threadIdx.x & 63);
 }
 
-// Workgroup form of the register path: one 256-thread workgroup per row, NV
-// 16-byte vectors per thread (rows up to 4096 vectors: 16384 f32 or 32768
-// 16-bit values), block-wide max and sum.  One read and one write of the row.
-// Body: the calling workgroup normalizes the row at xr into yr (every thread
-// calls it; it may be called again for another row).
+// Workgroup form of the register path (used by emitted kernels): one 256-thread
+// workgroup per row, NV 16-byte vectors per thread (rows up to 4096 vectors:
+// 16384 f32 or 32768 16-bit values), block-wide max and sum; one read and one
+// write of the row.  The calling workgroup normalizes the row at xr into yr
+// (every thread calls it; it may be called again for another row).
 template <int DT, int NV>
 __device__ __forceinline__ void softmax_row_wg(const char* __restrict__ xr, char* __restrict__ yr,
                                                uint32_t cols) {
@@ -137,16 +137,6 @@ __device__ __forceinline__ void softmax_row_wg(const char* __restrict__ xr, char
       stg128_nt(yr + static_cast<size_t>(vi) * 16, pack16<DT>(v[i]));
     }
   }
-}
-
-template <int DT, int NV>
-__global__ void __launch_bounds__(256)
-softmax_rows_wg(const void* __restrict__ x, void* __restrict__ y, uint32_t rows, uint32_t cols) {
-  constexpr int ESZ = (DT == kF32) ? 4 : 2;
-  const uint32_t row = blockIdx.x;
-  if (row >= rows) return;
-  const size_t off = static_cast<size_t>(row) * cols * ESZ;
-  softmax_row_wg<DT, NV>(static_cast<const char*>(x) + off, static_cast<char*>(y) + off, cols);
 }
 
 // Streaming workgroup form: a fixed grid of NT-thread workgroups walks the rows
