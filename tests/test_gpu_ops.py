@@ -395,7 +395,10 @@ def test_prefill_golden_vectors(dev, stream, golden):
     (1, 256, 0, 0, 2, 2, 128),     # one full query block
     (2, 300, 0, 4, 4, 1, 128),     # ragged, GQA 4:1
     (1, 100, 37, 0, 8, 2, 128),    # chunked prefill, start_pos > 0
-    (1, 600, 0, 0, 2, 2, 64),      # head_dim 64 -> general kernel
+    (1, 600, 0, 0, 2, 2, 64),      # head_dim 64: zero-padded to 128 for the MFMA kernel
+    (2, 300, 40, 3, 8, 2, 96),     # head_dim 96, GQA 4:1, start_pos > 0, padded
+    (1, 257, 0, 0, 4, 4, 80),      # head_dim 80, padded
+    (1, 70, 3, 0, 2, 1, 60),       # head_dim 60 (not a multiple of 8) -> general kernel
     (3, 1, 5, 2, 4, 4, 128),       # single query
 ])
 def test_prefill_shapes(dev, stream, dtype, B, S, start, extra, NH, NKV, Dh):

@@ -500,6 +500,31 @@ int th_attention(const void* q, const void* k, const void* v, void* o, uint32_t 
                              scale, dtype, as_stream(s));
 }
 
+// Copy `rows` rows of 16-bit values in 16-byte pieces: dst row r = src row r
+// (src_ld8 pieces) followed by zeros up to dst_ld8 pieces, or (cols8 < dst_ld8
+// pieces of the source copied) the first cols8 pieces of a wider source row.
+__global__ void __launch_bounds__(256)
+copy_rows16(const uint4* __restrict__ src, uint32_t src_ld8, uint4* __restrict__ dst,
+            uint32_t dst_ld8, uint32_t cols8, uint64_t rows) {
+  const uint64_t n = rows * dst_ld8;
+  for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * 256u + threadIdx.x; i < n;
+       i += static_cast<uint64_t>(gridDim.x) * 256u) {
+    const uint64_t r = i / dst_ld8;
+    const uint32_t c = static_cast<uint32_t>(i % dst_ld8);
+    dst[i] = c < cols8 ? src[r * src_ld8 + c] : make_uint4(0, 0, 0, 0);
+  }
+}
+
+static void copy_rows16_launch(const void* src, uint32_t src_ld, void* dst, uint32_t dst_ld,
+                               uint32_t cols, uint64_t rows, hipStream_t s) {
+  const uint64_t n = rows * (dst_ld / 8);
+  const uint32_t blocks =
+      static_cast<uint32_t>(std::min<uint64_t>((n + 255) / 256, 8ull * current_cu_count()));
+  hipLaunchKernelGGL(copy_rows16, dim3(std::max(blocks, 1u)), dim3(256), 0, s,
+                     static_cast<const uint4*>(src), src_ld / 8, static_cast<uint4*>(dst),
+                     dst_ld / 8, cols / 8, rows);
+}
+
 int th_attention_prefill(const void* q, const void* k, const void* v, void* o, uint32_t batch,
                          uint32_t seq_len, uint32_t start_pos, uint32_t max_seq,
                          uint32_t head_dim, uint32_t num_heads, uint32_t num_kv_heads,
@@ -513,9 +538,15 @@ int th_attention_prefill(const void* q, const void* k, const void* v, void* o, u
     return fail(TH_KERNEL_ERROR, "attention_prefill: start_pos + seq_len exceeds max_seq");
   if (head_dim == 0) return fail(TH_KERNEL_ERROR, "attention_prefill: head_dim == 0");
   const float scale = 1.0f / std::sqrt(static_cast<float>(head_dim));  // rsqrt(float(head_dim))
-  const bool fast = dtype != TH_F32 && head_dim == th::fa::D && aligned16(q) && aligned16(k) &&
-                    aligned16(v) && aligned16(o);
-  if (fast) {
+  const bool vec16 = aligned16(q) && aligned16(k) && aligned16(v) && aligned16(o);
+  const bool fast = dtype != TH_F32 && head_dim == th::fa::D && vec16;
+  // Head dims below 128 (multiples of 8) run the same kernel on copies zero-padded
+  // to 128 columns: the zero columns add nothing to Q.K^T and give zero O columns,
+  // so the result is that of the narrower head (with its own 1/sqrt(D) scale).
+  // Half the MFMA work is padding, against a general kernel ~500x slower
+  // (measured for D = 64, S = 2048-4096).
+  const bool pad = dtype != TH_F32 && head_dim < th::fa::D && head_dim % 8 == 0 && vec16;
+  if (fast || pad) {
     const uint64_t nqb = (seq_len + th::fa::BQ - 1) / th::fa::BQ;
     const uint64_t blocks = nqb * batch * num_heads;
     if (blocks > 0x7fffffffu) return fail(TH_KERNEL_ERROR, "attention_prefill: grid too large");
@@ -526,13 +557,38 @@ int th_attention_prefill(const void* q, const void* k, const void* v, void* o, u
     auto K = static_cast<const uint16_t*>(k);
     auto V = static_cast<const uint16_t*>(v);
     auto O = static_cast<uint16_t*>(o);
+    const uint64_t rows_q = static_cast<uint64_t>(batch) * seq_len * num_heads;
+    const uint64_t rows_kv = static_cast<uint64_t>(batch) * num_kv_heads * max_seq;
+    if (pad) {
+      constexpr uint64_t RB = th::fa::D * 2;  // bytes of a padded row
+      void* ws = nullptr;
+      TH_TRY(th::stream_scratch(as_stream(s), (2 * rows_q + 2 * rows_kv) * RB, &ws));
+      auto* base = static_cast<uint16_t*>(ws);
+      uint16_t* Qp = base;
+      uint16_t* Op = Qp + rows_q * th::fa::D;
+      uint16_t* Kp = Op + rows_q * th::fa::D;
+      uint16_t* Vp = Kp + rows_kv * th::fa::D;
+      copy_rows16_launch(q, head_dim, Qp, th::fa::D, head_dim, rows_q, as_stream(s));
+      copy_rows16_launch(k, head_dim, Kp, th::fa::D, head_dim, rows_kv, as_stream(s));
+      copy_rows16_launch(v, head_dim, Vp, th::fa::D, head_dim, rows_kv, as_stream(s));
+      TH_TRY(launch_status("attention_prefill padding"));
+      Q = Qp;
+      K = Kp;
+      V = Vp;
+      O = Op;
+    }
     if (dtype == TH_BF16)
       hipLaunchKernelGGL(th::attn_prefill_dma128<th::kBF16>, grid, block, 0, as_stream(s), Q, K, V, O,
                          batch, seq_len, start_pos, max_seq, num_heads, num_kv_heads, sl2);
     else
       hipLaunchKernelGGL(th::attn_prefill_dma128<th::kF16>, grid, block, 0, as_stream(s), Q, K, V, O,
                          batch, seq_len, start_pos, max_seq, num_heads, num_kv_heads, sl2);
-    return launch_status("attention_prefill launch");
+    TH_TRY(launch_status("attention_prefill launch"));
+    if (pad) {
+      copy_rows16_launch(O, th::fa::D, o, head_dim, head_dim, rows_q, as_stream(s));
+      return launch_status("attention_prefill unpadding");
+    }
+    return TH_OK;
   }
   return attn_general_launch(q, k, v, o, batch, seq_len, start_pos, max_seq, start_pos + seq_len,
                              head_dim, num_heads, num_kv_heads, 1, scale, dtype, as_stream(s));
