@@ -464,7 +464,10 @@ def test_decode_golden_vectors(dev, stream, golden):
     (1, 1, 0, 4, 4, 128, True),       # one position
     (3, 513, 7, 16, 1, 128, True),    # G=16, chunk boundary + 1
     (2, 1024, 0, 8, 8, 128, False),   # MHA
-    (2, 777, 0, 4, 2, 64, False),     # head_dim 64 -> general kernel
+    (2, 777, 0, 4, 2, 64, False),     # head_dim 64: live rows zero-padded to 128, split
+    (1, 9000, 40, 8, 1, 64, True),    # head_dim 64, G=8, rows past seq_len skipped by the copy
+    (64, 600, 0, 8, 8, 96, False),    # head_dim 96, unsplit
+    (1, 300, 0, 4, 2, 60, False),     # head_dim 60 (not a multiple of 8) -> general kernel
     (1, 200, 0, 6, 2, 128, False),   # G=3 -> general kernel
     (1, 4500, 3, 4, 2, 128, False),   # 9 chunks: one batch of 8 partials + 1 in the merge
     (1, 66000, 0, 2, 1, 128, True),   # 129 chunks: the merge stages partials in two passes

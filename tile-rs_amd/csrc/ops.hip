@@ -500,29 +500,33 @@ int th_attention(const void* q, const void* k, const void* v, void* o, uint32_t 
                              scale, dtype, as_stream(s));
 }
 
-// Copy `rows` rows of 16-bit values in 16-byte pieces: dst row r = src row r
-// (src_ld8 pieces) followed by zeros up to dst_ld8 pieces, or (cols8 < dst_ld8
-// pieces of the source copied) the first cols8 pieces of a wider source row.
+// Copy rows of 16-bit values in 16-byte pieces.  Destination row i (of `rows`)
+// is source row (i / grp) * src_grp + i % grp: the first `grp` rows of every
+// group of `src_grp` source rows.  Each row takes the first cols8 pieces of the
+// source row (src_ld8 pieces long) and zeros up to dst_ld8 pieces.
 __global__ void __launch_bounds__(256)
 copy_rows16(const uint4* __restrict__ src, uint32_t src_ld8, uint4* __restrict__ dst,
-            uint32_t dst_ld8, uint32_t cols8, uint64_t rows) {
+            uint32_t dst_ld8, uint32_t cols8, uint64_t rows, uint32_t grp, uint32_t src_grp) {
   const uint64_t n = rows * dst_ld8;
   for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * 256u + threadIdx.x; i < n;
        i += static_cast<uint64_t>(gridDim.x) * 256u) {
     const uint64_t r = i / dst_ld8;
+    const uint64_t sr = (r / grp) * src_grp + r % grp;
     const uint32_t c = static_cast<uint32_t>(i % dst_ld8);
-    dst[i] = c < cols8 ? src[r * src_ld8 + c] : make_uint4(0, 0, 0, 0);
+    dst[i] = c < cols8 ? src[sr * src_ld8 + c] : make_uint4(0, 0, 0, 0);
   }
 }
 
 static void copy_rows16_launch(const void* src, uint32_t src_ld, void* dst, uint32_t dst_ld,
-                               uint32_t cols, uint64_t rows, hipStream_t s) {
+                               uint32_t cols, uint64_t rows, hipStream_t s, uint32_t grp = 0,
+                               uint32_t src_grp = 0) {
   const uint64_t n = rows * (dst_ld / 8);
   const uint32_t blocks =
       static_cast<uint32_t>(std::min<uint64_t>((n + 255) / 256, 8ull * current_cu_count()));
+  if (grp == 0) grp = src_grp = 0xffffffffu;  // plain: row i <- row i
   hipLaunchKernelGGL(copy_rows16, dim3(std::max(blocks, 1u)), dim3(256), 0, s,
                      static_cast<const uint4*>(src), src_ld / 8, static_cast<uint4*>(dst),
-                     dst_ld / 8, cols / 8, rows);
+                     dst_ld / 8, cols / 8, rows, grp, src_grp);
 }
 
 int th_attention_prefill(const void* q, const void* k, const void* v, void* o, uint32_t batch,
@@ -674,10 +678,48 @@ int th_attention_decode(const void* q, const void* k, const void* v, void* o, ui
   }
   const bool fast = decode_fast(head_dim, num_heads, num_kv_heads, dtype) && aligned16(q) &&
                     aligned16(k) && aligned16(v);
-  if (!fast) {
+  // Head dims below 128 (multiples of 8): Q and the live rows of K and V (the first
+  // seq_len of each (batch, kv_head)) are copied zero-padded to 128 columns, the MFMA
+  // decode runs on the copies (zero columns change no score and give zero outputs)
+  // and O's first head_dim columns are copied back; a split then takes its
+  // workspace from the library's scratch.  The copies read K and V once more, but
+  // the general kernel is 20-70x slower (measured for head_dim 64).
+  const bool pad = !fast && head_dim < th::dec::D && head_dim % 8 == 0 &&
+                   decode_fast(th::dec::D, num_heads, num_kv_heads, dtype) && aligned16(q) &&
+                   aligned16(k) && aligned16(v) && aligned16(o);
+  if (!fast && !pad) {
     // one query per (batch, head): Q/O [B][1][NH][D]
     return attn_general_launch(q, k, v, o, batch, 1, 0, max_seq, seq_len, head_dim, num_heads,
                                num_kv_heads, 0, scale, dtype, as_stream(s));
+  }
+  const void* Q = q;
+  const void* K = k;
+  const void* V = v;
+  void* O = o;
+  if (pad) {
+    constexpr uint64_t RB = th::dec::D * 2;
+    const uint64_t rows_q = static_cast<uint64_t>(batch) * num_heads;
+    const uint64_t rows_kv = static_cast<uint64_t>(batch) * num_kv_heads * seq_len;
+    void* pw = nullptr;
+    TH_TRY(th::stream_scratch(as_stream(s), (2 * rows_q + 2 * rows_kv) * RB, &pw));
+    auto* base = static_cast<uint16_t*>(pw);
+    uint16_t* Qp = base;
+    uint16_t* Op = Qp + rows_q * th::dec::D;
+    uint16_t* Kp = Op + rows_q * th::dec::D;
+    uint16_t* Vp = Kp + rows_kv * th::dec::D;
+    copy_rows16_launch(q, head_dim, Qp, th::dec::D, head_dim, rows_q, as_stream(s));
+    copy_rows16_launch(k, head_dim, Kp, th::dec::D, head_dim, rows_kv, as_stream(s), seq_len,
+                       max_seq);
+    copy_rows16_launch(v, head_dim, Vp, th::dec::D, head_dim, rows_kv, as_stream(s), seq_len,
+                       max_seq);
+    TH_TRY(launch_status("attention_decode padding"));
+    Q = Qp;
+    K = Kp;
+    V = Vp;
+    O = Op;
+    max_seq = seq_len;  // the copies hold the live rows only
+    workspace = nullptr;
+    workspace_bytes = 0;
   }
   const uint64_t items = static_cast<uint64_t>(batch) * num_kv_heads;
   if (items > 0x7fffffffu) return fail(TH_KERNEL_ERROR, "attention_decode: grid too large");
@@ -687,7 +729,7 @@ int th_attention_decode(const void* q, const void* k, const void* v, void* o, ui
   if (blocks > 0x7fffffffu) return fail(TH_KERNEL_ERROR, "attention_decode: grid too large");
   // The workspace contract does not depend on the split chosen here: callers
   // size it with th_attention_decode_workspace_size (one record per chunk).
-  const size_t need = th_attention_decode_workspace_size(batch, seq_len, head_dim, num_heads,
+  const size_t need = th_attention_decode_workspace_size(batch, seq_len, th::dec::D, num_heads,
                                                          num_kv_heads);
   void* ws = workspace;
   if (ws) {
@@ -702,23 +744,31 @@ int th_attention_decode(const void* q, const void* k, const void* v, void* o, ui
   const uint32_t g = num_heads / num_kv_heads;
   float* wsf = static_cast<float*>(ws);
   if (dtype == TH_BF16)
-    decode_launch_g<th::kBF16>(g, q, k, v, o, wsf, batch, seq_len, max_seq, num_heads,
+    decode_launch_g<th::kBF16>(g, Q, K, V, O, wsf, batch, seq_len, max_seq, num_heads,
                                num_kv_heads, n_split, cps, sl2, as_stream(s));
   else
-    decode_launch_g<th::kF16>(g, q, k, v, o, wsf, batch, seq_len, max_seq, num_heads,
+    decode_launch_g<th::kF16>(g, Q, K, V, O, wsf, batch, seq_len, max_seq, num_heads,
                               num_kv_heads, n_split, cps, sl2, as_stream(s));
   TH_TRY(launch_status("attention_decode launch"));
-  if (n_split == 1) return TH_OK;  // each workgroup covered its whole sequence and wrote O
-  const dim3 cgrid(batch * num_heads), cblock(th::dec::CT);
-  if (dtype == TH_BF16)
-    hipLaunchKernelGGL(th::attn_decode_combine<th::kBF16>, cgrid, cblock, 0, as_stream(s),
-                       static_cast<const float*>(ws), static_cast<uint16_t*>(o), num_heads,
-                       num_kv_heads, n_split);
-  else
-    hipLaunchKernelGGL(th::attn_decode_combine<th::kF16>, cgrid, cblock, 0, as_stream(s),
-                       static_cast<const float*>(ws), static_cast<uint16_t*>(o), num_heads,
-                       num_kv_heads, n_split);
-  return launch_status("attention_decode combine launch");
+  // with one split each workgroup covered its whole sequence and wrote O
+  if (n_split > 1) {
+    const dim3 cgrid(batch * num_heads), cblock(th::dec::CT);
+    if (dtype == TH_BF16)
+      hipLaunchKernelGGL(th::attn_decode_combine<th::kBF16>, cgrid, cblock, 0, as_stream(s),
+                         static_cast<const float*>(ws), static_cast<uint16_t*>(O), num_heads,
+                         num_kv_heads, n_split);
+    else
+      hipLaunchKernelGGL(th::attn_decode_combine<th::kF16>, cgrid, cblock, 0, as_stream(s),
+                         static_cast<const float*>(ws), static_cast<uint16_t*>(O), num_heads,
+                         num_kv_heads, n_split);
+    TH_TRY(launch_status("attention_decode combine launch"));
+  }
+  if (pad) {
+    copy_rows16_launch(O, th::dec::D, o, head_dim, head_dim,
+                       static_cast<uint64_t>(batch) * num_heads, as_stream(s));
+    return launch_status("attention_decode unpadding");
+  }
+  return TH_OK;
 }
 
 int th_fill_random(void* dst, uint64_t n, th_dtype dtype, int dist, float p0, float p1,
