@@ -400,6 +400,11 @@ def test_prefill_golden_vectors(dev, stream, golden):
     (1, 257, 0, 0, 4, 4, 80),      # head_dim 80, padded
     (1, 70, 3, 0, 2, 1, 60),       # head_dim 60 (not a multiple of 8) -> general kernel
     (3, 1, 5, 2, 4, 4, 128),       # single query
+    (1, 64, 0, 0, 2, 2, 128),      # exactly one KV block
+    (1, 130, 0, 0, 2, 1, 128),     # three KV blocks, ragged query block
+    (1, 1500, 100, 7, 4, 4, 128),  # long loop, start_pos not a multiple of 64
+    (1, 100, 37, 3000, 8, 2, 128), # chunk of a long cache (max_seq >> start_pos + S)
+    (1, 200, 300, 4000, 4, 2, 64), # padded head_dim: only live cache rows are copied
 ])
 def test_prefill_shapes(dev, stream, dtype, B, S, start, extra, NH, NKV, Dh):
     rng = np.random.default_rng(S * 7 + start)

@@ -1,0 +1,482 @@
+"""Generate the main loop of the causal GQA prefill kernel (head_dim 128, bf16/f16)
+as gfx950 assembly for one inline-asm statement (prefill_asm.hpp wraps it).
+
+Semantics are those of the reference's fused prefill (causal softmax(Q.K^T *
+rsqrt(D)) . V over positions <= start_pos + query row;
+/root/reference/crates/rustc_codegen_tile/src/mlir_to_msl.rs:10928-11009), computed
+as a flash-attention online softmax in base 2 with lazy rescaling.
+
+Workgroup = 8 waves = 256 query rows of one (batch, head); wave w owns rows
+[32w, 32w+32) and runs two per SIMD.  KV advances 64 positions at a time through
+a ring of NS LDS stages filled by global_load_lds_dwordx4 (no register staging):
+  K stage [4 row groups][16 chunks][16 rows] x 16 B, so the 32 rows x 16 B that
+           one MFMA A operand needs sit at one lane address plus an immediate;
+  V stage [64 kv][128 d] row-major with chunk c of row r at c ^ 4(r & 3), read as
+           V^T with ds_read_b64_tr_b16.
+Per wave and period j (S = scores of 64 kv x 32 queries, as S^T accumulators):
+    MFMA:  S(j+1) = K(j+1).Q^T (16 x v_mfma_f32_32x32x16), then
+           O^T += V(j)^T.P(j)^T (16 MFMAs), fragments prefetched PD ahead
+    VALU:  phase B of block j (rescale check, 16-bit P, second half of the
+           exponentials, row sum, split decision), then phase A of block j+1
+           (causal mask, row max, running max, first half of the exponentials)
+           once S(j+1) is complete; both spread between the MFMAs.
+A block whose largest probability exceeds 1/ratio of the row's running sum also
+gets its 16-bit residual P - hi(P) multiplied in (rare; out of line).  Scores
+are double-buffered by block parity, so the loop is unrolled by two.  One
+s_barrier per period recycles the LDS stage of block j-1 for block j+NS-1.
+
+Register map (VGPRs only; the asm statement clobbers v16-v255, s48-s95):
+  v16 v17 v18 DMA offsets, v19 v20 temps
+  v[32:63] S (even blocks), v[64:95] S (odd blocks), v[96:111] P,
+  v[112:143] fragment ring (8 x 4), v[144:207] O^T (4 d-tiles x 16),
+  v[208:239] Q^T fragments (8 x 4),
+  v240-247 m l lim mblk mnew alpha ls0 ls1, v248 v249 temps, v250 -inf,
+  v251 K address, v252-255 V^T addresses.
+SGPRs: s[48:51] K bases (+0,+64), s[56:57] V base, s58 j, s59 nb-1, s60 stage of
+  block j+1, s61 stage of block j, s62 DMA stage, s63 DMA kv0, s64 s68 temps,
+  s65 stage end, s[66:67] saved exec, s[70:71] grow mask, s[74:75] DMA exec,
+  s[76:77] full exec, s[78:79] split mask, s[80:81] mask compare.
+
+Usage: python gen_prefill.py <out.inc>   (run by the library build)
+"""
+import sys
+from pathlib import Path
+
+NS = 5          # LDS ring stages of 64 KV positions (K 16 KB + V 16 KB each)
+PD = 6          # fragment prefetch distance (fragments in flight ahead of their MFMA)
+RING = 8        # fragment ring size (4 VGPRs per fragment)
+NLD = 4         # DMA instructions per lane per KV block
+
+# operand numbers of the asm statement (see prefill_asm.hpp)
+OP = dict(qp=0, op=1, lim=2, klane=3, vlane=4, krow=5, kcol=6, vrow=7, vcol=8,
+          kbase=9, vbase=10, kvlast=11, nb=12, jd=13, lds=14, wave2k=15,
+          scale=16, ratio=17, ok=18)
+
+
+def o(name):
+    return f"%{OP[name]}"
+
+
+S_BASE = [32, 64]
+P_BASE = 96
+RING_BASE = 112
+O_BASE = 144
+Q_BASE = 208
+STB = 240
+X0, X1, NINF, KADDR = "v248", "v249", "v250", "v251"
+VADDR = [252, 253, 254, 255]
+DK, DV = "v16", ["v17", "v18"]
+TA, TB = "v19", "v20"
+
+
+def st(name):
+    return f"v{STB + ['m', 'l', 'lim', 'mblk', 'mnew', 'alpha', 'ls0', 'ls1'].index(name)}"
+
+
+def names(dt):
+    mn = "v_mfma_f32_32x32x16_bf16" if dt == "bf16" else "v_mfma_f32_32x32x16_f16"
+    cvt = "v_cvt_pk_bf16_f32" if dt == "bf16" else "v_cvt_pk_f16_f32"
+    return mn, cvt
+
+
+def vr(a, b):
+    return f"v[{a}:{b}]"
+
+
+INF = 10 ** 9
+
+
+class Gen:
+    def __init__(self, dt):
+        self.dt = dt
+        self.mn, self.cvt = names(dt)
+        self.uid = 0
+        self.ool = []
+
+    def label(self, base):
+        self.uid += 1
+        return f"L{base}{self.uid}_%="
+
+    # ---------------- fragment streams ----------------
+    def qk_frags(self, par):
+        out = []
+        for i in range(16):
+            ds, kt = i // 2, i % 2
+            d0 = S_BASE[par] + 16 * kt
+            q0 = Q_BASE + 4 * ds
+            src_c = "0" if ds == 0 else vr(d0, d0 + 15)
+            out.append(dict(
+                reads=lambda R, kt=kt, ds=ds: [f"ds_read_b128 {vr(R, R + 3)}, {KADDR} offset:{8192 * kt + 512 * ds}"],
+                mfma=lambda R, d0=d0, q0=q0, src_c=src_c:
+                    f"{self.mn} {vr(d0, d0 + 15)}, {vr(R, R + 3)}, {vr(q0, q0 + 3)}, {src_c}",
+                pdep=None))
+        return out
+
+    def pv_frags(self):
+        out = []
+        for k in range(16):
+            stp, dtl = k // 4, k % 4
+            ob = O_BASE + 16 * dtl
+            pb = P_BASE + 4 * stp
+            va = f"v{VADDR[dtl]}"
+            out.append(dict(
+                reads=lambda R, va=va, stp=stp: [f"ds_read_b64_tr_b16 {vr(R, R + 1)}, {va} offset:{4096 * stp}",
+                                                 f"ds_read_b64_tr_b16 {vr(R + 2, R + 3)}, {va} offset:{4096 * stp + 2048}"],
+                mfma=lambda R, ob=ob, pb=pb: f"{self.mn} {vr(ob, ob + 15)}, {vr(R, R + 3)}, {vr(pb, pb + 3)}, {vr(ob, ob + 15)}",
+                pdep=stp))
+        return out
+
+    # ---------------- softmax ----------------
+    def phase_a(self, par, masked, earliest):
+        """Mask, row max, running max and alpha (grow mask -> s[70:71]),
+        exponentials and row sums of scores 0..15."""
+        S = [f"v{S_BASE[par] + e}" for e in range(32)]
+        scale = o("scale")
+        m_run, m_blk, m_new, alpha = st("m"), st("mblk"), st("mnew"), st("alpha")
+        ls0, ls1 = st("ls0"), st("ls1")
+        L = []
+        if masked:
+            for e in range(32):
+                kt, r = e // 16, e % 16
+                c = 32 * kt + 8 * (r >> 2) + (r & 3)
+                L.append([f"v_cmp_lt_i32 s[80:81], {st('lim')}, {c}", f"v_cndmask_b32 {S[e]}, {S[e]}, {NINF}, s[80:81]"])
+        ch = [m_blk, m_new, alpha]
+        seqs = []
+        for c in range(3):
+            g = list(range(c, 32, 3))
+            seq = [f"v_max3_f32 {ch[c]}, {S[g[0]]}, {S[g[1]]}, {S[g[2]]}"]
+            k = 3
+            while k < len(g):
+                if k + 1 < len(g):
+                    seq.append(f"v_max3_f32 {ch[c]}, {ch[c]}, {S[g[k]]}, {S[g[k + 1]]}")
+                    k += 2
+                else:
+                    seq.append(f"v_max_f32 {ch[c]}, {ch[c]}, {S[g[k]]}")
+                    k += 1
+            seqs.append(seq)
+        for i in range(max(len(q) for q in seqs)):
+            for q in seqs:
+                if i < len(q):
+                    L.append([q[i]])
+        L.append([f"v_max3_f32 {X0}, {m_blk}, {m_new}, {alpha}"])
+        L.append([f"v_mov_b32 {X1}, {X0}", "s_nop 1", f"v_permlane32_swap_b32 {X0}, {X1}", "s_nop 1"])
+        L.append([f"v_max_f32 {X0}, {X0}, {X1}"])
+        L.append([f"v_mul_f32 {m_blk}, {scale}, {X0}"])
+        L.append([f"v_add_f32 {X1}, 0x41000000, {m_run}"])
+        L.append([f"v_max_f32 {X0}, {m_run}, {m_blk}"])
+        L.append([f"v_cmp_gt_f32 s[70:71], {m_blk}, {X1}"])
+        L.append([f"v_cndmask_b32 {m_new}, {m_run}, {X0}, s[70:71]"])
+        L.append([f"v_sub_f32 {X1}, {m_run}, {m_new}"])
+        L.append([f"v_exp_f32 {alpha}, {X1}"])
+        L.append([f"v_mov_b32 {m_run}, {m_new}"])
+        L.append([f"v_mov_b32 {ls0}, 0", f"v_mov_b32 {ls1}, 0"])
+        for g0 in range(0, 16, 4):
+            for e in range(g0, g0 + 4):
+                L.append([f"v_fma_f32 {S[e]}, {S[e]}, {scale}, -{m_new}"])
+            for e in range(g0, g0 + 4):
+                L.append([f"v_exp_f32 {S[e]}, {S[e]}"])
+            for e in range(g0, g0 + 4):
+                L.append([f"v_add_f32 {ls0 if e % 2 == 0 else ls1}, {ls0 if e % 2 == 0 else ls1}, {S[e]}"])
+        return [dict(lines=x, deadline=INF, earliest=earliest) for x in L]
+
+    def phase_b(self, par, pv0):
+        """Rescale check (before the first PV MFMA at slot pv0), P st 0-1, the
+        other 16 exponentials with P st 2-3, l update and split decision."""
+        S = [f"v{S_BASE[par] + e}" for e in range(32)]
+        P = [f"v{P_BASE + q}" for q in range(16)]
+        scale, ratio = o("scale"), o("ratio")
+        m_blk, m_new, alpha, l_run = st("mblk"), st("mnew"), st("alpha"), st("l")
+        ls0, ls1 = st("ls0"), st("ls1")
+        ops = []
+
+        def add(lines, deadline=INF):
+            ops.append(dict(lines=lines, deadline=deadline, earliest=-1))
+
+        def pdl(q):
+            return (pv0 + 4 * (q // 4) - 2) if q % 4 == 3 else INF
+        lg, lb = self.label("grow"), self.label("growb")
+        body = ["s_nop 7", "s_nop 7", "s_nop 7"]
+        for k in range(64):
+            body.append(f"v_mul_f32 v{O_BASE + k}, {alpha}, v{O_BASE + k}")
+        self.ool.append([f"{lg}:"] + body + [f"s_branch {lb}"])
+        add(["s_cmp_lg_u64 s[70:71], 0", f"s_cbranch_scc1 {lg}", f"{lb}:"], pv0 - 1)
+        for q in range(8):
+            add([f"{self.cvt} {P[q]}, {S[2 * q]}, {S[2 * q + 1]}"], pdl(q))
+        for g0 in range(16, 32, 4):
+            for e in range(g0, g0 + 4):
+                add([f"v_fma_f32 {S[e]}, {S[e]}, {scale}, -{m_new}"])
+            for e in range(g0, g0 + 4):
+                add([f"v_exp_f32 {S[e]}, {S[e]}"])
+            for e in range(g0, g0 + 4):
+                add([f"v_add_f32 {ls0 if e % 2 == 0 else ls1}, {ls0 if e % 2 == 0 else ls1}, {S[e]}"])
+            for q in (g0 // 2, g0 // 2 + 1):
+                add([f"{self.cvt} {P[q]}, {S[2 * q]}, {S[2 * q + 1]}"], pdl(q))
+        add([f"v_add_f32 {X0}, {ls0}, {ls1}"])
+        add([f"v_fma_f32 {l_run}, {l_run}, {alpha}, {X0}"])
+        add([f"v_sub_f32 {X0}, {m_blk}, {m_new}"])
+        add([f"v_exp_f32 {X0}, {X0}"])
+        add([f"v_mov_b32 {X1}, {l_run}", f"v_mov_b32 {TA}, {l_run}", "s_nop 1",
+             f"v_permlane32_swap_b32 {X1}, {TA}", "s_nop 1"])
+        add([f"v_add_f32 {X1}, {X1}, {TA}"])
+        add([f"v_mul_f32 {X0}, {ratio}, {X0}"])
+        add([f"v_cmp_gt_f32 s[78:79], {X0}, {X1}"])
+        return ops
+
+    def split_tail(self, par):
+        """Residual PV of the block whose P was just consumed (rare): runs after
+        the period's last MFMA; lo = P - hi(P) overwrites P, fragments use the ring."""
+        ls, lsb = self.label("split"), self.label("splitb")
+        self.ool.append([f"{ls}:"] + self.residual(par) + [f"s_branch {lsb}"])
+        return ["s_cmp_lg_u64 s[78:79], 0", f"s_cbranch_scc1 {ls}", f"{lsb}:"]
+
+    def residual(self, par):
+        S = [f"v{S_BASE[par] + e}" for e in range(32)]
+        P = [f"v{P_BASE + q}" for q in range(16)]
+        out = ["s_waitcnt lgkmcnt(0)", "s_nop 7", "s_nop 7"]
+        for q in range(16):
+            if self.dt == "bf16":
+                out += [f"v_lshlrev_b32 {TA}, 16, {P[q]}", f"v_and_b32 {TB}, 0xffff0000, {P[q]}"]
+            else:
+                out += [f"v_cvt_f32_f16 {TA}, {P[q]}", f"v_lshrrev_b32 {TB}, 16, {P[q]}",
+                        f"v_cvt_f32_f16 {TB}, {TB}"]
+            out += [f"v_sub_f32 {TA}, {S[2 * q]}, {TA}", f"v_sub_f32 {TB}, {S[2 * q + 1]}, {TB}",
+                    f"{self.cvt} {P[q]}, {TA}, {TB}"]
+
+        def rd(k):
+            stp, dtl = k // 4, k % 4
+            R = RING_BASE + 4 * (k % 4)
+            va = f"v{VADDR[dtl]}"
+            return [f"ds_read_b64_tr_b16 {vr(R, R + 1)}, {va} offset:{4096 * stp}",
+                    f"ds_read_b64_tr_b16 {vr(R + 2, R + 3)}, {va} offset:{4096 * stp + 2048}"]
+        out += ["s_nop 2"] + rd(0) + rd(1)
+        for k in range(16):
+            if k + 2 < 16:
+                out += rd(k + 2)
+            out.append(f"s_waitcnt lgkmcnt({2 * min(2, 15 - k)})")
+            stp, dtl = k // 4, k % 4
+            R = RING_BASE + 4 * (k % 4)
+            ob = O_BASE + 16 * dtl
+            pb = P_BASE + 4 * stp
+            out.append(f"{self.mn} {vr(ob, ob + 15)}, {vr(R, R + 3)}, {vr(pb, pb + 3)}, {vr(ob, ob + 15)}")
+            out.append("s_nop 4")
+        out += ["s_nop 7", "s_nop 7", "s_nop 3"]
+        return out
+
+    # ---------------- scheduler ----------------
+    def schedule(self, frags, ops, pre_quota=12):
+        n = len(frags)
+        ring = [RING_BASE + 4 * (f % RING) for f in range(n)]
+        reads = [fr["reads"](ring[f]) for f, fr in enumerate(frags)]
+        tail = [op for op in ops if op["earliest"] >= n]
+        ops = [op for op in ops if op["earliest"] < n]
+        dl = [min(op["deadline"], n - 1) for op in ops]
+        for i in range(len(ops) - 2, -1, -1):
+            dl[i] = min(dl[i], dl[i + 1])
+        out = []
+        issued = min(PD - 1, n)
+        for f in range(issued):
+            out += reads[f]
+        pos = 0
+        p_slot = {}
+
+        def emit_ops(slot, quota):
+            nonlocal pos
+            k = 0
+            while pos < len(ops):
+                op = ops[pos]
+                forced = dl[pos] <= slot
+                if not forced and (k >= quota or op["earliest"] > slot):
+                    break
+                if op["earliest"] > slot:
+                    raise RuntimeError(f"infeasible op {op['lines']} at slot {slot}")
+                out.extend(op["lines"])
+                for ln in op["lines"]:
+                    if ln.startswith(self.cvt):
+                        reg = int(ln.split()[1].rstrip(",")[1:])
+                        if P_BASE <= reg < P_BASE + 16:
+                            p_slot[(reg - P_BASE) // 4] = slot
+                pos += 1
+                k += 1
+        emit_ops(-1, pre_quota)
+        for s in range(n):
+            if issued < n:
+                out += reads[issued]
+                issued += 1
+            later = sum(len(reads[x]) for x in range(s + 1, issued))
+            out.append(f"s_waitcnt lgkmcnt({min(later, 15)})")
+            pdep = frags[s]["pdep"]
+            if pdep is not None and p_slot.get(pdep, -99) >= s - 1:
+                out.append("s_nop 2")
+            out.append(frags[s]["mfma"](ring[s]))
+            rem_ops, rem_slots = len(ops) - pos, n - s
+            emit_ops(s, -(-rem_ops // rem_slots))
+        for op in ops[pos:]:
+            out.extend(op["lines"])
+        if tail:
+            out += ["s_nop 7", "s_nop 7", "s_nop 3"]
+            for op in tail:
+                out.extend(op["lines"])
+        return out
+
+    # ---------------- DMA ----------------
+    def dma_lines(self, masked_exec):
+        """Block s63 into the stage at s62: two K and two V loads per lane."""
+        ex0 = ["s_mov_b64 exec, s[74:75]"] if masked_exec else []
+        ex1 = ["s_mov_b64 exec, s[76:77]"] if masked_exec else []
+        groups = [[f"v_add_u32 {DK}, s63, {o('krow')}", f"v_min_u32 {DK}, {o('kvlast')}, {DK}",
+                   f"v_lshl_add_u32 {DK}, {DK}, 8, {o('kcol')}", f"s_add_u32 s64, s62, {o('wave2k')}"]]
+        for j in range(2):
+            groups.append([f"s_add_u32 m0, s64, {1024 * j}"] + ex0 +
+                          [f"global_load_lds_dwordx4 {DK}, s[{48 + 2 * j}:{49 + 2 * j}]"] + ex1)
+        for j in range(2):
+            groups.append([f"v_add3_u32 {DV[j]}, s63, {o('vrow')}, {4 * j}", f"v_min_u32 {DV[j]}, {o('kvlast')}, {DV[j]}",
+                           f"v_lshl_add_u32 {DV[j]}, {DV[j]}, 8, {o('vcol')}"])
+            groups.append([f"s_add_u32 m0, s64, {16384 + 1024 * j}"] + ex0 +
+                          [f"global_load_lds_dwordx4 {DV[j]}, s[56:57]"] + ex1)
+        return groups
+
+    def rotate(self, sreg):
+        return [f"s_add_u32 {sreg}, {sreg}, 32768", f"s_cmp_ge_u32 {sreg}, s65",
+                f"s_cselect_b32 {sreg}, {o('lds')}, {sreg}"]
+
+    def addr_k(self, sreg):
+        return [f"v_add_u32 {KADDR}, {sreg}, {o('klane')}"]
+
+    def addr_v(self, sreg):
+        out = ["s_add_u32 s68, " + sreg + ", 16384", f"v_add_u32 v{VADDR[0]}, s68, {o('vlane')}"]
+        for d in range(1, 4):
+            out.append(f"v_xor_b32 v{VADDR[d]}, {d << 6}, v{VADDR[0]}")
+        return out
+
+    # ---------------- bodies ----------------
+    def period(self, par, masked):
+        frags = self.qk_frags(1 - par) + self.pv_frags()
+        ops = [dict(lines=g, deadline=12, earliest=-1) for g in self.dma_lines(True)]
+        ops += self.phase_b(par, pv0=16) + self.phase_a(1 - par, masked, earliest=18)
+        pre = self.addr_k("s60") + self.addr_v("s61")
+        body = self.schedule(frags, ops)
+        tail = ["s_nop 7", "s_nop 7"] + self.split_tail(par)
+        return pre + body + tail
+
+    def last(self, par):
+        frags = self.pv_frags()
+        ops = self.phase_b(par, pv0=0)
+        pre = self.addr_v("s61")
+        return pre + self.schedule(frags, ops, pre_quota=10 ** 6) + ["s_nop 7", "s_nop 7"] + self.split_tail(par)
+
+    def pre_body(self):
+        frags = self.qk_frags(0)
+        ops = self.phase_a(0, True, earliest=18)
+        return self.addr_k("s61") + self.schedule(frags, ops)
+
+    def vm_wait_cases(self, sreg_count, cases, tag):
+        out = []
+        ends = self.label(tag + "e")
+        for k in sorted(cases, reverse=True):
+            if k == 0:
+                out += ["s_waitcnt vmcnt(0)"]
+            else:
+                nxt = self.label(tag)
+                out += [f"s_cmp_ge_u32 {sreg_count}, {k}", f"s_cbranch_scc0 {nxt}",
+                        f"s_waitcnt vmcnt({NLD * k})", f"s_branch {ends}", f"{nxt}:"]
+        out.append(f"{ends}:")
+        return out
+
+    def loop_top(self, last_label):
+        out = ["s_cmp_ge_u32 s58, s59", f"s_cbranch_scc1 {last_label}"]
+        # loads issued after block j+1: prologue blocks past it plus the last two
+        # loop DMAs (each iteration issues one, real or with no lanes)
+        out += [f"s_min_u32 s64, {o('nb')}, {NS}", "s_sub_u32 s64, s64, 2", "s_sub_u32 s64, s64, s58",
+                "s_max_i32 s64, s64, 0", "s_min_u32 s68, s58, 2", "s_add_u32 s64, s64, s68"]
+        out += self.vm_wait_cases("s64", list(range(4)), "wl")
+        out += ["s_barrier"]
+        skip = self.label("dsk")
+        out += self.rotate("s62") + ["s_add_u32 s63, s63, 64", "s_mov_b64 s[76:77], exec",
+                                     "s_mov_b64 s[74:75], 0",
+                                     "s_cmp_eq_u32 s58, 0", f"s_cbranch_scc1 {skip}",
+                                     f"s_add_u32 s64, s58, {NS - 1}", f"s_cmp_ge_u32 s64, {o('nb')}",
+                                     f"s_cbranch_scc1 {skip}", "s_mov_b64 s[74:75], exec", f"{skip}:",
+                                     f"v_subrev_u32 {st('lim')}, 64, {st('lim')}"]
+        return out
+
+    def program(self):
+        out = [f"v_mov_b32 {NINF}, 0xff800000"]
+        out += [f"v_mov_b32 v{O_BASE + k}, 0" for k in range(64)]
+        for ds in range(8):
+            q0 = Q_BASE + 4 * ds
+            out.append(f"global_load_dwordx4 {vr(q0, q0 + 3)}, {o('qp')}, off offset:{32 * ds}")
+        out += [f"v_mov_b32 {st('m')}, {NINF}", f"v_mov_b32 {st('l')}, 0", f"v_mov_b32 {st('lim')}, {o('lim')}"]
+        out += ["s_mov_b64 s[48:49], " + o("kbase"), "s_mov_b64 s[56:57], " + o("vbase"),
+                "s_add_u32 s50, s48, 64", "s_addc_u32 s51, s49, 0"]
+        out += [f"s_add_u32 s65, {o('lds')}, {NS * 32768}"]
+        out += [f"s_mov_b32 s62, {o('lds')}", "s_mov_b32 s63, 0"]
+        for s in range(NS):
+            skip = self.label("pd")
+            out += [f"s_cmp_lt_u32 {s}, {o('nb')}", f"s_cbranch_scc0 {skip}"]
+            for g in self.dma_lines(False):
+                out += g
+            out += [f"{skip}:", "s_add_u32 s62, s62, 32768", "s_add_u32 s63, s63, 64"]
+        out += [f"s_min_u32 s64, {o('nb')}, {NS}", "s_sub_u32 s64, s64, 1"]
+        out += self.vm_wait_cases("s64", list(range(NS)), "w0")
+        out += ["s_barrier"]
+        out += [f"s_mov_b32 s61, {o('lds')}", f"s_add_u32 s60, {o('lds')}, 32768",
+                f"s_add_u32 s62, {o('lds')}, {(NS - 2) * 32768}", f"s_mov_b32 s63, {(NS - 2) * 64}",
+                "s_mov_b32 s58, 0", f"s_sub_u32 s59, {o('nb')}, 1"]
+        out += self.pre_body()
+        top = [self.label("top0"), self.label("top1")]
+        last = [self.label("last0"), self.label("last1")]
+        epi = self.label("epi")
+        for par in (0, 1):
+            msk, nxt = self.label("msk"), self.label("nxt")
+            out += [f"{top[par]}:"] + self.loop_top(last[par])
+            out += ["s_add_u32 s64, s58, 1", f"s_cmp_ge_u32 s64, {o('jd')}", f"s_cbranch_scc1 {msk}"]
+            out += self.period(par, False)
+            out += [f"s_branch {nxt}", f"{msk}:"]
+            out += self.period(par, True)
+            out += [f"{nxt}:"] + self.rotate("s60") + self.rotate("s61") + ["s_add_u32 s58, s58, 1"]
+        out += [f"s_branch {top[0]}"]
+        for par in (0, 1):
+            out += [f"{last[par]}:"]
+            out += self.last(par) + [f"s_branch {epi}"]
+        out += [f"{epi}:", "s_waitcnt lgkmcnt(0)", "s_nop 7", "s_nop 7", "s_nop 7",
+                "s_mov_b64 s[66:67], exec"]
+        out += [f"v_mov_b32 v32, {st('l')}", f"v_mov_b32 v33, {st('l')}", "s_nop 1",
+                "v_permlane32_swap_b32 v32, v33", "s_nop 1",
+                "v_add_f32 v32, v32, v33", "v_rcp_f32 v34, v32", "s_nop 0",
+                f"s_mov_b64 exec, {o('ok')}"]
+        for dtl in range(4):
+            for q4 in range(4):
+                a = O_BASE + 16 * dtl + 4 * q4
+                out += [f"v_mul_f32 v{36 + k}, v34, v{a + k}" for k in range(4)]
+                out += [f"{self.cvt} v40, v36, v37", f"{self.cvt} v41, v38, v39",
+                        f"global_store_dwordx2 {o('op')}, v[40:41], off offset:{64 * dtl + 16 * q4}"]
+        out += ["s_mov_b64 exec, s[66:67]"]
+        end = self.label("end")
+        out += [f"s_branch {end}"]
+        for blk in self.ool:
+            out += blk
+        out += [f"{end}:", "s_waitcnt vmcnt(0)"]
+        return out
+
+
+def cstr(lines):
+    return "\\n\\t".join(lines)
+
+
+def main(path):
+    lines = ["// Generated by gen_prefill.py: prefill main loop (gfx950 asm).", "#pragma once"]
+    for dt in ("bf16", "f16"):
+        g = Gen(dt)
+        prog = g.program()
+        lines.append(f'#define TH_PREFILL_ASM_{dt.upper()} "{cstr(prog)}"')
+    clob = [f'"v{k}"' for k in range(16, 256)] + [f'"s{k}"' for k in range(48, 96)]
+    lines.append("#define TH_PREFILL_ASM_CLOBBERS " + ",".join(clob))
+    text = "\n".join(lines) + "\n"
+    p = Path(path)
+    if not p.exists() or p.read_text() != text:
+        p.parent.mkdir(parents=True, exist_ok=True)
+        p.write_text(text)
+
+
+if __name__ == "__main__":
+    main(sys.argv[1])

@@ -15,6 +15,7 @@
 #include <type_traits>
 
 #include "kernels/attention.hpp"
+#include "kernels/prefill_asm.hpp"
 #include "kernels/common.hpp"
 #include "kernels/gemm.hpp"
 #include "kernels/norm.hpp"
@@ -549,53 +550,59 @@ int th_attention_prefill(const void* q, const void* k, const void* v, void* o, u
   if (head_dim == 0) return fail(TH_KERNEL_ERROR, "attention_prefill: head_dim == 0");
   const float scale = 1.0f / std::sqrt(static_cast<float>(head_dim));  // rsqrt(float(head_dim))
   const bool vec16 = aligned16(q) && aligned16(k) && aligned16(v) && aligned16(o);
-  const bool fast = dtype != TH_F32 && head_dim == th::fa::D && vec16;
+  const bool fast = dtype != TH_F32 && head_dim == th::pfa::D && vec16;
   // Head dims below 128 (multiples of 8) run the same kernel on copies zero-padded
   // to 128 columns: the zero columns add nothing to Q.K^T and give zero O columns,
   // so the result is that of the narrower head (with its own 1/sqrt(D) scale).
   // Half the MFMA work is padding, against a general kernel ~500x slower
   // (measured for D = 64, S = 2048-4096).
-  const bool pad = dtype != TH_F32 && head_dim < th::fa::D && head_dim % 8 == 0 && vec16;
+  const bool pad = dtype != TH_F32 && head_dim < th::pfa::D && head_dim % 8 == 0 && vec16;
   if (fast || pad) {
-    const uint64_t nqb = (seq_len + th::fa::BQ - 1) / th::fa::BQ;
+    const uint64_t nqb = (seq_len + th::pfa::BQ - 1) / th::pfa::BQ;
     const uint64_t blocks = nqb * batch * num_heads;
     if (blocks > 0x7fffffffu) return fail(TH_KERNEL_ERROR, "attention_prefill: grid too large");
-    static_assert(th::fa::NT == th::fa2::NT && th::fa::BQ == th::fa2::BQ, "prefill launch shape");
-    const dim3 grid(static_cast<uint32_t>(blocks)), block(th::fa::NT);
+    const dim3 grid(static_cast<uint32_t>(blocks)), block(th::pfa::NT);
     const float sl2 = scale * th::kLog2e;
     auto Q = static_cast<const uint16_t*>(q);
     auto K = static_cast<const uint16_t*>(k);
     auto V = static_cast<const uint16_t*>(v);
     auto O = static_cast<uint16_t*>(o);
+    uint32_t kv_rows = max_seq;   // cache rows per (batch, kv head) seen by the kernel
     const uint64_t rows_q = static_cast<uint64_t>(batch) * seq_len * num_heads;
-    const uint64_t rows_kv = static_cast<uint64_t>(batch) * num_kv_heads * max_seq;
     if (pad) {
-      constexpr uint64_t RB = th::fa::D * 2;  // bytes of a padded row
+      // Only the live cache rows (positions < start_pos + seq_len) are read, so only
+      // those are copied: the padded cache holds kv_len rows per (batch, kv head).
+      const uint32_t kv_len = start_pos + seq_len;
+      const uint64_t rows_kv = static_cast<uint64_t>(batch) * num_kv_heads * kv_len;
+      constexpr uint64_t RB = th::pfa::D * 2;  // bytes of a padded row
       void* ws = nullptr;
       TH_TRY(th::stream_scratch(as_stream(s), (2 * rows_q + 2 * rows_kv) * RB, &ws));
       auto* base = static_cast<uint16_t*>(ws);
       uint16_t* Qp = base;
-      uint16_t* Op = Qp + rows_q * th::fa::D;
-      uint16_t* Kp = Op + rows_q * th::fa::D;
-      uint16_t* Vp = Kp + rows_kv * th::fa::D;
-      copy_rows16_launch(q, head_dim, Qp, th::fa::D, head_dim, rows_q, as_stream(s));
-      copy_rows16_launch(k, head_dim, Kp, th::fa::D, head_dim, rows_kv, as_stream(s));
-      copy_rows16_launch(v, head_dim, Vp, th::fa::D, head_dim, rows_kv, as_stream(s));
+      uint16_t* Op = Qp + rows_q * th::pfa::D;
+      uint16_t* Kp = Op + rows_q * th::pfa::D;
+      uint16_t* Vp = Kp + rows_kv * th::pfa::D;
+      copy_rows16_launch(q, head_dim, Qp, th::pfa::D, head_dim, rows_q, as_stream(s));
+      copy_rows16_launch(k, head_dim, Kp, th::pfa::D, head_dim, rows_kv, as_stream(s), kv_len,
+                         max_seq);
+      copy_rows16_launch(v, head_dim, Vp, th::pfa::D, head_dim, rows_kv, as_stream(s), kv_len,
+                         max_seq);
       TH_TRY(launch_status("attention_prefill padding"));
       Q = Qp;
       K = Kp;
       V = Vp;
       O = Op;
+      kv_rows = kv_len;
     }
     if (dtype == TH_BF16)
-      hipLaunchKernelGGL(th::attn_prefill_dma128<th::kBF16>, grid, block, 0, as_stream(s), Q, K, V, O,
-                         batch, seq_len, start_pos, max_seq, num_heads, num_kv_heads, sl2);
+      hipLaunchKernelGGL(th::pfa::attn_prefill_asm<th::kBF16>, grid, block, 0, as_stream(s), Q, K, V,
+                         O, batch, seq_len, start_pos, kv_rows, num_heads, num_kv_heads, sl2);
     else
-      hipLaunchKernelGGL(th::attn_prefill_dma128<th::kF16>, grid, block, 0, as_stream(s), Q, K, V, O,
-                         batch, seq_len, start_pos, max_seq, num_heads, num_kv_heads, sl2);
+      hipLaunchKernelGGL(th::pfa::attn_prefill_asm<th::kF16>, grid, block, 0, as_stream(s), Q, K, V,
+                         O, batch, seq_len, start_pos, kv_rows, num_heads, num_kv_heads, sl2);
     TH_TRY(launch_status("attention_prefill launch"));
     if (pad) {
-      copy_rows16_launch(O, th::fa::D, o, head_dim, head_dim, rows_q, as_stream(s));
+      copy_rows16_launch(O, th::pfa::D, o, head_dim, head_dim, rows_q, as_stream(s));
       return launch_status("attention_prefill unpadding");
     }
     return TH_OK;

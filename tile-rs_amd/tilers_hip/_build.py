@@ -97,8 +97,22 @@ def build_examples(verbose: bool = False) -> list:
     return built
 
 
+GENERATED = [
+    # (generator script, output) -- generated device code included by ops.hip
+    (CSRC / "kernels" / "gen_prefill.py", CSRC / "kernels" / "gen" / "prefill_asm.inc"),
+]
+
+
+def generate() -> None:
+    """Run the code generators (they rewrite their output only when it changes)."""
+    import sys
+    for script, out in GENERATED:
+        _run([sys.executable, str(script), str(out)])
+
+
 def build(verbose: bool = False) -> Path:
     """Compile every source and link the shared library; returns its path."""
+    generate()
     OBJ_DIR.mkdir(parents=True, exist_ok=True)
     LIB_DIR.mkdir(parents=True, exist_ok=True)
     jobs = []
