@@ -9,8 +9,12 @@ already resident in HBM (generated on the device by th_fill_random with seed
 JSON line.  Bandwidth-bound configs rotate input/output sets totalling more
 than 256 MB so the Infinity Cache cannot serve them.
 
-Timing: W untimed steps, then K steps bracketed by HIP events on the stream the
-kernels run on (stream synchronized on both sides); ms_per_step = elapsed / K.
+Timing: a clock-settle phase (steps run until --settle-ms of wall time have
+passed: MI355X ramps its clock over the first ~100 ms of sustained MFMA work, and
+a cold 4096^3 GEMM step takes 140-160 us against ~123 us settled), then W untimed
+steps, then K steps bracketed by stream synchronization, each step between its
+own pair of HIP events on the stream the kernels run on; ms_per_step is the
+median step (the mean is reported beside it).
 roofline.achieved = algorithmic work per step / ms_per_step (the step is one
 kernel launch except decode, which is the split kernel plus a small combine).
 cpu_baseline times the CPU oracle (test infrastructure, never the measured
@@ -373,7 +377,17 @@ def measured_traffic(name: str):
         return None
 
 
-def run(name: str, steps: int, warmup: int, cpu_seconds: float) -> dict:
+def cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def run(name: str, steps: int, warmup: int, cpu_seconds: float, settle_ms: float) -> dict:
     import tilers_hip as th
     w = WORKLOADS[name]()
     dev = th.HipDevice(0)
@@ -381,30 +395,40 @@ def run(name: str, steps: int, warmup: int, cpu_seconds: float) -> dict:
     log(f"[bench] {name}: setup on {dev.name()} ({dev.arch()})")
     w.setup(th, dev, s)
     s.synchronize()
+    settle_steps, t0 = 0, time.perf_counter()
+    while (time.perf_counter() - t0) * 1e3 < settle_ms:
+        for _ in range(10):
+            w.step(th, s, settle_steps)
+            settle_steps += 1
+        s.synchronize()
+    settle_wall = (time.perf_counter() - t0) * 1e3
     for i in range(warmup):
         w.step(th, s, i)
     s.synchronize()
-    e0, e1 = th.HipEvent(), th.HipEvent()
-    e0.record(s)
+    ev = [th.HipEvent() for _ in range(steps + 1)]
+    ev[0].record(s)
     for i in range(steps):
         w.step(th, s, warmup + i)
-    e1.record(s)
-    e1.synchronize()
+        ev[i + 1].record(s)
+    ev[-1].synchronize()
     s.synchronize()
-    ms = e0.elapsed_ms(e1) / steps
+    per = sorted(ev[i].elapsed_ms(ev[i + 1]) for i in range(steps))
+    ms = per[steps // 2] if steps % 2 else 0.5 * (per[steps // 2 - 1] + per[steps // 2])
+    ms_mean = ev[0].elapsed_ms(ev[-1]) / steps
     work = w.work()
     if w.unit == "TFLOP/s":
         value, peak = work / (ms * 1e-3) / 1e12, PEAK_MFMA_TFLOPS
     else:
         value, peak = work / (ms * 1e-3) / 1e9, PEAK_HBM_GBS
-    log(f"[bench] {name}: {ms * 1e3:.1f} us/step, {value:.1f} {w.unit} ({value / peak:.1%} of peak)")
+    log(f"[bench] {name}: median {ms * 1e3:.1f} us/step (mean {ms_mean * 1e3:.1f}, settle "
+        f"{settle_steps} steps / {settle_wall:.0f} ms), {value:.1f} {w.unit} ({value / peak:.1%} of peak)")
     cpu = None
     if cpu_seconds > 0:
         from oracle import oracle as orc
         log(f"[bench] {name}: timing the CPU oracle for ~{cpu_seconds:.0f} s")
         cv, sample = w.cpu_sample(th, s, cpu_seconds)
         cpu = {"value": round(cv, 6), "unit": w.unit, "cores": orc.num_threads(), "kind": "port",
-               "sample": sample}
+               "sample": sample, "cpu_model": cpu_model()}
     return {
         "metric": METRIC,
         "value": round(value, 3),
@@ -413,6 +437,9 @@ def run(name: str, steps: int, warmup: int, cpu_seconds: float) -> dict:
         "steps": steps,
         "warmup": warmup,
         "ms_per_step": round(ms, 6),
+        "ms_per_step_mean": round(ms_mean, 6),
+        "timing": {"statistic": "median of per-step HIP events", "settle_steps": settle_steps,
+                   "settle_ms": round(settle_wall, 1)},
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -433,6 +460,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=200)
     ap.add_argument("--config", default="gemm", choices=sorted(WORKLOADS) + ["all"])
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--settle-ms", type=float, default=300.0,
+                    help="wall time of untimed steps before the warmup (clock ramp)")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -442,7 +471,8 @@ def main() -> int:
         return 2
     names = list(BENCH_LINES) if args.config == "all" else [args.config]
     for n in names:
-        print(json.dumps(run(n, args.steps, args.warmup, args.cpu_seconds)), flush=True)
+        print(json.dumps(run(n, args.steps, args.warmup, args.cpu_seconds, args.settle_ms)),
+              flush=True)
     return 0
 
 
