@@ -98,6 +98,13 @@ int th_malloc(th_device dev, size_t bytes, void** dptr);
 int th_free(th_device dev, void* dptr);
 int th_memcpy_htod_async(void* dst, const void* src, size_t bytes, th_stream s);
 int th_memcpy_dtoh_async(void* dst, const void* src, size_t bytes, th_stream s);
+/* Blocking copies with the semantics of the reference CUDA HAL's
+ * cuMemcpyHtoD / cuMemcpyDtoH (crates/tile_hal/src/cuda.rs:181-199): they return
+ * once the data has arrived.  They run on the null stream, which does not wait
+ * for work on streams from th_stream_create (non-blocking): synchronize such a
+ * stream first when it may still write (or read) the device buffer. */
+int th_memcpy_htod(void* dst, const void* src, size_t bytes);
+int th_memcpy_dtoh(void* dst, const void* src, size_t bytes);
 int th_memcpy_dtod_async(void* dst, const void* src, size_t bytes, th_stream s);
 int th_memset_async(void* dst, int value, size_t bytes, th_stream s);
 
@@ -195,7 +202,8 @@ int th_attention_prefill(const void* q, const void* k, const void* v, void* o, u
  * positions [0, seq_len) are attended.
  * `workspace` may be NULL (the library keeps one per device, grown on demand;
  * calls that overlap on one device then race on it) or a device buffer of at
- * least th_attention_decode_workspace_size(...) bytes. */
+ * least th_attention_decode_workspace_size(...) bytes (non-zero for head_dim 128
+ * and for head dims below 128 that are multiples of 8, which run padded). */
 size_t th_attention_decode_workspace_size(uint32_t batch, uint32_t seq_len, uint32_t head_dim,
                                           uint32_t num_heads, uint32_t num_kv_heads);
 int th_attention_decode(const void* q, const void* k, const void* v, void* o, uint32_t batch,

@@ -128,7 +128,10 @@ def test_softmax_config1_full(dev, stream):
 @pytest.mark.parametrize("rows,cols", [(3, 1000), (5, 77), (7, 1), (2, 5000), (33, 4096),
                                        (4, 256), (1, 64), (9, 17000),
                                        # many rows per wave in the streaming kernel, ragged tail
-                                       (12345, 256), (20001, 128), (9000, 1024), (5000, 60)])
+                                       (12345, 256), (20001, 128), (9000, 1024), (5000, 60),
+                                       # rows of 513-1024 16-byte vectors, >= CU-count rows:
+                                       # the streaming workgroup form (ragged last vector)
+                                       (300, 4096), (1000, 2056)])
 def test_softmax_f32_shapes(dev, stream, rows, cols):
     rng = np.random.default_rng(rows * 131 + cols)
     x = (rng.standard_normal((rows, cols)) * 2).astype(np.float32)
@@ -140,7 +143,8 @@ def test_softmax_f32_shapes(dev, stream, rows, cols):
 
 
 @pytest.mark.parametrize("dtype", [D.F16, D.BF16])
-@pytest.mark.parametrize("rows,cols", [(64, 2048), (3, 100), (4, 8192), (17003, 512)])
+@pytest.mark.parametrize("rows,cols", [(64, 2048), (3, 100), (4, 8192), (17003, 512),
+                                       (512, 8192), (300, 5000)])
 def test_softmax_u16(dev, stream, dtype, rows, cols):
     rng = np.random.default_rng(cols)
     x = rand16(rng, rows * cols, dtype, 2.0)
@@ -478,6 +482,7 @@ def test_decode_golden_vectors(dev, stream, golden):
     (1, 66000, 0, 2, 1, 128, True),   # 129 chunks: the merge stages partials in two passes
     (16, 4196, 0, 16, 8, 128, False),  # 128 items x 9 chunks: splits of several chunks each
     (64, 1500, 0, 8, 8, 128, True),   # 512 items: one workgroup per item walks all chunks
+    (1, 5000, 9, 8, 2, 64, True),     # head_dim 64, split, caller's workspace (padded size)
 ])
 def test_decode_shapes(dev, stream, dtype, B, L, extra, NH, NKV, Dh, ws):
     rng = np.random.default_rng(L * 3 + NH)

@@ -636,7 +636,9 @@ static bool decode_fast(uint32_t head_dim, uint32_t nh, uint32_t nkv, th_dtype d
 size_t th_attention_decode_workspace_size(uint32_t batch, uint32_t seq_len, uint32_t head_dim,
                                           uint32_t num_heads, uint32_t num_kv_heads) {
   (void)num_kv_heads;
-  if (head_dim != th::dec::D) return 0;
+  // head dims below 128 (multiples of 8) run the 128-wide kernel on padded copies
+  if (head_dim > th::dec::D || head_dim == 0 || (head_dim != th::dec::D && head_dim % 8 != 0))
+    return 0;
   return static_cast<size_t>(batch) * num_heads * decode_chunks(seq_len) * (th::dec::D + 2) *
          sizeof(float);
 }
@@ -692,11 +694,12 @@ int th_attention_decode(const void* q, const void* k, const void* v, void* o, ui
   const bool fast = decode_fast(head_dim, num_heads, num_kv_heads, dtype) && aligned16(q) &&
                     aligned16(k) && aligned16(v);
   // Head dims below 128 (multiples of 8): Q and the live rows of K and V (the first
-  // seq_len of each (batch, kv_head)) are copied zero-padded to 128 columns, the MFMA
-  // decode runs on the copies (zero columns change no score and give zero outputs)
-  // and O's first head_dim columns are copied back; a split then takes its
-  // workspace from the library's scratch.  The copies read K and V once more, but
-  // the general kernel is 20-70x slower (measured for head_dim 64).
+  // seq_len of each (batch, kv_head)) are copied zero-padded to 128 columns into the
+  // stream's scratch, the MFMA decode runs on the copies (zero columns change no
+  // score and give zero outputs) and O's first head_dim columns are copied back.
+  // The split partials use the caller's workspace as for head_dim 128.  The copies
+  // read K and V once more, but the general kernel is 20-70x slower (measured for
+  // head_dim 64).
   const bool pad = !fast && head_dim < th::dec::D && head_dim % 8 == 0 &&
                    decode_fast(th::dec::D, num_heads, num_kv_heads, dtype) && aligned16(q) &&
                    aligned16(k) && aligned16(v) && aligned16(o);
@@ -731,8 +734,6 @@ int th_attention_decode(const void* q, const void* k, const void* v, void* o, ui
     V = Vp;
     O = Op;
     max_seq = seq_len;  // the copies hold the live rows only
-    workspace = nullptr;
-    workspace_bytes = 0;
   }
   const uint64_t items = static_cast<uint64_t>(batch) * num_kv_heads;
   if (items > 0x7fffffffu) return fail(TH_KERNEL_ERROR, "attention_decode: grid too large");

@@ -11,6 +11,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdlib>
 #include <cstring>
 #include <mutex>
@@ -68,6 +69,7 @@ int device_scratch(size_t bytes, void** out) {
   std::lock_guard<std::mutex> lock(g_scratch_mu);
   Scratch& s = g_scratch[dev];
   if (s.bytes < bytes) {
+    const size_t old_bytes = s.bytes;
     if (s.ptr) {
       // a stream may still read the old buffer: drain the device first
       TH_TRY(check_hip(hipDeviceSynchronize(), "hipDeviceSynchronize", TH_STREAM_ERROR));
@@ -75,7 +77,9 @@ int device_scratch(size_t bytes, void** out) {
       s.ptr = nullptr;
       s.bytes = 0;
     }
-    size_t want = bytes < (size_t(1) << 20) ? (size_t(1) << 20) : bytes;
+    // grow geometrically so that a slowly growing request (a decode loop adding
+    // one position per step) reallocates O(log n) times, not at every call
+    size_t want = std::max(bytes, std::max(size_t(1) << 20, 2 * old_bytes));
     TH_TRY(check_hip(hipMalloc(&s.ptr, want), "hipMalloc", TH_MEMORY_ERROR));
     s.bytes = want;
   }
@@ -89,6 +93,7 @@ int stream_scratch(hipStream_t stream, size_t bytes, void** out) {
   std::lock_guard<std::mutex> lock(g_scratch_mu);
   Scratch& s = g_stream_scratch[StreamKey{dev, stream}];
   if (s.bytes < bytes) {
+    const size_t old_bytes = s.bytes;
     if (s.ptr) {
       // earlier work on this stream may still read the old buffer
       TH_TRY(check_hip(hipStreamSynchronize(stream), "hipStreamSynchronize", TH_STREAM_ERROR));
@@ -96,7 +101,7 @@ int stream_scratch(hipStream_t stream, size_t bytes, void** out) {
       s.ptr = nullptr;
       s.bytes = 0;
     }
-    size_t want = bytes < (size_t(64) << 10) ? (size_t(64) << 10) : bytes;
+    size_t want = std::max(bytes, std::max(size_t(64) << 10, 2 * old_bytes));
     TH_TRY(check_hip(hipMalloc(&s.ptr, want), "hipMalloc", TH_MEMORY_ERROR));
     s.bytes = want;
   }
@@ -271,6 +276,23 @@ int th_memcpy_dtoh_async(void* dst, const void* src, size_t bytes, th_stream s) 
   if (bytes == 0) return TH_OK;
   return check_hip(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, static_cast<hipStream_t>(s)),
                    "hipMemcpyDtoHAsync", TH_MEMORY_ERROR);
+}
+
+// Blocking copies (the semantics of cuMemcpyHtoD / cuMemcpyDtoH in the reference's
+// CUDA HAL, crates/tile_hal/src/cuda.rs:181-199): hipMemcpy returns once the data
+// has arrived.  It runs on the null stream, which does not wait for work on the
+// library's (non-blocking) streams, so callers order it against such work by
+// synchronizing their stream first.
+int th_memcpy_htod(void* dst, const void* src, size_t bytes) {
+  if (bytes == 0) return TH_OK;
+  return check_hip(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice), "hipMemcpyHtoD",
+                   TH_MEMORY_ERROR);
+}
+
+int th_memcpy_dtoh(void* dst, const void* src, size_t bytes) {
+  if (bytes == 0) return TH_OK;
+  return check_hip(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost), "hipMemcpyDtoH",
+                   TH_MEMORY_ERROR);
 }
 
 int th_memcpy_dtod_async(void* dst, const void* src, size_t bytes, th_stream s) {

@@ -65,6 +65,8 @@ SIGNATURES: dict[str, tuple] = {
     "th_free": (_i, [_vp, _vp]),
     "th_memcpy_htod_async": (_i, [_vp, _vp, _sz, _vp]),
     "th_memcpy_dtoh_async": (_i, [_vp, _vp, _sz, _vp]),
+    "th_memcpy_htod": (_i, [_vp, _vp, _sz]),
+    "th_memcpy_dtoh": (_i, [_vp, _vp, _sz]),
     "th_memcpy_dtod_async": (_i, [_vp, _vp, _sz, _vp]),
     "th_memset_async": (_i, [_vp, _i, _sz, _vp]),
     "th_event_create": (_i, [_pp]),
