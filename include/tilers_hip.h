@@ -211,6 +211,21 @@ int th_attention_decode(const void* q, const void* k, const void* v, void* o, ui
                         uint32_t num_heads, uint32_t num_kv_heads, th_dtype dtype,
                         void* workspace, size_t workspace_bytes, th_stream s);
 
+/* th_attention_decode that allocates nothing.  No counterpart in the reference:
+ * it is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Same result
+ * as th_attention_decode.  The split partials go to a fixed 8 MiB array in each
+ * GPU's memory that is loaded with the library's code object and held until the
+ * process ends; a plan whose partials would need more returns TH_MEMORY_ERROR,
+ * and head dims below 128 (which run on padded copies) return TH_KERNEL_ERROR.
+ * Every call on one GPU shares that GPU's array, so calls that overlap on one
+ * GPU (on different streams, or replays of captured graphs running at the same
+ * time) race on it; calls ordered on one stream do not. */
+int th_attention_decode_static(const void* q, const void* k, const void* v, void* o,
+                               uint32_t batch, uint32_t seq_len, uint32_t max_seq,
+                               uint32_t head_dim, uint32_t num_heads, uint32_t num_kv_heads,
+                               th_dtype dtype, th_stream s);
+
 /* Synthetic data: fill `n` elements with i.i.d. samples, counter-based and
  * seeded (element i depends only on (seed, i)).  dist 0 = Uniform[p0, p1),
  * dist 1 = Normal(mean p0, std p1).  For benchmarks and tests only; no

@@ -11,6 +11,7 @@
 #include <cmath>
 #include <cstdint>
 #include <cstdlib>
+#include <mutex>
 #include <string>
 #include <type_traits>
 
@@ -671,6 +672,71 @@ static void decode_launch_g(uint32_t g, const void* q, const void* k, const void
   }
 }
 
+
+// ---- th_attention_decode_static: the decode without any allocation ----------------
+// Its split partials live in `scratch`, a fixed array in each GPU's memory that comes
+// with the code object (no hipMalloc) and is held until the process ends.  Host code
+// never passes the array's name to a kernel: its per-device address comes from
+// hipGetSymbolAddress, looked up once per device with that device current.
+constexpr size_t kDecodeStaticBytes = size_t(8) << 20;
+static __device__ __align__(256) float scratch[kDecodeStaticBytes / sizeof(float)];
+
+namespace {
+std::mutex g_scratch_addr_mu;
+float* g_scratch_addr[64] = {};
+
+// bytes of the current device set to zero (the decode of an empty sequence)
+__global__ void __launch_bounds__(256) zero_bytes(unsigned char* p, uint64_t n) {
+  for (uint64_t i = static_cast<uint64_t>(blockIdx.x) * 256u + threadIdx.x; i < n;
+       i += static_cast<uint64_t>(gridDim.x) * 256u)
+    p[i] = 0;
+}
+}  // namespace
+
+static int static_scratch_address(float** out) {
+  int dev = 0;
+  TH_TRY(th::check_hip(hipGetDevice(&dev), "hipGetDevice", TH_DEVICE_ERROR));
+  if (dev < 0 || dev >= 64) return fail(TH_DEVICE_ERROR, "attention_decode_static: device ordinal >= 64");
+  std::lock_guard<std::mutex> lock(g_scratch_addr_mu);
+  if (!g_scratch_addr[dev]) {
+    void* p = nullptr;
+    TH_TRY(th::check_hip(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress",
+                         TH_MEMORY_ERROR));
+    if (!p) return fail(TH_MEMORY_ERROR, "attention_decode_static: no address for the scratch array");
+    g_scratch_addr[dev] = static_cast<float*>(p);
+  }
+  *out = g_scratch_addr[dev];
+  return TH_OK;
+}
+
+// The 128-wide MFMA decode: split kernel, then (n_split > 1) the LSE combine of the
+// partials in ws.  Launches only; no allocation.
+static int decode_run(const void* Q, const void* K, const void* V, void* O, float* ws,
+                      uint32_t batch, uint32_t seq_len, uint32_t max_seq, uint32_t num_heads,
+                      uint32_t num_kv_heads, uint32_t n_split, uint32_t cps, float sl2,
+                      th_dtype dtype, hipStream_t s) {
+  const uint32_t g = num_heads / num_kv_heads;
+  if (dtype == TH_BF16)
+    decode_launch_g<th::kBF16>(g, Q, K, V, O, ws, batch, seq_len, max_seq, num_heads,
+                               num_kv_heads, n_split, cps, sl2, s);
+  else
+    decode_launch_g<th::kF16>(g, Q, K, V, O, ws, batch, seq_len, max_seq, num_heads,
+                              num_kv_heads, n_split, cps, sl2, s);
+  TH_TRY(launch_status("attention_decode launch"));
+  // with one split each workgroup covered its whole sequence and wrote O
+  if (n_split > 1) {
+    const dim3 cgrid(batch * num_heads), cblock(th::dec::CT);
+    if (dtype == TH_BF16)
+      hipLaunchKernelGGL(th::attn_decode_combine<th::kBF16>, cgrid, cblock, 0, s, ws,
+                         static_cast<uint16_t*>(O), num_heads, num_kv_heads, n_split);
+    else
+      hipLaunchKernelGGL(th::attn_decode_combine<th::kF16>, cgrid, cblock, 0, s, ws,
+                         static_cast<uint16_t*>(O), num_heads, num_kv_heads, n_split);
+    TH_TRY(launch_status("attention_decode combine launch"));
+  }
+  return TH_OK;
+}
+
 extern "C" {
 
 int th_attention_decode(const void* q, const void* k, const void* v, void* o, uint32_t batch,
@@ -754,35 +820,69 @@ int th_attention_decode(const void* q, const void* k, const void* v, void* o, ui
   } else if (n_split > 1) {
     TH_TRY(th::device_scratch(need, &ws));
   }
-  const float sl2 = scale * th::kLog2e;
-  const uint32_t g = num_heads / num_kv_heads;
-  float* wsf = static_cast<float*>(ws);
-  if (dtype == TH_BF16)
-    decode_launch_g<th::kBF16>(g, Q, K, V, O, wsf, batch, seq_len, max_seq, num_heads,
-                               num_kv_heads, n_split, cps, sl2, as_stream(s));
-  else
-    decode_launch_g<th::kF16>(g, Q, K, V, O, wsf, batch, seq_len, max_seq, num_heads,
-                              num_kv_heads, n_split, cps, sl2, as_stream(s));
-  TH_TRY(launch_status("attention_decode launch"));
-  // with one split each workgroup covered its whole sequence and wrote O
-  if (n_split > 1) {
-    const dim3 cgrid(batch * num_heads), cblock(th::dec::CT);
-    if (dtype == TH_BF16)
-      hipLaunchKernelGGL(th::attn_decode_combine<th::kBF16>, cgrid, cblock, 0, as_stream(s),
-                         static_cast<const float*>(ws), static_cast<uint16_t*>(O), num_heads,
-                         num_kv_heads, n_split);
-    else
-      hipLaunchKernelGGL(th::attn_decode_combine<th::kF16>, cgrid, cblock, 0, as_stream(s),
-                         static_cast<const float*>(ws), static_cast<uint16_t*>(O), num_heads,
-                         num_kv_heads, n_split);
-    TH_TRY(launch_status("attention_decode combine launch"));
-  }
+  TH_TRY(decode_run(Q, K, V, O, static_cast<float*>(ws), batch, seq_len, max_seq, num_heads,
+                    num_kv_heads, n_split, cps, scale * th::kLog2e, dtype, as_stream(s)));
   if (pad) {
     copy_rows16_launch(O, th::dec::D, o, head_dim, head_dim,
                        static_cast<uint64_t>(batch) * num_heads, as_stream(s));
     return launch_status("attention_decode unpadding");
   }
   return TH_OK;
+}
+
+int th_attention_decode_static(const void* q, const void* k, const void* v, void* o,
+                               uint32_t batch, uint32_t seq_len, uint32_t max_seq,
+                               uint32_t head_dim, uint32_t num_heads, uint32_t num_kv_heads,
+                               th_dtype dtype, th_stream s) {
+  if (!valid_dtype(dtype)) return fail(TH_KERNEL_ERROR, "attention_decode_static: unknown dtype");
+  if (batch == 0 || num_heads == 0) return TH_OK;
+  if (!q || !k || !v || !o) return fail(TH_KERNEL_ERROR, "attention_decode_static: null pointer");
+  if (num_kv_heads == 0 || num_heads % num_kv_heads != 0)
+    return fail(TH_KERNEL_ERROR,
+                "attention_decode_static: num_heads must be a multiple of num_kv_heads");
+  if (seq_len > max_seq)
+    return fail(TH_KERNEL_ERROR, "attention_decode_static: seq_len exceeds max_seq");
+  if (head_dim == 0) return fail(TH_KERNEL_ERROR, "attention_decode_static: head_dim == 0");
+  const float scale = 1.0f / std::sqrt(static_cast<float>(head_dim));
+  if (seq_len == 0) {
+    const uint64_t bytes = static_cast<uint64_t>(batch) * num_heads * head_dim * dtype_size(dtype);
+    const uint32_t blocks =
+        static_cast<uint32_t>(std::min<uint64_t>((bytes + 255) / 256, 4ull * current_cu_count()));
+    hipLaunchKernelGGL(zero_bytes, dim3(std::max(blocks, 1u)), dim3(256), 0, as_stream(s),
+                       static_cast<unsigned char*>(o), bytes);
+    return launch_status("attention_decode_static zero");
+  }
+  const bool fast = decode_fast(head_dim, num_heads, num_kv_heads, dtype) && aligned16(q) &&
+                    aligned16(k) && aligned16(v);
+  if (!fast) {
+    if (head_dim < th::dec::D && head_dim % 8 == 0 && dtype != TH_F32)
+      return fail(TH_KERNEL_ERROR,
+                  "attention_decode_static: head_dim " + std::to_string(head_dim) +
+                      " runs on zero-padded copies that need allocated memory; use "
+                      "th_attention_decode");
+    // the general kernel needs no scratch
+    return attn_general_launch(q, k, v, o, batch, 1, 0, max_seq, seq_len, head_dim, num_heads,
+                               num_kv_heads, 0, scale, dtype, as_stream(s));
+  }
+  const uint64_t items = static_cast<uint64_t>(batch) * num_kv_heads;
+  if (items > 0x7fffffffu) return fail(TH_KERNEL_ERROR, "attention_decode_static: grid too large");
+  uint32_t n_split, cps;
+  decode_plan(static_cast<uint32_t>(items), decode_chunks(seq_len), &n_split, &cps);
+  if (items * n_split > 0x7fffffffu)
+    return fail(TH_KERNEL_ERROR, "attention_decode_static: grid too large");
+  float* ws = nullptr;
+  if (n_split > 1) {
+    const uint64_t need =
+        static_cast<uint64_t>(batch) * num_heads * n_split * (th::dec::D + 2) * sizeof(float);
+    if (need > kDecodeStaticBytes)
+      return fail(TH_MEMORY_ERROR, "attention_decode_static: the split partials need " +
+                                       std::to_string(need) + " bytes, more than the " +
+                                       std::to_string(kDecodeStaticBytes) +
+                                       "-byte fixed scratch; use th_attention_decode");
+    TH_TRY(static_scratch_address(&ws));
+  }
+  return decode_run(q, k, v, o, ws, batch, seq_len, max_seq, num_heads, num_kv_heads, n_split,
+                    cps, scale * th::kLog2e, dtype, as_stream(s));
 }
 
 int th_fill_random(void* dst, uint64_t n, th_dtype dtype, int dist, float p0, float p1,

@@ -90,6 +90,8 @@ SIGNATURES: dict[str, tuple] = {
     "th_attention_decode_workspace_size": (_sz, [_u32, _u32, _u32, _u32, _u32]),
     "th_attention_decode": (_i, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32, _i, _vp,
                                  _sz, _vp]),
+    "th_attention_decode_static": (_i, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _u32, _u32, _u32,
+                                        _i, _vp]),
     "th_fill_random": (_i, [_vp, _u64, _i, _i, _f, _f, _u64, _vp]),
     "th_target_name": (_cp, []),
     "th_emit": (_i, [_cp, _sz, C.POINTER(EmitOpts), _ppc, _ppc, _ppc, _ppc]),
