@@ -321,6 +321,89 @@ ORC_EXPORT void orc_causal_mask_f32(const float* x, float* y, int64_t rows, int6
 }
 
 /* ------------------------------------------------------------------------ */
+/* Elementwise f32 ops of the linalg bridge (op table mlir_to_linalg.rs:     */
+/* 423-455): min/max = linalg.min/max; exp, log, tanh, abs, sqrt = the named */
+/* linalg/math ops; rsqrt = math.rsqrt; sigmoid = 1 / (exp(-x) + 1) and      */
+/* relu = maximumf(x, 0) (generic bodies :762-789).  Each value is computed   */
+/* in double from the f32 input and rounded once to f32.                    */
+/* ------------------------------------------------------------------------ */
+enum { ORC_EXP = 0, ORC_LOG, ORC_TANH, ORC_ABS, ORC_SQRT, ORC_RSQRT, ORC_SIGMOID, ORC_RELU,
+       ORC_NEG };
+
+static double unary1(int op, double x) {
+    switch (op) {
+        case ORC_EXP: return exp(x);
+        case ORC_LOG: return log(x);
+        case ORC_TANH: return tanh(x);
+        case ORC_ABS: return fabs(x);
+        case ORC_SQRT: return sqrt(x);
+        case ORC_RSQRT: return 1.0 / sqrt(x);
+        case ORC_SIGMOID: return 1.0 / (exp(-x) + 1.0);
+        case ORC_RELU: return x > 0.0 ? x : 0.0;
+        default: return -x;
+    }
+}
+
+ORC_EXPORT void orc_unary_f32(int op, const float* x, float* y, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) y[i] = (float)unary1(op, (double)x[i]);
+}
+
+/* op 0 = min, 1 = max (exact in f32) */
+ORC_EXPORT void orc_minmax_f32(int op, const float* a, const float* b, float* y, int64_t n) {
+    for (int64_t i = 0; i < n; ++i) y[i] = op ? (a[i] > b[i] ? a[i] : b[i]) : (a[i] < b[i] ? a[i] : b[i]);
+}
+
+/* ------------------------------------------------------------------------ */
+/* Row reductions, dimension 1 of a rows x cols f32 tensor (mlir_to_linalg.rs:*/
+/* 1496-1573): op 0 sum (init 0), 1 max (init -inf), 2 absmax = max of |x|   */
+/* (linalg.abs then the max reduce).  The sum is carried in double and       */
+/* rounded once.  op 3 argmax (:1576-1660): running (value, index) from      */
+/* (-inf, 0), replaced when x > value (ordered compare), so the result is    */
+/* the first index of the maximum and 0 for a row with no value above -inf.   */
+/* argmax writes int32 indices into y's 32-bit slots.                        */
+/* ------------------------------------------------------------------------ */
+ORC_EXPORT void orc_reduce_rows_f32(int op, const float* x, void* y, int64_t rows, int64_t cols) {
+    for (int64_t r = 0; r < rows; ++r) {
+        const float* xr = x + r * cols;
+        if (op == 0) {
+            double s = 0.0;
+            for (int64_t c = 0; c < cols; ++c) s += (double)xr[c];
+            ((float*)y)[r] = (float)s;
+        } else if (op == 3) {
+            float v = bits_f32(0xff800000u);
+            int32_t idx = 0;
+            for (int64_t c = 0; c < cols; ++c)
+                if (xr[c] > v) { v = xr[c]; idx = (int32_t)c; }
+            ((int32_t*)y)[r] = idx;
+        } else {
+            float m = bits_f32(0xff800000u);
+            for (int64_t c = 0; c < cols; ++c) {
+                const float v = op == 2 ? fabsf(xr[c]) : xr[c];
+                if (v > m) m = v;
+            }
+            ((float*)y)[r] = m;
+        }
+    }
+}
+
+/* Transpose (mlir_to_linalg.rs:1458-1490): rows x cols -> cols x rows. */
+ORC_EXPORT void orc_transpose_f32(const float* x, float* y, int64_t rows, int64_t cols) {
+    for (int64_t r = 0; r < rows; ++r)
+        for (int64_t c = 0; c < cols; ++c) y[c * rows + r] = x[r * cols + c];
+}
+
+/* Matvec (mlir_to_linalg.rs:1395-1440): linalg.fill 0 + linalg.matvec,       */
+/* y[r] = sum_c a[r][c] * x[c]; each sum carried in double, rounded once.   */
+ORC_EXPORT void orc_matvec_f32(const float* a, const float* x, float* y, int64_t rows,
+                               int64_t cols) {
+    for (int64_t r = 0; r < rows; ++r) {
+        double s = 0.0;
+        for (int64_t c = 0; c < cols; ++c) s += (double)a[r * cols + c] * (double)x[c];
+        y[r] = (float)s;
+    }
+}
+
+/* ------------------------------------------------------------------------ */
 /* Single-head attention (mlir_to_linalg.rs:1781-1902):                     */
 /*   Kt = transpose(K); S = Q * Kt; S *= (float)(1/sqrt(D)) computed in f64  */
 /*   (:1843); P = softmax(S, dim 1); O = P * V.  Non-causal, f32.            */

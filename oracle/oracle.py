@@ -48,6 +48,11 @@ def lib():
         L.orc_matmul_rows.argtypes = [vp, vp, vp, i64, i64, i64, i, i, i, i, i64, i64]
         L.orc_matmul.argtypes = [vp, vp, vp, i64, i64, i64, i, i, i, i]
         L.orc_causal_mask_f32.argtypes = [vp, vp, i64, i64]
+        L.orc_unary_f32.argtypes = [i, vp, vp, i64]
+        L.orc_minmax_f32.argtypes = [i, vp, vp, vp, i64]
+        L.orc_reduce_rows_f32.argtypes = [i, vp, vp, i64, i64]
+        L.orc_transpose_f32.argtypes = [vp, vp, i64, i64]
+        L.orc_matvec_f32.argtypes = [vp, vp, vp, i64, i64]
         L.orc_rms_norm.argtypes = [vp, vp, i64, i64, C.c_double, i]
         L.orc_silu_mul.argtypes = [vp, vp, vp, i64, i]
         L.orc_rope.argtypes = [vp, vp, i64, i64, i64, i]
@@ -159,6 +164,50 @@ def causal_mask_f32(x: np.ndarray, rows: int, cols: int) -> np.ndarray:
     x = np.ascontiguousarray(x, np.float32)
     y = np.empty_like(x)
     lib().orc_causal_mask_f32(_ptr(x), _ptr(y), rows, cols)
+    return y
+
+
+UNARY = {"exp": 0, "log": 1, "tanh": 2, "abs": 3, "sqrt": 4, "rsqrt": 5, "sigmoid": 6, "relu": 7,
+         "neg": 8}
+ROW_REDUCE = {"sum": 0, "max": 1, "absmax": 2, "argmax": 3}
+
+
+def unary_f32(op: str, x: np.ndarray) -> np.ndarray:
+    """Elementwise f32 op of the linalg bridge (oracle.c orc_unary_f32)."""
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty_like(x)
+    lib().orc_unary_f32(UNARY[op], _ptr(x), _ptr(y), x.size)
+    return y
+
+
+def minmax_f32(op: str, a: np.ndarray, b: np.ndarray) -> np.ndarray:
+    a = np.ascontiguousarray(a, np.float32)
+    b = np.ascontiguousarray(b, np.float32)
+    y = np.empty_like(a)
+    lib().orc_minmax_f32(1 if op == "max" else 0, _ptr(a), _ptr(b), _ptr(y), a.size)
+    return y
+
+
+def reduce_rows_f32(op: str, x: np.ndarray, rows: int, cols: int) -> np.ndarray:
+    """Row sum / max / absmax (f32) or argmax (int32) of a rows x cols tensor."""
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty(rows, np.int32 if op == "argmax" else np.float32)
+    lib().orc_reduce_rows_f32(ROW_REDUCE[op], _ptr(x), _ptr(y), rows, cols)
+    return y
+
+
+def transpose_f32(x: np.ndarray, rows: int, cols: int) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty(rows * cols, np.float32)
+    lib().orc_transpose_f32(_ptr(x), _ptr(y), rows, cols)
+    return y
+
+
+def matvec_f32(a: np.ndarray, x: np.ndarray, rows: int, cols: int) -> np.ndarray:
+    a = np.ascontiguousarray(a, np.float32)
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty(rows, np.float32)
+    lib().orc_matvec_f32(_ptr(a), _ptr(x), _ptr(y), rows, cols)
     return y
 
 

@@ -1,0 +1,12 @@
+module {
+  llvm.func @tile_add(%arg0: !llvm.ptr<1>, %arg1: !llvm.ptr<1>, %arg2: !llvm.ptr<1>) attributes {hacc.entry} {
+    ^bb0:
+    %1 = llvm.mlir.constant(1 : i32) : i32
+    %2 = llvm.mlir.constant(512 : i32) : i32
+    %3 = llvm.call @__tile_load_f32(%arg0, %1, %2) : (!llvm.ptr<1>, i32, i32) -> i32
+    %4 = llvm.call @__tile_load_f32(%arg1, %1, %2) : (!llvm.ptr<1>, i32, i32) -> i32
+    %5 = llvm.call @__tile_add_f32(%3, %3, %4, %1, %2) : (i32, i32, i32, i32, i32) -> i32
+    llvm.call @__tile_store_f32(%arg2, %5, %1, %2) : (!llvm.ptr<1>, i32, i32, i32) -> ()
+    llvm.return
+  }
+}

@@ -1,0 +1,12 @@
+module {
+  llvm.func @tile_rms_large(%arg0: !llvm.ptr<1>, %arg1: !llvm.ptr<1>) attributes {hacc.entry} {
+    ^bb0:
+    %r = llvm.mlir.constant(1 : i32) : i32
+    %c = llvm.mlir.constant(1536 : i32) : i32
+    %eps = llvm.mlir.constant(1.0e-6 : f32) : f32
+    %src = llvm.call @__tile_load_f32(%arg0, %r, %c) : (!llvm.ptr<1>, i32, i32) -> i32
+    %res = llvm.call @__tile_rms_norm_f32(%src, %src, %eps, %r, %c) : (i32, i32, f32, i32, i32) -> i32
+    llvm.call @__tile_store_f32(%arg1, %res, %r, %c) : (!llvm.ptr<1>, i32, i32, i32) -> ()
+    llvm.return
+  }
+}

@@ -1,0 +1,12 @@
+module {
+  llvm.func @tile_cast_rt(%arg0: !llvm.ptr<1>, %arg1: !llvm.ptr<1>) attributes {hacc.entry} {
+    ^bb0:
+    %r = llvm.mlir.constant(1 : i32) : i32
+    %c = llvm.mlir.constant(1024 : i32) : i32
+    %x = llvm.call @__tile_load_f32(%arg0, %r, %c) : (!llvm.ptr<1>, i32, i32) -> i32
+    %h = llvm.call @__tile_cast_f32_f16(%x, %x, %r, %c) : (i32, i32, i32, i32) -> i32
+    %y = llvm.call @__tile_cast_f16_f32(%h, %h, %r, %c) : (i32, i32, i32, i32) -> i32
+    llvm.call @__tile_store_f32(%arg1, %y, %r, %c) : (!llvm.ptr<1>, i32, i32, i32) -> ()
+    llvm.return
+  }
+}

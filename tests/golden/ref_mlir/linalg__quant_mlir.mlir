@@ -1,0 +1,12 @@
+module {
+  llvm.func @sk(%arg0: !llvm.ptr<1>, %arg1: !llvm.ptr<1>) attributes {hacc.entry} {
+    ^bb0:
+    %r = llvm.mlir.constant(1 : i32) : i32
+    %c = llvm.mlir.constant(64 : i32) : i32
+    %s = llvm.mlir.constant(1.250000e-01 : f32) : f32
+    %a = llvm.call @__tile_load_f32(%arg0, %r, %c) : (!llvm.ptr<1>, i32, i32) -> i32
+    %y = llvm.call @__tile_quantize_f32_i8(%a, %a, %s, %r, %c) : (i32, i32, f32, i32, i32) -> i32
+    llvm.call @__tile_store_f32(%arg1, %y, %r, %c) : (!llvm.ptr<1>, i32, i32, i32) -> ()
+    llvm.return
+  }
+}

@@ -1,0 +1,14 @@
+module {
+  llvm.func @tile_sample(%arg0: !llvm.ptr<1>, %arg1: !llvm.ptr<1>) attributes {hacc.entry} {
+    ^bb0:
+    %r = llvm.mlir.constant(2 : i32) : i32
+    %c = llvm.mlir.constant(64 : i32) : i32
+    %temp = llvm.mlir.constant(0.8 : f32) : f32
+    %topp = llvm.mlir.constant(0.9 : f32) : f32
+    %seed = llvm.mlir.constant(42 : i32) : i32
+    %x = llvm.call @__tile_load_f32(%arg0, %r, %c) : (!llvm.ptr<1>, i32, i32) -> i32
+    %y = llvm.call @__tile_sample_top_p_f32(%x, %x, %temp, %topp, %seed, %r, %c) : (i32, i32, f32, f32, i32, i32, i32) -> i32
+    llvm.call @__tile_store_f32(%arg1, %y, %r, %c) : (!llvm.ptr<1>, i32, i32, i32) -> ()
+    llvm.return
+  }
+}

@@ -1,0 +1,12 @@
+module {
+  llvm.func @tile_scale(%arg0: !llvm.ptr<1>, %arg1: !llvm.ptr<1>) attributes {hacc.entry} {
+    ^bb0:
+    %r = llvm.mlir.constant(1 : i32) : i32
+    %c = llvm.mlir.constant(1024 : i32) : i32
+    %s = llvm.mlir.constant(2.500000e-01 : f32) : f32
+    %x = llvm.call @__tile_load_f32(%arg0, %r, %c) : (!llvm.ptr<1>, i32, i32) -> i32
+    %y = llvm.call @__tile_scale_f32(%x, %x, %s, %r, %c) : (i32, i32, f32, i32, i32) -> i32
+    llvm.call @__tile_store_f32(%arg1, %y, %r, %c) : (!llvm.ptr<1>, i32, i32, i32) -> ()
+    llvm.return
+  }
+}

@@ -310,3 +310,56 @@ def test_fused_swiglu_rejects_up_in_another_dtype():
 def test_silu_mul_without_matmul_stays_elementwise():
     out = th.emit((EXAMPLES / "swiglu_mask.mlir").read_text()).source
     assert "elementwise" in out and "kEpiSiluMul" not in out
+
+
+# ---- the reference's own MLIR test inputs (tests/golden/ref_mlir, extracted by
+#      tests/golden/extract_ref_mlir.py from mlir_to_linalg.rs:1912-2990,
+#      mlir_to_gpu.rs tests and tile_spec/tests/cucumber.rs:97-234) ----------------------
+
+REF_MLIR = Path(__file__).resolve().parent / "golden" / "ref_mlir"
+# Model-level ops outside the tile-op hot path (sampling, speculative decoding,
+# gather/scatter, int8 quantization, KV-cache writes, rope variants, head-major GQA
+# attention): the hip target rejects them with an explicit error.
+REF_REJECTED = {
+    "cucumber__sample_top_p_mlir", "cucumber__token_accept_mlir", "gpu__attention_gqa_mlir_0",
+    "gpu__concat_mlir_0", "gpu__gather_mlir_0", "gpu__scatter_mlir_0", "gpu__slice_mlir_0",
+    "gpu__test_gpu_draft_verify_0", "gpu__test_gpu_sample_top_p_0", "gpu__test_gpu_token_accept_0",
+    "gpu__topk_mlir_0", "linalg__dequant_mlir", "linalg__kv_cache_update_kernel",
+    "linalg__kvup_prefill_mlir", "linalg__quant_mlir", "linalg__rope_inplace_kernel",
+    "linalg__rope_prefill_mlir", "linalg__sample_top_p",
+}
+
+
+def _ref_fixtures():
+    return sorted(REF_MLIR.glob("*.mlir"))
+
+
+def test_reference_fixtures_are_present():
+    names = {p.stem for p in _ref_fixtures()}
+    assert len(names) == 87
+    assert REF_REJECTED <= names
+
+
+@pytest.mark.parametrize("path", _ref_fixtures(), ids=lambda p: p.stem)
+def test_reference_fixture_through_hip_target(path):
+    text = path.read_text()
+    if path.stem in REF_REJECTED:
+        with pytest.raises(th.HalError) as e:
+            th.emit(text)
+        assert "unsupported intrinsic" in str(e.value)
+        return
+    out = th.emit(text)
+    assert out.ext == "hip" and "extern \"C\" __global__" in out.source
+    assert th.emit(text).source == out.source   # deterministic
+
+
+def test_new_ops_lower_to_their_entries():
+    out = th.emit((EXAMPLES / "ops_extra.mlir").read_text())
+    src = out.source
+    for evidence in ("logf(", "tanhf(", "fabsf(", "(1.0f / sqrtf(", "(1.0f / (expf(-", "fminf(",
+                     "th::entry::reduce_rows<th::entry::kRowSum>", "kRowMax>", "kRowAbsMax>",
+                     "kRowArgMax>", "th::entry::transpose(", "th::entry::matvec("):
+        assert evidence in src, evidence
+    # reduction outputs: one value per row, the stored view of tile t at t * rows
+    assert "th_tiles, 8u, 1000u, 8ull);" in src
+    assert "th_tiles, 96u, 200u, 200ull, 96ull);" in src

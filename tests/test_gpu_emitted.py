@@ -27,7 +27,7 @@ def launcher(dev):
     lau = dev.create_launcher()
     for stem in ("softmax_rows", "softmax_generic", "matmul_bf16", "matmul_f16_t", "matmul_f32",
                  "attention_f32", "prefill_bf16", "decode_bf16", "swiglu_mask", "rms_norm_rows",
-                 "swiglu_gate_bf16", "matmul_bf16_tiles", "rope", "rows_long"):
+                 "swiglu_gate_bf16", "matmul_bf16_tiles", "rope", "rows_long", "ops_extra"):
         lau.load(_build.example_path(stem), th.KernelMode.GENERAL)
     return lau
 
@@ -272,3 +272,98 @@ def test_unknown_kernel_name_is_a_kernel_error(dev, stream, launcher):
     with pytest.raises(th.HalError) as e:
         launcher.launch("no_such_kernel", th.LaunchGrid.blocks_only(1), [], stream)
     assert e.value.kind == "KernelError" and "no_such_kernel" in str(e.value)
+
+
+# ---- elementwise ops, row reductions, transpose and matvec (examples/ops_extra.mlir) ----
+
+def _ulp_diff(a, b):
+    a = np.asarray(a, np.float32).view(np.int32).astype(np.int64)
+    b = np.asarray(b, np.float32).view(np.int32).astype(np.int64)
+    return np.abs(a - b)
+
+
+@pytest.mark.parametrize("op,ulps", [("log", 2), ("tanh", 2), ("abs", 0), ("sqrt", 1),
+                                     ("rsqrt", 2), ("sigmoid", 2), ("relu", 0)])
+def test_elementwise_unary(dev, stream, launcher, op, ulps):
+    tiles, n = 3, 4 * 256
+    rng = np.random.default_rng(sum(map(ord, op)))
+    x = (rng.standard_normal(tiles * n) * 3).astype(np.float32)
+    if op in ("log", "sqrt", "rsqrt"):
+        x = np.abs(x) + np.float32(1e-3)
+    xb, yb = up(dev, stream, x, D.F32), dev.alloc(x.size, D.F32)
+    launcher.launch(f"ew_{op}", th.LaunchGrid.blocks_only(tiles), [ptr(xb), ptr(yb)], stream)
+    got = yb.copy_to_host(stream)
+    d = _ulp_diff(got, orc.unary_f32(op, x))
+    assert d.max() <= ulps, f"{op}: {d.max()} ulp"
+
+
+def test_elementwise_min_and_four_operand_mul(dev, stream, launcher):
+    tiles = 3
+    rng = np.random.default_rng(31)
+    a, b = (rng.standard_normal(tiles * 1024).astype(np.float32) for _ in range(2))
+    ab, bb, yb = up(dev, stream, a, D.F32), up(dev, stream, b, D.F32), dev.alloc(a.size, D.F32)
+    launcher.launch("ew_min", th.LaunchGrid.blocks_only(tiles), [ptr(ab), ptr(bb), ptr(yb)], stream)
+    assert np.array_equal(yb.copy_to_host(stream), orc.minmax_f32("min", a, b))
+    # mul(silu(g), u) with the four-operand binary form (a, b, rows, cols)
+    g, u = (rng.standard_normal(2 * 1000).astype(np.float32) for _ in range(2))
+    gb, ub, ob = up(dev, stream, g, D.F32), up(dev, stream, u, D.F32), dev.alloc(g.size, D.F32)
+    launcher.launch("ew_silu_mul4", th.LaunchGrid.blocks_only(2), [ptr(gb), ptr(ub), ptr(ob)], stream)
+    assert np.allclose(ob.copy_to_host(stream), orc.silu_mul(g, u), rtol=2e-6, atol=1e-7)
+
+
+@pytest.mark.parametrize("op", ["reduce_sum", "reduce_max", "absmax", "argmax"])
+def test_row_reductions(dev, stream, launcher, op):
+    tiles, R, C = 5, 8, 1000
+    rng = np.random.default_rng(32)
+    x = rng.standard_normal(tiles * R * C).astype(np.float32)
+    xr = x.reshape(tiles * R, C)
+    xr[3, 17] = xr[3, 900] = 9.0          # tied maxima: the first index wins
+    xr[7, :] = -np.inf                      # nothing above -inf: index 0
+    if op == "argmax":
+        xr[7, 5] = -np.inf
+    xb, yb = up(dev, stream, x, D.F32), dev.alloc(tiles * R, D.F32)
+    launcher.launch(f"row_{op}", th.LaunchGrid.blocks_only(tiles), [ptr(xb), ptr(yb)], stream)
+    got = yb.copy_to_host(stream)
+    ref = orc.reduce_rows_f32(op.replace("reduce_", ""), x, tiles * R, C)
+    if op == "argmax":
+        assert np.array_equal(got.view(np.int32), ref)
+        assert got.view(np.int32)[3] == 17 and got.view(np.int32)[7] == 0
+    elif op == "reduce_sum":
+        fin = np.isfinite(ref)
+        bound = np.abs(xr[fin]).sum(axis=1) * 2e-7 + 1e-6
+        assert (np.abs(got[fin] - ref[fin]) <= bound).all()
+        assert np.array_equal(got[~fin], ref[~fin])
+    else:
+        assert np.array_equal(got, ref)
+
+
+def test_row_sum_vectorised_rows(dev, stream, launcher):
+    tiles, R, C = 4, 6, 4096
+    rng = np.random.default_rng(33)
+    xi = rng.integers(-64, 64, tiles * R * C).astype(np.float32)   # exact in any order
+    xb, yb = up(dev, stream, xi, D.F32), dev.alloc(tiles * R, D.F32)
+    launcher.launch("row_sum_aligned", th.LaunchGrid.blocks_only(tiles), [ptr(xb), ptr(yb)], stream)
+    assert np.array_equal(yb.copy_to_host(stream), xi.reshape(-1, C).sum(axis=1))
+
+
+def test_transpose_and_matvec(dev, stream, launcher):
+    tiles = 3
+    rng = np.random.default_rng(34)
+    R, C = 48, 80
+    x = rng.standard_normal(tiles * R * C).astype(np.float32)
+    xb, yb = up(dev, stream, x, D.F32), dev.alloc(x.size, D.F32)
+    launcher.launch("xpose", th.LaunchGrid.blocks_only(tiles), [ptr(xb), ptr(yb)], stream)
+    got = yb.copy_to_host(stream).reshape(tiles, C * R)
+    for t in range(tiles):
+        assert np.array_equal(got[t], orc.transpose_f32(x[t * R * C:(t + 1) * R * C], R, C))
+    R, C = 96, 200
+    a = rng.standard_normal(tiles * R * C).astype(np.float32)
+    v = rng.standard_normal(tiles * C).astype(np.float32)
+    ab, vb, ob = up(dev, stream, a, D.F32), up(dev, stream, v, D.F32), dev.alloc(tiles * R, D.F32)
+    launcher.launch("mv", th.LaunchGrid.blocks_only(tiles), [ptr(ab), ptr(vb), ptr(ob)], stream)
+    got = ob.copy_to_host(stream).reshape(tiles, R)
+    for t in range(tiles):
+        at, vt = a[t * R * C:(t + 1) * R * C], v[t * C:(t + 1) * C]
+        ref = orc.matvec_f32(at, vt, R, C)
+        bound = np.abs(at.reshape(R, C)) @ np.abs(vt) * 2e-7 + 1e-6
+        assert (np.abs(got[t] - ref) <= bound).all()

@@ -1,0 +1,111 @@
+"""BASELINE's five configurations through the unchanged tile_std path: MLIR ->
+th_emit (the `hip` CodegenTarget) -> gfx950 code object -> th_launcher_launch,
+compared with the CPU oracle.  Configs 1, 2, 3 and 5 are checked on every output
+element; config 4 on two (batch, head) pairs in full and the first/last 64 query
+rows of eight more (the oracle on all of it would take minutes)."""
+from __future__ import annotations
+
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import tilers_hip as th
+from oracle import oracle as orc
+from tests.tolerances import assert_attn_close, assert_gemm_close, assert_softmax_close
+from tilers_hip import _build
+
+pytestmark = pytest.mark.gpu
+D = th.TileDtype
+SEED0 = 0x71130000
+
+
+@pytest.fixture(scope="module")
+def launcher(dev):
+    lau = dev.create_launcher()
+    for stem in ("softmax_rows", "config_gemms", "prefill_bf16", "decode_bf16"):
+        lau.load(_build.example_path(stem), th.KernelMode.GENERAL)
+    return lau
+
+
+def ptr(b):
+    return C.c_void_p(b.as_raw_ptr())
+
+
+def rnd(dev, stream, n, dtype, dist, p0, p1, seed):
+    b = dev.alloc(n, dtype)
+    th.fill_random(b, n, dtype, dist, p0, p1, seed, stream)
+    return b
+
+
+def test_config1_softmax_emitted(dev, stream, launcher):
+    rows, cols = 8192, 1024          # 8192 logical 1 x 1024 tiles
+    x = rnd(dev, stream, rows * cols, D.F32, "normal", 0.0, 2.0, SEED0 + 1)
+    y = dev.alloc(rows * cols, D.F32)
+    launcher.launch("softmax_rows_f32", th.LaunchGrid.cuda(rows, cols), [ptr(x), ptr(y)], stream)
+    xh = x.copy_to_host(stream).reshape(rows, cols)
+    assert_softmax_close(y.copy_to_host(stream).reshape(rows, cols), orc.softmax(xh, rows, cols),
+                         "emitted config1")
+
+
+def test_config2_gemm_emitted(dev, stream, launcher):
+    M = N = K = 4096
+    a = rnd(dev, stream, M * K, D.BF16, "uniform", -1.0, 1.0, SEED0 + 2)
+    b = rnd(dev, stream, K * N, D.BF16, "uniform", -1.0, 1.0, SEED0 + 102)
+    c = dev.alloc(M * N, D.F32)
+    launcher.launch("gemm_4096_bf16_acc_f32", th.LaunchGrid.blocks_only(1), [ptr(a), ptr(b), ptr(c)],
+                    stream)
+    ref = orc.matmul(a.copy_to_host(stream), b.copy_to_host(stream), M, K, N, orc.BF16)
+    assert_gemm_close(c.copy_to_host(stream).reshape(M, N), ref.reshape(M, N), "emitted config2")
+
+
+def test_config3_mlp_emitted(dev, stream, launcher):
+    M, K, N = 8192, 4096, 14336
+    a = rnd(dev, stream, M * K, D.F16, "normal", 0.0, 1.0, SEED0 + 3)
+    b = rnd(dev, stream, K * N, D.F16, "normal", 0.0, 0.02, SEED0 + 103)
+    c = dev.alloc(M * N, D.F16)
+    launcher.launch("mlp_up_f16", th.LaunchGrid.blocks_only(1), [ptr(a), ptr(b), ptr(c)], stream)
+    ref = orc.matmul(a.copy_to_host(stream), b.copy_to_host(stream), M, K, N, orc.F16, orc.F32)
+    got = orc.widen(c.copy_to_host(stream), orc.F16).reshape(M, N)
+    assert_gemm_close(got, orc.widen(orc.narrow(ref, orc.F16), orc.F16).reshape(M, N),
+                      "emitted config3", u16_dtype=orc.F16)
+
+
+def test_config4_prefill_emitted(dev, stream, launcher):
+    B, H, S, Dh = 4, 32, 4096, 128     # batch = logical tiles
+    n = B * S * H * Dh
+    q = rnd(dev, stream, n, D.BF16, "normal", 0.0, 1.0, SEED0 + 4)
+    k = rnd(dev, stream, n, D.BF16, "normal", 0.0, 1.0, SEED0 + 104)
+    v = rnd(dev, stream, n, D.BF16, "normal", 0.0, 1.0, SEED0 + 204)
+    o = dev.alloc(n, D.BF16)
+    scal = [C.c_uint32(x) for x in (S, 0, S, Dh, H, H)]
+    launcher.launch("prefill_bf16", th.LaunchGrid.blocks_only(B), [ptr(q), ptr(k), ptr(v), ptr(o)] + scal,
+                    stream)
+    qh, kh, vh = (t.copy_to_host(stream) for t in (q, k, v))
+    got = orc.widen(o.copy_to_host(stream), orc.BF16).reshape(B, S, H, Dh)
+    assert np.isfinite(got).all()
+    for bh in (0, 127):
+        b, h = divmod(bh, H)
+        ref = orc.attention_prefill(qh, kh, vh, orc.BF16, B, S, 0, S, Dh, H, H, bh0=bh, nbh=1)
+        assert_attn_close(got[b, :, h], ref.reshape(B, S, H, Dh)[b, :, h], f"emitted config4 bh={bh}")
+    for bh in (5, 33, 64, 90, 101, 110, 120, 126):
+        b, h = divmod(bh, H)
+        for q0 in (0, S - 64):
+            ref = orc.attention_prefill(qh, kh, vh, orc.BF16, B, S, 0, S, Dh, H, H, bh0=bh, nbh=1,
+                                        q0=q0, nq=64).reshape(B, S, H, Dh)
+            assert_attn_close(got[b, q0:q0 + 64, h], ref[b, q0:q0 + 64, h],
+                              f"emitted config4 bh={bh} rows {q0}..")
+
+
+def test_config5_decode_emitted(dev, stream, launcher):
+    B, NH, NKV, L, Dh = 64, 32, 8, 8192, 128
+    q = rnd(dev, stream, B * NH * Dh, D.BF16, "normal", 0.0, 1.0, SEED0 + 5)
+    k = rnd(dev, stream, B * NKV * L * Dh, D.BF16, "normal", 0.0, 1.0, SEED0 + 105)
+    v = rnd(dev, stream, B * NKV * L * Dh, D.BF16, "normal", 0.0, 1.0, SEED0 + 205)
+    o = dev.alloc(B * NH * Dh, D.BF16)
+    scal = [C.c_uint32(x) for x in (L, L, Dh, NH, NKV)]
+    launcher.launch("decode_bf16", th.LaunchGrid.blocks_only(B), [ptr(q), ptr(k), ptr(v), ptr(o)] + scal,
+                    stream)
+    ref = orc.attention_decode(q.copy_to_host(stream), k.copy_to_host(stream),
+                               v.copy_to_host(stream), orc.BF16, B, L, L, Dh, NH, NKV)
+    assert_attn_close(orc.widen(o.copy_to_host(stream), orc.BF16), ref, "emitted config5")

@@ -319,38 +319,31 @@ def test_matmul_batched(dev, stream):
         assert_gemm_close(got[i], ref, f"batch {i}")
 
 
-GEMM_ROWS = np.r_[0:64, 1000:1032, 2047:2080, 4032:4096]
-
-
 def test_matmul_config2_full(dev, stream):
-    """4096^3, A,B bf16 U[-1,1], C f32, rel 1e-2 (row subset)."""
+    """4096^3, A,B bf16 U[-1,1], C f32, rel 1e-2, every element of C."""
     M = N = K = 4096
     a = device_random(dev, stream, M * K, D.BF16, "uniform", -1.0, 1.0, 0x71130000 + 2)
     b = device_random(dev, stream, K * N, D.BF16, "uniform", -1.0, 1.0, 0x71130000 + 102)
     c = dev.alloc(M * N, D.F32)
     th.matmul(a, b, c, M, K, N, D.BF16, D.F32, False, stream=stream)
-    ah, bh = a.copy_to_host(stream).reshape(M, K), b.copy_to_host(stream)
+    ah, bh = a.copy_to_host(stream), b.copy_to_host(stream)
     got = c.copy_to_host(stream).reshape(M, N)
-    rows = GEMM_ROWS
-    ref = orc.matmul(np.ascontiguousarray(ah[rows]), bh, len(rows), K, N, orc.BF16)
-    assert_gemm_close(got[rows], ref, "config2")
-    assert np.isfinite(got).all()
+    ref = orc.matmul(ah, bh, M, K, N, orc.BF16).reshape(M, N)
+    assert_gemm_close(got, ref, "config2")
 
 
 def test_matmul_config3_full(dev, stream):
-    """M=8192 K=4096 N=14336, f16, f32 acc, C f16 (row subset)."""
+    """M=8192 K=4096 N=14336, f16, f32 acc, C f16, every element of C."""
     M, K, N = 8192, 4096, 14336
     a = device_random(dev, stream, M * K, D.F16, "normal", 0.0, 1.0, 0x71130000 + 3)
     b = device_random(dev, stream, K * N, D.F16, "normal", 0.0, 0.02, 0x71130000 + 103)
     c = dev.alloc(M * N, D.F16)
     th.matmul(a, b, c, M, K, N, D.F16, D.F16, False, stream=stream)
-    ah, bh = a.copy_to_host(stream).reshape(M, K), b.copy_to_host(stream)
+    ah, bh = a.copy_to_host(stream), b.copy_to_host(stream)
     got = orc.widen(c.copy_to_host(stream), orc.F16).reshape(M, N)
-    rows = np.r_[0:32, 4095:4111, 8160:8192]
-    ref = orc.matmul(np.ascontiguousarray(ah[rows]), bh, len(rows), K, N, orc.F16, orc.F32)
+    ref = orc.matmul(ah, bh, M, K, N, orc.F16, orc.F32).reshape(M, N)
     ref16 = orc.widen(orc.narrow(ref, orc.F16), orc.F16)
-    assert_gemm_close(got[rows], ref16, "config3", u16_dtype=orc.F16)
-    assert np.isfinite(got).all()
+    assert_gemm_close(got, ref16, "config3", u16_dtype=orc.F16)
 
 
 # ---- causal mask / single-head attention ----------------------------------------------

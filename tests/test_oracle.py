@@ -377,3 +377,85 @@ def test_decode_single_position_returns_value():
     o = orc.attention_decode(q, k, v, BF16, B, 1, max_seq, D, NH, NKV).reshape(NH, D)
     v0 = orc.widen(v, BF16)[:D]
     assert all(np.array_equal(o[h], v0) for h in range(NH))
+
+
+# ---- elementwise, row reductions, transpose, matvec -----------------------------------------
+
+def _ulps(a, b):
+    a = np.asarray(a, np.float32).view(np.int32).astype(np.int64)
+    b = np.asarray(b, np.float32).view(np.int32).astype(np.int64)
+    return np.abs(a - b)
+
+
+def test_unary_closed_forms():
+    e = np.float32(np.e)
+    assert orc.unary_f32("exp", np.float32([0.0]))[0] == 1.0
+    assert orc.unary_f32("log", np.float32([1.0]))[0] == 0.0
+    assert _ulps(orc.unary_f32("log", np.float32([e, e * e])), [1.0, 2.0]).max() <= 1
+    assert orc.unary_f32("sqrt", np.float32([4.0, 0.25]))[:].tolist() == [2.0, 0.5]
+    assert orc.unary_f32("rsqrt", np.float32([4.0, 0.25]))[:].tolist() == [0.5, 2.0]
+    assert orc.unary_f32("sigmoid", np.float32([0.0]))[0] == 0.5
+    assert orc.unary_f32("tanh", np.float32([0.0]))[0] == 0.0
+    assert orc.unary_f32("abs", np.float32([-3.5, 2.0])).tolist() == [3.5, 2.0]
+    x = np.float32([-2.0, -0.0, 0.0, 1.5])
+    assert orc.unary_f32("relu", x).tolist() == [0.0, 0.0, 0.0, 1.5]
+    assert orc.unary_f32("neg", x).tolist() == [2.0, 0.0, -0.0, -1.5]
+
+
+def test_unary_properties_and_numpy():
+    rng = np.random.default_rng(21)
+    x = (rng.standard_normal(4096) * 3).astype(np.float32)
+    # odd / complementary functions
+    assert np.array_equal(orc.unary_f32("tanh", -x), -orc.unary_f32("tanh", x))
+    s, sm = orc.unary_f32("sigmoid", x), orc.unary_f32("sigmoid", -x)
+    assert np.abs(s.astype(np.float64) + sm - 1.0).max() < 1.2e-7
+    p = np.abs(x) + np.float32(1e-3)
+    assert np.abs(orc.unary_f32("sqrt", p).astype(np.float64) ** 2 / p - 1).max() < 3e-7
+    x64 = x.astype(np.float64)
+    p64 = p.astype(np.float64)
+    for op, ref in (("exp", np.exp(x64)), ("tanh", np.tanh(x64)), ("abs", np.abs(x64)),
+                    ("sigmoid", 1.0 / (np.exp(-x64) + 1.0)), ("relu", np.maximum(x64, 0.0))):
+        assert _ulps(orc.unary_f32(op, x), ref.astype(np.float32)).max() <= 1, op
+    for op, ref in (("log", np.log(p64)), ("sqrt", np.sqrt(p64)), ("rsqrt", 1.0 / np.sqrt(p64))):
+        assert _ulps(orc.unary_f32(op, p), ref.astype(np.float32)).max() <= 1, op
+
+
+def test_minmax_exact():
+    rng = np.random.default_rng(22)
+    a, b = (rng.standard_normal(1000).astype(np.float32) for _ in range(2))
+    b[::7] = a[::7]
+    assert np.array_equal(orc.minmax_f32("min", a, b), np.minimum(a, b))
+    assert np.array_equal(orc.minmax_f32("max", a, b), np.maximum(a, b))
+
+
+def test_reduce_rows():
+    rng = np.random.default_rng(23)
+    R, C = 37, 301
+    xi = rng.integers(-50, 50, (R, C)).astype(np.float32)  # integer sums are exact
+    assert np.array_equal(orc.reduce_rows_f32("sum", xi, R, C), xi.sum(axis=1))
+    x = rng.standard_normal((R, C)).astype(np.float32)
+    assert np.array_equal(orc.reduce_rows_f32("max", x, R, C), x.max(axis=1))
+    assert np.array_equal(orc.reduce_rows_f32("absmax", x, R, C), np.abs(x).max(axis=1))
+    assert np.array_equal(orc.reduce_rows_f32("sum", x, R, C),
+                          x.astype(np.float64).sum(axis=1).astype(np.float32))
+    # argmax: first index of the maximum (ties planted), 0 when nothing exceeds -inf
+    x[3, 10] = x[3, 200] = 50.0
+    x[5, :] = -np.inf
+    got = orc.reduce_rows_f32("argmax", x, R, C)
+    assert got.dtype == np.int32 and got[3] == 10 and got[5] == 0
+    assert np.array_equal(got, np.argmax(x, axis=1).astype(np.int32))
+
+
+def test_transpose_and_matvec():
+    rng = np.random.default_rng(24)
+    R, C = 33, 70
+    x = rng.standard_normal((R, C)).astype(np.float32)
+    t = orc.transpose_f32(x, R, C).reshape(C, R)
+    assert np.array_equal(t, x.T)
+    assert np.array_equal(orc.transpose_f32(t, C, R).reshape(R, C), x)
+    a = rng.integers(-20, 20, (R, C)).astype(np.float32)
+    v = rng.integers(-20, 20, C).astype(np.float32)
+    assert np.array_equal(orc.matvec_f32(a, v, R, C), (a.astype(np.int64) @ v.astype(np.int64)).astype(np.float32))
+    e = np.zeros(C, np.float32)
+    e[17] = 1.0
+    assert np.array_equal(orc.matvec_f32(x, e, R, C), x[:, 17])  # picks one column

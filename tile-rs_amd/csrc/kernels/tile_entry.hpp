@@ -233,5 +233,110 @@ __device__ __forceinline__ void decode(const void* q, const void* k, const void*
                                    scale, w);
 }
 
+// ---- row reductions of f32 rows (crates/rustc_codegen_tile/src/mlir_to_linalg.rs:
+//      1496-1573 sum / max / absmax, :1576-1660 argmax): `tiles` x R rows of C
+//      values -> one value per row, written at y[t * out_stride + r] (the stored
+//      view of tile t starts t * out_stride elements in).  One wavefront per row;
+//      lanes stride over 16-byte vectors when the row allows it. ----
+enum RowReduce : int { kRowSum = 0, kRowMax = 1, kRowAbsMax = 2, kRowArgMax = 3 };
+
+template <int OP>
+__device__ __forceinline__ void row_reduce_step(float v, uint32_t c, float& acc, uint32_t& idx) {
+  if constexpr (OP == kRowSum) acc += v;
+  else if constexpr (OP == kRowMax) acc = fmaxf(acc, v);
+  else if constexpr (OP == kRowAbsMax) acc = fmaxf(acc, fabsf(v));
+  else if (v > acc) { acc = v; idx = c; }   // strict: the first index of the maximum
+}
+
+template <int OP>
+__device__ __forceinline__ void reduce_rows(const float* __restrict__ x, float* __restrict__ y,
+                                            uint32_t tiles, uint32_t R, uint32_t C,
+                                            uint64_t out_stride) {
+  const uint32_t wpg = blockDim.x >> 6;
+  const uint32_t lane = threadIdx.x & 63;
+  const uint64_t rows = static_cast<uint64_t>(tiles) * R;
+  const bool vec = (C % 4 == 0) && ((reinterpret_cast<uintptr_t>(x) & 15) == 0);
+  for (uint64_t r = static_cast<uint64_t>(blockIdx.x) * wpg + (threadIdx.x >> 6); r < rows;
+       r += static_cast<uint64_t>(gridDim.x) * wpg) {
+    const float* xr = x + r * C;
+    float acc = OP == kRowSum ? 0.0f : -INFINITY;
+    uint32_t idx = 0;
+    if (vec) {
+      for (uint32_t c4 = lane; c4 < C / 4; c4 += 64) {
+        const float4 v = reinterpret_cast<const float4*>(xr)[c4];
+        row_reduce_step<OP>(v.x, 4 * c4, acc, idx);
+        row_reduce_step<OP>(v.y, 4 * c4 + 1, acc, idx);
+        row_reduce_step<OP>(v.z, 4 * c4 + 2, acc, idx);
+        row_reduce_step<OP>(v.w, 4 * c4 + 3, acc, idx);
+      }
+    } else {
+      for (uint32_t c = lane; c < C; c += 64) row_reduce_step<OP>(xr[c], c, acc, idx);
+    }
+    float* yr = y + (r / R) * out_stride + (r % R);
+    if constexpr (OP == kRowArgMax) {
+      for (int m = 1; m < 64; m <<= 1) {
+        const float ov = __shfl_xor(acc, m);
+        const uint32_t oi = static_cast<uint32_t>(__shfl_xor(static_cast<int>(idx), m));
+        if (ov > acc || (ov == acc && oi < idx)) {
+          acc = ov;
+          idx = oi;
+        }
+      }
+      if (lane == 0) *reinterpret_cast<int32_t*>(yr) = static_cast<int32_t>(idx);
+    } else {
+      acc = OP == kRowSum ? wave_sum(acc) : wave_max(acc);
+      if (lane == 0) *yr = acc;
+    }
+  }
+}
+
+// ---- transpose (mlir_to_linalg.rs:1458-1490): each tile's R x C f32 -> C x R,
+//      32 x 32 blocks staged through LDS so that reads and writes are both
+//      row-contiguous (256 threads) ----
+__device__ __forceinline__ void transpose(const float* __restrict__ x, float* __restrict__ y,
+                                          uint32_t tiles, uint32_t R, uint32_t C) {
+  __shared__ float blk[32][33];
+  const uint32_t br = (R + 31) / 32, bc = (C + 31) / 32;
+  const uint64_t per = static_cast<uint64_t>(br) * bc;
+  const uint32_t tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+  for (uint64_t w = blockIdx.x; w < static_cast<uint64_t>(tiles) * per; w += gridDim.x) {
+    const uint64_t t = w / per;
+    const uint32_t b = static_cast<uint32_t>(w % per);
+    const uint32_t r0 = (b / bc) * 32, c0 = (b % bc) * 32;
+    const float* xt = x + t * R * C;
+    float* yt = y + t * R * C;
+    for (uint32_t i = ty; i < 32; i += 8) {
+      const uint32_t r = r0 + i, c = c0 + tx;
+      if (r < R && c < C) blk[i][tx] = xt[static_cast<uint64_t>(r) * C + c];
+    }
+    __syncthreads();
+    for (uint32_t i = ty; i < 32; i += 8) {
+      const uint32_t c = c0 + i, r = r0 + tx;
+      if (r < R && c < C) yt[static_cast<uint64_t>(c) * R + r] = blk[tx][i];
+    }
+    __syncthreads();
+  }
+}
+
+// ---- matvec (mlir_to_linalg.rs:1395-1440): y[R] = A[R x C] . x[C] per tile (A at
+//      t*R*C, x at t*x_stride, y at t*y_stride), f32, one wavefront per row ----
+__device__ __forceinline__ void matvec(const float* __restrict__ a, const float* __restrict__ x,
+                                       float* __restrict__ y, uint32_t tiles, uint32_t R,
+                                       uint32_t C, uint64_t x_stride, uint64_t y_stride) {
+  const uint32_t wpg = blockDim.x >> 6;
+  const uint32_t lane = threadIdx.x & 63;
+  const uint64_t rows = static_cast<uint64_t>(tiles) * R;
+  for (uint64_t r = static_cast<uint64_t>(blockIdx.x) * wpg + (threadIdx.x >> 6); r < rows;
+       r += static_cast<uint64_t>(gridDim.x) * wpg) {
+    const uint64_t t = r / R;
+    const float* ar = a + r * C;
+    const float* xt = x + t * x_stride;
+    float acc = 0.0f;
+    for (uint32_t c = lane; c < C; c += 64) acc = __builtin_fmaf(ar[c], xt[c], acc);
+    acc = wave_sum(acc);
+    if (lane == 0) y[t * y_stride + (r % R)] = acc;
+  }
+}
+
 }  // namespace entry
 }  // namespace th

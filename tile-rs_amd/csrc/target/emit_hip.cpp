@@ -305,11 +305,16 @@ class Lowerer {
       return true;
     };
     static const std::set<std::string> kBin = {"add_f32", "sub_f32", "mul_f32", "div_f32",
-                                               "max_f32", "add_f16", "mul_f16"};
-    static const std::set<std::string> kUn = {"exp_f32", "neg_f32", "silu_f32",
+                                               "max_f32", "min_f32", "add_f16", "mul_f16"};
+    static const std::set<std::string> kUn = {"exp_f32", "neg_f32", "silu_f32", "log_f32",
+                                              "tanh_f32", "abs_f32", "sqrt_f32", "rsqrt_f32",
+                                              "sigmoid_f32", "relu_f32",
                                               "causal_mask_f32", "exp_f16", "neg_f16", "silu_f16",
                                               "cast_f32_f16", "cast_f16_f32", "cast_f32_bf16",
                                               "cast_bf16_f32"};
+    // row reductions and transpose: (dst, src, rows, cols), mlir_to_linalg.rs:1458-1660
+    static const std::set<std::string> kRow = {"reduce_sum_f32", "reduce_max_f32", "absmax_f32",
+                                               "argmax_f32", "transpose_f32"};
     if (base == "softmax_f32" || base == "softmax_f16") {
       if (a.size() < 4 || !tile(a[1]) || !shape_from(2, 3)) return fail("softmax arity: " + line);
       t.ins = {a[1]};
@@ -343,8 +348,24 @@ class Lowerer {
       t.ins = {a[1], a[2], a[3]};
       t.dtype = tile(a[1])->dtype;
     } else if (kBin.count(base)) {
+      // (dst, a, b, rows, cols) as in the linalg bridge (mlir_to_linalg.rs:620-633), or
+      // (a, b, rows, cols) as the gpu emitter's inputs also use
+      if (a.size() == 4 && tile(a[0]) && tile(a[1]) && shape_from(2, 3)) {
+        t.ins = {a[0], a[1]};
+      } else {
+        if (a.size() < 5 || !tile(a[1]) || !tile(a[2]) || !shape_from(3, 4))
+          return fail(base + " arity: " + line);
+        t.ins = {a[1], a[2]};
+      }
+      t.dtype = F32;
+    } else if (kRow.count(base)) {
+      if (a.size() < 4 || !tile(a[1]) || !shape_from(2, 3)) return fail(base + " arity: " + line);
+      t.ins = {a[1]};
+      t.dtype = F32;
+    } else if (base == "matvec_f32") {
+      // (dst, a, b, rows, cols): a rows x cols, b cols -> rows (mlir_to_linalg.rs:1395-1440)
       if (a.size() < 5 || !tile(a[1]) || !tile(a[2]) || !shape_from(3, 4))
-        return fail(base + " arity: " + line);
+        return fail("matvec arity: " + line);
       t.ins = {a[1], a[2]};
       t.dtype = F32;
     } else if (kUn.count(base)) {
@@ -421,9 +442,10 @@ void signature(std::ostringstream& os, const Kernel& k, unsigned threads,
 }
 
 bool is_elementwise(const std::string& op) {
-  return op != "load" && op.find("softmax") == std::string::npos &&
-         op.find("rms_norm") == std::string::npos && op.find("matmul") == std::string::npos &&
-         op.find("attention") == std::string::npos;
+  for (const char* hot : {"softmax", "rms_norm", "matmul", "attention", "reduce_", "absmax",
+                          "argmax", "transpose", "matvec"})
+    if (op.find(hot) != std::string::npos) return false;
+  return op != "load";
 }
 
 // Pointer expressions of a loaded view / the stored view (per-tile offsets are
@@ -628,6 +650,15 @@ bool emit_kernel(const Kernel& k, std::ostringstream& os, std::string* err) {
         else if (o == "mul_f32" || o == "mul_f16") e << in(0) << " * " << in(1);
         else if (o == "div_f32") e << in(0) << " / " << in(1);
         else if (o == "max_f32") e << "fmaxf(" << in(0) << ", " << in(1) << ")";
+        else if (o == "min_f32") e << "fminf(" << in(0) << ", " << in(1) << ")";
+        else if (o == "log_f32") e << "logf(" << in(0) << ")";
+        else if (o == "tanh_f32") e << "tanhf(" << in(0) << ")";
+        else if (o == "abs_f32") e << "fabsf(" << in(0) << ")";
+        else if (o == "sqrt_f32") e << "sqrtf(" << in(0) << ")";
+        else if (o == "rsqrt_f32") e << "(1.0f / sqrtf(" << in(0) << "))";
+        // sigmoid and relu as the linalg bridge's generic bodies (mlir_to_linalg.rs:765-789)
+        else if (o == "sigmoid_f32") e << "(1.0f / (expf(-" << in(0) << ") + 1.0f))";
+        else if (o == "relu_f32") e << "fmaxf(" << in(0) << ", 0.0f)";
         else if (o == "exp_f32" || o == "exp_f16") e << "expf(" << in(0) << ")";
         else if (o == "neg_f32" || o == "neg_f16") e << "-" << in(0);
         else if (o == "silu_f32" || o == "silu_f16") e << in(0) << " / (1.0f + expf(-" << in(0) << "))";
@@ -751,6 +782,68 @@ bool emit_kernel(const Kernel& k, std::ostringstream& os, std::string* err) {
     const unsigned tpw = R >= per_wg ? 1 : static_cast<unsigned>(per_wg / R);
     const unsigned wpt = R >= per_wg ? static_cast<unsigned>((R + per_wg - 1) / per_wg) : 1;
     desc(os, k.name, 256, wpt, tpw);
+    return true;
+  }
+  if (o == "reduce_sum_f32" || o == "reduce_max_f32" || o == "absmax_f32" || o == "argmax_f32") {
+    const TileVal& x = k.tiles.at(hot->ins[0]);
+    const long long R = hot->rows, C = hot->cols;
+    if (x.rows * x.cols != R * C || x.dtype != F32) {
+      *err = "mlir_to_hip: " + k.name + ": " + o + " input must be an f32 " + std::to_string(R) +
+             "x" + std::to_string(C) + " tile";
+      return false;
+    }
+    // one value per row; the stored view is rows x 1 (or declares the rows)
+    if (st->rows * st->cols != R && st->rows != R) {
+      *err = "mlir_to_hip: " + k.name + ": " + o + " stores one value per row";
+      return false;
+    }
+    const char* op = o == "reduce_sum_f32" ? "th::entry::kRowSum"
+                     : o == "reduce_max_f32" ? "th::entry::kRowMax"
+                     : o == "absmax_f32" ? "th::entry::kRowAbsMax" : "th::entry::kRowArgMax";
+    os << "row " << o.substr(0, o.size() - 4) << " " << R << "x" << C << " f32 per tile"
+       << (o == "argmax_f32" ? " (i32 indices)" : "") << " -> th::entry::reduce_rows\n";
+    signature(os, k, 256, {});
+    os << "  th::entry::reduce_rows<" << op << ">(" << in_ptr(0, "float") << ", "
+       << out_ptr("float") << ", th_tiles, " << u(R) << ", " << u(C) << ", "
+       << st->rows * st->cols << "ull);\n}\n";
+    const long long wpt = (R + 3) / 4;
+    desc(os, k.name, 256, static_cast<unsigned>(wpt > 1024 ? 1024 : wpt), 1);
+    return true;
+  }
+  if (o == "transpose_f32") {
+    const TileVal& x = k.tiles.at(hot->ins[0]);
+    const long long R = hot->rows, C = hot->cols;
+    if (x.rows * x.cols != R * C || st->rows * st->cols != R * C || x.dtype != F32 ||
+        st->dtype != F32) {
+      *err = "mlir_to_hip: " + k.name + ": transpose needs f32 tiles of " + std::to_string(R * C) +
+             " elements";
+      return false;
+    }
+    os << "transpose " << R << "x" << C << " f32 per tile -> th::entry::transpose\n";
+    signature(os, k, 256, {});
+    os << "  th::entry::transpose(" << in_ptr(0, "float") << ", " << out_ptr("float")
+       << ", th_tiles, " << u(R) << ", " << u(C) << ");\n}\n";
+    const long long blocks = ((R + 31) / 32) * ((C + 31) / 32);
+    desc(os, k.name, 256, static_cast<unsigned>(blocks > 1024 ? 1024 : blocks), 1);
+    return true;
+  }
+  if (o == "matvec_f32") {
+    const TileVal& a = k.tiles.at(hot->ins[0]);
+    const TileVal& x = k.tiles.at(hot->ins[1]);
+    const long long R = hot->rows, C = hot->cols;
+    if (a.rows * a.cols != R * C || x.rows * x.cols != C || st->rows * st->cols != R ||
+        a.dtype != F32 || x.dtype != F32 || st->dtype != F32) {
+      *err = "mlir_to_hip: " + k.name + ": matvec needs f32 a (" + std::to_string(R) + "x" +
+             std::to_string(C) + "), x (" + std::to_string(C) + ") and y (" + std::to_string(R) + ")";
+      return false;
+    }
+    os << "matvec " << R << "x" << C << " f32 per tile -> th::entry::matvec\n";
+    signature(os, k, 256, {});
+    os << "  th::entry::matvec(" << in_ptr(0, "float") << ", " << in_ptr(1, "float") << ", "
+       << out_ptr("float") << ", th_tiles, " << u(R) << ", " << u(C) << ", " << C << "ull, " << R
+       << "ull);\n}\n";
+    const long long wpt = (R + 3) / 4;
+    desc(os, k.name, 256, static_cast<unsigned>(wpt > 1024 ? 1024 : wpt), 1);
     return true;
   }
   if (o == "attention_f32") {

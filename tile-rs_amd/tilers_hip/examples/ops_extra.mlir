@@ -1,0 +1,156 @@
+module {
+  llvm.func @ew_log(%arg0: !llvm.ptr<1>, %arg1: !llvm.ptr<1>) attributes {hacc.entry} {
+    ^bb0:
+    %r = llvm.mlir.constant(4 : i32) : i32
+    %c = llvm.mlir.constant(256 : i32) : i32
+    %x = llvm.call @__tile_load_f32(%arg0, %r, %c) : (!llvm.ptr<1>, i32, i32) -> i32
+    %y = llvm.call @__tile_log_f32(%x, %x, %r, %c) : (i32, i32, i32, i32) -> i32
+    llvm.call @__tile_store_f32(%arg1, %y, %r, %c) : (!llvm.ptr<1>, i32, i32, i32) -> ()
+    llvm.return
+  }
+  llvm.func @ew_tanh(%arg0: !llvm.ptr<1>, %arg1: !llvm.ptr<1>) attributes {hacc.entry} {
+    ^bb0:
+    %r = llvm.mlir.constant(4 : i32) : i32
+    %c = llvm.mlir.constant(256 : i32) : i32
+    %x = llvm.call @__tile_load_f32(%arg0, %r, %c) : (!llvm.ptr<1>, i32, i32) -> i32
+    %y = llvm.call @__tile_tanh_f32(%x, %x, %r, %c) : (i32, i32, i32, i32) -> i32
+    llvm.call @__tile_store_f32(%arg1, %y, %r, %c) : (!llvm.ptr<1>, i32, i32, i32) -> ()
+    llvm.return
+  }
+  llvm.func @ew_abs(%arg0: !llvm.ptr<1>, %arg1: !llvm.ptr<1>) attributes {hacc.entry} {
+    ^bb0:
+    %r = llvm.mlir.constant(4 : i32) : i32
+    %c = llvm.mlir.constant(256 : i32) : i32
+    %x = llvm.call @__tile_load_f32(%arg0, %r, %c) : (!llvm.ptr<1>, i32, i32) -> i32
+    %y = llvm.call @__tile_abs_f32(%x, %x, %r, %c) : (i32, i32, i32, i32) -> i32
+    llvm.call @__tile_store_f32(%arg1, %y, %r, %c) : (!llvm.ptr<1>, i32, i32, i32) -> ()
+    llvm.return
+  }
+  llvm.func @ew_sqrt(%arg0: !llvm.ptr<1>, %arg1: !llvm.ptr<1>) attributes {hacc.entry} {
+    ^bb0:
+    %r = llvm.mlir.constant(4 : i32) : i32
+    %c = llvm.mlir.constant(256 : i32) : i32
+    %x = llvm.call @__tile_load_f32(%arg0, %r, %c) : (!llvm.ptr<1>, i32, i32) -> i32
+    %y = llvm.call @__tile_sqrt_f32(%x, %x, %r, %c) : (i32, i32, i32, i32) -> i32
+    llvm.call @__tile_store_f32(%arg1, %y, %r, %c) : (!llvm.ptr<1>, i32, i32, i32) -> ()
+    llvm.return
+  }
+  llvm.func @ew_rsqrt(%arg0: !llvm.ptr<1>, %arg1: !llvm.ptr<1>) attributes {hacc.entry} {
+    ^bb0:
+    %r = llvm.mlir.constant(4 : i32) : i32
+    %c = llvm.mlir.constant(256 : i32) : i32
+    %x = llvm.call @__tile_load_f32(%arg0, %r, %c) : (!llvm.ptr<1>, i32, i32) -> i32
+    %y = llvm.call @__tile_rsqrt_f32(%x, %x, %r, %c) : (i32, i32, i32, i32) -> i32
+    llvm.call @__tile_store_f32(%arg1, %y, %r, %c) : (!llvm.ptr<1>, i32, i32, i32) -> ()
+    llvm.return
+  }
+  llvm.func @ew_sigmoid(%arg0: !llvm.ptr<1>, %arg1: !llvm.ptr<1>) attributes {hacc.entry} {
+    ^bb0:
+    %r = llvm.mlir.constant(4 : i32) : i32
+    %c = llvm.mlir.constant(256 : i32) : i32
+    %x = llvm.call @__tile_load_f32(%arg0, %r, %c) : (!llvm.ptr<1>, i32, i32) -> i32
+    %y = llvm.call @__tile_sigmoid_f32(%x, %x, %r, %c) : (i32, i32, i32, i32) -> i32
+    llvm.call @__tile_store_f32(%arg1, %y, %r, %c) : (!llvm.ptr<1>, i32, i32, i32) -> ()
+    llvm.return
+  }
+  llvm.func @ew_relu(%arg0: !llvm.ptr<1>, %arg1: !llvm.ptr<1>) attributes {hacc.entry} {
+    ^bb0:
+    %r = llvm.mlir.constant(4 : i32) : i32
+    %c = llvm.mlir.constant(256 : i32) : i32
+    %x = llvm.call @__tile_load_f32(%arg0, %r, %c) : (!llvm.ptr<1>, i32, i32) -> i32
+    %y = llvm.call @__tile_relu_f32(%x, %x, %r, %c) : (i32, i32, i32, i32) -> i32
+    llvm.call @__tile_store_f32(%arg1, %y, %r, %c) : (!llvm.ptr<1>, i32, i32, i32) -> ()
+    llvm.return
+  }
+  llvm.func @ew_min(%arg0: !llvm.ptr<1>, %arg1: !llvm.ptr<1>, %arg2: !llvm.ptr<1>) attributes {hacc.entry} {
+    ^bb0:
+    %r = llvm.mlir.constant(4 : i32) : i32
+    %c = llvm.mlir.constant(256 : i32) : i32
+    %a = llvm.call @__tile_load_f32(%arg0, %r, %c) : (!llvm.ptr<1>, i32, i32) -> i32
+    %b = llvm.call @__tile_load_f32(%arg1, %r, %c) : (!llvm.ptr<1>, i32, i32) -> i32
+    %y = llvm.call @__tile_min_f32(%a, %a, %b, %r, %c) : (i32, i32, i32, i32, i32) -> i32
+    llvm.call @__tile_store_f32(%arg2, %y, %r, %c) : (!llvm.ptr<1>, i32, i32, i32) -> ()
+    llvm.return
+  }
+  llvm.func @ew_silu_mul4(%arg0: !llvm.ptr<1>, %arg1: !llvm.ptr<1>, %arg2: !llvm.ptr<1>) attributes {hacc.entry} {
+    ^bb0:
+    %r = llvm.mlir.constant(1 : i32) : i32
+    %c = llvm.mlir.constant(1000 : i32) : i32
+    %g = llvm.call @__tile_load_f32(%arg0, %r, %c) : (!llvm.ptr<1>, i32, i32) -> i32
+    %u = llvm.call @__tile_load_f32(%arg1, %r, %c) : (!llvm.ptr<1>, i32, i32) -> i32
+    %s = llvm.call @__tile_silu_f32(%g, %g, %r, %c) : (i32, i32, i32, i32) -> i32
+    %y = llvm.call @__tile_mul_f32(%s, %u, %r, %c) : (i32, i32, i32, i32) -> i32
+    llvm.call @__tile_store_f32(%arg2, %y, %r, %c) : (!llvm.ptr<1>, i32, i32, i32) -> ()
+    llvm.return
+  }
+  llvm.func @row_reduce_sum(%arg0: !llvm.ptr<1>, %arg1: !llvm.ptr<1>) attributes {hacc.entry} {
+    ^bb0:
+    %r = llvm.mlir.constant(8 : i32) : i32
+    %c = llvm.mlir.constant(1000 : i32) : i32
+    %one = llvm.mlir.constant(1 : i32) : i32
+    %x = llvm.call @__tile_load_f32(%arg0, %r, %c) : (!llvm.ptr<1>, i32, i32) -> i32
+    %y = llvm.call @__tile_reduce_sum_f32(%x, %x, %r, %c) : (i32, i32, i32, i32) -> i32
+    llvm.call @__tile_store_f32(%arg1, %y, %r, %one) : (!llvm.ptr<1>, i32, i32, i32) -> ()
+    llvm.return
+  }
+  llvm.func @row_reduce_max(%arg0: !llvm.ptr<1>, %arg1: !llvm.ptr<1>) attributes {hacc.entry} {
+    ^bb0:
+    %r = llvm.mlir.constant(8 : i32) : i32
+    %c = llvm.mlir.constant(1000 : i32) : i32
+    %one = llvm.mlir.constant(1 : i32) : i32
+    %x = llvm.call @__tile_load_f32(%arg0, %r, %c) : (!llvm.ptr<1>, i32, i32) -> i32
+    %y = llvm.call @__tile_reduce_max_f32(%x, %x, %r, %c) : (i32, i32, i32, i32) -> i32
+    llvm.call @__tile_store_f32(%arg1, %y, %r, %one) : (!llvm.ptr<1>, i32, i32, i32) -> ()
+    llvm.return
+  }
+  llvm.func @row_absmax(%arg0: !llvm.ptr<1>, %arg1: !llvm.ptr<1>) attributes {hacc.entry} {
+    ^bb0:
+    %r = llvm.mlir.constant(8 : i32) : i32
+    %c = llvm.mlir.constant(1000 : i32) : i32
+    %one = llvm.mlir.constant(1 : i32) : i32
+    %x = llvm.call @__tile_load_f32(%arg0, %r, %c) : (!llvm.ptr<1>, i32, i32) -> i32
+    %y = llvm.call @__tile_absmax_f32(%x, %x, %r, %c) : (i32, i32, i32, i32) -> i32
+    llvm.call @__tile_store_f32(%arg1, %y, %r, %one) : (!llvm.ptr<1>, i32, i32, i32) -> ()
+    llvm.return
+  }
+  llvm.func @row_argmax(%arg0: !llvm.ptr<1>, %arg1: !llvm.ptr<1>) attributes {hacc.entry} {
+    ^bb0:
+    %r = llvm.mlir.constant(8 : i32) : i32
+    %c = llvm.mlir.constant(1000 : i32) : i32
+    %one = llvm.mlir.constant(1 : i32) : i32
+    %x = llvm.call @__tile_load_f32(%arg0, %r, %c) : (!llvm.ptr<1>, i32, i32) -> i32
+    %y = llvm.call @__tile_argmax_f32(%x, %x, %r, %c) : (i32, i32, i32, i32) -> i32
+    llvm.call @__tile_store_f32(%arg1, %y, %r, %one) : (!llvm.ptr<1>, i32, i32, i32) -> ()
+    llvm.return
+  }
+  llvm.func @row_sum_aligned(%arg0: !llvm.ptr<1>, %arg1: !llvm.ptr<1>) attributes {hacc.entry} {
+    ^bb0:
+    %r = llvm.mlir.constant(6 : i32) : i32
+    %c = llvm.mlir.constant(4096 : i32) : i32
+    %one = llvm.mlir.constant(1 : i32) : i32
+    %x = llvm.call @__tile_load_f32(%arg0, %r, %c) : (!llvm.ptr<1>, i32, i32) -> i32
+    %y = llvm.call @__tile_reduce_sum_f32(%x, %x, %r, %c) : (i32, i32, i32, i32) -> i32
+    llvm.call @__tile_store_f32(%arg1, %y, %r, %one) : (!llvm.ptr<1>, i32, i32, i32) -> ()
+    llvm.return
+  }
+  llvm.func @xpose(%arg0: !llvm.ptr<1>, %arg1: !llvm.ptr<1>) attributes {hacc.entry} {
+    ^bb0:
+    %r = llvm.mlir.constant(48 : i32) : i32
+    %c = llvm.mlir.constant(80 : i32) : i32
+    %x = llvm.call @__tile_load_f32(%arg0, %r, %c) : (!llvm.ptr<1>, i32, i32) -> i32
+    %y = llvm.call @__tile_transpose_f32(%x, %x, %r, %c) : (i32, i32, i32, i32) -> i32
+    llvm.call @__tile_store_f32(%arg1, %y, %c, %r) : (!llvm.ptr<1>, i32, i32, i32) -> ()
+    llvm.return
+  }
+  llvm.func @mv(%arg0: !llvm.ptr<1>, %arg1: !llvm.ptr<1>, %arg2: !llvm.ptr<1>) attributes {hacc.entry} {
+    ^bb0:
+    %r = llvm.mlir.constant(96 : i32) : i32
+    %c = llvm.mlir.constant(200 : i32) : i32
+    %one = llvm.mlir.constant(1 : i32) : i32
+    %a = llvm.call @__tile_load_f32(%arg0, %r, %c) : (!llvm.ptr<1>, i32, i32) -> i32
+    %b = llvm.call @__tile_load_f32(%arg1, %c, %one) : (!llvm.ptr<1>, i32, i32) -> i32
+    %y = llvm.call @__tile_matvec_f32(%a, %a, %b, %r, %c) : (i32, i32, i32, i32, i32) -> i32
+    llvm.call @__tile_store_f32(%arg2, %y, %r, %one) : (!llvm.ptr<1>, i32, i32, i32) -> ()
+    llvm.return
+  }
+}
