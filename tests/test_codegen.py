@@ -363,3 +363,120 @@ def test_new_ops_lower_to_their_entries():
     # reduction outputs: one value per row, the stored view of tile t at t * rows
     assert "th_tiles, 8u, 1000u, 8ull);" in src
     assert "th_tiles, 96u, 200u, 200ull, 96ull);" in src
+
+
+# ---- counted tile loops and the pipelined_for marker (tile.rs:2168-2221) --------------------
+
+def loop_module(body: str, bound: str = "%arg2", pred: str = "uge", depth: int | None = 2,
+                step: str = "%one", start: str = "%zero", cols: int = 1024, name: str = "lp",
+                extra: str = "") -> str:
+    """The loop of tile.rs:2196-2210 (`loop { if i >= n_tiles { break; } ... i += 1 }`)
+    around a softmax over one 1 x `cols` row per iteration."""
+    marker = ("    %depth = llvm.mlir.constant(" + str(depth) + " : i32) : i32\n"
+              "    llvm.call @__tile_pipelined_for_begin(%depth) : (i32) -> ()\n") if depth else ""
+    end = "    llvm.call @__tile_pipelined_for_end() : () -> ()\n" if depth else ""
+    return ("module {\n  llvm.func @" + name + "(%arg0: !llvm.ptr<1>, %arg1: !llvm.ptr<1>, %arg2: i32)"
+            " attributes {hacc.entry} {\n    ^bb0:\n" + marker +
+            "    %zero = llvm.mlir.constant(0 : i32) : i32\n"
+            "    %one = llvm.mlir.constant(1 : i32) : i32\n"
+            "    %two = llvm.mlir.constant(2 : i32) : i32\n"
+            f"    %cols = llvm.mlir.constant({cols} : i32) : i32\n"
+            f"    %cols64 = llvm.mlir.constant({cols} : i64) : i64\n" + extra +
+            f"    llvm.br ^bb1({start} : i32)\n"
+            "  ^bb1(%i: i32):\n"
+            f"    %done = llvm.icmp \"{pred}\" %i, {bound} : i32\n"
+            "    llvm.cond_br %done, ^bb3, ^bb2\n"
+            "  ^bb2:\n" + body +
+            f"    %next = llvm.add %i, {step} : i32\n"
+            "    llvm.br ^bb1(%next : i32)\n"
+            "  ^bb3:\n" + end + "    llvm.return\n  }\n}\n")
+
+
+LOOP_BODY = (
+    "    %iw = llvm.zext %i : i32 to i64\n"
+    "    %off = llvm.mul %iw, %cols64 : i64\n"
+    "    %src = llvm.getelementptr %arg0[%off] : (!llvm.ptr<1>, i64) -> !llvm.ptr<1>, f32\n"
+    "    %dst = llvm.getelementptr %arg1[%off] : (!llvm.ptr<1>, i64) -> !llvm.ptr<1>, f32\n"
+    "    %t = llvm.call @__tile_load_f32(%src, %one, %cols) : (!llvm.ptr<1>, i32, i32) -> i32\n"
+    "    %y = llvm.call @__tile_softmax_f32(%t, %t, %one, %cols) : (i32, i32, i32, i32) -> i32\n"
+    "    llvm.call @__tile_store_f32(%dst, %y, %one, %cols) : (!llvm.ptr<1>, i32, i32, i32) -> ()\n")
+
+
+def test_loop_example_lowers_to_a_tile_grid():
+    """The reference's loop example: iteration i becomes logical tile i, the trip count
+    comes from the kernel's scalar argument and scales the grid through the descriptor
+    (arg 2, ceil(n / 16) workgroups: 16 rows per workgroup)."""
+    src = th.emit((EXAMPLES / "softmax_loop.mlir").read_text()).source
+    assert ("softmax_loop_f32(void* __restrict__ p0, void* __restrict__ p1, uint32_t s2, "
+            "uint32_t th_tiles_in)") in src
+    assert "const uint32_t th_tiles = th_tiles_in ? static_cast<uint32_t>(s2) : 0u;" in src
+    assert "th::entry::softmax_rows<th::kF32, 4>(" in src and "th_tiles * 1u, 1024u);" in src
+    assert "__th_desc_softmax_loop_f32 = {th::kLaunchDescMagic, 256u, 1u, 1u, 0u, 3u, 16u, 65536u};" in src
+    # an i64 bound, `ult` with the body on the true edge, `1 + i`, a shl-scaled offset
+    assert "uint64_t s3, uint32_t th_tiles_in)" in src
+    assert "th_tiles_in ? static_cast<uint32_t>(s3) : 0u;" in src
+    assert "__th_desc_add_loop_f32 = {th::kLaunchDescMagic, 256u, 2u, 1u, 0u, 4u, 1u, 65536u};" in src
+
+
+def test_loop_generic_form_and_constant_trip():
+    src = th.emit((EXAMPLES / "softmax_loop_generic.mlir").read_text()).source
+    assert "const uint32_t th_tiles = th_tiles_in ? 48u : 0u;" in src
+    # 48 iterations of one 4-row tile, one workgroup each
+    assert "__th_desc_softmax_loop_bf16_generic = {th::kLaunchDescMagic, 256u, 48u, 1u, 0u, 0u, 0u, 0u};" in src
+
+
+def test_pipelined_for_marker_sets_the_pipeline_depth():
+    """depth >= 2 keeps the next row in flight (streaming softmax); depth == 1 is the
+    explicit opt-out (tile.rs:2179-2180); no marker behaves like depth 2."""
+    two = th.emit(loop_module(LOOP_BODY, depth=2)).source
+    one = th.emit(loop_module(LOOP_BODY, depth=1)).source
+    none = th.emit(loop_module(LOOP_BODY, depth=None)).source
+    assert "softmax_rows<th::kF32, 4>(" in two and "pipelined_for(2)" in two
+    assert "softmax_rows<th::kF32, 4, false>(" in one and "pipelined_for(1)" in one
+    assert "softmax_rows<th::kF32, 4>(" in none and "pipelined_for" not in none.split("->")[0]
+    # 16 rows per streaming workgroup, 4 without streaming
+    assert "0u, 3u, 16u, 65536u};" in two and "0u, 3u, 4u, 65536u};" in one
+
+
+def test_pipelined_for_depth_is_the_gemm_lds_ring_depth():
+    text = (EXAMPLES / "matmul_bf16.mlir").read_text()
+    marker = ("    %pd = llvm.mlir.constant(5 : i32) : i32\n"
+              "    llvm.call @__tile_pipelined_for_begin(%pd) : (i32) -> ()\n    %m =")
+    src = th.emit(text.replace("    %m =", marker, 1)).source
+    assert "th::entry::gemm_dma<th::kBF16, th::kF32, false, th::gemm::kEpiStore, 5>" in src
+    plain = th.emit(text).source
+    assert "th::entry::gemm_dma<th::kBF16, th::kF32, false, th::gemm::kEpiStore>" in plain
+
+
+@pytest.mark.parametrize("mutate,message", [
+    (dict(step="%two"), "the loop must step by 1"),
+    (dict(start="%one"), "the loop must start at 0"),
+    (dict(pred="ult"), "the loop must run while iv < n"),
+    (dict(bound="%zero", body=LOOP_BODY.replace("%cols64 : i64", "%two64 : i64"),
+          extra="    %two64 = llvm.mlir.constant(512 : i64) : i64\n"),
+     "loop views must advance one tile"),
+])
+def test_loop_shapes_outside_the_counted_tile_loop_are_rejected(mutate, message):
+    kw = dict(body=LOOP_BODY)
+    kw.update(mutate)
+    body = kw.pop("body")
+    with pytest.raises(th.HalError) as e:
+        th.emit(loop_module(body, **kw))
+    assert message in str(e.value)
+
+
+def test_loop_with_a_per_tile_offset_is_rejected():
+    body = ("    %b = llvm.call @get_block_idx() : () -> i64\n"
+            "    %bo = llvm.mul %b, %cols64 : i64\n"
+            "    %a0 = llvm.getelementptr %arg0[%bo] : (!llvm.ptr<1>, i64) -> !llvm.ptr<1>, f32\n"
+            + LOOP_BODY.replace("%arg0[%off]", "%a0[%off]"))
+    with pytest.raises(th.HalError) as e:
+        th.emit(loop_module(body))
+    assert "per-tile (block index) offset" in str(e.value)
+
+
+def test_loop_compiles_for_gfx950(tmp_path):
+    for stem in ("softmax_loop", "softmax_loop_generic"):
+        co = tmp_path / f"{stem}.hsaco"
+        th.compile_source(th.emit((EXAMPLES / f"{stem}.mlir").read_text()).source, co)
+        assert co.stat().st_size > 1000

@@ -27,7 +27,8 @@ def launcher(dev):
     lau = dev.create_launcher()
     for stem in ("softmax_rows", "softmax_generic", "matmul_bf16", "matmul_f16_t", "matmul_f32",
                  "attention_f32", "prefill_bf16", "decode_bf16", "swiglu_mask", "rms_norm_rows",
-                 "swiglu_gate_bf16", "matmul_bf16_tiles", "rope", "rows_long", "ops_extra"):
+                 "swiglu_gate_bf16", "matmul_bf16_tiles", "rope", "rows_long", "ops_extra",
+                 "softmax_loop", "softmax_loop_generic"):
         lau.load(_build.example_path(stem), th.KernelMode.GENERAL)
     return lau
 
@@ -367,3 +368,55 @@ def test_transpose_and_matvec(dev, stream, launcher):
         ref = orc.matvec_f32(at, vt, R, C)
         bound = np.abs(at.reshape(R, C)) @ np.abs(vt) * 2e-7 + 1e-6
         assert (np.abs(got[t] - ref) <= bound).all()
+
+
+# ---- counted tile loops (tile.rs:2196-2210) -------------------------------------------------
+
+def test_softmax_loop_runs_every_iteration(dev, stream, launcher):
+    """The reference's loop example (a 1 x 1024 f32 softmax per iteration, n_tiles from the
+    kernel argument, pipelined_for(2)): one launched tile walks all n rows; three
+    launched tiles compute the same rows; n = 0 leaves the output untouched."""
+    n = 300
+    rng = np.random.default_rng(71)
+    x = (rng.standard_normal((n, 1024)) * 2).astype(np.float32)
+    ref = orc.softmax(x, n, 1024)
+    xb = up(dev, stream, x, D.F32)
+    for launched in (1, 3):
+        yb = up(dev, stream, np.full(x.size + 1024, 7.0, np.float32), D.F32)
+        launcher.launch("softmax_loop_f32", th.LaunchGrid.blocks_only(launched),
+                        [ptr(xb), ptr(yb), C.c_uint32(n)], stream)
+        got = yb.copy_to_host(stream)
+        assert_softmax_close(got[:x.size].reshape(n, 1024), ref)
+        assert np.all(got[x.size:] == 7.0), "the loop ran past n"
+    yb = up(dev, stream, np.full(x.size, 7.0, np.float32), D.F32)
+    launcher.launch("softmax_loop_f32", th.LaunchGrid.blocks_only(1),
+                    [ptr(xb), ptr(yb), C.c_uint32(0)], stream)
+    assert np.all(yb.copy_to_host(stream) == 7.0)
+
+
+def test_add_loop_i64_bound(dev, stream, launcher):
+    """i64 trip count, `i < n` loop test, offsets from `i << 9` (2 x 256 tiles): exact."""
+    n = 77
+    rng = np.random.default_rng(72)
+    a = rng.standard_normal(n * 512).astype(np.float32)
+    b = rng.standard_normal(n * 512).astype(np.float32)
+    ab, bb = up(dev, stream, a, D.F32), up(dev, stream, b, D.F32)
+    cb = up(dev, stream, np.full(n * 512 + 512, 7.0, np.float32), D.F32)
+    launcher.launch("add_loop_f32", th.LaunchGrid.blocks_only(1), [ptr(ab), ptr(bb), ptr(cb), C.c_uint64(n)],
+                    stream)
+    got = cb.copy_to_host(stream)
+    np.testing.assert_array_equal(got[:n * 512], a + b)
+    assert np.all(got[n * 512:] == 7.0)
+
+
+def test_softmax_loop_generic_form_depth_one(dev, stream, launcher):
+    """Generic-form loop, constant trip 48 over 4 x 512 bf16 tiles, pipelined_for(1)
+    (the non-streaming row loop)."""
+    rng = np.random.default_rng(73)
+    rows = 48 * 4
+    x = orc.narrow((rng.standard_normal(rows * 512) * 2).astype(np.float32), orc.BF16)
+    xb, yb = up(dev, stream, x, D.BF16), dev.alloc(x.size, D.BF16)
+    launcher.launch("softmax_loop_bf16_generic", th.LaunchGrid.blocks_only(1), [ptr(xb), ptr(yb)], stream)
+    got = orc.widen(yb.copy_to_host(stream), orc.BF16)
+    ref = orc.softmax(orc.widen(x, orc.BF16), rows, 512)
+    assert_within_ulp16(got, ref.reshape(-1), orc.BF16)

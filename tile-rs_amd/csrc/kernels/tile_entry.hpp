@@ -22,9 +22,11 @@ namespace entry {
 // ---- row softmax over `rows` contiguous rows of `cols` (one wavefront per row;
 //      rows of up to 256 16-byte vectors take the streaming loop of the library
 //      kernel: each wave walks several rows with its next row's loads in flight) ----
-template <int DT, int NV>
+// STREAM = false (pipelined_for(1), the explicit opt-out of pipelining) keeps one
+// row per wave with no next row in flight.
+template <int DT, int NV, bool STREAM = true>
 __device__ __forceinline__ void softmax_rows(const void* x, void* y, uint32_t rows, uint32_t cols) {
-  if constexpr (NV > 0 && NV <= 4) {
+  if constexpr (STREAM && NV > 0 && NV <= 4) {
     softmax_rows_stream_body<DT, NV>(x, y, rows, cols);
     return;
   }
@@ -106,7 +108,8 @@ __device__ __forceinline__ void gemm(const uint16_t* A, const uint16_t* B, void*
 // for K a multiple of 32 (and N of 8).  Operands that are not 16-byte aligned
 // (checked at run time; the emitter fixes only the view offsets) take the
 // per-element kernel instead, which fits in the same workgroup.
-template <int DT, int DTO, bool BT, int EPI = gemm::kEpiStore>
+// NS: LDS ring stages (4 or 5: the staged epilogue needs four stages of LDS).
+template <int DT, int DTO, bool BT, int EPI = gemm::kEpiStore, int NS = gemm::NSTAGE>
 __device__ __forceinline__ void gemm_dma(const uint16_t* A, const uint16_t* B, void* C, uint32_t M,
                                          uint32_t N, uint32_t K, uint32_t batch,
                                          const void* up = nullptr) {
@@ -128,8 +131,8 @@ __device__ __forceinline__ void gemm_dma(const uint16_t* A, const uint16_t* B, v
     char* c = static_cast<char*>(C) + bi * sc;
     const void* u = up ? static_cast<const char*>(up) + bi * sc : nullptr;
     if (vec)
-      gemm_dma_tile_256<DT, DTO, BT, gemm::DBK, gemm::NSTAGE, gemm::DWAVES, EPI>(a, b, c, M, N, K,
-                                                                                tm, tn, u);
+      gemm_dma_tile_256<DT, DTO, BT, gemm::DBK, NS, gemm::DWAVES, EPI>(a, b, c, M, N, K, tm, tn,
+                                                                      u);
     else
       gemm_dot_tile_256<DT, DTO, BT, EPI>(a, b, c, M, N, K, tm, tn, u);
   }

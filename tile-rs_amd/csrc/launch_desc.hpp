@@ -23,13 +23,32 @@ struct LaunchDesc {
   uint32_t wg_per_tile;   // workgroups per logical tile (>= 1)
   uint32_t tiles_per_wg;  // logical tiles per workgroup (>= 1)
   uint32_t lds_bytes;     // dynamic LDS per workgroup
-  uint32_t reserved[3];
+  // Work that depends on run-time scalar arguments (a loop's trip count, the
+  // heads and sequence length of attention): wg_per_tile is multiplied by
+  // ceil(arg[a0] / d0) and by ceil(arg[a1] / d1), where a0/a1 index the
+  // kernel's uint32 arguments, then capped at wg_cap.  Zero fields disable a
+  // factor (descriptors without them launch as before).
+  uint32_t scale_args;    // (a0 + 1) | (a1 + 1) << 8; 0 = none
+  uint32_t scale_div;     // d0 | d1 << 16 (0 reads as 1)
+  uint32_t wg_cap;        // maximum workgroups per tile after scaling (0 = none)
 };
 
-// hardware workgroups for `tiles` logical tiles
-inline uint64_t desc_grid(const LaunchDesc& d, uint64_t tiles) {
+// hardware workgroups for `tiles` logical tiles; `args` are the kernel's
+// argument pointers (the driver's kernelParams convention)
+inline uint64_t desc_grid(const LaunchDesc& d, uint64_t tiles, void* const* args = nullptr,
+                          size_t nargs = 0) {
   const uint64_t tpw = d.tiles_per_wg ? d.tiles_per_wg : 1;
-  const uint64_t wpt = d.wg_per_tile ? d.wg_per_tile : 1;
+  uint64_t wpt = d.wg_per_tile ? d.wg_per_tile : 1;
+  for (int f = 0; f < 2; ++f) {
+    const uint32_t a = (d.scale_args >> (8 * f)) & 0xffu;
+    if (a == 0 || a > nargs || !args || !args[a - 1]) continue;
+    uint64_t div = (d.scale_div >> (16 * f)) & 0xffffu;
+    if (div == 0) div = 1;
+    const uint64_t v = *static_cast<const uint32_t*>(args[a - 1]);
+    wpt *= (v + div - 1) / div;
+  }
+  if (d.wg_cap && wpt > d.wg_cap) wpt = d.wg_cap;
+  if (wpt == 0) wpt = 1;
   return (tiles + tpw - 1) / tpw * wpt;
 }
 

@@ -416,7 +416,7 @@ int th_launcher_launch(th_launcher l, const char* name, uint32_t blocks, uint32_
                                            nullptr),
                      "hipModuleLaunchKernel", TH_KERNEL_ERROR);
   }
-  const uint64_t grid = th::desc_grid(fn.desc, blocks);
+  const uint64_t grid = th::desc_grid(fn.desc, blocks, args, nargs);
   if (grid > 0x7fffffffu) return fail(TH_KERNEL_ERROR, "launch grid too large");
   std::vector<void*> full(args, args + nargs);
   uint32_t tiles = blocks;

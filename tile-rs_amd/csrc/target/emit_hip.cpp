@@ -59,8 +59,23 @@ const char* dt_enum(int d) { return d == F32 ? "th::kF32" : d == F16 ? "th::kF16
 const char* dt_ctype(int d) { return d == F32 ? "float" : "uint16_t"; }
 
 struct PtrRef {
-  int arg = -1;         // index into the kernel's GM pointer list
-  long long offset = 0; // element offset from the argument
+  int arg = -1;            // index into the kernel's GM pointer list
+  long long offset = 0;    // element offset from the argument
+  long long iv_stride = 0; // elements added per iteration of the lowered loop
+};
+
+// a * iv + b for the induction variable of a lowered loop
+struct Affine {
+  long long stride = 0, offset = 0;
+};
+
+// A counted tile loop `for iv in 0..n` whose views advance one tile per
+// iteration (tile.rs:2196-2210): lowered by mapping iteration i to logical
+// tile i, so the loop's tiles run in parallel over the grid.
+struct Loop {
+  bool present = false;
+  long long trip = 0;    // constant trip count, or
+  int trip_arg = -1;     // position of the uint32 kernel argument holding it
 };
 
 struct TileVal {
@@ -81,6 +96,7 @@ struct Store {
 
 struct Kernel {
   std::string name;
+  std::vector<mlir::FuncArg> args;            // all args in order
   std::vector<mlir::FuncArg> gm;              // pointer args in order
   std::map<std::string, int> gm_index;        // arg name -> position
   std::map<std::string, double> consts;       // SSA -> numeric constant
@@ -89,6 +105,10 @@ struct Kernel {
   std::map<std::string, TileVal> tiles;       // SSA -> tile
   std::vector<Store> stores;
   bool bf16_hint = false;
+  std::map<std::string, Affine> affine;       // SSA -> affine in the loop's induction variable
+  Loop loop;
+  int depth = 0;                              // pipelined_for(depth), 0 = no marker
+  bool block_offset = false;                  // some view carries the per-tile offset
 };
 
 std::string ssa_token(const std::string& s) {
@@ -116,6 +136,7 @@ class Lowerer {
 
   bool analyze(Kernel* k) {
     k->name = f_.name;
+    k->args = f_.args;
     for (const auto& a : f_.args) {
       if (a.is_gm) {
         k->gm_index[a.name] = static_cast<int>(k->gm.size());
@@ -126,12 +147,230 @@ class Lowerer {
     }
     if (k->name.find("bf16") != std::string::npos) k->bf16_hint = true;
     for (const std::string& raw : f_.body_lines) {
+      const std::string l = mlir::trim(raw);
+      if (l.rfind("^bb", 0) == 0 || l.find(".br ") != std::string::npos ||
+          l.find(".cond_br ") != std::string::npos)
+        return loop_(k);
+    }
+    for (const std::string& raw : f_.body_lines) {
       const std::string line = mlir::trim(raw);
       if (line.empty() || line == "llvm.return" || line.rfind("llvm.return", 0) == 0) continue;
       if (!line_(k, line)) return false;
     }
     return true;
   }
+
+ private:
+  // ---- control flow: the counted tile loop ----
+  struct Block {
+    std::string label;                // "" for the entry block
+    std::vector<std::string> params;  // block argument SSA names
+    std::vector<std::string> lines;
+  };
+
+  static Block parse_label(const std::string& l) {
+    Block b;
+    const size_t paren = l.find('(');
+    b.label = l.substr(0, paren == std::string::npos ? l.size() - 1 : paren);
+    if (paren != std::string::npos) {
+      const size_t close = l.rfind(')');
+      std::stringstream ss(l.substr(paren + 1, close - paren - 1));
+      std::string part;
+      while (std::getline(ss, part, ',')) {
+        part = mlir::trim(part);
+        b.params.push_back(mlir::trim(part.substr(0, part.find(':'))));
+      }
+    }
+    return b;
+  }
+
+  // SSA operands of a branch target `^bbN(%a, %b : i32, i32)` or `^bbN(%a : i32, %b : i32)`
+  static std::string branch_target(const std::string& t, std::vector<std::string>* args) {
+    const size_t paren = t.find('(');
+    args->clear();
+    if (paren != std::string::npos) {
+      std::stringstream ss(t.substr(paren + 1, t.rfind(')') - paren - 1));
+      std::string part;
+      while (std::getline(ss, part, ',')) {
+        part = mlir::trim(part);
+        if (!part.empty() && part[0] == '%') args->push_back(ssa_token(part));
+      }
+    }
+    return mlir::trim(t.substr(0, paren));
+  }
+
+  static bool parse_br(const std::string& l, std::string* target, std::vector<std::string>* args) {
+    for (const char* op : {"llvm.br ", "cf.br "}) {
+      if (l.rfind(op, 0) == 0) {
+        *target = branch_target(mlir::trim(l.substr(std::strlen(op))), args);
+        return true;
+      }
+    }
+    return false;
+  }
+
+  // `llvm.cond_br %c, ^bbT, ^bbF` -> (cond, T, F); targets must take no arguments
+  static bool parse_cond_br(const std::string& l, std::string* cond, std::string* t,
+                            std::string* f) {
+    std::string rest;
+    for (const char* op : {"llvm.cond_br ", "cf.cond_br "})
+      if (l.rfind(op, 0) == 0) rest = mlir::trim(l.substr(std::strlen(op)));
+    if (rest.empty()) return false;
+    std::vector<std::string> parts;
+    int depth = 0;
+    std::string cur;
+    for (char c : rest) {
+      if (c == '(' || c == '[') ++depth;
+      if (c == ')' || c == ']') --depth;
+      if (c == ',' && depth == 0) {
+        parts.push_back(mlir::trim(cur));
+        cur.clear();
+      } else {
+        cur += c;
+      }
+    }
+    parts.push_back(mlir::trim(cur));
+    if (parts.size() != 3) return false;
+    std::vector<std::string> ta, fa;
+    *cond = ssa_token(parts[0]);
+    *t = branch_target(parts[1], &ta);
+    *f = branch_target(parts[2], &fa);
+    return ta.empty() && fa.empty();
+  }
+
+  bool loop_(Kernel* k) {
+    std::vector<Block> blocks(1);
+    for (const std::string& raw : f_.body_lines) {
+      const std::string l = mlir::trim(raw);
+      if (l.empty() || l.rfind("llvm.return", 0) == 0) continue;
+      if (l.rfind("^bb", 0) == 0 && l.back() == ':') blocks.push_back(parse_label(l));
+      else blocks.back().lines.push_back(l);
+    }
+    auto find = [&](const std::string& lab) -> const Block* {
+      for (const Block& b : blocks)
+        if (!lab.empty() && b.label == lab) return &b;
+      return nullptr;
+    };
+    const std::string shape =
+        "control flow: only a counted tile loop is lowered (entry -> header(iv) -> body -> "
+        "header, exit on iv >= n)";
+    const Block& entry = blocks[0];
+    std::string hlab;
+    std::vector<std::string> hargs;
+    if (entry.lines.empty() || !parse_br(entry.lines.back(), &hlab, &hargs) || hargs.size() != 1)
+      return fail(shape);
+    const Block* H = find(hlab);
+    if (!H || H->params.size() != 1 || H->lines.size() < 2) return fail(shape);
+    const std::string iv = H->params[0];
+    std::string cond, ta, fb;
+    if (!parse_cond_br(H->lines.back(), &cond, &ta, &fb)) return fail(shape);
+    // the compare that defines the condition
+    std::string pred, x, y;
+    for (const std::string& l : H->lines) {
+      const auto r = mlir::result_ssa(l);
+      const size_t p = l.find("llvm.icmp \"");
+      if (r && *r == cond && p != std::string::npos) {
+        const size_t q = l.find('"', p + 11);
+        pred = l.substr(p + 11, q - p - 11);
+        std::string ops = mlir::trim(l.substr(q + 1));
+        ops = ops.substr(0, ops.find(" : "));
+        x = mlir::trim(ops.substr(0, ops.find(',')));
+        y = mlir::trim(ops.substr(ops.find(',') + 1));
+      }
+    }
+    if (pred.empty()) return fail(shape);
+    auto latches = [&](const Block* b) {
+      std::string t;
+      std::vector<std::string> a;
+      return b && !b->lines.empty() && parse_br(b->lines.back(), &t, &a) && t == hlab &&
+             a.size() == 1;
+    };
+    const Block* A = find(ta);
+    const Block* B = find(fb);
+    if (!A || !B || latches(A) == latches(B)) return fail(shape);
+    const bool true_is_body = latches(A);
+    const Block* body = true_is_body ? A : B;
+    const Block* exitb = true_is_body ? B : A;
+    std::string n_tok;
+    bool ok = false;
+    if (x == iv) {
+      n_tok = y;
+      ok = true_is_body ? (pred == "ult" || pred == "slt" || pred == "ne")
+                        : (pred == "uge" || pred == "sge" || pred == "eq");
+    } else if (y == iv) {
+      n_tok = x;
+      ok = true_is_body ? (pred == "ugt" || pred == "sgt" || pred == "ne")
+                        : (pred == "ule" || pred == "sle" || pred == "eq");
+    }
+    if (!ok) return fail("control flow: the loop must run while iv < n: " + H->lines.back());
+    // entry block (constants, the pipelined_for marker)
+    for (size_t i = 0; i + 1 < entry.lines.size(); ++i)
+      if (!line_(k, entry.lines[i])) return false;
+    double start = -1;
+    if (!resolve(k, hargs[0], &start) || start != 0) return fail("control flow: the loop must start at 0");
+    for (const std::string& l : H->lines) {
+      if (l.find("llvm.icmp") != std::string::npos || l.find("cond_br") != std::string::npos) continue;
+      if (!line_(k, l)) return false;
+    }
+    double nv = 0;
+    if (resolve(k, n_tok, &nv)) {
+      if (nv < 0) return fail("control flow: negative trip count");
+      k->loop.trip = static_cast<long long>(nv);
+    } else {
+      for (size_t i = 0; i < f_.args.size(); ++i)
+        if (f_.args[i].name == n_tok && !f_.args[i].is_gm) k->loop.trip_arg = static_cast<int>(i);
+      if (k->loop.trip_arg < 0)
+        return fail("control flow: the loop bound must be a constant or a scalar kernel argument");
+    }
+    if (!k->tiles.empty() || !k->stores.empty())
+      return fail("control flow: tile operations outside the loop body are not lowered");
+    // body: iv is affine; the latch increments it by one
+    std::string next_t;
+    std::vector<std::string> next_a;
+    parse_br(body->lines.back(), &next_t, &next_a);
+    bool stepped = false;
+    k->affine[iv] = Affine{1, 0};
+    for (size_t i = 0; i + 1 < body->lines.size(); ++i) {
+      const std::string& l = body->lines[i];
+      const auto r = mlir::result_ssa(l);
+      if (r && *r == next_a[0] && l.find("llvm.add ") != std::string::npos) {
+        std::string ops = mlir::trim(l.substr(l.find("llvm.add ") + 9));
+        ops = ops.substr(0, ops.find(" : "));
+        const std::string a0 = mlir::trim(ops.substr(0, ops.find(',')));
+        const std::string a1 = mlir::trim(ops.substr(ops.find(',') + 1));
+        double one = 0;
+        stepped = (a0 == iv && resolve(k, a1, &one) && one == 1) ||
+                  (a1 == iv && resolve(k, a0, &one) && one == 1);
+        if (!stepped) return fail("control flow: the loop must step by 1: " + l);
+        continue;
+      }
+      if (!line_(k, l)) return false;
+    }
+    if (!stepped) return fail("control flow: the loop must step its index by 1");
+    for (const std::string& l : exitb->lines) {
+      const auto c = mlir::callee(l);
+      if (!c || *c != "__tile_pipelined_for_end")
+        return fail("control flow: the loop exit may only end the pipelined_for marker: " + l);
+    }
+    for (const auto& kv : k->tiles) {
+      const TileVal& t = kv.second;
+      if (t.op == "load" && t.src.iv_stride != t.rows * t.cols)
+        return fail("control flow: loop views must advance one tile (rows * cols) per iteration");
+    }
+    for (const Store& st : k->stores)
+      if (st.dst.iv_stride != st.rows * st.cols)
+        return fail("control flow: loop views must advance one tile (rows * cols) per iteration");
+    if (k->stores.empty()) return fail("control flow: the loop body stores nothing");
+    // Every launched tile of such a kernel walks the same n tiles; a view that
+    // also carried the per-tile offset would need that offset's stride, which
+    // the folding cannot check.
+    if (k->block_offset)
+      return fail("control flow: loop views may not also carry the per-tile (block index) offset");
+    k->loop.present = true;
+    return true;
+  }
+
+ public:
 
  private:
   bool fail(const std::string& m) {
@@ -176,6 +415,7 @@ class Lowerer {
       if (p != std::string::npos && res) {
         const std::string src = ssa_token(mlir::trim(line.substr(p + std::strlen(op))));
         if (k->consts.count(src)) k->consts[*res] = k->consts[src];
+        if (k->affine.count(src)) k->affine[*res] = k->affine[src];
         if (k->block_derived.count(src)) k->block_derived.insert(*res);
         if (k->ptrs.count(src)) k->ptrs[*res] = k->ptrs[src];
         return true;
@@ -194,6 +434,38 @@ class Lowerer {
         const std::string b = mlir::trim(rest.substr(comma + 1));
         if (k->block_derived.count(a) || k->block_derived.count(b)) {
           k->block_derived.insert(*res);
+          return true;
+        }
+        if (k->affine.count(a) || k->affine.count(b)) {
+          // affine in the loop index: (s*iv + o) op constant, or a sum of two
+          const std::string o = op;
+          Affine fa, fb;
+          double ca = 0, cb = 0;
+          const bool aa = k->affine.count(a), ab = k->affine.count(b);
+          if (aa) fa = k->affine[a];
+          else if (!resolve(k, a, &ca)) return fail("non-affine use of the loop index: " + line);
+          if (ab) fb = k->affine[b];
+          else if (!resolve(k, b, &cb)) return fail("non-affine use of the loop index: " + line);
+          const long long ia = static_cast<long long>(ca), ib = static_cast<long long>(cb);
+          Affine r;
+          if (o == "llvm.add ") {
+            r.stride = fa.stride + fb.stride;
+            r.offset = (aa ? fa.offset : ia) + (ab ? fb.offset : ib);
+          } else if (o == "llvm.sub ") {
+            r.stride = fa.stride - fb.stride;
+            r.offset = (aa ? fa.offset : ia) - (ab ? fb.offset : ib);
+          } else if (o == "llvm.mul " && aa != ab) {
+            const Affine& f = aa ? fa : fb;
+            const long long c = aa ? ib : ia;
+            r.stride = f.stride * c;
+            r.offset = f.offset * c;
+          } else if (o == "llvm.shl " && aa && !ab) {
+            r.stride = fa.stride << ib;
+            r.offset = fa.offset << ib;
+          } else {
+            return fail("non-affine use of the loop index: " + line);
+          }
+          k->affine[*res] = r;
           return true;
         }
         double x = 0, y = 0;
@@ -224,6 +496,10 @@ class Lowerer {
       double off = 0;
       if (k->block_derived.count(idx)) {
         // the #[tile_kernel] per-tile offset: applied implicitly per logical tile
+        k->block_offset = true;
+      } else if (k->affine.count(idx)) {
+        r.offset += k->affine[idx].offset;
+        r.iv_stride += k->affine[idx].stride;
       } else if (resolve(k, idx, &off)) {
         r.offset += static_cast<long long>(off);
       } else {
@@ -243,7 +519,13 @@ class Lowerer {
       if (res) k->block_derived.insert(*res);
       return true;
     }
-    if (c == "__tile_pipelined_for_begin" || c == "__tile_pipelined_for_end") return true;
+    if (c == "__tile_pipelined_for_begin") {
+      // pipelined_for(depth) (tile.rs:2183-2221): recorded for the loop's kernel
+      double d = 0;
+      if (!a.empty() && resolve(k, a[0], &d)) k->depth = static_cast<int>(d);
+      return true;
+    }
+    if (c == "__tile_pipelined_for_end") return true;
     if (c.rfind("__tile_load_", 0) == 0) {
       if (a.size() < 3 || !res) return fail("load: expected (ptr, rows, cols): " + line);
       auto p = k->ptrs.find(a[0]);
@@ -422,23 +704,79 @@ std::string fconst(double v) {
   return os.str();
 }
 
-void desc(std::ostringstream& os, const std::string& name, unsigned threads, unsigned wg_per_tile,
-          unsigned tiles_per_wg) {
-  os << "extern \"C\" __device__ th::LaunchDesc __th_desc_" << name << " = {th::kLaunchDescMagic, "
-     << threads << "u, " << (wg_per_tile ? wg_per_tile : 1) << "u, "
-     << (tiles_per_wg ? tiles_per_wg : 1) << "u, 0u, {0u, 0u, 0u}};\n\n";
+// scale_args / scale_div / wg_cap: grid factors from run-time scalar arguments
+// (launch_desc.hpp); a lowered loop multiplies the workgroups per tile by its
+// trip count.
+void desc(std::ostringstream& os, const Kernel& k, unsigned threads, unsigned wg_per_tile,
+          unsigned tiles_per_wg, unsigned scale_args = 0, unsigned scale_div = 0,
+          unsigned wg_cap = 0) {
+  unsigned long long wpt = wg_per_tile ? wg_per_tile : 1;
+  if (k.loop.present) {
+    // the kernel runs n tiles for any launched tile count: size the grid for
+    // ceil(n / tiles_per_wg) workgroups per launched tile (usually one)
+    constexpr unsigned long long kCap = 1u << 16;
+    const unsigned long long tpw = tiles_per_wg ? tiles_per_wg : 1;
+    tiles_per_wg = 1;
+    if (k.loop.trip_arg >= 0) {
+      const unsigned slot = (scale_args & 0xffu) ? 8u : 0u;
+      scale_args |= static_cast<unsigned>(k.loop.trip_arg + 1) << slot;
+      scale_div |= static_cast<unsigned>(tpw) << (2 * slot);
+      wg_cap = wg_cap ? wg_cap : static_cast<unsigned>(kCap);
+    } else {
+      const unsigned long long n = k.loop.trip > 0 ? static_cast<unsigned long long>(k.loop.trip) : 1;
+      wpt *= (n + tpw - 1) / tpw;
+      if (wpt > kCap) wpt = kCap;
+    }
+  }
+  os << "extern \"C\" __device__ th::LaunchDesc __th_desc_" << k.name << " = {th::kLaunchDescMagic, "
+     << threads << "u, " << wpt << "u, " << (tiles_per_wg ? tiles_per_wg : 1) << "u, 0u, "
+     << scale_args << "u, " << scale_div << "u, " << wg_cap << "u};\n\n";
+}
+
+// C type of a scalar kernel argument
+std::string scalar_ctype(const std::string& ty) {
+  if (ty.find("f32") != std::string::npos) return "float";
+  if (ty.find("f64") != std::string::npos) return "double";
+  if (ty.find("i64") != std::string::npos) return "uint64_t";
+  return "uint32_t";
 }
 
 // min_groups > 0 asks for that many resident workgroups per CU (it caps the
 // registers per wave accordingly).
+// Parameters follow the MLIR function's arguments (pointers p<i>, scalars s<pos>),
+// then the trailing run-time scalars `extra`, then the hidden tile count.  A
+// lowered loop folds its iterations into the tile count.
 void signature(std::ostringstream& os, const Kernel& k, unsigned threads,
                const std::vector<std::string>& extra, unsigned min_groups = 0) {
   os << "extern \"C\" __global__ void __launch_bounds__(" << threads;
   if (min_groups) os << ", " << min_groups;
   os << ") " << k.name << "(";
-  for (size_t i = 0; i < k.gm.size(); ++i) os << (i ? ", " : "") << "void* __restrict__ p" << i;
-  for (const std::string& e : extra) os << ", uint32_t " << e;
-  os << (k.gm.empty() && extra.empty() ? "" : ", ") << "uint32_t th_tiles) {\n";
+  bool first = true;
+  for (size_t i = 0; i < k.args.size(); ++i) {
+    const mlir::FuncArg& a = k.args[i];
+    os << (first ? "" : ", ");
+    if (a.is_gm) os << "void* __restrict__ p" << k.gm_index.at(a.name);
+    else os << scalar_ctype(a.ty) << " s" << i;
+    first = false;
+  }
+  for (const std::string& e : extra) {
+    os << (first ? "" : ", ") << "uint32_t " << e;
+    first = false;
+  }
+  os << (first ? "" : ", ");
+  if (!k.loop.present) {
+    os << "uint32_t th_tiles) {\n";
+    return;
+  }
+  os << "uint32_t th_tiles_in) {\n";
+  os << "  // counted tile loop: iteration i is tile i.  Every launched tile walks the\n"
+        "  // same iterations, so any number of launched tiles computes them once.\n";
+  os << "  const uint32_t th_tiles = th_tiles_in ? "
+     << (k.loop.trip_arg >= 0 ? "static_cast<uint32_t>(s" + std::to_string(k.loop.trip_arg) + ")"
+                              : std::to_string(k.loop.trip) + "u")
+     << " : 0u;\n";
+  for (size_t i = 0; i < k.args.size(); ++i)
+    if (!k.args[i].is_gm && static_cast<int>(i) != k.loop.trip_arg) os << "  (void)s" << i << ";\n";
 }
 
 bool is_elementwise(const std::string& op) {
@@ -492,23 +830,27 @@ bool matmul_entry(const Kernel& k, const TileVal& mm, const Store& st, const cha
   signature(os, k, threads, {});
   const std::string tmpl = std::string(dt_enum(in)) + ", " + dt_enum(out) + ", " +
                            (bt ? "true" : "false") + ", " + epi;
+  // pipelined_for(depth >= 2): the LDS ring depth (4 or 5 stages; the staged
+  // epilogue needs four stages of LDS)
+  const int ns = k.depth >= 2 ? (k.depth > 5 ? 5 : (k.depth < 4 ? 4 : k.depth)) : 0;
+  const std::string tmpl_dma = ns ? tmpl + ", " + std::to_string(ns) : tmpl;
   const std::string tail = up ? ", th_tiles, " + view_ptr(*up, dt_ctype(out)) + ");\n}\n"
                               : ", th_tiles);\n}\n";
   if (dma) {
-    os << "  th::entry::gemm_dma<" << tmpl << ">(" << view_ptr(a, "uint16_t") << ", "
+    os << "  th::entry::gemm_dma<" << tmpl_dma << ">(" << view_ptr(a, "uint16_t") << ", "
        << view_ptr(b, "uint16_t") << ", " << store_ptr(st, dt_ctype(out)) << ", " << u(M) << ", "
        << u(N) << ", " << u(K) << tail;
-    desc(os, k.name, threads, static_cast<unsigned>(((M + 255) / 256) * ((N + 255) / 256)), 1);
+    desc(os, k, threads, static_cast<unsigned>(((M + 255) / 256) * ((N + 255) / 256)), 1);
   } else if (mfma) {
     os << "  th::entry::gemm<" << tmpl << ">(" << view_ptr(a, "uint16_t") << ", "
        << view_ptr(b, "uint16_t") << ", " << store_ptr(st, dt_ctype(out)) << ", " << u(M) << ", "
        << u(N) << ", " << u(K) << tail;
-    desc(os, k.name, 256, static_cast<unsigned>(((M + 255) / 256) * ((N + 255) / 256)), 1);
+    desc(os, k, 256, static_cast<unsigned>(((M + 255) / 256) * ((N + 255) / 256)), 1);
   } else {
     os << "  th::entry::gemm_fma<" << tmpl << ">(" << view_ptr(a, dt_ctype(in)) << ", "
        << view_ptr(b, dt_ctype(in)) << ", " << store_ptr(st, dt_ctype(out)) << ", " << u(M)
        << ", " << u(N) << ", " << u(K) << tail;
-    desc(os, k.name, 256, static_cast<unsigned>(((M + 63) / 64) * ((N + 63) / 64)), 1);
+    desc(os, k, 256, static_cast<unsigned>(((M + 63) / 64) * ((N + 63) / 64)), 1);
   }
   return true;
 }
@@ -690,7 +1032,7 @@ bool emit_kernel(const Kernel& k, std::ostringstream& os, std::string* err) {
     }
     os << "  }\n}\n";
     const long long per = (R * C + 255) / 256;
-    desc(os, k.name, 256, static_cast<unsigned>(per > 1024 ? 1024 : per), 1);
+    desc(os, k, 256, static_cast<unsigned>(per > 1024 ? 1024 : per), 1);
     return true;
   }
 
@@ -716,6 +1058,7 @@ bool emit_kernel(const Kernel& k, std::ostringstream& os, std::string* err) {
     int nv = 0;  // 0 = any-cols path
     const bool aligned = (C % E == 0) && (x.src.offset % E == 0) && (st->dst.offset % E == 0);
     if (aligned && nvec <= 64 * 16) nv = nvec <= 64 ? 1 : nvec <= 128 ? 2 : nvec <= 256 ? 4 : nvec <= 512 ? 8 : 16;
+    const bool stream = k.depth != 1;   // pipelined_for(1): no next row in flight
     if (aligned && nvec > 64 * 16 && nvec <= 256 * 16) {
       // one workgroup per row, the row in registers
       const int wnv = nvec <= 256 * 8 ? 8 : 16;
@@ -725,19 +1068,22 @@ bool emit_kernel(const Kernel& k, std::ostringstream& os, std::string* err) {
       os << "  th::entry::softmax_rows_wg<" << dt_enum(x.dtype) << ", " << wnv << ">("
          << in_ptr(0, dt_ctype(x.dtype)) << ", " << out_ptr(dt_ctype(x.dtype)) << ", th_tiles * "
          << u(R) << ", " << u(C) << ");\n}\n";
-      desc(os, k.name, 256, static_cast<unsigned>(R), 1);
+      desc(os, k, 256, static_cast<unsigned>(R), 1);
       return true;
     }
-    os << "row softmax " << R << "x" << C << " " << dt_name(x.dtype) << " per tile -> th::entry::softmax_rows\n";
+    os << "row softmax " << R << "x" << C << " " << dt_name(x.dtype) << " per tile"
+       << (k.loop.present ? " (counted loop" + std::string(k.depth ? ", pipelined_for(" + std::to_string(k.depth) + ")" : "") + ")" : "")
+       << " -> th::entry::softmax_rows\n";
     signature(os, k, 256, {});
-    os << "  th::entry::softmax_rows<" << dt_enum(x.dtype) << ", " << nv << ">(" << in_ptr(0, dt_ctype(x.dtype))
-       << ", " << out_ptr(dt_ctype(x.dtype)) << ", th_tiles * " << u(R) << ", " << u(C) << ");\n}\n";
+    os << "  th::entry::softmax_rows<" << dt_enum(x.dtype) << ", " << nv << (stream ? "" : ", false")
+       << ">(" << in_ptr(0, dt_ctype(x.dtype)) << ", " << out_ptr(dt_ctype(x.dtype)) << ", th_tiles * "
+       << u(R) << ", " << u(C) << ");\n}\n";
     // Rows per workgroup: 16 for the streaming loop (nv <= 4: each of the 4 waves
     // walks about 4 rows, next row in flight), 4 (one per wave) otherwise.
-    const long long per_wg = (nv > 0 && nv <= 4) ? 16 : 4;
+    const long long per_wg = (stream && nv > 0 && nv <= 4) ? 16 : 4;
     const unsigned tpw = R >= per_wg ? 1 : static_cast<unsigned>(per_wg / R);
     const unsigned wpt = R >= per_wg ? static_cast<unsigned>((R + per_wg - 1) / per_wg) : 1;
-    desc(os, k.name, 256, wpt, tpw);
+    desc(os, k, 256, wpt, tpw);
     return true;
   }
   if (o.rfind("matmul", 0) == 0) {
@@ -757,7 +1103,8 @@ bool emit_kernel(const Kernel& k, std::ostringstream& os, std::string* err) {
     const long long nvec = C / E;
     int nv = 0;
     const bool aligned = (C % E == 0) && (x.src.offset % E == 0) && (st->dst.offset % E == 0);
-    if (aligned && nvec <= 64 * 16) nv = nvec <= 64 ? 1 : nvec <= 128 ? 2 : nvec <= 256 ? 4 : nvec <= 512 ? 8 : 16;
+    if (aligned && nvec <= 64 * 16 && k.depth != 1)
+      nv = nvec <= 64 ? 1 : nvec <= 128 ? 2 : nvec <= 256 ? 4 : nvec <= 512 ? 8 : 16;
     if (aligned && nvec > 64 * 16 && nvec <= 256 * 16) {
       // one workgroup per row, the row in registers
       const int wnv = nvec <= 256 * 8 ? 8 : 16;
@@ -767,7 +1114,7 @@ bool emit_kernel(const Kernel& k, std::ostringstream& os, std::string* err) {
       os << "  th::entry::rms_norm_rows_wg<" << dt_enum(x.dtype) << ", " << wnv << ">("
          << in_ptr(0, dt_ctype(x.dtype)) << ", " << out_ptr(dt_ctype(x.dtype)) << ", th_tiles * "
          << u(R) << ", " << u(C) << ", " << fconst(hot->scalars[0]) << ");\n}\n";
-      desc(os, k.name, 256, static_cast<unsigned>(R), 1);
+      desc(os, k, 256, static_cast<unsigned>(R), 1);
       return true;
     }
     os << "row rms_norm " << R << "x" << C << " " << dt_name(x.dtype) << " eps "
@@ -781,7 +1128,7 @@ bool emit_kernel(const Kernel& k, std::ostringstream& os, std::string* err) {
     const long long per_wg = nv > 0 ? 8 : 4;
     const unsigned tpw = R >= per_wg ? 1 : static_cast<unsigned>(per_wg / R);
     const unsigned wpt = R >= per_wg ? static_cast<unsigned>((R + per_wg - 1) / per_wg) : 1;
-    desc(os, k.name, 256, wpt, tpw);
+    desc(os, k, 256, wpt, tpw);
     return true;
   }
   if (o == "reduce_sum_f32" || o == "reduce_max_f32" || o == "absmax_f32" || o == "argmax_f32") {
@@ -807,7 +1154,7 @@ bool emit_kernel(const Kernel& k, std::ostringstream& os, std::string* err) {
        << out_ptr("float") << ", th_tiles, " << u(R) << ", " << u(C) << ", "
        << st->rows * st->cols << "ull);\n}\n";
     const long long wpt = (R + 3) / 4;
-    desc(os, k.name, 256, static_cast<unsigned>(wpt > 1024 ? 1024 : wpt), 1);
+    desc(os, k, 256, static_cast<unsigned>(wpt > 1024 ? 1024 : wpt), 1);
     return true;
   }
   if (o == "transpose_f32") {
@@ -824,7 +1171,7 @@ bool emit_kernel(const Kernel& k, std::ostringstream& os, std::string* err) {
     os << "  th::entry::transpose(" << in_ptr(0, "float") << ", " << out_ptr("float")
        << ", th_tiles, " << u(R) << ", " << u(C) << ");\n}\n";
     const long long blocks = ((R + 31) / 32) * ((C + 31) / 32);
-    desc(os, k.name, 256, static_cast<unsigned>(blocks > 1024 ? 1024 : blocks), 1);
+    desc(os, k, 256, static_cast<unsigned>(blocks > 1024 ? 1024 : blocks), 1);
     return true;
   }
   if (o == "matvec_f32") {
@@ -843,7 +1190,7 @@ bool emit_kernel(const Kernel& k, std::ostringstream& os, std::string* err) {
        << out_ptr("float") << ", th_tiles, " << u(R) << ", " << u(C) << ", " << C << "ull, " << R
        << "ull);\n}\n";
     const long long wpt = (R + 3) / 4;
-    desc(os, k.name, 256, static_cast<unsigned>(wpt > 1024 ? 1024 : wpt), 1);
+    desc(os, k, 256, static_cast<unsigned>(wpt > 1024 ? 1024 : wpt), 1);
     return true;
   }
   if (o == "attention_f32") {
@@ -859,7 +1206,7 @@ bool emit_kernel(const Kernel& k, std::ostringstream& os, std::string* err) {
     os << "  th::entry::attention_tiles<" << dt_enum(q.dtype) << ", 256>(" << in_ptr(0, dt_ctype(q.dtype))
        << ", " << in_ptr(1, dt_ctype(q.dtype)) << ", " << in_ptr(2, dt_ctype(q.dtype)) << ", "
        << out_ptr(dt_ctype(st->dtype)) << ", " << u(S) << ", " << u(D) << ", th_tiles);\n}\n";
-    desc(os, k.name, 256, static_cast<unsigned>(S), 1);
+    desc(os, k, 256, static_cast<unsigned>(S), 1);
     return true;
   }
   if (o == "attention_prefill_f32") {
@@ -874,7 +1221,7 @@ bool emit_kernel(const Kernel& k, std::ostringstream& os, std::string* err) {
     // One workgroup per (head, 256-query block) up to 1024 per tile (e.g. 32 heads x
     // 8192 queries), so the hardware balances the causal work; workgroups past the
     // work exit at once (they are dispatched last).
-    desc(os, k.name, 512, 1024, 1);
+    desc(os, k, 512, 1024, 1);
     return true;
   }
   if (o == "attention_decode_f32") {
@@ -889,7 +1236,7 @@ bool emit_kernel(const Kernel& k, std::ostringstream& os, std::string* err) {
     os << "  th::entry::decode<" << dt_enum(q.dtype) << ">(" << in_ptr(0, ct) << ", " << in_ptr(1, ct)
        << ", " << in_ptr(2, ct) << ", " << out_ptr(ct)
        << ", th_tiles, seq_len, max_seq, head_dim, num_heads, num_kv_heads);\n}\n";
-    desc(os, k.name, 256, 64, 1);
+    desc(os, k, 256, 64, 1);
     return true;
   }
   *err = "mlir_to_hip: " + k.name + ": unsupported intrinsic " + hot->op;

@@ -2,6 +2,7 @@
 #include "target/mlir_parse.hpp"
 
 #include <cctype>
+#include <cstdlib>
 #include <sstream>
 
 namespace th {
@@ -163,6 +164,76 @@ std::string normalize_generic(const std::string& raw) {
            types_of(rest) + ", " + elem;
   }
   if (rest.rfind("\"llvm.return\"", 0) == 0) return "llvm.return";
+  // control flow and integer arithmetic of a lowered loop (mlir_parse.rs:564-611)
+  auto successors = [&](const std::string& r) {
+    const size_t lb = r.find(")["), rb = r.find(']', lb == std::string::npos ? 0 : lb);
+    if (lb == std::string::npos || rb == std::string::npos) return std::vector<std::string>();
+    return split_top(r.substr(lb + 2, rb - lb - 2));
+  };
+  auto operand_types = [&](const std::string& r) {
+    std::string t = types_of(r);
+    const size_t arrow = t.find("->");
+    if (arrow != std::string::npos) t = trim(t.substr(0, arrow));
+    if (!t.empty() && t.front() == '(') t = paren_body(t, 0);
+    return split_top(t);
+  };
+  if (rest.rfind("\"llvm.br\"", 0) == 0) {
+    const std::vector<std::string> ops = split_top(paren_body(rest, rest.find('(')));
+    const std::vector<std::string> succ = successors(rest);
+    if (succ.empty()) return line;
+    if (ops.empty() || ops[0].empty()) return "llvm.br " + succ[0];
+    const std::vector<std::string> tys = operand_types(rest);
+    std::string a = "llvm.br " + succ[0] + "(";
+    for (size_t i = 0; i < ops.size(); ++i) a += (i ? ", " : "") + ops[i];
+    a += " : ";
+    for (size_t i = 0; i < tys.size(); ++i) a += (i ? ", " : "") + tys[i];
+    return a + ")";
+  }
+  if (rest.rfind("\"llvm.cond_br\"", 0) == 0) {
+    const std::vector<std::string> ops = split_top(paren_body(rest, rest.find('(')));
+    const std::vector<std::string> succ = successors(rest);
+    if (ops.empty() || succ.size() < 2) return line;
+    return "llvm.cond_br " + ops[0] + ", " + succ[0] + ", " + succ[1];
+  }
+  static const char* kPred[] = {"eq", "ne", "slt", "sle", "sgt", "sge", "ult", "ule", "ugt", "uge"};
+  if (rest.rfind("\"llvm.icmp\"", 0) == 0) {
+    const std::vector<std::string> ops = split_top(paren_body(rest, rest.find('(')));
+    const std::string pv = property(rest, "predicate");
+    // `predicate = 9 : i64`, or the enum spelled out (`#llvm<icmp_predicate uge>`)
+    int pi = std::isdigit(static_cast<unsigned char>(pv.empty() ? ' ' : pv[0]))
+                 ? std::atoi(pv.c_str()) : -1;
+    for (int i = 0; i < 10 && pi < 0; ++i) {
+      const std::string nm = std::string(" ") + kPred[i] + ">";
+      if (pv.find(nm) != std::string::npos) pi = i;
+    }
+    const std::vector<std::string> tys = operand_types(rest);
+    if (ops.size() != 2 || pi < 0 || pi > 9) return line;
+    return lhs + "llvm.icmp \"" + kPred[pi] + "\" " + ops[0] + ", " + ops[1] + " : " +
+           (tys.empty() ? std::string("i32") : tys[0]);
+  }
+  for (const char* op : {"add", "sub", "mul", "shl"}) {
+    const std::string g = std::string("\"llvm.") + op + "\"";
+    if (rest.rfind(g, 0) == 0) {
+      const std::vector<std::string> ops = split_top(paren_body(rest, rest.find('(')));
+      const std::vector<std::string> tys = operand_types(rest);
+      if (ops.size() != 2) return line;
+      return lhs + "llvm." + op + " " + ops[0] + ", " + ops[1] + " : " +
+             (tys.empty() ? std::string("i32") : tys[0]);
+    }
+  }
+  // `%r = "llvm.zext"(%v) : (i32) -> i64` -> `%r = llvm.zext %v : i32 to i64`
+  for (const char* op : {"zext", "sext", "trunc", "bitcast"}) {
+    const std::string g = std::string("\"llvm.") + op + "\"";
+    if (rest.rfind(g, 0) == 0) {
+      const std::vector<std::string> ops = split_top(paren_body(rest, rest.find('(')));
+      const std::string t = types_of(rest);
+      const size_t arrow = t.find("->");
+      const std::vector<std::string> tys = operand_types(rest);
+      if (ops.size() != 1 || arrow == std::string::npos) return line;
+      return lhs + "llvm." + op + " " + ops[0] + " : " + (tys.empty() ? std::string("i32") : tys[0]) +
+             " to " + trim(t.substr(arrow + 2));
+    }
+  }
   return line;
 }
 
@@ -204,8 +275,9 @@ bool parse_module(const std::string& text, Module* out, std::string* err) {
         const std::string& bl = lines[i];
         depth += count(bl, '{') - count(bl, '}');
         if (depth > 0) {
+          // block labels after the entry block are kept (control flow lowering)
           const std::string t = trim(bl);
-          if (!t.empty() && t.rfind("^bb", 0) != 0) f.body_lines.push_back(t);
+          if (!t.empty() && t.rfind("^bb0", 0) != 0) f.body_lines.push_back(t);
         }
         ++i;
       }
@@ -241,8 +313,8 @@ bool parse_module(const std::string& text, Module* out, std::string* err) {
           f.is_entry = bl.find("hacc.entry") != std::string::npos;
         } else if (bl.rfind("^bb0(", 0) == 0) {
           bb_args = parse_named_args(paren_body(bl, bl.find('(')));
-        } else if (!bl.empty() && bl.rfind("^bb", 0) != 0) {
-          f.body_lines.push_back(normalize_generic(bl));
+        } else if (!bl.empty() && bl.rfind("^bb0", 0) != 0) {
+          f.body_lines.push_back(bl.rfind("^bb", 0) == 0 ? bl : normalize_generic(bl));
         }
         ++i;
       }
