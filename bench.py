@@ -64,6 +64,20 @@ class Workload:
     def cpu_sample(self, th, s, seconds: float):
         raise NotImplementedError
 
+    # The same step through the `hip` codegen target: the example module's kernel
+    # (tilers_hip/examples/<stem>.mlir, emitted and compiled by the build) launched
+    # by name on `tiles` logical tiles.
+    emitted = None  # (module stem, kernel name)
+
+    def emitted_args(self, i: int):
+        raise NotImplementedError
+
+    def emitted_step(self, th, s, i: int):
+        import ctypes as C
+        tiles, bufs, scalars = self.emitted_args(i)
+        args = [C.c_void_p(b.as_raw_ptr()) for b in bufs] + [C.c_uint32(x) for x in scalars]
+        self.launcher.launch(self.emitted[1], th.LaunchGrid.blocks_only(tiles), args, s)
+
 
 def rotation_sets(bytes_per_set: int) -> int:
     return max(1, -(-2 * MALL_BYTES // bytes_per_set))
@@ -92,6 +106,12 @@ class Softmax(Workload):
     def step(self, th, s, i):
         x, y = self.sets[i % len(self.sets)]
         th.softmax(x, y, self.rows, self.cols, th.TileDtype.F32, s)
+
+    emitted = ("softmax_rows", "softmax_rows_f32")   # one 1 x 1024 row per tile
+
+    def emitted_args(self, i):
+        x, y = self.sets[i % len(self.sets)]
+        return self.rows, [x, y], []
 
     def cpu_sample(self, th, s, seconds):
         from oracle import oracle as orc
@@ -133,6 +153,11 @@ class Gemm(Workload):
         th.matmul(self.a, self.b, self.c, self.M, self.K, self.N, getattr(D, self.in_dt),
                   getattr(D, self.out_dt), False, stream=s)
 
+    emitted = ("config_gemms", "gemm_4096_bf16_acc_f32")
+
+    def emitted_args(self, i):
+        return 1, [self.a, self.b, self.c], []
+
     def cpu_sample(self, th, s, seconds):
         from oracle import oracle as orc
         import numpy as np
@@ -161,6 +186,8 @@ class Mlp(Gemm):
         return {"workload": "MLP GEMM M=8192 K=4096 N=14336, f16 in, f32 acc, f16 out",
                 "M": self.M, "N": self.N, "K": self.K}
 
+    emitted = ("config_gemms", "mlp_up_f16")
+
     def setup(self, th, dev, s):
         D = th.TileDtype
         self.a = dev.alloc(self.M * self.K, D.F16)
@@ -173,6 +200,7 @@ class Mlp(Gemm):
 class Swiglu(Mlp):
     """Config 3's MLP shape with the gate epilogue fused: C = silu(A.B) * UP (f16)."""
     name = "swiglu"
+    emitted = None
 
     def config(self):
         return {"workload": "MLP gate GEMM M=8192 K=4096 N=14336 with fused silu*mul "
@@ -276,6 +304,11 @@ class Attn(Workload):
         th.attention_prefill(q, k, v, self.o, self.B, self.S, 0, self.S, self.Dh, self.H, self.H,
                              th.TileDtype.BF16, s)
 
+    emitted = ("prefill_bf16", "prefill_bf16")   # one tile per batch element
+
+    def emitted_args(self, i):
+        return self.B, self.bufs + [self.o], [self.S, 0, self.S, self.Dh, self.H, self.H]
+
     def cpu_sample(self, th, s, seconds):
         from oracle import oracle as orc
         q, k, v = (b.copy_to_host(s) for b in self.bufs)
@@ -321,6 +354,11 @@ class Decode(Workload):
     def step(self, th, s, i):
         th.attention_decode(self.q, self.k, self.v, self.o, self.B, self.L, self.L, self.Dh,
                             self.NH, self.NKV, th.TileDtype.BF16, self.ws, self.wsz, s)
+
+    emitted = ("decode_bf16", "decode_bf16")   # one tile per batch element
+
+    def emitted_args(self, i):
+        return self.B, [self.q, self.k, self.v, self.o], [self.L, self.L, self.Dh, self.NH, self.NKV]
 
     def cpu_sample(self, th, s, seconds):
         from oracle import oracle as orc
@@ -387,13 +425,21 @@ def cpu_model() -> str:
     return "unknown"
 
 
-def run(name: str, steps: int, warmup: int, cpu_seconds: float, settle_ms: float) -> dict:
+def run(name: str, steps: int, warmup: int, cpu_seconds: float, settle_ms: float,
+        path: str = "library") -> dict:
     import tilers_hip as th
     w = WORKLOADS[name]()
     dev = th.HipDevice(0)
     s = dev.create_stream()
-    log(f"[bench] {name}: setup on {dev.name()} ({dev.arch()})")
+    log(f"[bench] {name}: setup on {dev.name()} ({dev.arch()}), {path} path")
     w.setup(th, dev, s)
+    if path == "emitted":
+        from tilers_hip import _build
+        if w.emitted is None:
+            raise SystemExit(f"bench.py: no emitted kernel for --config {name}")
+        w.launcher = dev.create_launcher()
+        w.launcher.load(_build.example_path(w.emitted[0]), th.KernelMode.GENERAL)
+        w.step = lambda th_, s_, i: w.emitted_step(th_, s_, i)
     s.synchronize()
     settle_steps, t0 = 0, time.perf_counter()
     while (time.perf_counter() - t0) * 1e3 < settle_ms:
@@ -445,7 +491,7 @@ def run(name: str, steps: int, warmup: int, cpu_seconds: float, settle_ms: float
         "vs_baseline": None,
         "dtype": w.dtype,
         "data": "synthetic (seeded on-device PRNG, inputs resident in HBM)",
-        "config": w.config(),
+        "config": dict(w.config(), **({"path": "emitted: " + w.emitted[1]} if path == "emitted" else {})),
         "roofline": {"bound": w.bound, "achieved": round(value, 3), "peak": peak, "unit": w.unit,
                      "frac": round(value / peak, 4), "traffic": measured_traffic(name)},
         "cpu_baseline": cpu,
@@ -462,6 +508,9 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--settle-ms", type=float, default=300.0,
                     help="wall time of untimed steps before the warmup (clock ramp)")
+    ap.add_argument("--path", default="library", choices=("library", "emitted"),
+                    help="library: the C-ABI tile op; emitted: the tile_std kernel from the "
+                         "hip codegen target (tilers_hip/examples), launched by name")
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -471,8 +520,8 @@ def main() -> int:
         return 2
     names = list(BENCH_LINES) if args.config == "all" else [args.config]
     for n in names:
-        print(json.dumps(run(n, args.steps, args.warmup, args.cpu_seconds, args.settle_ms)),
-              flush=True)
+        print(json.dumps(run(n, args.steps, args.warmup, args.cpu_seconds, args.settle_ms,
+                             args.path)), flush=True)
     return 0
 
 

@@ -134,6 +134,12 @@ int th_launcher_destroy(th_launcher l);
 int th_launcher_load(th_launcher l, const char* path, th_kernel_mode mode);
 int th_launcher_launch(th_launcher l, const char* name, uint32_t blocks, uint32_t threads_per_block,
                        uint32_t shared_mem_bytes, void** args, size_t nargs, th_stream s);
+/* The hardware grid (workgroups) and workgroup size th_launcher_launch would use
+ * for the same arguments, without launching; `*threads` = 0 for a kernel without
+ * a descriptor (it runs with the caller's block size).  No reference
+ * counterpart: the reference launches exactly the grid it is given. */
+int th_launcher_grid(th_launcher l, const char* name, uint32_t blocks, void** args, size_t nargs,
+                     uint64_t* grid, uint32_t* threads);
 
 /* ======================================================================== */
 /* 2. Tile ops                                                                */

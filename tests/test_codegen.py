@@ -411,18 +411,18 @@ def test_loop_example_lowers_to_a_tile_grid():
             "uint32_t th_tiles_in)") in src
     assert "const uint32_t th_tiles = th_tiles_in ? static_cast<uint32_t>(s2) : 0u;" in src
     assert "th::entry::softmax_rows<th::kF32, 4>(" in src and "th_tiles * 1u, 1024u);" in src
-    assert "__th_desc_softmax_loop_f32 = {th::kLaunchDescMagic, 256u, 1u, 1u, 0u, 3u, 16u, 65536u};" in src
+    assert "__th_desc_softmax_loop_f32 = {th::kLaunchDescMagic, 256u, 1u, 1u, 0u, 3u, 16u, 65536u, 0u};" in src
     # an i64 bound, `ult` with the body on the true edge, `1 + i`, a shl-scaled offset
     assert "uint64_t s3, uint32_t th_tiles_in)" in src
     assert "th_tiles_in ? static_cast<uint32_t>(s3) : 0u;" in src
-    assert "__th_desc_add_loop_f32 = {th::kLaunchDescMagic, 256u, 2u, 1u, 0u, 4u, 1u, 65536u};" in src
+    assert "__th_desc_add_loop_f32 = {th::kLaunchDescMagic, 256u, 2u, 1u, 0u, 4u, 1u, 65536u, 0u};" in src
 
 
 def test_loop_generic_form_and_constant_trip():
     src = th.emit((EXAMPLES / "softmax_loop_generic.mlir").read_text()).source
     assert "const uint32_t th_tiles = th_tiles_in ? 48u : 0u;" in src
     # 48 iterations of one 4-row tile, one workgroup each
-    assert "__th_desc_softmax_loop_bf16_generic = {th::kLaunchDescMagic, 256u, 48u, 1u, 0u, 0u, 0u, 0u};" in src
+    assert "__th_desc_softmax_loop_bf16_generic = {th::kLaunchDescMagic, 256u, 48u, 1u, 0u, 0u, 0u, 0u, 0u};" in src
 
 
 def test_pipelined_for_marker_sets_the_pipeline_depth():
@@ -435,7 +435,7 @@ def test_pipelined_for_marker_sets_the_pipeline_depth():
     assert "softmax_rows<th::kF32, 4, false>(" in one and "pipelined_for(1)" in one
     assert "softmax_rows<th::kF32, 4>(" in none and "pipelined_for" not in none.split("->")[0]
     # 16 rows per streaming workgroup, 4 without streaming
-    assert "0u, 3u, 16u, 65536u};" in two and "0u, 3u, 4u, 65536u};" in one
+    assert "0u, 3u, 16u, 65536u, 0u};" in two and "0u, 3u, 4u, 65536u, 0u};" in one
 
 
 def test_pipelined_for_depth_is_the_gemm_lds_ring_depth():

@@ -79,8 +79,10 @@ def test_config4_prefill_emitted(dev, stream, launcher):
     v = rnd(dev, stream, n, D.BF16, "normal", 0.0, 1.0, SEED0 + 204)
     o = dev.alloc(n, D.BF16)
     scal = [C.c_uint32(x) for x in (S, 0, S, Dh, H, H)]
-    launcher.launch("prefill_bf16", th.LaunchGrid.blocks_only(B), [ptr(q), ptr(k), ptr(v), ptr(o)] + scal,
-                    stream)
+    args = [ptr(q), ptr(k), ptr(v), ptr(o)] + scal
+    # one 512-thread workgroup per (batch, head, 256-query block), as the library launches
+    assert launcher.hardware_grid("prefill_bf16", th.LaunchGrid.blocks_only(B), args) == (B * H * S // 256, 512)
+    launcher.launch("prefill_bf16", th.LaunchGrid.blocks_only(B), args, stream)
     qh, kh, vh = (t.copy_to_host(stream) for t in (q, k, v))
     got = orc.widen(o.copy_to_host(stream), orc.BF16).reshape(B, S, H, Dh)
     assert np.isfinite(got).all()
@@ -104,8 +106,51 @@ def test_config5_decode_emitted(dev, stream, launcher):
     v = rnd(dev, stream, B * NKV * L * Dh, D.BF16, "normal", 0.0, 1.0, SEED0 + 205)
     o = dev.alloc(B * NH * Dh, D.BF16)
     scal = [C.c_uint32(x) for x in (L, L, Dh, NH, NKV)]
-    launcher.launch("decode_bf16", th.LaunchGrid.blocks_only(B), [ptr(q), ptr(k), ptr(v), ptr(o)] + scal,
-                    stream)
+    args = [ptr(q), ptr(k), ptr(v), ptr(o)] + scal
+    # two workgroups per CU; 512 (batch, kv_head) items on MI355X's 256 CUs run unsplit
+    grid, threads = launcher.hardware_grid("decode_bf16", th.LaunchGrid.blocks_only(B), args)
+    assert threads == 256 and grid == min(B * NKV * (L // 512), 2 * dev.cu_count())
+    launcher.launch("decode_bf16", th.LaunchGrid.blocks_only(B), args, stream)
     ref = orc.attention_decode(q.copy_to_host(stream), k.copy_to_host(stream),
                                v.copy_to_host(stream), orc.BF16, B, L, L, Dh, NH, NKV)
     assert_attn_close(orc.widen(o.copy_to_host(stream), orc.BF16), ref, "emitted config5")
+
+
+def test_decode_long_context_splits_in_kernel(dev, stream, launcher):
+    """B = 1, L = 32K: 8 (batch, kv_head) items over a grid of two workgroups per CU.
+    Each item's 64 chunks are split over 64 workgroups and the last to finish merges
+    the partials; a second launch (arrival counters reset by the first) gives the same
+    bits."""
+    B, NH, NKV, L, Dh = 1, 32, 8, 32768, 128
+    q = rnd(dev, stream, B * NH * Dh, D.BF16, "normal", 0.0, 1.0, SEED0 + 6)
+    k = rnd(dev, stream, B * NKV * L * Dh, D.BF16, "normal", 0.0, 1.0, SEED0 + 106)
+    v = rnd(dev, stream, B * NKV * L * Dh, D.BF16, "normal", 0.0, 1.0, SEED0 + 206)
+    o = dev.alloc(B * NH * Dh, D.BF16)
+    scal = [C.c_uint32(x) for x in (L, L, Dh, NH, NKV)]
+    args = [ptr(q), ptr(k), ptr(v), ptr(o)] + scal
+    grid, _ = launcher.hardware_grid("decode_bf16", th.LaunchGrid.blocks_only(B), args)
+    assert grid == min(NKV * (L // 512), 2 * dev.cu_count()) and grid > B * NKV
+    launcher.launch("decode_bf16", th.LaunchGrid.blocks_only(B), args, stream)
+    first = o.copy_to_host(stream)
+    ref = orc.attention_decode(q.copy_to_host(stream), k.copy_to_host(stream),
+                               v.copy_to_host(stream), orc.BF16, B, L, L, Dh, NH, NKV)
+    assert_attn_close(orc.widen(first, orc.BF16), ref, "emitted decode B=1 L=32K")
+    launcher.launch("decode_bf16", th.LaunchGrid.blocks_only(B), args, stream)
+    np.testing.assert_array_equal(o.copy_to_host(stream), first)
+
+
+@pytest.mark.parametrize("B,L,max_seq", [(1, 40000, 40003), (3, 513, 600), (1, 1, 8)])
+def test_decode_split_ragged(dev, stream, launcher, B, L, max_seq):
+    """79 chunks over 4 items: 40 splits of two chunks, the last of one; two chunks
+    with a one-position last chunk; a single position (nothing to split)."""
+    NH, NKV, Dh = 16, 4, 128
+    q = rnd(dev, stream, B * NH * Dh, D.BF16, "normal", 0.0, 1.0, SEED0 + 7 + L)
+    k = rnd(dev, stream, B * NKV * max_seq * Dh, D.BF16, "normal", 0.0, 1.0, SEED0 + 107 + L)
+    v = rnd(dev, stream, B * NKV * max_seq * Dh, D.BF16, "normal", 0.0, 1.0, SEED0 + 207 + L)
+    o = dev.alloc(B * NH * Dh, D.BF16)
+    scal = [C.c_uint32(x) for x in (L, max_seq, Dh, NH, NKV)]
+    launcher.launch("decode_bf16", th.LaunchGrid.blocks_only(B), [ptr(q), ptr(k), ptr(v), ptr(o)] + scal,
+                    stream)
+    ref = orc.attention_decode(q.copy_to_host(stream), k.copy_to_host(stream),
+                               v.copy_to_host(stream), orc.BF16, B, L, max_seq, Dh, NH, NKV)
+    assert_attn_close(orc.widen(o.copy_to_host(stream), orc.BF16), ref, f"emitted decode B={B} L={L}")

@@ -769,18 +769,27 @@ attn_decode_combine(const float* __restrict__ ws, uint16_t* __restrict__ O, uint
 // q_pos_stride is the element stride between consecutive query rows of one head
 // (NH*D for [S][NH][D]); kv tensors are [B][NKV][max_seq][D].
 // ============================================================================
+namespace gen_attn {
+constexpr int CH = 1024;   // scores per pass
+template <int NT>
+constexpr int smem_floats() { return 256 + CH + NT / 64; }
+}  // namespace gen_attn
+
+// `smem` (LDS, gen_attn::smem_floats<NT>() floats) holds the query row, one pass of
+// scores and the cross-wave reduction slots; a kernel that also runs an
+// LDS-filling path passes part of that path's arena.
 template <int DT, int NT = 256>
-__device__ __forceinline__ void attn_general_item(
+__device__ __forceinline__ void attn_general_item_smem(
     const void* __restrict__ Q, const void* __restrict__ K, const void* __restrict__ V,
     void* __restrict__ O, uint32_t seq_len, uint32_t start_pos, uint32_t max_seq,
     uint32_t kv_len, uint32_t head_dim, uint32_t nh, uint32_t nkv, int causal, float scale,
-    uint32_t item) {
-  constexpr int CH = 1024;
+    uint32_t item, float* smem) {
+  constexpr int CH = gen_attn::CH;
   constexpr int NW = NT / 64;
   static_assert(NT >= 256 && NT % 64 == 0, "head_dim up to 256 needs >= 256 threads");
-  __shared__ float qs[256];
-  __shared__ float sc[CH];
-  __shared__ float red[NW];
+  float* qs = smem;
+  float* sc = smem + 256;
+  float* red = smem + 256 + CH;
   const uint32_t h = item % nh;
   const uint32_t qi = (item / nh) % seq_len;
   const uint32_t b = item / (nh * seq_len);
@@ -843,6 +852,18 @@ __device__ __forceinline__ void attn_general_item(
     if constexpr (DT == kF32) static_cast<float*>(O)[q_off + t] = o;
     else static_cast<uint16_t*>(O)[q_off + t] = f32_to_u16<DT>(o);
   }
+  __syncthreads();  // smem is reused by the next item
+}
+
+template <int DT, int NT = 256>
+__device__ __forceinline__ void attn_general_item(
+    const void* __restrict__ Q, const void* __restrict__ K, const void* __restrict__ V,
+    void* __restrict__ O, uint32_t seq_len, uint32_t start_pos, uint32_t max_seq,
+    uint32_t kv_len, uint32_t head_dim, uint32_t nh, uint32_t nkv, int causal, float scale,
+    uint32_t item) {
+  __shared__ float smem[gen_attn::smem_floats<NT>()];
+  attn_general_item_smem<DT, NT>(Q, K, V, O, seq_len, start_pos, max_seq, kv_len, head_dim, nh,
+                                 nkv, causal, scale, item, smem);
 }
 
 template <int DT>

@@ -4,7 +4,8 @@
 // these.  Each loops over its work items grid-stride (item w is handled by
 // workgroup w mod gridDim.x), so results never depend on the hardware grid the
 // launcher picks from the kernel's launch descriptor; the descriptor only sizes
-// the grid.  Per-tile pointer offsets follow the #[tile_kernel] prelude: logical
+// the grid.  (One exception: the decode splits each sequence over as many
+// workgroups as the grid allows, and the split changes the summation order.)  Per-tile pointer offsets follow the #[tile_kernel] prelude: logical
 // tile t sees every view offset by t * rows * cols of that view
 // (crates/tile_std_macros/src/lib.rs:217-266).
 #pragma once
@@ -14,6 +15,7 @@
 #include "common.hpp"
 #include "gemm.hpp"
 #include "norm.hpp"
+#include "prefill_asm.hpp"
 #include "softmax.hpp"
 
 namespace th {
@@ -171,41 +173,174 @@ __device__ __forceinline__ void prefill(const void* q, const void* k, const void
                                         uint32_t batch, uint32_t seq_len, uint32_t start_pos,
                                         uint32_t max_seq, uint32_t head_dim, uint32_t nh,
                                         uint32_t nkv) {
-  if (nkv == 0 || nh % nkv != 0 || start_pos + seq_len > max_seq || head_dim == 0) return;
+  if (nkv == 0 || nh % nkv != 0 || start_pos + seq_len > max_seq || head_dim == 0 ||
+      seq_len == 0)
+    return;
   const float scale = 1.0f / __builtin_sqrtf(static_cast<float>(head_dim));
+  // the library's kernel (512 threads, the whole LDS as its K/V ring); the general
+  // path below borrows the start of the same arena
+  u32x4* arena = lds::dma_lds_arena<pfa::NS * 2 * pfa::BKV * pfa::D * 2>();
   if constexpr (DT != kF32) {
     const uintptr_t align = reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) |
                             reinterpret_cast<uintptr_t>(v) | reinterpret_cast<uintptr_t>(o);
-    if (head_dim == fa::D && (align & 15) == 0) {
-      const uint32_t nqb = (seq_len + fa::BQ - 1) / fa::BQ;
+    if (head_dim == pfa::D && (align & 15) == 0) {
+      const uint32_t nqb = (seq_len + pfa::BQ - 1) / pfa::BQ;
       for (uint32_t w = blockIdx.x; w < batch * nh * nqb; w += gridDim.x) {
         uint32_t bh, qb;
         prefill_work(w, batch * nh, nqb, bh, qb);
-        // 4-stage ring: the general kernel below needs LDS in the same entry
-        prefill_tile_dma<DT, 4>(static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
-                             static_cast<const uint16_t*>(v), static_cast<uint16_t*>(o), seq_len,
-                             start_pos, max_seq, nh, nkv, scale * kLog2e, bh, qb);
+        pfa::prefill_tile<DT>(static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
+                              static_cast<const uint16_t*>(v), static_cast<uint16_t*>(o), seq_len,
+                              start_pos, max_seq, nh, nkv, scale * kLog2e, bh, qb);
+        __syncthreads();  // every wave is done with the ring before the next item's DMA
       }
       return;
     }
   }
+  static_assert(gen_attn::smem_floats<pfa::NT>() * 4 <= pfa::NS * 2 * pfa::BKV * pfa::D * 2,
+                "general path's LDS inside the arena");
   if (head_dim <= 256) {
     for (uint32_t w = blockIdx.x; w < batch * seq_len * nh; w += gridDim.x)
-      attn_general_item<DT, fa::NT>(q, k, v, o, seq_len, start_pos, max_seq, start_pos + seq_len,
-                                    head_dim, nh, nkv, 1, scale, w);
+      attn_general_item_smem<DT, pfa::NT>(q, k, v, o, seq_len, start_pos, max_seq,
+                                          start_pos + seq_len, head_dim, nh, nkv, 1, scale, w,
+                                          reinterpret_cast<float*>(arena));
   }
 }
 
 // ---- GQA decode, one query token; runtime params in the Metal target's order ----
+//
+// KV split inside one launch: the (batch, kv_head) items are split into
+// n_split = ceil(gridDim / items) chunk ranges (at most kDecodeMaxSplit, and
+// only as many as the partials area holds); every split writes its partial
+// (m, l, O) to `decode_partials`, counts itself in `decode_arrivals[item]`, and
+// the workgroup that arrives last merges the item's partials into O and resets
+// the count for the next launch.  The launcher sizes the grid to about two
+// workgroups per CU, so one long sequence spreads over the whole chip while a
+// large batch runs unsplit (one workgroup per item).
+//
+// The partials and counters are arrays of this code object in GPU memory: calls
+// of one decode kernel that overlap on a device (other streams) race on them.
+namespace dsplit {
+constexpr uint32_t kMaxSplit = 64;                 // chunk ranges per item
+constexpr uint32_t kMaxItems = 4096;               // counters: split items per launch
+constexpr size_t kPartialFloats = size_t(2) << 20; // 8 MiB of partial records
+}  // namespace dsplit
+static __device__ __align__(256) float decode_partials[dsplit::kPartialFloats];
+static __device__ uint32_t decode_arrivals[dsplit::kMaxItems];
+
+// O rows of item bk = sum_s 2^(m_s - M) O_s / sum_s 2^(m_s - M) l_s over its
+// n_split records (as decode_tile writes them), for all G heads of the item.
+template <int DT, int G>
+__device__ __forceinline__ void decode_merge(const float* __restrict__ ws, uint16_t* __restrict__ O,
+                                             uint32_t bk, uint32_t nh, uint32_t nkv,
+                                             uint32_t n_split) {
+  constexpr int D = dec::D, NT = dec::NT, R = D + 2;
+  constexpr int NP = G * D / 2;                  // output pairs (d, d+1)
+  constexpr int NG = NP >= NT ? 1 : NT / NP;     // thread groups splitting the records
+  constexpr int UNR = 8;
+  __shared__ float s_w[G][dsplit::kMaxSplit];
+  __shared__ float s_den[G];
+  __shared__ float2 s_part[NG > 1 ? NG : 1][NG > 1 ? NP : 1];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const float* base = ws + static_cast<size_t>(bk) * G * n_split * R;
+  for (int q = wave; q < G; q += NT / 64) {
+    const float* rq = base + static_cast<size_t>(q) * n_split * R;
+    const bool has = static_cast<uint32_t>(lane) < n_split;
+    const float m = has ? rq[lane * R] : -INFINITY;
+    const float l = has ? rq[lane * R + 1] : 0.0f;
+    const float M = wave_max(m);
+    const float w = (m == -INFINITY) ? 0.0f : exp2_fast(m - M);
+    if (has) s_w[q][lane] = w;
+    const float den = wave_sum(w * l);
+    if (lane == 0) s_den[q] = den;
+  }
+  __syncthreads();
+  const uint32_t b = bk / nkv, kvh = bk % nkv;
+  for (int i = t % (NG > 1 ? NP : NT); i < NP; i += (NG > 1 ? NP : NT)) {
+    const int q = i / (D / 2), d = 2 * (i % (D / 2));
+    const int grp = NG > 1 ? t / NP : 0;
+    const float* rd = base + static_cast<size_t>(q) * n_split * R + 2 + d;
+    float2 acc = {0.0f, 0.0f};
+    uint32_t s = grp;
+    for (; s + (UNR - 1) * NG < n_split; s += UNR * NG) {
+      float2 o[UNR];
+#pragma unroll
+      for (int u = 0; u < UNR; ++u) o[u] = *reinterpret_cast<const float2*>(rd + (s + u * NG) * R);
+#pragma unroll
+      for (int u = 0; u < UNR; ++u) {
+        const float w = s_w[q][s + u * NG];
+        acc.x = __builtin_fmaf(w, o[u].x, acc.x);
+        acc.y = __builtin_fmaf(w, o[u].y, acc.y);
+      }
+    }
+    for (; s < n_split; s += NG) {
+      const float2 o = *reinterpret_cast<const float2*>(rd + s * R);
+      acc.x = __builtin_fmaf(s_w[q][s], o.x, acc.x);
+      acc.y = __builtin_fmaf(s_w[q][s], o.y, acc.y);
+    }
+    if constexpr (NG > 1) {
+      s_part[grp][i] = acc;
+    } else {
+      const float den = s_den[q];
+      uint16_t* op = O + (static_cast<size_t>(b) * nh + kvh * G + q) * D + d;
+      op[0] = f32_to_u16<DT>(den > 0.0f ? acc.x / den : 0.0f);
+      op[1] = f32_to_u16<DT>(den > 0.0f ? acc.y / den : 0.0f);
+    }
+  }
+  if constexpr (NG > 1) {
+    __syncthreads();
+    for (int i = t; i < NP; i += NT) {
+      const int q = i / (D / 2), d = 2 * (i % (D / 2));
+      float2 acc = s_part[0][i];
+#pragma unroll
+      for (int g = 1; g < NG; ++g) {
+        acc.x += s_part[g][i].x;
+        acc.y += s_part[g][i].y;
+      }
+      const float den = s_den[q];
+      uint16_t* op = O + (static_cast<size_t>(b) * nh + kvh * G + q) * D + d;
+      op[0] = f32_to_u16<DT>(den > 0.0f ? acc.x / den : 0.0f);
+      op[1] = f32_to_u16<DT>(den > 0.0f ? acc.y / den : 0.0f);
+    }
+  }
+  __syncthreads();  // s_w / s_den / s_part are reused by the next item
+}
+
 template <int DT, int G>
 __device__ __forceinline__ void decode_group(const uint16_t* q, const uint16_t* k,
                                              const uint16_t* v, uint16_t* o, uint32_t batch,
                                              uint32_t seq_len, uint32_t max_seq, uint32_t nh,
                                              uint32_t nkv, float scale_log2) {
   const uint32_t nchunks = (seq_len + dec::CHUNK - 1) / dec::CHUNK;
-  for (uint32_t w = blockIdx.x; w < batch * nkv; w += gridDim.x)
-    decode_tile<DT, G>(q, k, v, o, nullptr, seq_len, max_seq, nh, nkv, 1, scale_log2, w, 0, 0,
-                       nchunks);
+  const uint32_t items = batch * nkv;
+  uint32_t n_split = (gridDim.x + items - 1) / items;
+  n_split = min(n_split, min(nchunks, dsplit::kMaxSplit));
+  const size_t per_split = static_cast<size_t>(items) * G * (dec::D + 2);
+  n_split = min(static_cast<size_t>(n_split), dsplit::kPartialFloats / per_split);
+  if (items > dsplit::kMaxItems || n_split < 2) n_split = 1;
+  const uint32_t cps = (nchunks + n_split - 1) / n_split;
+  n_split = (nchunks + cps - 1) / cps;   // no empty split
+  __shared__ uint32_t s_last;
+  for (uint32_t w = blockIdx.x; w < items * n_split; w += gridDim.x) {
+    const uint32_t bk = w / n_split, split = w % n_split;
+    const uint32_t c0 = split * cps, c1 = min(nchunks, c0 + cps);
+    // unsplit: the workgroup covers the whole sequence and writes O itself
+    decode_tile<DT, G>(q, k, v, o, n_split > 1 ? decode_partials : nullptr, seq_len, max_seq, nh,
+                       nkv, n_split, scale_log2, bk, split, c0, c1);
+    if (n_split == 1) continue;
+    // decode_tile ends on a barrier: every wave's partial stores are issued.  The
+    // release fence makes them visible device-wide before the arrival counts.
+    if (threadIdx.x == 0) {
+      __threadfence();
+      s_last = atomicAdd(&decode_arrivals[bk], 1u) == n_split - 1;
+    }
+    __syncthreads();
+    if (s_last) {
+      __threadfence();   // acquire: the other splits' partials
+      decode_merge<DT, G>(decode_partials, o, bk, nh, nkv, n_split);
+      if (threadIdx.x == 0) decode_arrivals[bk] = 0;   // ready for the next launch
+    }
+    __syncthreads();   // s_last is rewritten by the next item
+  }
 }
 
 template <int DT>

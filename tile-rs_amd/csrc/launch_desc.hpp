@@ -31,12 +31,17 @@ struct LaunchDesc {
   uint32_t scale_args;    // (a0 + 1) | (a1 + 1) << 8; 0 = none
   uint32_t scale_div;     // d0 | d1 << 16 (0 reads as 1)
   uint32_t wg_cap;        // maximum workgroups per tile after scaling (0 = none)
+  // Cap on the whole grid, in workgroups per compute unit (0 = none): kernels
+  // that size their own work split from gridDim (the decode's KV split) are
+  // launched with about as many workgroups as stay resident.
+  uint32_t grid_per_cu;
 };
 
 // hardware workgroups for `tiles` logical tiles; `args` are the kernel's
-// argument pointers (the driver's kernelParams convention)
+// argument pointers (the driver's kernelParams convention); `cus` the device's
+// compute units (for grid_per_cu)
 inline uint64_t desc_grid(const LaunchDesc& d, uint64_t tiles, void* const* args = nullptr,
-                          size_t nargs = 0) {
+                          size_t nargs = 0, uint32_t cus = 0) {
   const uint64_t tpw = d.tiles_per_wg ? d.tiles_per_wg : 1;
   uint64_t wpt = d.wg_per_tile ? d.wg_per_tile : 1;
   for (int f = 0; f < 2; ++f) {
@@ -49,7 +54,12 @@ inline uint64_t desc_grid(const LaunchDesc& d, uint64_t tiles, void* const* args
   }
   if (d.wg_cap && wpt > d.wg_cap) wpt = d.wg_cap;
   if (wpt == 0) wpt = 1;
-  return (tiles + tpw - 1) / tpw * wpt;
+  uint64_t grid = (tiles + tpw - 1) / tpw * wpt;
+  if (d.grid_per_cu && cus) {
+    const uint64_t cap = static_cast<uint64_t>(d.grid_per_cu) * cus;
+    if (grid > cap) grid = cap;
+  }
+  return grid;
 }
 
 }  // namespace th

@@ -375,11 +375,12 @@ int th_launcher_load(th_launcher l, const char* path, th_kernel_mode mode) {
   return TH_OK;
 }
 
-int th_launcher_launch(th_launcher l, const char* name, uint32_t blocks, uint32_t threads_per_block,
-                       uint32_t shared_mem_bytes, void** args, size_t nargs, th_stream s) {
-  if (!l || !name) return fail(TH_KERNEL_ERROR, "null launcher or kernel name");
-  TH_TRY(th::use_device(l->dev->ordinal));
-  th_launcher_s::Fn fn;
+}  // extern "C"
+
+namespace {
+// The kernel `name` in the launcher's modules, with its launch descriptor (cached
+// per name).
+int find_kernel(th_launcher l, const char* name, th_launcher_s::Fn* out) {
   {
     std::lock_guard<std::mutex> lock(l->mu);
     auto it = l->cache.find(name);
@@ -407,8 +408,36 @@ int th_launcher_launch(th_launcher l, const char* name, uint32_t blocks, uint32_
         return fail(TH_KERNEL_ERROR, std::string("kernel not found in loaded modules: ") + name);
       it = l->cache.emplace(name, found).first;
     }
-    fn = it->second;
+    *out = it->second;
   }
+  return TH_OK;
+}
+}  // namespace
+
+extern "C" {
+
+int th_launcher_grid(th_launcher l, const char* name, uint32_t blocks, void** args, size_t nargs,
+                     uint64_t* grid, uint32_t* threads) {
+  if (!l || !name || !grid || !threads) return fail(TH_KERNEL_ERROR, "null launcher, name or output");
+  TH_TRY(th::use_device(l->dev->ordinal));
+  th_launcher_s::Fn fn;
+  TH_TRY(find_kernel(l, name, &fn));
+  if (!fn.has_desc || blocks == 0) {
+    *grid = blocks;
+    *threads = 0;   // the caller's block size
+    return TH_OK;
+  }
+  *grid = th::desc_grid(fn.desc, blocks, args, nargs, static_cast<uint32_t>(l->dev->cus));
+  *threads = fn.desc.threads;
+  return TH_OK;
+}
+
+int th_launcher_launch(th_launcher l, const char* name, uint32_t blocks, uint32_t threads_per_block,
+                       uint32_t shared_mem_bytes, void** args, size_t nargs, th_stream s) {
+  if (!l || !name) return fail(TH_KERNEL_ERROR, "null launcher or kernel name");
+  TH_TRY(th::use_device(l->dev->ordinal));
+  th_launcher_s::Fn fn;
+  TH_TRY(find_kernel(l, name, &fn));
   if (blocks == 0) return TH_OK;
   if (!fn.has_desc) {
     return check_hip(hipModuleLaunchKernel(fn.fn, blocks, 1, 1, threads_per_block, 1, 1,
@@ -416,7 +445,7 @@ int th_launcher_launch(th_launcher l, const char* name, uint32_t blocks, uint32_
                                            nullptr),
                      "hipModuleLaunchKernel", TH_KERNEL_ERROR);
   }
-  const uint64_t grid = th::desc_grid(fn.desc, blocks, args, nargs);
+  const uint64_t grid = th::desc_grid(fn.desc, blocks, args, nargs, static_cast<uint32_t>(l->dev->cus));
   if (grid > 0x7fffffffu) return fail(TH_KERNEL_ERROR, "launch grid too large");
   std::vector<void*> full(args, args + nargs);
   uint32_t tiles = blocks;

@@ -709,7 +709,7 @@ std::string fconst(double v) {
 // trip count.
 void desc(std::ostringstream& os, const Kernel& k, unsigned threads, unsigned wg_per_tile,
           unsigned tiles_per_wg, unsigned scale_args = 0, unsigned scale_div = 0,
-          unsigned wg_cap = 0) {
+          unsigned wg_cap = 0, unsigned grid_per_cu = 0) {
   unsigned long long wpt = wg_per_tile ? wg_per_tile : 1;
   if (k.loop.present) {
     // the kernel runs n tiles for any launched tile count: size the grid for
@@ -730,7 +730,7 @@ void desc(std::ostringstream& os, const Kernel& k, unsigned threads, unsigned wg
   }
   os << "extern \"C\" __device__ th::LaunchDesc __th_desc_" << k.name << " = {th::kLaunchDescMagic, "
      << threads << "u, " << wpt << "u, " << (tiles_per_wg ? tiles_per_wg : 1) << "u, 0u, "
-     << scale_args << "u, " << scale_div << "u, " << wg_cap << "u};\n\n";
+     << scale_args << "u, " << scale_div << "u, " << wg_cap << "u, " << grid_per_cu << "u};\n\n";
 }
 
 // C type of a scalar kernel argument
@@ -1213,15 +1213,18 @@ bool emit_kernel(const Kernel& k, std::ostringstream& os, std::string* err) {
     const TileVal& q = k.tiles.at(hot->ins[0]);
     os << "causal GQA prefill " << dt_name(q.dtype) << " (runtime seq_len, start_pos, max_seq, head_dim, "
        << "num_heads, num_kv_heads) -> th::entry::prefill\n";
-    signature(os, k, 512, {"seq_len", "start_pos", "max_seq", "head_dim", "num_heads", "num_kv_heads"});
+    // the library's kernel: one 512-thread workgroup per (head, 256-query block),
+    // all of LDS, one workgroup per CU
+    signature(os, k, 512, {"seq_len", "start_pos", "max_seq", "head_dim", "num_heads", "num_kv_heads"}, 1);
     const char* ct = dt_ctype(q.dtype);
     os << "  th::entry::prefill<" << dt_enum(q.dtype) << ">(" << in_ptr(0, ct) << ", " << in_ptr(1, ct)
        << ", " << in_ptr(2, ct) << ", " << out_ptr(ct)
        << ", th_tiles, seq_len, start_pos, max_seq, head_dim, num_heads, num_kv_heads);\n}\n";
-    // One workgroup per (head, 256-query block) up to 1024 per tile (e.g. 32 heads x
-    // 8192 queries), so the hardware balances the causal work; workgroups past the
-    // work exit at once (they are dispatched last).
-    desc(os, k, 512, 1024, 1);
+    // Workgroups per tile (batch element) = num_heads x ceil(seq_len / 256), read from
+    // the scalar arguments at launch.
+    const unsigned a_seq = static_cast<unsigned>(k.args.size()) + 0;
+    const unsigned a_nh = static_cast<unsigned>(k.args.size()) + 4;
+    desc(os, k, 512, 1, 1, (a_seq + 1) | ((a_nh + 1) << 8), 256u | (1u << 16), 1u << 20);
     return true;
   }
   if (o == "attention_decode_f32") {
@@ -1236,7 +1239,13 @@ bool emit_kernel(const Kernel& k, std::ostringstream& os, std::string* err) {
     os << "  th::entry::decode<" << dt_enum(q.dtype) << ">(" << in_ptr(0, ct) << ", " << in_ptr(1, ct)
        << ", " << in_ptr(2, ct) << ", " << out_ptr(ct)
        << ", th_tiles, seq_len, max_seq, head_dim, num_heads, num_kv_heads);\n}\n";
-    desc(os, k, 256, 64, 1);
+    // Workgroups per tile (batch element) = num_kv_heads x ceil(seq_len / 512), one
+    // per 512-position chunk, the whole grid capped at two per CU; the kernel splits
+    // each (batch, kv_head)'s chunks over ceil(grid / items) workgroups and the last
+    // of them merges the partials.
+    const unsigned a_seq = static_cast<unsigned>(k.args.size()) + 0;
+    const unsigned a_nkv = static_cast<unsigned>(k.args.size()) + 4;
+    desc(os, k, 256, 1, 1, (a_nkv + 1) | ((a_seq + 1) << 8), 1u | (512u << 16), 1u << 20, 2);
     return true;
   }
   *err = "mlir_to_hip: " + k.name + ": unsupported intrinsic " + hot->op;

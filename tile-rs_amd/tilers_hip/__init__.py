@@ -211,16 +211,31 @@ class HipLauncher:
     def load(self, path: str | os.PathLike, mode: KernelMode = KernelMode.VECTOR) -> None:
         check(lib().th_launcher_load(self.handle, os.fspath(path).encode(), int(mode)))
 
-    def launch(self, name: str, grid: LaunchGrid, args: Sequence[C._SimpleCData | C.c_void_p],
-               stream: HipStream) -> None:
-        """`args` are ctypes values; pointers to them form the kernelParams array."""
+    @staticmethod
+    def _params(args):
         holders = list(args)
         arr = (C.c_void_p * max(1, len(holders)))()
         for i, a in enumerate(holders):
             arr[i] = C.cast(C.pointer(a), C.c_void_p)
+        return holders, arr
+
+    def launch(self, name: str, grid: LaunchGrid, args: Sequence[C._SimpleCData | C.c_void_p],
+               stream: HipStream) -> None:
+        """`args` are ctypes values; pointers to them form the kernelParams array."""
+        holders, arr = self._params(args)
         check(lib().th_launcher_launch(self.handle, name.encode(), grid.blocks,
                                        grid.threads_per_block, grid.shared_mem_bytes, arr,
                                        len(holders), stream.handle))
+
+    def hardware_grid(self, name: str, grid: LaunchGrid,
+                      args: Sequence[C._SimpleCData | C.c_void_p]) -> tuple[int, int]:
+        """(workgroups, threads per workgroup) that `launch` would use; threads is 0
+        for a kernel without a launch descriptor."""
+        holders, arr = self._params(args)
+        g, t = C.c_uint64(), C.c_uint32()
+        check(lib().th_launcher_grid(self.handle, name.encode(), grid.blocks, arr, len(holders),
+                                     C.byref(g), C.byref(t)))
+        return g.value, t.value
 
     def __del__(self):
         try:

@@ -78,6 +78,7 @@ SIGNATURES: dict[str, tuple] = {
     "th_launcher_destroy": (_i, [_vp]),
     "th_launcher_load": (_i, [_vp, _cp, _i]),
     "th_launcher_launch": (_i, [_vp, _cp, _u32, _u32, _u32, _pp, _sz, _vp]),
+    "th_launcher_grid": (_i, [_vp, _cp, _u32, _pp, _sz, C.POINTER(C.c_uint64), C.POINTER(C.c_uint32)]),
     "th_softmax": (_i, [_vp, _vp, _u32, _u32, _i, _vp]),
     "th_matmul": (_i, [_vp, _vp, _vp, _u32, _u32, _u32, _i, _i, _i, _u32, _u64, _u64, _u64, _vp]),
     "th_matmul_silu_mul": (_i, [_vp, _vp, _vp, _vp, _u32, _u32, _u32, _i, _i, _i, _u32, _u64, _u64,
