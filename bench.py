@@ -36,6 +36,7 @@ for _p in (ROOT, ROOT / "tile-rs_amd"):
 
 METRIC = "GEMM/attention TFLOP/s, softmax GB/s, % of MI355X roofline (1 GPU)"
 PEAK_MFMA_TFLOPS = 2500.0   # MI355X dense bf16/f16 MFMA
+PEAK_MFMA_F32_TFLOPS = 157.3  # MI355X dense fp32 MFMA
 PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
 SEED0 = 0x71130000
 MALL_BYTES = 256 << 20
@@ -51,6 +52,7 @@ class Workload:
     bound = "mfma"
     dtype = "bf16"
     unit = "TFLOP/s"
+    peak = None  # TFLOP/s or GB/s; None = the bf16 MFMA or the HBM peak by unit
 
     def work(self) -> float:  # FLOP or bytes per step
         raise NotImplementedError
@@ -195,6 +197,43 @@ class Mlp(Gemm):
         self.c = dev.alloc(self.M * self.N, D.F16)
         th.fill_random(self.a, self.M * self.K, D.F16, "normal", 0.0, 1.0, SEED0 + 3, s)
         th.fill_random(self.b, self.K * self.N, D.F16, "normal", 0.0, 0.02, SEED0 + 103, s)
+
+
+class GemmF32(Gemm):
+    """__tile_matmul_f32 on the fp32 MFMA: 4096^3, A, B and C f32."""
+    name, index, dtype = "gemm_f32", 7, "f32"
+    in_dt, out_dt = "F32", "F32"
+    peak = PEAK_MFMA_F32_TFLOPS
+    emitted = None
+
+    def config(self):
+        return {"workload": "dense GEMM C=A*B, 4096^3, A,B f32 U[-1,1], C f32 (fp32 MFMA)",
+                "M": self.M, "N": self.N, "K": self.K}
+
+    def setup(self, th, dev, s):
+        D = th.TileDtype
+        self.a = dev.alloc(self.M * self.K, D.F32)
+        self.b = dev.alloc(self.K * self.N, D.F32)
+        self.c = dev.alloc(self.M * self.N, D.F32)
+        th.fill_random(self.a, self.M * self.K, D.F32, "uniform", -1.0, 1.0, SEED0 + 7, s)
+        th.fill_random(self.b, self.K * self.N, D.F32, "uniform", -1.0, 1.0, SEED0 + 107, s)
+
+    def cpu_sample(self, th, s, seconds):
+        from oracle import oracle as orc
+        import numpy as np
+        a = self.a.copy_to_host(s).reshape(self.M, self.K)
+        b = self.b.copy_to_host(s)
+        rows, t0, chunk = 0, time.perf_counter(), 64
+        while True:
+            r0 = rows % self.M
+            orc.matmul(np.ascontiguousarray(a[r0:r0 + chunk]), b, chunk, self.K, self.N, orc.F32,
+                       orc.F32)
+            rows += chunk
+            el = time.perf_counter() - t0
+            if el >= seconds:
+                break
+        return 2.0 * rows * self.K * self.N / el / 1e12, (
+            f"{rows} rows of C ({self.M}x{self.N}x{self.K}), oracle f32 FMA")
 
 
 class Swiglu(Mlp):
@@ -401,7 +440,7 @@ class Copy(Workload):
         return 0.0, "none"
 
 
-WORKLOADS = {w.name: w for w in (Softmax, Gemm, Mlp, Attn, Decode, Swiglu, RmsNorm, Copy)}
+WORKLOADS = {w.name: w for w in (Softmax, Gemm, Mlp, Attn, Decode, Swiglu, RmsNorm, GemmF32, Copy)}
 BENCH_LINES = ("attn", "decode", "gemm", "mlp", "softmax")
 
 
@@ -463,9 +502,9 @@ def run(name: str, steps: int, warmup: int, cpu_seconds: float, settle_ms: float
     ms_mean = ev[0].elapsed_ms(ev[-1]) / steps
     work = w.work()
     if w.unit == "TFLOP/s":
-        value, peak = work / (ms * 1e-3) / 1e12, PEAK_MFMA_TFLOPS
+        value, peak = work / (ms * 1e-3) / 1e12, w.peak or PEAK_MFMA_TFLOPS
     else:
-        value, peak = work / (ms * 1e-3) / 1e9, PEAK_HBM_GBS
+        value, peak = work / (ms * 1e-3) / 1e9, w.peak or PEAK_HBM_GBS
     log(f"[bench] {name}: median {ms * 1e3:.1f} us/step (mean {ms_mean * 1e3:.1f}, settle "
         f"{settle_steps} steps / {settle_wall:.0f} ms), {value:.1f} {w.unit} ({value / peak:.1%} of peak)")
     cpu = None

@@ -110,7 +110,7 @@ def test_registry_hip_matches_direct_emit():
     ("softmax_generic", "th::entry::softmax_rows<th::kBF16, 4>"),
     ("matmul_bf16", "th::entry::gemm_dma<th::kBF16, th::kF32, false, th::gemm::kEpiStore>"),
     ("matmul_f16_t", "th::entry::gemm_dma<th::kF16, th::kF16, true, th::gemm::kEpiStore>"),
-    ("matmul_f32", "th::entry::gemm_fma<th::kF32, th::kF32, false, th::gemm::kEpiStore>"),
+    ("matmul_f32", "th::entry::gemm_f32<th::kF32, false, true, th::gemm::kEpiStore>"),
     ("attention_f32", "th::entry::attention_tiles<th::kF32, 256>"),
     ("prefill_bf16", "th::entry::prefill<th::kBF16>"),
     ("decode_bf16", "th::entry::decode<th::kBF16>"),

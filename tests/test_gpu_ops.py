@@ -261,6 +261,31 @@ def test_matmul_integer_bit_exact(dev, stream, in_dt, trans, m, k, n):
     assert np.array_equal(got, ref), f"max diff {np.abs(got - ref).max()}"
 
 
+@pytest.mark.parametrize("m,k,n,trans,out_dt,bsz", [
+    (1000, 777, 1030, False, D.F32, 1),    # ragged in every dimension, K % 4 != 0
+    (513, 1024, 264, True, D.F32, 2),      # B stored N x K, batched
+    (256, 4096, 384, False, D.F16, 1),     # long K, 16-bit output
+    (130, 20, 5, True, D.BF16, 3),         # one partial tile per batch entry
+])
+def test_matmul_f32_mfma(dev, stream, m, k, n, trans, out_dt, bsz):
+    """f32 operands on the fp32 MFMA kernel against the oracle's sequential f32 FMA;
+    the K sum runs in another order, so the check is the GEMM tolerance."""
+    rng = np.random.default_rng(m * 3 + k + n + bsz)
+    a = rng.standard_normal(bsz * m * k).astype(np.float32)
+    b = (rng.standard_normal(bsz * k * n) * 0.05).astype(np.float32)
+    ab, bb = upload(dev, stream, a, D.F32), upload(dev, stream, b, D.F32)
+    cb = dev.alloc(bsz * m * n, out_dt)
+    th.matmul(ab, bb, cb, m, k, n, D.F32, out_dt, trans, batch=bsz, stream=stream)
+    raw = cb.copy_to_host(stream)
+    got = (raw if out_dt == D.F32 else orc.widen(raw, ORC[out_dt])).reshape(bsz, m, n)
+    for i in range(bsz):
+        ref = orc.matmul(a[i * m * k:(i + 1) * m * k], b[i * k * n:(i + 1) * k * n], m, k, n,
+                         orc.F32, ORC[out_dt], b_trans=trans)
+        ref32 = ref if out_dt == D.F32 else orc.widen(ref, ORC[out_dt])
+        assert_gemm_close(got[i], ref32.reshape(m, n), f"f32 {m}x{k}x{n} batch {i}",
+                          u16_dtype=None if out_dt == D.F32 else ORC[out_dt])
+
+
 @pytest.mark.parametrize("out_dt", [D.F16, D.BF16])
 def test_matmul_u16_output_rounding(dev, stream, out_dt):
     rng = np.random.default_rng(5)

@@ -14,6 +14,7 @@
 #include "attention.hpp"
 #include "common.hpp"
 #include "gemm.hpp"
+#include "gemm_f32.hpp"
 #include "norm.hpp"
 #include "prefill_asm.hpp"
 #include "softmax.hpp"
@@ -137,6 +138,31 @@ __device__ __forceinline__ void gemm_dma(const uint16_t* A, const uint16_t* B, v
                                                                       u);
     else
       gemm_dot_tile_256<DT, DTO, BT, EPI>(a, b, c, M, N, K, tm, tn, u);
+  }
+}
+
+// ---- f32 operands: the fp32 MFMA kernel, 128 x 128 tiles (tiles of one
+//      batch entry in XCD-grouped order) ----
+template <int DTO, bool BT, bool VEC, int EPI = gemm::kEpiStore>
+__device__ __forceinline__ void gemm_f32(const float* A, const float* B, void* C, uint32_t M,
+                                         uint32_t N, uint32_t K, uint32_t batch,
+                                         const void* up = nullptr) {
+  constexpr int OSZ = (DTO == kF32) ? 4 : 2;
+  const uint32_t tiles_m = (M + gf32::BM - 1) / gf32::BM, tiles_n = (N + gf32::BN - 1) / gf32::BN;
+  const uint32_t per = tiles_m * tiles_n;
+  // the 16-byte path also needs 16-byte aligned bases (the views' offsets are)
+  const bool vec = VEC && ((reinterpret_cast<uintptr_t>(A) | reinterpret_cast<uintptr_t>(B)) & 15) == 0;
+  for (uint32_t w = blockIdx.x; w < per * batch; w += gridDim.x) {
+    const uint32_t bi = w / per;
+    uint32_t tm, tn;
+    gemm::tile_coords(w % per, tiles_m, tiles_n, tm, tn);
+    const size_t co = static_cast<size_t>(bi) * M * N * OSZ;
+    const float* a = A + static_cast<size_t>(bi) * M * K;
+    const float* b = B + static_cast<size_t>(bi) * K * N;
+    const void* u = up ? static_cast<const char*>(up) + co : nullptr;
+    if (vec) gemm_f32_tile_128<DTO, BT, true, EPI>(a, b, static_cast<char*>(C) + co, M, N, K, tm, tn, u);
+    else gemm_f32_tile_128<DTO, BT, false, EPI>(a, b, static_cast<char*>(C) + co, M, N, K, tm, tn, u);
+    __syncthreads();  // the LDS buffers are refilled by the next tile
   }
 }
 

@@ -19,6 +19,7 @@
 #include "kernels/prefill_asm.hpp"
 #include "kernels/common.hpp"
 #include "kernels/gemm.hpp"
+#include "kernels/gemm_f32.hpp"
 #include "kernels/norm.hpp"
 #include "kernels/softmax.hpp"
 #include "runtime.hpp"
@@ -322,6 +323,24 @@ int gemm_launch(const GemmArgs& g, bool mfma) {
     }
   }
   (void)mfma;
+  if constexpr (DT == th::kF32) {
+    // the fp32 MFMA kernel; 16-byte loads when every row start is 16-byte aligned
+    const bool vec = aligned16(g.a) && aligned16(g.b) && g.k % 4 == 0 && (g.bt || g.n % 4 == 0) &&
+                     g.sa % 4 == 0 && g.sb % 4 == 0;
+    const dim3 grid(((g.m + th::gf32::BM - 1) / th::gf32::BM) * ((g.n + th::gf32::BN - 1) / th::gf32::BN),
+                    g.batch),
+        block(th::gf32::NT);
+    auto A = static_cast<const float*>(g.a);
+    auto B = static_cast<const float*>(g.b);
+    if (g.bt) {
+      if (vec) hipLaunchKernelGGL((th::gemm_f32_mfma<DTO, true, true, EPI>), grid, block, 0, g.s, A, B, g.c, g.m, g.n, g.k, g.sa, g.sb, g.sc, g.up);
+      else hipLaunchKernelGGL((th::gemm_f32_mfma<DTO, true, false, EPI>), grid, block, 0, g.s, A, B, g.c, g.m, g.n, g.k, g.sa, g.sb, g.sc, g.up);
+    } else {
+      if (vec) hipLaunchKernelGGL((th::gemm_f32_mfma<DTO, false, true, EPI>), grid, block, 0, g.s, A, B, g.c, g.m, g.n, g.k, g.sa, g.sb, g.sc, g.up);
+      else hipLaunchKernelGGL((th::gemm_f32_mfma<DTO, false, false, EPI>), grid, block, 0, g.s, A, B, g.c, g.m, g.n, g.k, g.sa, g.sb, g.sc, g.up);
+    }
+    return launch_status("matmul (fp32 MFMA) launch");
+  }
   const dim3 grid(((g.m + 63) / 64) * ((g.n + 63) / 64), g.batch), block(256);
   if (g.bt)
     hipLaunchKernelGGL((th::gemm_fma_64<DT, DTO, true, EPI>), grid, block, 0, g.s, g.a, g.b, g.c,

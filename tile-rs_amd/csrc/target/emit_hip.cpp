@@ -824,7 +824,8 @@ bool matmul_entry(const Kernel& k, const TileVal& mm, const Store& st, const cha
   os << "matmul " << M << "x" << K << "x" << N << (bt ? " (B transposed)" : "") << " " << dt_name(in)
      << " -> " << dt_name(out) << (up ? " with silu*mul epilogue" : "")
      << (dma ? " -> th::entry::gemm_dma (MFMA, LDS-DMA)"
-             : mfma ? " -> th::entry::gemm (MFMA)" : " -> th::entry::gemm_fma")
+             : mfma ? " -> th::entry::gemm (MFMA)"
+             : in == F32 ? " -> th::entry::gemm_f32 (fp32 MFMA)" : " -> th::entry::gemm_fma")
      << "\n";
   const unsigned threads = dma ? 512 : 256;
   signature(os, k, threads, {});
@@ -846,6 +847,16 @@ bool matmul_entry(const Kernel& k, const TileVal& mm, const Store& st, const cha
        << view_ptr(b, "uint16_t") << ", " << store_ptr(st, dt_ctype(out)) << ", " << u(M) << ", "
        << u(N) << ", " << u(K) << tail;
     desc(os, k, 256, static_cast<unsigned>(((M + 255) / 256) * ((N + 255) / 256)), 1);
+  } else if (in == F32) {
+    // 16-byte pieces when every row start is 16-byte aligned (the base's alignment
+    // is checked at run time by the entry)
+    const bool vec = K % 4 == 0 && (bt || N % 4 == 0) && a.src.offset % 4 == 0 &&
+                     b.src.offset % 4 == 0;
+    os << "  th::entry::gemm_f32<" << dt_enum(out) << ", " << (bt ? "true" : "false") << ", "
+       << (vec ? "true" : "false") << ", " << epi << ">(" << view_ptr(a, "float") << ", "
+       << view_ptr(b, "float") << ", " << store_ptr(st, dt_ctype(out)) << ", " << u(M) << ", "
+       << u(N) << ", " << u(K) << tail;
+    desc(os, k, 256, static_cast<unsigned>(((M + 127) / 128) * ((N + 127) / 128)), 1);
   } else {
     os << "  th::entry::gemm_fma<" << tmpl << ">(" << view_ptr(a, dt_ctype(in)) << ", "
        << view_ptr(b, dt_ctype(in)) << ", " << store_ptr(st, dt_ctype(out)) << ", " << u(M)
