@@ -365,6 +365,50 @@ class Attn(Workload):
         return flops / el / 1e12, f"{bh} x 64 query rows (last rows of a head), oracle f32"
 
 
+class AttnF32(Workload):
+    """__tile_attention_f32 on the fp32 MFMA: 32 single-head S=4096 D=128 problems."""
+    name, index, bound, dtype, unit = "attn_f32", 8, "mfma", "f32", "TFLOP/s"
+    peak = PEAK_MFMA_F32_TFLOPS
+    tiles, S, Dh = 32, 4096, 128
+
+    def work(self):
+        return 4.0 * self.tiles * self.S * self.S * self.Dh
+
+    def config(self):
+        return {"workload": "single-head attention f32 (non-causal), 32 problems S=4096 D=128",
+                "tiles": self.tiles, "seq_len": self.S, "head_dim": self.Dh}
+
+    def setup(self, th, dev, s):
+        D = th.TileDtype
+        n = self.tiles * self.S * self.Dh
+        self.bufs = []
+        for j in range(3):
+            b = dev.alloc(n, D.F32)
+            th.fill_random(b, n, D.F32, "normal", 0.0, 1.0, SEED0 + 8 + 100 * j, s)
+            self.bufs.append(b)
+        self.o = dev.alloc(n, D.F32)
+
+    def step(self, th, s, i):
+        q, k, v = self.bufs
+        th.attention(q, k, v, self.o, self.S, self.Dh, self.tiles, th.TileDtype.F32, s)
+
+    def cpu_sample(self, th, s, seconds):
+        from oracle import oracle as orc
+        q, k, v = (b.copy_to_host(s) for b in self.bufs)
+        n = self.S * self.Dh
+        t0, done = time.perf_counter(), 0
+        while True:
+            t = done % self.tiles
+            sl = slice(t * n, (t + 1) * n)
+            orc.attention_f32(q[sl], k[sl], v[sl], self.S, self.Dh)
+            done += 1
+            el = time.perf_counter() - t0
+            if el >= seconds:
+                break
+        return (done * 4.0 * self.S * self.S * self.Dh / el / 1e12,
+                f"{done} whole problem(s) (S=4096 D=128), oracle f32")
+
+
 class Decode(Workload):
     name, index, bound, dtype, unit = "decode", 5, "hbm", "bf16", "GB/s"
     B, NH, NKV, L, Dh = 64, 32, 8, 8192, 128
@@ -440,7 +484,8 @@ class Copy(Workload):
         return 0.0, "none"
 
 
-WORKLOADS = {w.name: w for w in (Softmax, Gemm, Mlp, Attn, Decode, Swiglu, RmsNorm, GemmF32, Copy)}
+WORKLOADS = {w.name: w for w in (Softmax, Gemm, Mlp, Attn, Decode, Swiglu, RmsNorm, GemmF32,
+                                  AttnF32, Copy)}
 BENCH_LINES = ("attn", "decode", "gemm", "mlp", "softmax")
 
 

@@ -395,6 +395,37 @@ def test_attention_f32_golden(dev, stream, golden):
     assert np.abs(got - orc.attention_f32(g["q"], g["k"], g["v"], s, d)).max() < 1e-5
 
 
+@pytest.mark.parametrize("s,d,tiles,offset", [
+    (200, 128, 3, 0),     # ragged last query and position blocks, three problems
+    (1000, 64, 1, 0),     # many position blocks
+    (1, 64, 2, 0),        # one position
+    (33, 128, 2, 0),      # one full and one single-position block
+    (130, 96, 2, 0),      # head_dim 96: the one-workgroup-per-query kernel
+    (70, 64, 1, 1),       # views 4 bytes off 16-byte alignment: the same
+])
+def test_attention_f32_shapes(dev, stream, s, d, tiles, offset):
+    """f32 single-head attention against the oracle on every element: the fp32 MFMA
+    flash kernel (head_dim 64/128, 16-byte aligned views) sums in another order than
+    the oracle's sequential loops and uses exp2, so the bound is 1e-5 absolute on
+    outputs of size ~1 (the values are weighted means of V ~ N(0, 1))."""
+    rng = np.random.default_rng(s * 7 + d + tiles + offset)
+    q, k, v = (rng.standard_normal(tiles * s * d).astype(np.float32) for _ in range(3))
+    bufs = []
+    for x in (q, k, v):
+        b = dev.alloc(x.size + offset, D.F32)
+        b.copy_from_host(np.concatenate([np.zeros(offset, np.float32), x]), stream)
+        bufs.append(b)
+    ob = dev.alloc(tiles * s * d + offset, D.F32)
+    ptrs = [b.as_raw_ptr() + 4 * offset for b in bufs + [ob]]
+    th.attention(*ptrs, s, d, tiles, D.F32, stream)
+    got = ob.copy_to_host(stream)[offset:].reshape(tiles, s, d)
+    for t in range(tiles):
+        sl = slice(t * s * d, (t + 1) * s * d)
+        ref = orc.attention_f32(q[sl], k[sl], v[sl], s, d).reshape(s, d)
+        err = np.abs(got[t] - ref).max()
+        assert err < 1e-5, f"tile {t}: max err {err:.3e}"
+
+
 # ---- prefill ------------------------------------------------------------------------------
 
 def run_prefill(dev, stream, q, k, v, dtype, B, S, start, max_seq, Dh, NH, NKV):

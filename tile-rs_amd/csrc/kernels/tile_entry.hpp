@@ -12,6 +12,7 @@
 
 #include "../launch_desc.hpp"
 #include "attention.hpp"
+#include "attention_f32.hpp"
 #include "common.hpp"
 #include "gemm.hpp"
 #include "gemm_f32.hpp"
@@ -185,10 +186,28 @@ __device__ __forceinline__ void gemm_fma(const void* A, const void* B, void* C, 
 }
 
 // ---- single-head non-causal attention on S x D tiles (__tile_attention_f32) ----
+// f32 tiles with head_dim 64 or 128 and 16-byte aligned views run the fp32 MFMA
+// flash kernel (one item per 128 queries); others one workgroup per query.
 template <int DT, int NT>
 __device__ __forceinline__ void attention_tiles(const void* q, const void* k, const void* v,
                                                 void* o, uint32_t s, uint32_t d, uint32_t tiles) {
   const float scale = static_cast<float>(1.0 / __builtin_sqrt(static_cast<double>(d)));
+  if constexpr (DT == kF32) {
+    const uintptr_t align = reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) |
+                            reinterpret_cast<uintptr_t>(v);
+    if ((d == 64 || d == 128) && (align & 15) == 0 && s > 0) {
+      const uint32_t nqb = (s + af32::BQ - 1) / af32::BQ;
+      auto Q = static_cast<const float*>(q);
+      auto K = static_cast<const float*>(k);
+      auto V = static_cast<const float*>(v);
+      auto O = static_cast<float*>(o);
+      for (uint32_t w = blockIdx.x; w < tiles * nqb; w += gridDim.x) {
+        if (d == 64) attn_f32_tile<64>(Q, K, V, O, s, scale * kLog2e, w / nqb, w % nqb);
+        else attn_f32_tile<128>(Q, K, V, O, s, scale * kLog2e, w / nqb, w % nqb);
+      }
+      return;
+    }
+  }
   for (uint32_t w = blockIdx.x; w < tiles * s; w += gridDim.x)
     attn_general_item<DT, NT>(q, k, v, o, s, 0, s, s, d, 1, 1, 0, scale, w);
 }

@@ -16,6 +16,7 @@
 #include <type_traits>
 
 #include "kernels/attention.hpp"
+#include "kernels/attention_f32.hpp"
 #include "kernels/prefill_asm.hpp"
 #include "kernels/common.hpp"
 #include "kernels/gemm.hpp"
@@ -523,6 +524,24 @@ int th_attention(const void* q, const void* k, const void* v, void* o, uint32_t 
   if (!q || !k || !v || !o) return fail(TH_KERNEL_ERROR, "attention: null pointer");
   // scale printed by the linalg bridge: 1.0f64 / sqrt(d), then used as f32
   const float scale = static_cast<float>(1.0 / std::sqrt(static_cast<double>(head_dim)));
+  if (dtype == TH_F32 && (head_dim == 64 || head_dim == 128) && aligned16(q) && aligned16(k) &&
+      aligned16(v)) {
+    // the fp32 MFMA flash kernel: one workgroup per (tile, 128 queries)
+    const uint64_t blocks = static_cast<uint64_t>(tiles) * ((seq_len + th::af32::BQ - 1) / th::af32::BQ);
+    if (blocks > 0x7fffffffu) return fail(TH_KERNEL_ERROR, "attention: too many tiles");
+    const dim3 grid(static_cast<uint32_t>(blocks)), block(th::af32::NT);
+    auto Q = static_cast<const float*>(q);
+    auto K = static_cast<const float*>(k);
+    auto V = static_cast<const float*>(v);
+    auto O = static_cast<float*>(o);
+    if (head_dim == 64)
+      hipLaunchKernelGGL(th::attn_f32_mfma<64>, grid, block, 0, as_stream(s), Q, K, V, O, seq_len,
+                         scale * th::kLog2e);
+    else
+      hipLaunchKernelGGL(th::attn_f32_mfma<128>, grid, block, 0, as_stream(s), Q, K, V, O,
+                         seq_len, scale * th::kLog2e);
+    return launch_status("attention (fp32 MFMA) launch");
+  }
   return attn_general_launch(q, k, v, o, tiles, seq_len, 0, seq_len, seq_len, head_dim, 1, 1, 0,
                              scale, dtype, as_stream(s));
 }

@@ -1217,7 +1217,10 @@ bool emit_kernel(const Kernel& k, std::ostringstream& os, std::string* err) {
     os << "  th::entry::attention_tiles<" << dt_enum(q.dtype) << ", 256>(" << in_ptr(0, dt_ctype(q.dtype))
        << ", " << in_ptr(1, dt_ctype(q.dtype)) << ", " << in_ptr(2, dt_ctype(q.dtype)) << ", "
        << out_ptr(dt_ctype(st->dtype)) << ", " << u(S) << ", " << u(D) << ", th_tiles);\n}\n";
-    desc(os, k, 256, static_cast<unsigned>(S), 1);
+    // f32 with head_dim 64/128: the MFMA flash kernel, one workgroup per 128 queries;
+    // otherwise one per query
+    const bool flash = q.dtype == F32 && (D == 64 || D == 128);
+    desc(os, k, 256, static_cast<unsigned>(flash ? (S + 127) / 128 : S), 1);
     return true;
   }
   if (o == "attention_prefill_f32") {
