@@ -1,6 +1,7 @@
 """Benchmark of the MI355X tile-op path on BASELINE.json's configs (1 GPU).
 
-  python bench.py [--config gemm|softmax|mlp|attn|decode|all] [--steps K] [--warmup W]
+  python bench.py [--config gemm|softmax|mlp|attn|decode|all|...] [--steps K] [--warmup W]
+                  [--path library|emitted]
 
 A step is one launch of the tile op over one batch of synthetic, seeded input
 already resident in HBM (generated on the device by th_fill_random with seed
@@ -12,9 +13,12 @@ than 256 MB so the Infinity Cache cannot serve them.
 Timing: a clock-settle phase (steps run until --settle-ms of wall time have
 passed: MI355X ramps its clock over the first ~100 ms of sustained MFMA work, and
 a cold 4096^3 GEMM step takes 140-160 us against ~123 us settled), then W untimed
-steps, then K steps bracketed by stream synchronization, each step between its
-own pair of HIP events on the stream the kernels run on; ms_per_step is the
-median step (the mean is reported beside it).
+steps, then K steps bracketed by stream synchronization, with HIP events on the
+stream the kernels run on between groups of consecutive steps (about 1 ms of work
+per group, at least ten groups; an event after every 10 us step would add its own
+gap); ms_per_step is the median over groups of the per-step time (the mean over
+all K steps is reported beside it).  --path emitted runs the same step through the
+kernel the hip codegen target emits for the config (tilers_hip/examples).
 roofline.achieved = algorithmic work per step / ms_per_step (the step is one
 kernel launch except decode, which is the split kernel plus a small combine).
 cpu_baseline times the CPU oracle (test infrastructure, never the measured
@@ -535,15 +539,23 @@ def run(name: str, steps: int, warmup: int, cpu_seconds: float, settle_ms: float
     for i in range(warmup):
         w.step(th, s, i)
     s.synchronize()
-    ev = [th.HipEvent() for _ in range(steps + 1)]
+    # Events go between groups of consecutive steps (about 1 ms of work each, at least
+    # ten groups): an event between every step of a ~10 us kernel adds a few us of gap.
+    est_ms = settle_wall / max(settle_steps, 1)
+    group = max(1, min(max(steps // 10, 1), int(round(1.0 / max(est_ms, 1e-3)))))
+    bounds = list(range(0, steps, group)) + [steps]
+    ev = [th.HipEvent() for _ in bounds]
     ev[0].record(s)
-    for i in range(steps):
-        w.step(th, s, warmup + i)
-        ev[i + 1].record(s)
+    for g in range(len(bounds) - 1):
+        for i in range(bounds[g], bounds[g + 1]):
+            w.step(th, s, warmup + i)
+        ev[g + 1].record(s)
     ev[-1].synchronize()
     s.synchronize()
-    per = sorted(ev[i].elapsed_ms(ev[i + 1]) for i in range(steps))
-    ms = per[steps // 2] if steps % 2 else 0.5 * (per[steps // 2 - 1] + per[steps // 2])
+    per = sorted(ev[g].elapsed_ms(ev[g + 1]) / (bounds[g + 1] - bounds[g])
+                 for g in range(len(bounds) - 1))
+    n = len(per)
+    ms = per[n // 2] if n % 2 else 0.5 * (per[n // 2 - 1] + per[n // 2])
     ms_mean = ev[0].elapsed_ms(ev[-1]) / steps
     work = w.work()
     if w.unit == "TFLOP/s":
@@ -568,7 +580,8 @@ def run(name: str, steps: int, warmup: int, cpu_seconds: float, settle_ms: float
         "warmup": warmup,
         "ms_per_step": round(ms, 6),
         "ms_per_step_mean": round(ms_mean, 6),
-        "timing": {"statistic": "median of per-step HIP events", "settle_steps": settle_steps,
+        "timing": {"statistic": "median over groups of consecutive steps (HIP events)",
+                   "steps_per_group": group, "groups": n, "settle_steps": settle_steps,
                    "settle_ms": round(settle_wall, 1)},
         "higher_is_better": True,
         "scaling": "weak",
