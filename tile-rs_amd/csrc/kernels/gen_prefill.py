@@ -20,13 +20,15 @@ Per wave and period j (S = scores of 64 kv x 32 queries, as S^T accumulators):
            exponentials, row sum, split decision), then phase A of block j+1
            (causal mask, row max, running max, first half of the exponentials)
            once S(j+1) is complete; both spread between the MFMAs.
-A block whose largest probability exceeds 1/ratio of the row's running sum also
-gets its 16-bit residual P - hi(P) multiplied in (rare; out of line).  Scores
+A 16-position PV step whose largest probability exceeds 1/ratio of the row's
+running sum also gets its 16-bit residual P - hi(P) multiplied in (out of line,
+only for those steps: 4 MFMAs per step instead of 16 per block).  Scores
 are double-buffered by block parity, so the loop is unrolled by two.  One
 s_barrier per period recycles the LDS stage of block j-1 for block j+NS-1.
 
 Register map (VGPRs only; the asm statement clobbers v16-v255, s48-s95):
-  v16 v17 v18 DMA offsets, v19 v20 temps
+  v16 v17 v18 DMA offsets, v19 v20 temps, v[24:27] v[28:31] per-step score maxima
+  (by block parity),
   v[32:63] S (even blocks), v[64:95] S (odd blocks), v[96:111] P,
   v[112:143] fragment ring (8 x 4), v[144:207] O^T (4 d-tiles x 16),
   v[208:239] Q^T fragments (8 x 4),
@@ -35,7 +37,8 @@ Register map (VGPRs only; the asm statement clobbers v16-v255, s48-s95):
 SGPRs: s[48:51] K bases (+0,+64), s[56:57] V base, s58 j, s59 nb-1, s60 stage of
   block j+1, s61 stage of block j, s62 DMA stage, s63 DMA kv0, s64 s68 temps,
   s65 stage end, s[66:67] saved exec, s[70:71] grow mask, s[74:75] DMA exec,
-  s[76:77] full exec, s[78:79] split mask, s[80:81] mask compare.
+  s[76:77] full exec, s[78:79] split mask (any step), s[80:81] mask compare,
+  s[84:91] split masks of the four PV steps.
 
 Usage: python gen_prefill.py <out.inc>   (run by the library build)
 """
@@ -64,6 +67,10 @@ O_BASE = 144
 Q_BASE = 208
 STB = 240
 X0, X1, NINF, KADDR = "v248", "v249", "v250", "v251"
+# Raw score maxima of the block's four 16-position PV steps (this lane's 8 scores of
+# each), by block parity: the residual split is decided, and run, per step.
+STEPMAX = [24, 28]
+SPLIT_MASK = ["s[84:85]", "s[86:87]", "s[88:89]", "s[90:91]"]
 VADDR = [252, 253, 254, 255]
 DK, DV = "v16", ["v17", "v18"]
 TA, TB = "v19", "v20"
@@ -140,25 +147,20 @@ class Gen:
                 kt, r = e // 16, e % 16
                 c = 32 * kt + 8 * (r >> 2) + (r & 3)
                 L.append([f"v_cmp_lt_i32 s[80:81], {st('lim')}, {c}", f"v_cndmask_b32 {S[e]}, {S[e]}, {NINF}, s[80:81]"])
-        ch = [m_blk, m_new, alpha]
+        # per-step maxima (PV step t holds this lane's scores 8t .. 8t+7), four chains
+        mx = [f"v{STEPMAX[par] + t}" for t in range(4)]
         seqs = []
-        for c in range(3):
-            g = list(range(c, 32, 3))
-            seq = [f"v_max3_f32 {ch[c]}, {S[g[0]]}, {S[g[1]]}, {S[g[2]]}"]
-            k = 3
-            while k < len(g):
-                if k + 1 < len(g):
-                    seq.append(f"v_max3_f32 {ch[c]}, {ch[c]}, {S[g[k]]}, {S[g[k + 1]]}")
-                    k += 2
-                else:
-                    seq.append(f"v_max_f32 {ch[c]}, {ch[c]}, {S[g[k]]}")
-                    k += 1
-            seqs.append(seq)
-        for i in range(max(len(q) for q in seqs)):
+        for t in range(4):
+            g = list(range(8 * t, 8 * t + 8))
+            seqs.append([f"v_max3_f32 {mx[t]}, {S[g[0]]}, {S[g[1]]}, {S[g[2]]}",
+                         f"v_max3_f32 {mx[t]}, {mx[t]}, {S[g[3]]}, {S[g[4]]}",
+                         f"v_max3_f32 {mx[t]}, {mx[t]}, {S[g[5]]}, {S[g[6]]}",
+                         f"v_max_f32 {mx[t]}, {mx[t]}, {S[g[7]]}"])
+        for i in range(4):
             for q in seqs:
-                if i < len(q):
-                    L.append([q[i]])
-        L.append([f"v_max3_f32 {X0}, {m_blk}, {m_new}, {alpha}"])
+                L.append([q[i]])
+        L.append([f"v_max3_f32 {X0}, {mx[0]}, {mx[1]}, {mx[2]}"])
+        L.append([f"v_max_f32 {X0}, {X0}, {mx[3]}"])
         L.append([f"v_mov_b32 {X1}, {X0}", "s_nop 1", f"v_permlane32_swap_b32 {X0}, {X1}", "s_nop 1"])
         L.append([f"v_max_f32 {X0}, {X0}, {X1}"])
         L.append([f"v_mul_f32 {m_blk}, {scale}, {X0}"])
@@ -213,13 +215,20 @@ class Gen:
                 add([f"{self.cvt} {P[q]}, {S[2 * q]}, {S[2 * q + 1]}"], pdl(q))
         add([f"v_add_f32 {X0}, {ls0}, {ls1}"])
         add([f"v_fma_f32 {l_run}, {l_run}, {alpha}, {X0}"])
-        add([f"v_sub_f32 {X0}, {m_blk}, {m_new}"])
-        add([f"v_exp_f32 {X0}, {X0}"])
         add([f"v_mov_b32 {X1}, {l_run}", f"v_mov_b32 {TA}, {l_run}", "s_nop 1",
              f"v_permlane32_swap_b32 {X1}, {TA}", "s_nop 1"])
         add([f"v_add_f32 {X1}, {X1}, {TA}"])
-        add([f"v_mul_f32 {X0}, {ratio}, {X0}"])
-        add([f"v_cmp_gt_f32 s[78:79], {X0}, {X1}"])
+        # Split step t when its largest probability exceeds 1/ratio of the row's sum:
+        # only those steps' residual MFMAs run (out of line, after the period).
+        mx = [f"v{STEPMAX[par] + t}" for t in range(4)]
+        for t in range(4):
+            add([f"v_fma_f32 {X0}, {mx[t]}, {scale}, -{m_new}"])
+            add([f"v_exp_f32 {X0}, {X0}"])
+            add([f"v_mul_f32 {X0}, {ratio}, {X0}"])
+            add([f"v_cmp_gt_f32 {SPLIT_MASK[t]}, {X0}, {X1}"])
+        add([f"s_or_b64 s[78:79], {SPLIT_MASK[0]}, {SPLIT_MASK[1]}",
+             f"s_or_b64 s[78:79], s[78:79], {SPLIT_MASK[2]}",
+             f"s_or_b64 s[78:79], s[78:79], {SPLIT_MASK[3]}"])
         return ops
 
     def split_tail(self, par):
@@ -230,35 +239,37 @@ class Gen:
         return ["s_cmp_lg_u64 s[78:79], 0", f"s_cbranch_scc1 {ls}", f"{lsb}:"]
 
     def residual(self, par):
+        """lo = P - hi(P) for the split steps only, and O^T += V^T . lo for them: per
+        step, its four V fragments are read while lo is computed."""
         S = [f"v{S_BASE[par] + e}" for e in range(32)]
         P = [f"v{P_BASE + q}" for q in range(16)]
+        # the period's last MFMAs may still read P: 16 wait states before overwriting it
         out = ["s_waitcnt lgkmcnt(0)", "s_nop 7", "s_nop 7"]
-        for q in range(16):
-            if self.dt == "bf16":
-                out += [f"v_lshlrev_b32 {TA}, 16, {P[q]}", f"v_and_b32 {TB}, 0xffff0000, {P[q]}"]
-            else:
-                out += [f"v_cvt_f32_f16 {TA}, {P[q]}", f"v_lshrrev_b32 {TB}, 16, {P[q]}",
-                        f"v_cvt_f32_f16 {TB}, {TB}"]
-            out += [f"v_sub_f32 {TA}, {S[2 * q]}, {TA}", f"v_sub_f32 {TB}, {S[2 * q + 1]}, {TB}",
-                    f"{self.cvt} {P[q]}, {TA}, {TB}"]
-
-        def rd(k):
-            stp, dtl = k // 4, k % 4
-            R = RING_BASE + 4 * (k % 4)
-            va = f"v{VADDR[dtl]}"
-            return [f"ds_read_b64_tr_b16 {vr(R, R + 1)}, {va} offset:{4096 * stp}",
-                    f"ds_read_b64_tr_b16 {vr(R + 2, R + 3)}, {va} offset:{4096 * stp + 2048}"]
-        out += ["s_nop 2"] + rd(0) + rd(1)
-        for k in range(16):
-            if k + 2 < 16:
-                out += rd(k + 2)
-            out.append(f"s_waitcnt lgkmcnt({2 * min(2, 15 - k)})")
-            stp, dtl = k // 4, k % 4
-            R = RING_BASE + 4 * (k % 4)
-            ob = O_BASE + 16 * dtl
-            pb = P_BASE + 4 * stp
-            out.append(f"{self.mn} {vr(ob, ob + 15)}, {vr(R, R + 3)}, {vr(pb, pb + 3)}, {vr(ob, ob + 15)}")
-            out.append("s_nop 4")
+        for t in range(4):
+            skip = self.label("rskip")
+            out += [f"s_cmp_lg_u64 {SPLIT_MASK[t]}, 0", f"s_cbranch_scc0 {skip}"]
+            for dtl in range(4):
+                R = RING_BASE + 4 * dtl
+                va = f"v{VADDR[dtl]}"
+                out += [f"ds_read_b64_tr_b16 {vr(R, R + 1)}, {va} offset:{4096 * t}",
+                        f"ds_read_b64_tr_b16 {vr(R + 2, R + 3)}, {va} offset:{4096 * t + 2048}"]
+            for q in range(4 * t, 4 * t + 4):
+                if self.dt == "bf16":
+                    out += [f"v_lshlrev_b32 {TA}, 16, {P[q]}", f"v_and_b32 {TB}, 0xffff0000, {P[q]}"]
+                else:
+                    out += [f"v_cvt_f32_f16 {TA}, {P[q]}", f"v_lshrrev_b32 {TB}, 16, {P[q]}",
+                            f"v_cvt_f32_f16 {TB}, {TB}"]
+                out += [f"v_sub_f32 {TA}, {S[2 * q]}, {TA}", f"v_sub_f32 {TB}, {S[2 * q + 1]}, {TB}",
+                        f"{self.cvt} {P[q]}, {TA}, {TB}"]
+            out.append("s_nop 2")
+            pb = P_BASE + 4 * t
+            for dtl in range(4):
+                R = RING_BASE + 4 * dtl
+                ob = O_BASE + 16 * dtl
+                out.append(f"s_waitcnt lgkmcnt({2 * (3 - dtl)})")
+                out.append(f"{self.mn} {vr(ob, ob + 15)}, {vr(R, R + 3)}, {vr(pb, pb + 3)}, {vr(ob, ob + 15)}")
+            # the ring slots are refilled by the next split step: its reads wait for these MFMAs
+            out += ["s_nop 7", "s_nop 7", f"{skip}:"]
         out += ["s_nop 7", "s_nop 7", "s_nop 3"]
         return out
 
