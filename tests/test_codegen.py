@@ -480,3 +480,11 @@ def test_loop_compiles_for_gfx950(tmp_path):
         co = tmp_path / f"{stem}.hsaco"
         th.compile_source(th.emit((EXAMPLES / f"{stem}.mlir").read_text()).source, co)
         assert co.stat().st_size > 1000
+
+
+def test_loop_around_a_matmul_is_a_batched_gemm():
+    src = th.emit((EXAMPLES / "gemm_loop.mlir").read_text()).source
+    assert "th::entry::gemm_dma<th::kBF16, th::kF32, false, th::gemm::kEpiStore, 5>" in src
+    assert "256u, 384u, 320u, th_tiles);" in src
+    # two 256x256 output tiles per GEMM, times the trip count in argument 3
+    assert "__th_desc_gemm_loop_bf16 = {th::kLaunchDescMagic, 512u, 2u, 1u, 0u, 4u, 1u, 65536u, 0u};" in src

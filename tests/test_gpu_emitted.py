@@ -28,7 +28,7 @@ def launcher(dev):
     for stem in ("softmax_rows", "softmax_generic", "matmul_bf16", "matmul_f16_t", "matmul_f32",
                  "attention_f32", "prefill_bf16", "decode_bf16", "swiglu_mask", "rms_norm_rows",
                  "swiglu_gate_bf16", "matmul_bf16_tiles", "rope", "rows_long", "ops_extra",
-                 "softmax_loop", "softmax_loop_generic"):
+                 "softmax_loop", "softmax_loop_generic", "gemm_loop"):
         lau.load(_build.example_path(stem), th.KernelMode.GENERAL)
     return lau
 
@@ -420,3 +420,21 @@ def test_softmax_loop_generic_form_depth_one(dev, stream, launcher):
     got = orc.widen(yb.copy_to_host(stream), orc.BF16)
     ref = orc.softmax(orc.widen(x, orc.BF16), rows, 512)
     assert_within_ulp16(got, ref.reshape(-1), orc.BF16)
+
+
+def test_gemm_loop_is_a_batched_gemm(dev, stream, launcher):
+    """A loop over n (A_i, B_i, C_i) views of 256x320x384 bf16 -> f32 GEMMs with
+    pipelined_for(5) (a 5-stage LDS ring): n batch entries of the DMA GEMM."""
+    n, M, K, N = 3, 256, 320, 384
+    rng = np.random.default_rng(74)
+    a = orc.narrow(rng.uniform(-1, 1, n * M * K).astype(np.float32), orc.BF16)
+    b = orc.narrow(rng.uniform(-1, 1, n * K * N).astype(np.float32), orc.BF16)
+    ab, bb = up(dev, stream, a, D.BF16), up(dev, stream, b, D.BF16)
+    cb = up(dev, stream, np.full(n * M * N + 64, 7.0, np.float32), D.F32)
+    launcher.launch("gemm_loop_bf16", th.LaunchGrid.blocks_only(1), [ptr(ab), ptr(bb), ptr(cb), C.c_uint32(n)],
+                    stream)
+    got = cb.copy_to_host(stream)
+    assert np.all(got[n * M * N:] == 7.0)
+    for i in range(n):
+        ref = orc.matmul(a[i * M * K:(i + 1) * M * K], b[i * K * N:(i + 1) * K * N], M, K, N, orc.BF16)
+        assert_gemm_close(got[i * M * N:(i + 1) * M * N].reshape(M, N), ref.reshape(M, N), f"loop GEMM {i}")
