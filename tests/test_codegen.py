@@ -409,13 +409,17 @@ def test_loop_example_lowers_to_a_tile_grid():
     src = th.emit((EXAMPLES / "softmax_loop.mlir").read_text()).source
     assert ("softmax_loop_f32(void* __restrict__ p0, void* __restrict__ p1, uint32_t s2, "
             "uint32_t th_tiles_in)") in src
-    assert "const uint32_t th_tiles = th_tiles_in ? static_cast<uint32_t>(s2) : 0u;" in src
+    assert "const uint32_t th_tiles = th_tiles_in ? s2 : 0u;" in src
     assert "th::entry::softmax_rows<th::kF32, 4>(" in src and "th_tiles * 1u, 1024u);" in src
     assert "__th_desc_softmax_loop_f32 = {th::kLaunchDescMagic, 256u, 1u, 1u, 0u, 3u, 16u, 65536u, 0u};" in src
-    # an i64 bound, `ult` with the body on the true edge, `1 + i`, a shl-scaled offset
+    # an i64 bound (0x40 | 4 in the descriptor), `ult` with the body on the true edge,
+    # `1 + i`, a shl-scaled offset
     assert "uint64_t s3, uint32_t th_tiles_in)" in src
-    assert "th_tiles_in ? static_cast<uint32_t>(s3) : 0u;" in src
-    assert "__th_desc_add_loop_f32 = {th::kLaunchDescMagic, 256u, 2u, 1u, 0u, 4u, 1u, 65536u, 0u};" in src
+    assert "th_tiles_in ? (s3 > 0xffffffffull ? 0xffffffffu : static_cast<uint32_t>(s3)) : 0u;" in src
+    assert "__th_desc_add_loop_f32 = {th::kLaunchDescMagic, 256u, 2u, 1u, 0u, 68u, 1u, 65536u, 0u};" in src
+    # a signed `i < n`: negative n is zero tiles, in the kernel and in the grid (0x80 | 3)
+    assert "th_tiles_in ? (static_cast<int32_t>(s2) <= 0 ? 0u : s2) : 0u;" in src
+    assert "__th_desc_softmax_loop_signed_f32 = {th::kLaunchDescMagic, 256u, 1u, 1u, 0u, 131u, 16u," in src
 
 
 def test_loop_generic_form_and_constant_trip():
@@ -463,6 +467,28 @@ def test_loop_shapes_outside_the_counted_tile_loop_are_rejected(mutate, message)
     with pytest.raises(th.HalError) as e:
         th.emit(loop_module(body, **kw))
     assert message in str(e.value)
+
+
+def test_signed_loop_bounds_run_no_iteration_when_negative():
+    """`icmp sge %i, %n` (the loop of a signed `i >= n` test): a negative n runs no
+    iteration, so the tile count is clamped at zero instead of wrapping to 2^32 - k."""
+    src = th.emit(loop_module(LOOP_BODY, pred="sge")).source
+    assert "th_tiles_in ? (static_cast<int32_t>(s2) <= 0 ? 0u : s2) : 0u;" in src
+    neg = th.emit(loop_module(LOOP_BODY, pred="sge", bound="%neg",
+                              extra="    %neg = llvm.mlir.constant(-5 : i32) : i32\n")).source
+    assert "const uint32_t th_tiles = th_tiles_in ? 0u : 0u;" in neg
+    # under an unsigned compare the same constant is 2^32 - 5 iterations: rejected
+    with pytest.raises(th.HalError) as e:
+        th.emit(loop_module(LOOP_BODY, pred="uge", bound="%neg",
+                            extra="    %neg = llvm.mlir.constant(-5 : i32) : i32\n"))
+    assert "negative trip count" in str(e.value)
+
+
+def test_loop_bound_must_be_an_integer_argument():
+    text = loop_module(LOOP_BODY).replace("%arg2: i32)", "%arg2: f32)")
+    with pytest.raises(th.HalError) as e:
+        th.emit(text)
+    assert "must be an i32 or i64 argument" in str(e.value)
 
 
 def test_loop_with_a_per_tile_offset_is_rejected():

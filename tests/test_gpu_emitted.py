@@ -394,6 +394,26 @@ def test_softmax_loop_runs_every_iteration(dev, stream, launcher):
     assert np.all(yb.copy_to_host(stream) == 7.0)
 
 
+def test_softmax_loop_signed_bound(dev, stream, launcher):
+    """`icmp slt %i, %n` with an i32 n: n = 300 walks 300 rows; a negative n runs no
+    iteration (the kernel clamps its tile count and the grid stays one workgroup)."""
+    n = 300
+    rng = np.random.default_rng(74)
+    x = (rng.standard_normal((n, 1024)) * 2).astype(np.float32)
+    xb = up(dev, stream, x, D.F32)
+    yb = up(dev, stream, np.full(x.size + 1024, 7.0, np.float32), D.F32)
+    launcher.launch("softmax_loop_signed_f32", th.LaunchGrid.blocks_only(1),
+                    [ptr(xb), ptr(yb), C.c_uint32(n)], stream)
+    got = yb.copy_to_host(stream)
+    assert_softmax_close(got[:x.size].reshape(n, 1024), orc.softmax(x, n, 1024))
+    assert np.all(got[x.size:] == 7.0), "the loop ran past n"
+    yb = up(dev, stream, np.full(x.size, 7.0, np.float32), D.F32)
+    args = [ptr(xb), ptr(yb), C.c_int32(-5)]
+    assert launcher.hardware_grid("softmax_loop_signed_f32", th.LaunchGrid.blocks_only(1), args)[0] == 1
+    launcher.launch("softmax_loop_signed_f32", th.LaunchGrid.blocks_only(1), args, stream)
+    assert np.all(yb.copy_to_host(stream) == 7.0)
+
+
 def test_add_loop_i64_bound(dev, stream, launcher):
     """i64 trip count, `i < n` loop test, offsets from `i << 9` (2 x 256 tiles): exact."""
     n = 77

@@ -71,10 +71,11 @@ __device__ __forceinline__ void gemm_f32_tile_128(const float* __restrict__ A,
 
   // staging: A piece i covers rows (t + 256 i) % 128, k (t + 256 i) / 128 * 4 ..+3,
   // so the 64 lanes of a wave write 64 consecutive m of one A^T row.
-  f32x4 ra[2], rb[2];
+  constexpr int NP = BM * BK / 4 / NT;   // 16-byte pieces per thread per operand
+  f32x4 ra[NP], rb[NP];
   auto load = [&](uint32_t k0) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < NP; ++i) {
       const int e = t + 256 * i;
       ra[i] = load4<VEC>(A, m0 + (e & 127), k0 + (e >> 7) * 4, M, K, K);
       if constexpr (B_TRANS) rb[i] = load4<VEC>(B, n0 + (e & 127), k0 + (e >> 7) * 4, N, K, K);
@@ -83,7 +84,7 @@ __device__ __forceinline__ void gemm_f32_tile_128(const float* __restrict__ A,
   };
   auto store = [&](int buf) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < NP; ++i) {
       const int e = t + 256 * i;
       const int r = e & 127, k4 = (e >> 7) * 4;
 #pragma unroll

@@ -16,6 +16,9 @@
 namespace th {
 
 constexpr uint32_t kLaunchDescMagic = 0x54484431u;  // "THD1"
+constexpr uint32_t kScaleIndex = 0x3fu;    // scale_args byte: argument index + 1
+constexpr uint32_t kScaleWide = 0x40u;     // ... the argument is 64-bit
+constexpr uint32_t kScaleSigned = 0x80u;   // ... the argument is signed
 
 struct LaunchDesc {
   uint32_t magic;         // kLaunchDescMagic
@@ -26,9 +29,11 @@ struct LaunchDesc {
   // Work that depends on run-time scalar arguments (a loop's trip count, the
   // heads and sequence length of attention): wg_per_tile is multiplied by
   // ceil(arg[a0] / d0) and by ceil(arg[a1] / d1), where a0/a1 index the
-  // kernel's uint32 arguments, then capped at wg_cap.  Zero fields disable a
-  // factor (descriptors without them launch as before).
-  uint32_t scale_args;    // (a0 + 1) | (a1 + 1) << 8; 0 = none
+  // kernel's integer arguments, then capped at wg_cap.  Zero fields disable a
+  // factor (descriptors without them launch as before).  Each byte is
+  // (a + 1) | kScaleWide | kScaleSigned: the argument is 64-bit, or a signed
+  // value whose negative values count as zero.
+  uint32_t scale_args;    // byte 0: a0, byte 1: a1; 0 = none
   uint32_t scale_div;     // d0 | d1 << 16 (0 reads as 1)
   uint32_t wg_cap;        // maximum workgroups per tile after scaling (0 = none)
   // Cap on the whole grid, in workgroups per compute unit (0 = none): kernels
@@ -45,11 +50,20 @@ inline uint64_t desc_grid(const LaunchDesc& d, uint64_t tiles, void* const* args
   const uint64_t tpw = d.tiles_per_wg ? d.tiles_per_wg : 1;
   uint64_t wpt = d.wg_per_tile ? d.wg_per_tile : 1;
   for (int f = 0; f < 2; ++f) {
-    const uint32_t a = (d.scale_args >> (8 * f)) & 0xffu;
+    const uint32_t b = (d.scale_args >> (8 * f)) & 0xffu;
+    const uint32_t a = b & kScaleIndex;
     if (a == 0 || a > nargs || !args || !args[a - 1]) continue;
     uint64_t div = (d.scale_div >> (16 * f)) & 0xffffu;
     if (div == 0) div = 1;
-    const uint64_t v = *static_cast<const uint32_t*>(args[a - 1]);
+    uint64_t v;
+    if (b & kScaleWide) {
+      const uint64_t w = *static_cast<const uint64_t*>(args[a - 1]);
+      v = (b & kScaleSigned) && static_cast<int64_t>(w) < 0 ? 0 : w;
+    } else {
+      const uint32_t w = *static_cast<const uint32_t*>(args[a - 1]);
+      v = (b & kScaleSigned) && static_cast<int32_t>(w) < 0 ? 0 : w;
+    }
+    if (v > 0xffffffffull) v = 0xffffffffull;   // kernels count tiles in 32 bits
     wpt *= (v + div - 1) / div;
   }
   if (d.wg_cap && wpt > d.wg_cap) wpt = d.wg_cap;

@@ -75,7 +75,8 @@ struct Affine {
 struct Loop {
   bool present = false;
   long long trip = 0;    // constant trip count, or
-  int trip_arg = -1;     // position of the uint32 kernel argument holding it
+  int trip_arg = -1;     // position of the scalar kernel argument holding it
+  bool is_signed = false;  // signed compare: a negative bound runs no iteration
 };
 
 struct TileVal {
@@ -303,6 +304,7 @@ class Lowerer {
                         : (pred == "ule" || pred == "sle" || pred == "eq");
     }
     if (!ok) return fail("control flow: the loop must run while iv < n: " + H->lines.back());
+    k->loop.is_signed = pred[0] == 's';
     // entry block (constants, the pipelined_for marker)
     for (size_t i = 0; i + 1 < entry.lines.size(); ++i)
       if (!line_(k, entry.lines[i])) return false;
@@ -314,13 +316,19 @@ class Lowerer {
     }
     double nv = 0;
     if (resolve(k, n_tok, &nv)) {
-      if (nv < 0) return fail("control flow: negative trip count");
-      k->loop.trip = static_cast<long long>(nv);
+      if (nv < 0 && !k->loop.is_signed) return fail("control flow: negative trip count");
+      k->loop.trip = nv < 0 ? 0 : static_cast<long long>(nv);
+      if (k->loop.trip > 0xffffffffll) return fail("control flow: trip count beyond 2^32 - 1");
     } else {
       for (size_t i = 0; i < f_.args.size(); ++i)
         if (f_.args[i].name == n_tok && !f_.args[i].is_gm) k->loop.trip_arg = static_cast<int>(i);
       if (k->loop.trip_arg < 0)
         return fail("control flow: the loop bound must be a constant or a scalar kernel argument");
+      const std::string& ty = f_.args[k->loop.trip_arg].ty;
+      if (ty.find("i32") == std::string::npos && ty.find("i64") == std::string::npos)
+        return fail("control flow: the loop bound must be an i32 or i64 argument, not " + ty);
+      if (k->loop.trip_arg + 1 > static_cast<int>(th::kScaleIndex))
+        return fail("control flow: the loop bound must be one of the first 63 arguments");
     }
     if (!k->tiles.empty() || !k->stores.empty())
       return fail("control flow: tile operations outside the loop body are not lowered");
@@ -719,7 +727,10 @@ void desc(std::ostringstream& os, const Kernel& k, unsigned threads, unsigned wg
     tiles_per_wg = 1;
     if (k.loop.trip_arg >= 0) {
       const unsigned slot = (scale_args & 0xffu) ? 8u : 0u;
-      scale_args |= static_cast<unsigned>(k.loop.trip_arg + 1) << slot;
+      unsigned b = static_cast<unsigned>(k.loop.trip_arg + 1);
+      if (k.args[k.loop.trip_arg].ty.find("i64") != std::string::npos) b |= th::kScaleWide;
+      if (k.loop.is_signed) b |= th::kScaleSigned;
+      scale_args |= b << slot;
       scale_div |= static_cast<unsigned>(tpw) << (2 * slot);
       wg_cap = wg_cap ? wg_cap : static_cast<unsigned>(kCap);
     } else {
@@ -771,10 +782,25 @@ void signature(std::ostringstream& os, const Kernel& k, unsigned threads,
   os << "uint32_t th_tiles_in) {\n";
   os << "  // counted tile loop: iteration i is tile i.  Every launched tile walks the\n"
         "  // same iterations, so any number of launched tiles computes them once.\n";
-  os << "  const uint32_t th_tiles = th_tiles_in ? "
-     << (k.loop.trip_arg >= 0 ? "static_cast<uint32_t>(s" + std::to_string(k.loop.trip_arg) + ")"
-                              : std::to_string(k.loop.trip) + "u")
-     << " : 0u;\n";
+  std::string n;
+  if (k.loop.trip_arg < 0) {
+    n = std::to_string(k.loop.trip) + "u";
+  } else {
+    // the bound as the loop compares it: a negative signed bound runs no iteration;
+    // a 64-bit one is capped at 2^32 - 1 tiles
+    const std::string a = "s" + std::to_string(k.loop.trip_arg);
+    const bool wide = k.args[k.loop.trip_arg].ty.find("i64") != std::string::npos;
+    const std::string cap = "(" + a + " > 0xffffffffull ? 0xffffffffu : static_cast<uint32_t>(" + a + "))";
+    if (wide && k.loop.is_signed)
+      n = "(static_cast<int64_t>(" + a + ") <= 0 ? 0u : " + cap + ")";
+    else if (wide)
+      n = cap;
+    else if (k.loop.is_signed)
+      n = "(static_cast<int32_t>(" + a + ") <= 0 ? 0u : " + a + ")";
+    else
+      n = a;
+  }
+  os << "  const uint32_t th_tiles = th_tiles_in ? " << n << " : 0u;\n";
   for (size_t i = 0; i < k.args.size(); ++i)
     if (!k.args[i].is_gm && static_cast<int>(i) != k.loop.trip_arg) os << "  (void)s" << i << ";\n";
 }

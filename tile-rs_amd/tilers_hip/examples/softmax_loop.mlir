@@ -50,4 +50,27 @@ module {
   ^bb3:
     llvm.return
   }
+  llvm.func @softmax_loop_signed_f32(%arg0: !llvm.ptr<1>, %arg1: !llvm.ptr<1>, %arg2: i32) attributes {hacc.entry} {
+    ^bb0:
+    %zero = llvm.mlir.constant(0 : i32) : i32
+    %one = llvm.mlir.constant(1 : i32) : i32
+    %cols = llvm.mlir.constant(1024 : i32) : i32
+    %cols64 = llvm.mlir.constant(1024 : i64) : i64
+    llvm.br ^bb1(%zero : i32)
+  ^bb1(%i: i32):
+    %more = llvm.icmp "slt" %i, %arg2 : i32
+    llvm.cond_br %more, ^bb2, ^bb3
+  ^bb2:
+    %iw = llvm.zext %i : i32 to i64
+    %off = llvm.mul %iw, %cols64 : i64
+    %src = llvm.getelementptr %arg0[%off] : (!llvm.ptr<1>, i64) -> !llvm.ptr<1>, f32
+    %dst = llvm.getelementptr %arg1[%off] : (!llvm.ptr<1>, i64) -> !llvm.ptr<1>, f32
+    %t = llvm.call @__tile_load_f32(%src, %one, %cols) : (!llvm.ptr<1>, i32, i32) -> i32
+    %y = llvm.call @__tile_softmax_f32(%t, %t, %one, %cols) : (i32, i32, i32, i32) -> i32
+    llvm.call @__tile_store_f32(%dst, %y, %one, %cols) : (!llvm.ptr<1>, i32, i32, i32) -> ()
+    %next = llvm.add %i, %one : i32
+    llvm.br ^bb1(%next : i32)
+  ^bb3:
+    llvm.return
+  }
 }
