@@ -1,0 +1,173 @@
+"""Control flow of the generated prefill main loop, checked on the CPU.
+
+kernels/gen_prefill.py emits the loop as one asm statement.  Every wave of a
+workgroup must pass the same number of s_barrier instructions, and before each
+barrier a wave must have waited for its own DMA share of the K/V block the next
+period reads.  Waves leave the compute loop at different blocks (the causal
+diagonal), so this walks the scalar instructions of the program for every wave of
+a range of (seq_len, start_pos, query block) shapes and checks both properties.
+Vector instructions are skipped; vector compares that write scalar masks (the
+rescale and residual-split decisions) take random values.
+"""
+import random
+import re
+import sys
+from pathlib import Path
+
+import pytest
+
+sys.path.insert(0, str(Path(__file__).resolve().parents[1] / "tile-rs_amd" / "csrc" / "kernels"))
+import gen_prefill as G  # noqa: E402
+
+BQ, BKV = 256, 64
+
+
+def operands(seq_len, start_pos, qb, wave):
+    """The scalar operands prefill_asm.hpp hands to the asm statement (kernels/prefill_asm.hpp)."""
+    q0 = qb * BQ
+    q_hi = min(q0 + BQ, seq_len)
+    nb = (start_pos + q_hi + BKV - 1) // BKV
+    return {"nb": nb, "jd": (start_pos + q0 + 32 * wave + 1) // BKV,
+            "jl": (start_pos + q0 + 32 * wave + 31) // BKV, "lds": 0, "wave2k": 2048 * wave,
+            "kbase": 1 << 32, "vbase": 1 << 33, "kvlast": start_pos + seq_len - 1, "ok": (1 << 64) - 1}
+
+
+def sreg(tok):
+    if tok == "m0":
+        return tok, False
+    m = re.fullmatch(r"s\[(\d+):(\d+)\]", tok)
+    if m:
+        return f"s{m.group(1)}", True
+    m = re.fullmatch(r"s(\d+)", tok)
+    return (tok, False) if m else (None, False)
+
+
+class Wave:
+    def __init__(self, prog, ops, rng):
+        self.prog = [l.strip() for l in prog]
+        self.labels = {l[:-1]: i for i, l in enumerate(self.prog) if l.endswith(":")}
+        self.ops = {G.OP[k]: v for k, v in ops.items() if k in G.OP}
+        self.s = {}
+        self.exec = (1 << 64) - 1
+        self.scc = 0
+        self.rng = rng
+        self.vmem = []            # kv0 of each vector memory op in issue order (None: not a DMA)
+        self.barriers = []        # (s58, completed DMA kv0 set) at each barrier
+        self.done_upto = 0        # vmem ops known complete (prefix length)
+        self.mfmas = 0
+
+    def val(self, tok):
+        tok = tok.strip()
+        if tok == "exec":
+            return self.exec
+        if tok.startswith("%"):
+            return self.ops[int(tok[1:])]
+        r, _ = sreg(tok)
+        if r is not None:
+            return self.s.get(r, 0)
+        return int(tok, 0)
+
+    def put(self, tok, v):
+        if tok == "exec":
+            self.exec = v
+        else:
+            r, _ = sreg(tok)
+            assert r is not None, tok
+            self.s[r] = v
+
+    def run(self, limit=2_000_000):
+        pc, steps = 0, 0
+        while pc < len(self.prog):
+            steps += 1
+            assert steps < limit, "no exit"
+            line = self.prog[pc]
+            pc += 1
+            if not line or line.endswith(":"):
+                continue
+            op, _, rest = line.partition(" ")
+            a = [x.strip() for x in rest.split(",")] if rest else []
+            if op.startswith("global_load") or op.startswith("global_store"):
+                real_dma = op == "global_load_lds_dwordx4" and self.exec != 0
+                self.vmem.append(self.s.get("s63", 0) if real_dma else None)
+            elif op.startswith("v_mfma"):
+                self.mfmas += 1
+            elif op.startswith("v_cmp") and a and a[0].startswith("s["):
+                self.put(a[0], self.rng.choice([0, 1, 1 << 40]))
+            elif op.startswith("v_") or op.startswith("ds_") or op in ("s_nop",):
+                pass
+            elif op == "s_waitcnt":
+                m = re.search(r"vmcnt\((\d+)\)", rest)
+                if m:
+                    self.done_upto = max(self.done_upto, len(self.vmem) - int(m.group(1)))
+            elif op == "s_barrier":
+                done = {kv for kv in self.vmem[:self.done_upto] if kv is not None}
+                self.barriers.append((self.s.get("s58", -1), done))
+            elif op in ("s_mov_b32", "s_mov_b64"):
+                self.put(a[0], self.val(a[1]))
+            elif op in ("s_add_u32", "s_addc_u32"):
+                self.put(a[0], (self.val(a[1]) + self.val(a[2])) & 0xffffffff)
+            elif op == "s_sub_u32":
+                self.put(a[0], (self.val(a[1]) - self.val(a[2])) & 0xffffffff)
+            elif op == "s_min_u32":
+                self.put(a[0], min(self.val(a[1]), self.val(a[2])))
+            elif op == "s_max_i32":
+                sv = lambda x: x - (1 << 32) if x & (1 << 31) else x
+                self.put(a[0], max(sv(self.val(a[1])), sv(self.val(a[2]))) & 0xffffffff)
+            elif op == "s_or_b64":
+                self.put(a[0], self.val(a[1]) | self.val(a[2]))
+            elif op == "s_cselect_b32":
+                self.put(a[0], self.val(a[1]) if self.scc else self.val(a[2]))
+            elif op.startswith("s_cmp_"):
+                x, y = self.val(a[0]), self.val(a[1])
+                self.scc = int({"ge": x >= y, "gt": x > y, "lt": x < y, "eq": x == y,
+                                "lg": x != y}[op.split("_")[2]])
+            elif op in ("s_cbranch_scc0", "s_cbranch_scc1", "s_branch"):
+                if op == "s_branch" or self.scc == int(op[-1]):
+                    pc = self.labels[a[0]]
+            else:
+                raise AssertionError("unmodelled scalar instruction: " + line)
+        return self
+
+
+PROG = G.Gen("bf16").program()
+
+SHAPES = [(1, 0), (40, 0), (64, 0), (65, 0), (200, 0), (256, 0), (300, 0), (700, 0),
+          (1000, 0), (130, 5), (256, 64), (100, 1000), (513, 77)]
+
+
+@pytest.mark.parametrize("seq_len,start_pos", SHAPES)
+def test_every_wave_passes_the_same_barriers(seq_len, start_pos):
+    rng = random.Random(seq_len * 131 + start_pos)
+    for qb in range((seq_len + BQ - 1) // BQ):
+        counts = set()
+        for wave in range(8):
+            ops = operands(seq_len, start_pos, qb, wave)
+            w = Wave(PROG, ops, rng).run()
+            nb = ops["nb"]
+            counts.add(len(w.barriers))
+            # one barrier after the prologue, then one per period j = 0 .. nb-2
+            assert len(w.barriers) == nb, (seq_len, start_pos, qb, wave, len(w.barriers), nb)
+            # before the barrier of period j this wave's DMA of block j+1 has landed
+            # (the prologue's barrier covers block 0)
+            for i, (j, done) in enumerate(w.barriers):
+                need = 0 if i == 0 else BKV * (j + 1)
+                issued = {kv for kv in w.vmem if kv is not None}
+                if need in issued:
+                    assert need in done, (seq_len, start_pos, qb, wave, i, j)
+            # every DMA of the ring was issued (blocks 0 .. nb-1, one real batch each)
+            assert {kv for kv in w.vmem if kv is not None} >= set(range(0, BKV * nb, BKV))
+        assert len(counts) == 1
+
+
+def test_waves_past_the_diagonal_drain():
+    """A wave whose rows end before the workgroup's last block skips the compute of the
+    fully masked periods (wave 0 of a 256-row block: 3 of its 4 diagonal periods)."""
+    ops = operands(256, 0, 0, 0)
+    assert ops["jl"] == 0 and ops["nb"] == 4
+    w0 = Wave(PROG, ops, random.Random(1)).run()
+    w7 = Wave(PROG, operands(256, 0, 0, 7), random.Random(1)).run()
+    assert len(w0.barriers) == len(w7.barriers) == 4
+    # wave 0: S(0), one period (16 + 32) and at most 4 x 4 residual MFMAs of its
+    # split steps; wave 7: S(0), three periods and the last PV block
+    assert w0.mfmas <= 16 + 32 + 16
+    assert w7.mfmas >= 16 + 3 * 32 + 16

@@ -25,6 +25,12 @@ running sum also gets its 16-bit residual P - hi(P) multiplied in (out of line,
 only for those steps: 4 MFMAs per step instead of 16 per block).  Scores
 are double-buffered by block parity, so the loop is unrolled by two.  One
 s_barrier per period recycles the LDS stage of block j-1 for block j+NS-1.
+A wave whose rows end before the workgroup's last block (the causal diagonal:
+wave 0 of a 256-row block needs one of the last four blocks) leaves the compute
+loop after its last unmasked block jl and drains: each remaining period only
+waits for its DMA share, passes the barrier and issues the next DMA, so every
+wave passes the same barriers (tests/test_prefill_flow.py walks the scalar
+control flow of this program for every wave and checks it).
 
 Register map (VGPRs only; the asm statement clobbers v16-v255, s48-s95):
   v16 v17 v18 DMA offsets, v19 v20 temps, v[24:27] v[28:31] per-step score maxima
@@ -34,7 +40,8 @@ Register map (VGPRs only; the asm statement clobbers v16-v255, s48-s95):
   v[208:239] Q^T fragments (8 x 4),
   v240-247 m l lim mblk mnew alpha ls0 ls1, v248 v249 temps, v250 -inf,
   v251 K address, v252-255 V^T addresses.
-SGPRs: s[48:51] K bases (+0,+64), s[56:57] V base, s58 j, s59 nb-1, s60 stage of
+SGPRs: s[48:51] K bases (+0,+64), s[56:57] V base, s58 j, s59 nb-1 (jl and jd are
+  operands), s60 stage of
   block j+1, s61 stage of block j, s62 DMA stage, s63 DMA kv0, s64 s68 temps,
   s65 stage end, s[66:67] saved exec, s[70:71] grow mask, s[74:75] DMA exec,
   s[76:77] full exec, s[78:79] split mask (any step), s[80:81] mask compare,
@@ -53,7 +60,7 @@ NLD = 4         # DMA instructions per lane per KV block
 # operand numbers of the asm statement (see prefill_asm.hpp)
 OP = dict(qp=0, op=1, lim=2, klane=3, vlane=4, krow=5, kcol=6, vrow=7, vcol=8,
           kbase=9, vbase=10, kvlast=11, nb=12, jd=13, lds=14, wave2k=15,
-          scale=16, ratio=17, ok=18)
+          scale=16, ratio=17, ok=18, jl=19)
 
 
 def o(name):
@@ -410,6 +417,19 @@ class Gen:
                                      f"v_subrev_u32 {st('lim')}, 64, {st('lim')}"]
         return out
 
+    def drain(self, label, epi):
+        """Periods after the wave's last unmasked block: the same vmcnt wait, barrier
+        and DMA issue as a loop period (so every wave passes the same barriers and
+        fills its share of the ring), no MFMA, softmax or LDS reads; the final PV
+        block is skipped as well."""
+        done = self.label("dlast")
+        top = self.loop_top(done)
+        out = [f"{label}:"] + top
+        for g in self.dma_lines(True):
+            out += g
+        out += ["s_add_u32 s58, s58, 1", f"s_branch {label}", f"{done}:", f"s_branch {epi}"]
+        return out
+
     def program(self):
         out = [f"v_mov_b32 {NINF}, 0xff800000"]
         out += [f"v_mov_b32 v{O_BASE + k}, 0" for k in range(64)]
@@ -437,9 +457,13 @@ class Gen:
         top = [self.label("top0"), self.label("top1")]
         last = [self.label("last0"), self.label("last1")]
         epi = self.label("epi")
+        drain = self.label("drain")
         for par in (0, 1):
             msk, nxt = self.label("msk"), self.label("nxt")
-            out += [f"{top[par]}:"] + self.loop_top(last[par])
+            # past the wave's last block (jl) every score is masked: only the ring
+            # duties (DMA share, barrier) remain
+            out += [f"{top[par]}:", f"s_cmp_gt_u32 s58, {o('jl')}", f"s_cbranch_scc1 {drain}"]
+            out += self.loop_top(last[par])
             out += ["s_add_u32 s64, s58, 1", f"s_cmp_ge_u32 s64, {o('jd')}", f"s_cbranch_scc1 {msk}"]
             out += self.period(par, False)
             out += [f"s_branch {nxt}", f"{msk}:"]
@@ -449,6 +473,7 @@ class Gen:
         for par in (0, 1):
             out += [f"{last[par]}:"]
             out += self.last(par) + [f"s_branch {epi}"]
+        out += self.drain(drain, epi)
         out += [f"{epi}:", "s_waitcnt lgkmcnt(0)", "s_nop 7", "s_nop 7", "s_nop 7",
                 "s_mov_b64 s[66:67], exec"]
         out += [f"v_mov_b32 v32, {st('l')}", f"v_mov_b32 v33, {st('l')}", "s_nop 1",

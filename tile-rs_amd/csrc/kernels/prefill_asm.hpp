@@ -57,6 +57,8 @@ __device__ __forceinline__ void prefill_tile(const uint16_t* __restrict__ Q,
   const uint32_t q_hi_wg = min(q0 + BQ, seq_len);
   const uint32_t nb = (start_pos + q_hi_wg + BKV - 1) / BKV;
   const uint32_t jd = __builtin_amdgcn_readfirstlane((start_pos + q0 + 32 * wave + 1) / BKV);
+  // the wave's last kv block with an unmasked score (row q0 + 32 wave + 31)
+  const uint32_t jl = __builtin_amdgcn_readfirstlane((start_pos + q0 + 32 * wave + 31) / BKV);
 
   // LDS read offsets: K fragment rows (l32) and chunk g; V^T transposed reads
   const uint32_t klane = 16u * (256u * (l32 >> 4) + 16u * g + (l32 & 15));
@@ -81,7 +83,8 @@ __device__ __forceinline__ void prefill_tile(const uint16_t* __restrict__ Q,
                :                                                                           \
                : "v"(qp), "v"(op), "v"(lim), "v"(klane), "v"(vlane), "v"(krow), "v"(kcol), \
                  "v"(vrow), "v"(vcol), "s"(kbase), "s"(vbase), "s"(kvlast), "s"(nb),       \
-                 "s"(jd), "s"(lds_base), "s"(wave2k), "s"(scale_log2), "s"(ratio), "s"(ok) \
+                 "s"(jd), "s"(lds_base), "s"(wave2k), "s"(scale_log2), "s"(ratio), "s"(ok), \
+                 "s"(jl)                                                                   \
                : TH_PREFILL_ASM_CLOBBERS, "vcc", "scc", "m0", "memory")
   if constexpr (DT == kBF16) TH_PREFILL_OPS(TH_PREFILL_ASM_BF16); else TH_PREFILL_OPS(TH_PREFILL_ASM_F16);
 #undef TH_PREFILL_OPS
