@@ -167,7 +167,7 @@ def test_waves_past_the_diagonal_drain():
     w0 = Wave(PROG, ops, random.Random(1)).run()
     w7 = Wave(PROG, operands(256, 0, 0, 7), random.Random(1)).run()
     assert len(w0.barriers) == len(w7.barriers) == 4
-    # wave 0: S(0), one period (16 + 32) and at most 4 x 4 residual MFMAs of its
-    # split steps; wave 7: S(0), three periods and the last PV block
-    assert w0.mfmas <= 16 + 32 + 16
+    # wave 0: S(0), the PV of its only block (16 + 16) and at most 4 x 4 residual
+    # MFMAs of its split steps; wave 7: S(0), three periods and the last PV block
+    assert w0.mfmas <= 16 + 16 + 16
     assert w7.mfmas >= 16 + 3 * 32 + 16

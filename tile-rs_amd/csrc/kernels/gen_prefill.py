@@ -27,7 +27,8 @@ are double-buffered by block parity, so the loop is unrolled by two.  One
 s_barrier per period recycles the LDS stage of block j-1 for block j+NS-1.
 A wave whose rows end before the workgroup's last block (the causal diagonal:
 wave 0 of a 256-row block needs one of the last four blocks) leaves the compute
-loop after its last unmasked block jl and drains: each remaining period only
+loop after its last unmasked block jl (whose period runs PV(jl) without the
+all-masked S(jl+1)) and drains: each remaining period only
 waits for its DMA share, passes the barrier and issues the next DMA, so every
 wave passes the same barriers (tests/test_prefill_flow.py walks the scalar
 control flow of this program for every wave and checks it).
@@ -417,6 +418,17 @@ class Gen:
                                      f"v_subrev_u32 {st('lim')}, 64, {st('lim')}"]
         return out
 
+    def fin(self, par, last_label, drain):
+        """Period j = jl of a wave whose last unmasked block jl is not the workgroup's
+        last: PV(jl) with the period's DMA and barrier, without S(jl+1) (all masked);
+        then the drain."""
+        frags = self.pv_frags()
+        ops = [dict(lines=g, deadline=12, earliest=-1) for g in self.dma_lines(True)]
+        ops += self.phase_b(par, pv0=0)
+        body = self.schedule(frags, ops, pre_quota=10 ** 6)
+        return (self.loop_top(last_label) + self.addr_v("s61") + body + ["s_nop 7", "s_nop 7"] +
+                self.split_tail(par) + ["s_add_u32 s58, s58, 1", f"s_branch {drain}"])
+
     def drain(self, label, epi):
         """Periods after the wave's last unmasked block: the same vmcnt wait, barrier
         and DMA issue as a loop period (so every wave passes the same barriers and
@@ -458,11 +470,13 @@ class Gen:
         last = [self.label("last0"), self.label("last1")]
         epi = self.label("epi")
         drain = self.label("drain")
+        fin = [self.label("fin0"), self.label("fin1")]
         for par in (0, 1):
             msk, nxt = self.label("msk"), self.label("nxt")
             # past the wave's last block (jl) every score is masked: only the ring
             # duties (DMA share, barrier) remain
-            out += [f"{top[par]}:", f"s_cmp_gt_u32 s58, {o('jl')}", f"s_cbranch_scc1 {drain}"]
+            out += [f"{top[par]}:", f"s_cmp_gt_u32 s58, {o('jl')}", f"s_cbranch_scc1 {drain}",
+                    f"s_cmp_eq_u32 s58, {o('jl')}", f"s_cbranch_scc1 {fin[par]}"]
             out += self.loop_top(last[par])
             out += ["s_add_u32 s64, s58, 1", f"s_cmp_ge_u32 s64, {o('jd')}", f"s_cbranch_scc1 {msk}"]
             out += self.period(par, False)
@@ -473,6 +487,8 @@ class Gen:
         for par in (0, 1):
             out += [f"{last[par]}:"]
             out += self.last(par) + [f"s_branch {epi}"]
+        for par in (0, 1):
+            out += [f"{fin[par]}:"] + self.fin(par, last[par], drain)
         out += self.drain(drain, epi)
         out += [f"{epi}:", "s_waitcnt lgkmcnt(0)", "s_nop 7", "s_nop 7", "s_nop 7",
                 "s_mov_b64 s[66:67], exec"]
