@@ -318,10 +318,10 @@ def test_silu_mul_without_matmul_stays_elementwise():
 
 REF_MLIR = Path(__file__).resolve().parent / "golden" / "ref_mlir"
 # Model-level ops outside the tile-op hot path (sampling, speculative decoding,
-# gather/scatter, int8 quantization, KV-cache writes, rope variants, head-major GQA
-# attention): the hip target rejects them with an explicit error.
+# gather/scatter, int8 quantization, KV-cache writes, rope variants): the hip target
+# rejects them with an explicit error.
 REF_REJECTED = {
-    "cucumber__sample_top_p_mlir", "cucumber__token_accept_mlir", "gpu__attention_gqa_mlir_0",
+    "cucumber__sample_top_p_mlir", "cucumber__token_accept_mlir",
     "gpu__concat_mlir_0", "gpu__gather_mlir_0", "gpu__scatter_mlir_0", "gpu__slice_mlir_0",
     "gpu__test_gpu_draft_verify_0", "gpu__test_gpu_sample_top_p_0", "gpu__test_gpu_token_accept_0",
     "gpu__topk_mlir_0", "linalg__dequant_mlir", "linalg__kv_cache_update_kernel",
@@ -351,6 +351,25 @@ def test_reference_fixture_through_hip_target(path):
     out = th.emit(text)
     assert out.ext == "hip" and "extern \"C\" __global__" in out.source
     assert th.emit(text).source == out.source   # deterministic
+
+
+def test_attention_gqa_lowers_to_the_head_major_prefill():
+    """__tile_attention_gqa_* (the gpu emitter's causal GQA attention with head-major
+    Q/O, mlir_to_gpu.rs:1627-1712): the prefill entry in its head-major form, sizes
+    from the intrinsic's constant operands."""
+    src = th.emit((REF_MLIR / "gpu__attention_gqa_mlir_0.mlir").read_text()).source
+    assert "th::entry::prefill<th::kF32, true>(" in src
+    assert "th_tiles, 32u, 0u, 32u, 64u, 8u, 2u);" in src
+    # f32: one workgroup per (head, query)
+    assert "__th_desc_tile_attention_gqa = {th::kLaunchDescMagic, 512u, 256u, 1u," in src
+    ex = th.emit((EXAMPLES / "attention_gqa.mlir").read_text()).source
+    # bf16 with head_dim 128: the MFMA kernel, one workgroup per (head, 256 queries)
+    assert "th::entry::prefill<th::kBF16, true>(" in ex and "th_tiles, 300u, 0u, 300u, 128u, 8u, 2u);" in ex
+    assert "__th_desc_attention_gqa_bf16 = {th::kLaunchDescMagic, 512u, 16u, 1u," in ex
+    bad = (REF_MLIR / "gpu__attention_gqa_mlir_0.mlir").read_text().replace(
+        "constant(2 : i32) : i32\n    %seq", "constant(3 : i32) : i32\n    %seq")
+    with pytest.raises(th.HalError, match="multiple of num_kv_heads"):
+        th.emit(bad)
 
 
 def test_new_ops_lower_to_their_entries():

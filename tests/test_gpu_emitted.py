@@ -28,7 +28,7 @@ def launcher(dev):
     for stem in ("softmax_rows", "softmax_generic", "matmul_bf16", "matmul_f16_t", "matmul_f32",
                  "attention_f32", "prefill_bf16", "decode_bf16", "swiglu_mask", "rms_norm_rows",
                  "swiglu_gate_bf16", "matmul_bf16_tiles", "rope", "rows_long", "ops_extra",
-                 "softmax_loop", "softmax_loop_generic", "gemm_loop"):
+                 "softmax_loop", "softmax_loop_generic", "gemm_loop", "attention_gqa"):
         lau.load(_build.example_path(stem), th.KernelMode.GENERAL)
     return lau
 
@@ -211,6 +211,35 @@ def test_attention_f32_tiles(dev, stream, launcher, golden):
     assert np.abs(got[0] - g["o"]).max() < 1e-4
     ref1 = orc.attention_f32(q[s * d:], k[s * d:], v[s * d:], s, d)
     assert np.abs(got[1] - ref1).max() < 1e-5
+
+
+@pytest.mark.parametrize("name,NH,NKV,S,Dh,dt", [("attention_gqa_f32", 8, 2, 32, 64, "f32"),
+                                                   ("attention_gqa_wide_f32", 4, 1, 1500, 96, "f32"),
+                                                   ("attention_gqa_bf16", 8, 2, 300, 128, "bf16")])
+def test_attention_gqa_head_major(dev, stream, launcher, name, NH, NKV, S, Dh, dt):
+    """__tile_attention_gqa_* (mlir_to_gpu.rs:1627-1712): causal GQA attention with
+    Q/O [NH][S][D] and K/V [NKV][S][D], two logical tiles (batch elements); the
+    oracle's token-major prefill on transposed Q/O is the reference."""
+    B = 2
+    rng = np.random.default_rng(NH * S + Dh)
+    odt = orc.F32 if dt == "f32" else orc.BF16
+    tdt = D.F32 if dt == "f32" else D.BF16
+    def gen(n):
+        x = rng.standard_normal(n).astype(np.float32)
+        return x if dt == "f32" else orc.narrow(x, orc.BF16)
+    q, k, v = gen(B * NH * S * Dh), gen(B * NKV * S * Dh), gen(B * NKV * S * Dh)
+    bufs = [up(dev, stream, t, tdt) for t in (q, k, v)]
+    ob = dev.alloc(q.size, tdt)
+    launcher.launch(name, th.LaunchGrid.blocks_only(B), [ptr(b) for b in bufs] + [ptr(ob)], stream)
+    got = ob.copy_to_host(stream)
+    got = got if dt == "f32" else orc.widen(got, orc.BF16)
+    q_tm = q.reshape(B, NH, S, Dh).transpose(0, 2, 1, 3).copy()
+    ref = orc.attention_prefill(q_tm, k, v, odt, B, S, 0, S, Dh, NH, NKV)
+    ref = ref.reshape(B, S, NH, Dh).transpose(0, 2, 1, 3).reshape(-1)
+    if dt == "f32":
+        np.testing.assert_allclose(got, ref, rtol=1e-4, atol=1e-5)
+    else:
+        assert_attn_close(got, ref, "head-major gqa")
 
 
 @pytest.mark.parametrize("S,start,NH,NKV,Dh", [(200, 0, 4, 2, 128), (70, 9, 2, 1, 64)])

@@ -26,7 +26,7 @@ __device__ __forceinline__ void prefill_tile(const uint16_t* __restrict__ Q,
                                              uint16_t* __restrict__ O, uint32_t seq_len,
                                              uint32_t start_pos, uint32_t max_seq, uint32_t nh,
                                              uint32_t nkv, float scale_log2, uint32_t bh,
-                                             uint32_t qb) {
+                                             uint32_t qb, bool head_major = false) {
   u32x4* arena = lds::dma_lds_arena<NS * 2 * BKV * D * 2>();
   typedef __attribute__((address_space(3))) const void* lds_cptr;
   const uint32_t lds_base =
@@ -40,12 +40,14 @@ __device__ __forceinline__ void prefill_tile(const uint16_t* __restrict__ Q,
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l32 = lane & 31, g = lane >> 5;
 
-  // Rows past seq_len are computed on the last row's data and not stored.
-  const size_t q_row_stride = static_cast<size_t>(nh) * D;
+  // Rows past seq_len are computed on the last row's data and not stored.  Q and O
+  // are [B][S][NH][D], or [B][NH][S][D] with head_major.
   const uint32_t qt = q0 + 32 * wave + l32;
   const uint32_t qc = min(qt, seq_len - 1);
-  const uint16_t* qp = Q + (static_cast<size_t>(b) * seq_len + qc) * q_row_stride + h * D + 8 * g;
-  uint16_t* op = O + (static_cast<size_t>(b) * seq_len + qc) * q_row_stride + h * D + 4 * g;
+  const size_t q_row = head_major ? (static_cast<size_t>(b) * nh + h) * seq_len + qc
+                                  : (static_cast<size_t>(b) * seq_len + qc) * nh + h;
+  const uint16_t* qp = Q + q_row * D + 8 * g;
+  uint16_t* op = O + q_row * D + 4 * g;
   const uint64_t ok = __builtin_amdgcn_ballot_w64(qt < seq_len);
   // score (kt, r) of lane is kv position kv0 + 32kt + 8(r/4) + r%4 + 4g: masked
   // when that offset exceeds lim - kv0

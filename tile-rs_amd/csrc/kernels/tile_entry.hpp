@@ -213,7 +213,9 @@ __device__ __forceinline__ void attention_tiles(const void* q, const void* k, co
 }
 
 // ---- causal GQA prefill; runtime params in the Metal target's order ----
-template <int DT>
+// HM: Q and O head-major, [B][NH][S][D] (the gpu emitter's __tile_attention_gqa_*,
+// mlir_to_gpu.rs:1627-1712), instead of [B][S][NH][D].
+template <int DT, bool HM = false>
 __device__ __forceinline__ void prefill(const void* q, const void* k, const void* v, void* o,
                                         uint32_t batch, uint32_t seq_len, uint32_t start_pos,
                                         uint32_t max_seq, uint32_t head_dim, uint32_t nh,
@@ -235,7 +237,7 @@ __device__ __forceinline__ void prefill(const void* q, const void* k, const void
         prefill_work(w, batch * nh, nqb, bh, qb);
         pfa::prefill_tile<DT>(static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
                               static_cast<const uint16_t*>(v), static_cast<uint16_t*>(o), seq_len,
-                              start_pos, max_seq, nh, nkv, scale * kLog2e, bh, qb);
+                              start_pos, max_seq, nh, nkv, scale * kLog2e, bh, qb, HM);
         __syncthreads();  // every wave is done with the ring before the next item's DMA
       }
       return;
@@ -247,7 +249,7 @@ __device__ __forceinline__ void prefill(const void* q, const void* k, const void
     for (uint32_t w = blockIdx.x; w < batch * seq_len * nh; w += gridDim.x)
       attn_general_item_smem<DT, pfa::NT>(q, k, v, o, seq_len, start_pos, max_seq,
                                           start_pos + seq_len, head_dim, nh, nkv, 1, scale, w,
-                                          reinterpret_cast<float*>(arena));
+                                          reinterpret_cast<float*>(arena), HM);
   }
 }
 

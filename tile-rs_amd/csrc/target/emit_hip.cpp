@@ -16,6 +16,7 @@
 //   load, load -> __tile_matmul_transposed_*     -> store : same, B stored N x K
 //   load x3 -> __tile_attention_f32              -> store : th::entry::attention_tiles
 //   load x3 -> __tile_attention_prefill_f32      -> store : th::entry::prefill
+//   load x3 -> __tile_attention_gqa_{f32,f16}    -> store : th::entry::prefill (head-major)
 //   load x3 -> __tile_attention_decode_f32       -> store : th::entry::decode
 //   any DAG of elementwise tile ops              -> a plain HIP per-element kernel
 // Per-tile pointer offsets follow the #[tile_kernel] prelude: logical tile t
@@ -636,6 +637,18 @@ class Lowerer {
       if (a.size() < 6 || !tile(a[1]) || !tile(a[2]) || !tile(a[3]) || !shape_from(4, 5))
         return fail(base + " arity: " + line);
       t.ins = {a[1], a[2], a[3]};
+      t.dtype = tile(a[1])->dtype;
+    } else if (base == "attention_gqa_f32" || base == "attention_gqa_f16") {
+      // (dst, q, k, v, num_heads, num_kv_heads, seq_len, head_dim), all four sizes
+      // compile-time constants (mlir_to_gpu.rs:1627-1647); result [NH * S][D]
+      double nh = 0, nkv = 0, seq = 0, hd = 0;
+      if (a.size() < 8 || !tile(a[1]) || !tile(a[2]) || !tile(a[3]) || !num(a[4], &nh) ||
+          !num(a[5], &nkv) || !num(a[6], &seq) || !num(a[7], &hd))
+        return fail(base + " arity: " + line);
+      t.ins = {a[1], a[2], a[3]};
+      t.rows = static_cast<long long>(nh * seq);
+      t.cols = static_cast<long long>(hd);
+      t.scalars = {nh, nkv, seq, hd};
       t.dtype = tile(a[1])->dtype;
     } else if (kBin.count(base)) {
       // (dst, a, b, rows, cols) as in the linalg bridge (mlir_to_linalg.rs:620-633), or
@@ -1265,6 +1278,33 @@ bool emit_kernel(const Kernel& k, std::ostringstream& os, std::string* err) {
     const unsigned a_seq = static_cast<unsigned>(k.args.size()) + 0;
     const unsigned a_nh = static_cast<unsigned>(k.args.size()) + 4;
     desc(os, k, 512, 1, 1, (a_seq + 1) | ((a_nh + 1) << 8), 256u | (1u << 16), 1u << 20);
+    return true;
+  }
+  if (o == "attention_gqa_f32" || o == "attention_gqa_f16") {
+    const TileVal& q = k.tiles.at(hot->ins[0]);
+    const long long NH = static_cast<long long>(hot->scalars[0]);
+    const long long NKV = static_cast<long long>(hot->scalars[1]);
+    const long long S = static_cast<long long>(hot->scalars[2]);
+    const long long HD = static_cast<long long>(hot->scalars[3]);
+    if (NH <= 0 || NKV <= 0 || NH % NKV != 0 || S <= 0 || HD <= 0 || HD > 256 ||
+        NH * S * HD > 0xffffffffll) {
+      *err = "mlir_to_hip: " + k.name + ": " + o + " needs num_heads a multiple of num_kv_heads, " +
+             "seq_len > 0 and 0 < head_dim <= 256";
+      return false;
+    }
+    os << "causal GQA attention, head-major Q/O [" << NH << "][" << S << "][" << HD << "], K/V [" << NKV
+       << "][" << S << "][" << HD << "] " << dt_name(q.dtype) << " -> th::entry::prefill (head-major)\n";
+    signature(os, k, 512, {}, 1);
+    const char* ct = dt_ctype(q.dtype);
+    os << "  th::entry::prefill<" << dt_enum(q.dtype) << ", true>(" << in_ptr(0, ct) << ", "
+       << in_ptr(1, ct) << ", " << in_ptr(2, ct) << ", " << out_ptr(ct) << ", th_tiles, " << u(S)
+       << ", 0u, " << u(S) << ", " << u(HD) << ", " << u(NH) << ", " << u(NKV) << ");\n}\n";
+    // 16-bit with head_dim 128: the library's kernel, one workgroup per (head,
+    // 256-query block); otherwise one workgroup per (head, query)
+    const bool fast = q.dtype != F32 && HD == 128;
+    long long wpt = fast ? NH * ((S + 255) / 256) : NH * S;
+    if (wpt > (1 << 20)) wpt = 1 << 20;
+    desc(os, k, 512, static_cast<unsigned>(wpt), 1);
     return true;
   }
   if (o == "attention_decode_f32") {
