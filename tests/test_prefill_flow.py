@@ -171,3 +171,68 @@ def test_waves_past_the_diagonal_drain():
     # MFMAs of its split steps; wave 7: S(0), three periods and the last PV block
     assert w0.mfmas <= 16 + 16 + 16
     assert w7.mfmas >= 16 + 3 * 32 + 16
+
+
+# ---------------------------------------------------------------------------
+# Issue hazards of the hand-written loop.  The assembler inserts no wait states
+# into an asm statement, so the generator must: on gfx950 a non-transcendental
+# VALU instruction that reads or writes the destination of a transcendental op
+# (v_exp/v_rcp/v_log/v_sqrt/v_rsq) in the very next issue slot can see the value
+# from before it (found as run-to-run output drift of 1-2 bf16 ulp at config 4).
+# ---------------------------------------------------------------------------
+TRANS = ("v_exp_f32", "v_rcp_f32", "v_log_f32", "v_sqrt_f32", "v_rsq_f32")
+
+
+def vregs(text):
+    out = set()
+    for a, b in re.findall(r"\bv\[(\d+):(\d+)\]", text):
+        out |= set(range(int(a), int(b) + 1))
+    out |= {int(a) for a in re.findall(r"\bv(\d+)\b", text)}
+    return out
+
+
+def trans_hazards(prog):
+    """(trans line, next line) pairs where the instruction issued right after a
+    transcendental op touches its destination with no wait state between.  Labels
+    are transparent; an unconditional branch continues at its target."""
+    lines = [l.strip() for l in prog]
+    labels = {l[:-1]: i for i, l in enumerate(lines) if l.endswith(":")}
+
+    def next_issued(i):
+        seen = set()
+        while i < len(lines) and i not in seen:
+            seen.add(i)
+            ln = lines[i]
+            if ln.endswith(":"):
+                i += 1
+            elif ln.startswith("s_branch "):
+                i = labels[ln.split()[1]] + 1
+            else:
+                return ln
+        return None
+
+    bad = []
+    for i, ln in enumerate(lines):
+        op = ln.split()[0] if ln else ""
+        if op not in TRANS:
+            continue
+        dst = vregs(ln.split(None, 1)[1].split(",")[0])
+        nxt = next_issued(i + 1)
+        if nxt is None or not nxt.startswith("v_") or nxt.split()[0] in TRANS:
+            continue
+        if dst & vregs(nxt.split(None, 1)[1]):
+            bad.append((ln, nxt))
+    return bad
+
+
+def test_trans_hazard_check_finds_a_planted_case():
+    planted = ["v_exp_f32 v248, v248", "Lx_%=:", "v_mul_f32 v248, %17, v248"]
+    assert trans_hazards(planted) == [("v_exp_f32 v248, v248", "v_mul_f32 v248, %17, v248")]
+    assert trans_hazards(["v_exp_f32 v40, v40", "s_branch L1", "L1:", "v_add_f32 v41, v41, v40"])
+    assert not trans_hazards(["v_exp_f32 v40, v40", "s_nop 0", "v_add_f32 v41, v41, v40"])
+    assert not trans_hazards(["v_exp_f32 v40, v40", "v_exp_f32 v42, v42", "v_add_f32 v41, v41, v40"])
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+def test_no_trans_forwarding_hazard(dt):
+    assert trans_hazards(G.Gen(dt).program()) == []

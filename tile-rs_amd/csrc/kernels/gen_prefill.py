@@ -61,7 +61,7 @@ NLD = 4         # DMA instructions per lane per KV block
 # operand numbers of the asm statement (see prefill_asm.hpp)
 OP = dict(qp=0, op=1, lim=2, klane=3, vlane=4, krow=5, kcol=6, vrow=7, vcol=8,
           kbase=9, vbase=10, kvlast=11, nb=12, jd=13, lds=14, wave2k=15,
-          scale=16, ratio=17, ok=18, jl=19)
+          scale=16, lratio=17, ok=18, jl=19)
 
 
 def o(name):
@@ -194,7 +194,7 @@ class Gen:
         other 16 exponentials with P st 2-3, l update and split decision."""
         S = [f"v{S_BASE[par] + e}" for e in range(32)]
         P = [f"v{P_BASE + q}" for q in range(16)]
-        scale, ratio = o("scale"), o("ratio")
+        scale, lratio = o("scale"), o("lratio")
         m_blk, m_new, alpha, l_run = st("mblk"), st("mnew"), st("alpha"), st("l")
         ls0, ls1 = st("ls0"), st("ls1")
         ops = []
@@ -228,12 +228,17 @@ class Gen:
         add([f"v_add_f32 {X1}, {X1}, {TA}"])
         # Split step t when its largest probability exceeds 1/ratio of the row's sum:
         # only those steps' residual MFMAs run (out of line, after the period).
+        # Compared in the log2 domain: scale*mx - m_new + log2(ratio) > log2(sum), one
+        # v_log per block instead of four v_exp.  The log's result is read four slots
+        # later: a non-transcendental VALU op must not touch a transcendental op's
+        # destination in the next issue slot (gfx950 trans forwarding).
         mx = [f"v{STEPMAX[par] + t}" for t in range(4)]
+        add([f"v_log_f32 {X1}, {X1}"])
+        add([f"v_subrev_f32 {X0}, {lratio}, {m_new}"])
         for t in range(4):
-            add([f"v_fma_f32 {X0}, {mx[t]}, {scale}, -{m_new}"])
-            add([f"v_exp_f32 {X0}, {X0}"])
-            add([f"v_mul_f32 {X0}, {ratio}, {X0}"])
-            add([f"v_cmp_gt_f32 {SPLIT_MASK[t]}, {X0}, {X1}"])
+            add([f"v_fma_f32 {mx[t]}, {mx[t]}, {scale}, -{X0}"])
+        for t in range(4):
+            add([f"v_cmp_gt_f32 {SPLIT_MASK[t]}, {mx[t]}, {X1}"])
         add([f"s_or_b64 s[78:79], {SPLIT_MASK[0]}, {SPLIT_MASK[1]}",
              f"s_or_b64 s[78:79], s[78:79], {SPLIT_MASK[2]}",
              f"s_or_b64 s[78:79], s[78:79], {SPLIT_MASK[3]}"])

@@ -78,14 +78,15 @@ __device__ __forceinline__ void prefill_tile(const uint16_t* __restrict__ Q,
   const uint32_t vrow = 8 * wave + (lane >> 4);
   const uint32_t vcol = 16 * ((lane & 15) ^ (4 * (lane >> 4)));
   const uint32_t wave2k = 2048 * wave;
-  const float ratio = fa::kSplitRatio<DT>;
+  // log2 of the residual-split ratio (a power of two, so exact)
+  const float lratio = __builtin_log2f(fa::kSplitRatio<DT>);
 
 #define TH_PREFILL_OPS(STR)                                                                \
   asm volatile(STR                                                                         \
                :                                                                           \
                : "v"(qp), "v"(op), "v"(lim), "v"(klane), "v"(vlane), "v"(krow), "v"(kcol), \
                  "v"(vrow), "v"(vcol), "s"(kbase), "s"(vbase), "s"(kvlast), "s"(nb),       \
-                 "s"(jd), "s"(lds_base), "s"(wave2k), "s"(scale_log2), "s"(ratio), "s"(ok), \
+                 "s"(jd), "s"(lds_base), "s"(wave2k), "s"(scale_log2), "s"(lratio), "s"(ok), \
                  "s"(jl)                                                                   \
                : TH_PREFILL_ASM_CLOBBERS, "vcc", "scc", "m0", "memory")
   if constexpr (DT == kBF16) TH_PREFILL_OPS(TH_PREFILL_ASM_BF16); else TH_PREFILL_OPS(TH_PREFILL_ASM_F16);
