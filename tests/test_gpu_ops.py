@@ -458,6 +458,9 @@ def test_prefill_golden_vectors(dev, stream, golden):
     (1, 1500, 100, 7, 4, 4, 128),  # long loop, start_pos not a multiple of 64
     (1, 100, 37, 3000, 8, 2, 128), # chunk of a long cache (max_seq >> start_pos + S)
     (1, 200, 300, 4000, 4, 2, 64), # padded head_dim: only live cache rows are copied
+    (2, 600, 0, 0, 32, 8, 128),    # 16 (batch, kv head) units on 8 XCDs: grouped work order
+    (1, 520, 64, 0, 16, 8, 128),   # 8 units, GQA 2:1, start_pos > 0
+    (4, 300, 0, 0, 16, 4, 128),    # 16 units, GQA 4:1, ragged query block
 ])
 def test_prefill_shapes(dev, stream, dtype, B, S, start, extra, NH, NKV, Dh):
     rng = np.random.default_rng(S * 7 + start)

@@ -103,7 +103,7 @@ attn_prefill_asm(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
                  uint32_t nkv, float scale_log2) {
   const uint32_t nqb = (seq_len + BQ - 1) / BQ;
   uint32_t bh, qb;
-  prefill_work(blockIdx.x, batch * nh, nqb, bh, qb);
+  prefill_work(blockIdx.x, batch, nh, nkv, nqb, bh, qb);
   prefill_tile<DT>(Q, K, V, O, seq_len, start_pos, max_seq, nh, nkv, scale_log2, bh, qb);
 }
 }  // namespace pfa

@@ -234,7 +234,7 @@ __device__ __forceinline__ void prefill(const void* q, const void* k, const void
       const uint32_t nqb = (seq_len + pfa::BQ - 1) / pfa::BQ;
       for (uint32_t w = blockIdx.x; w < batch * nh * nqb; w += gridDim.x) {
         uint32_t bh, qb;
-        prefill_work(w, batch * nh, nqb, bh, qb);
+        prefill_work(w, batch, nh, nkv, nqb, bh, qb);
         pfa::prefill_tile<DT>(static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
                               static_cast<const uint16_t*>(v), static_cast<uint16_t*>(o), seq_len,
                               start_pos, max_seq, nh, nkv, scale * kLog2e, bh, qb, HM);
