@@ -124,3 +124,15 @@ def test_prefill_gqa_chunk(dev, stream):
     o = dev.alloc(B * S * NH * Dh, D.BF16)
     same_bits(lambda: th.attention_prefill(q, k, v, o, B, S, start, max_seq, Dh, NH, NKV, D.BF16,
                                            stream), o, stream)
+
+
+def test_prefill_split_kv(dev, stream):
+    """A 512-token chunk after 7680 cached positions: split-KV parts and their merge."""
+    B, S, start, NH, NKV, Dh = 1, 512, 7680, 32, 8, 128
+    max_seq = start + S
+    q = rnd(dev, stream, B * S * NH * Dh, D.BF16, 0xE6)
+    k = rnd(dev, stream, B * NKV * max_seq * Dh, D.BF16, 0xE7)
+    v = rnd(dev, stream, B * NKV * max_seq * Dh, D.BF16, 0xE8)
+    o = dev.alloc(B * S * NH * Dh, D.BF16)
+    same_bits(lambda: th.attention_prefill(q, k, v, o, B, S, start, max_seq, Dh, NH, NKV, D.BF16,
+                                           stream), o, stream)

@@ -461,6 +461,12 @@ def test_prefill_golden_vectors(dev, stream, golden):
     (2, 600, 0, 0, 32, 8, 128),    # 16 (batch, kv head) units on 8 XCDs: grouped work order
     (1, 520, 64, 0, 16, 8, 128),   # 8 units, GQA 2:1, start_pos > 0
     (4, 300, 0, 0, 16, 4, 128),    # 16 units, GQA 4:1, ragged query block
+    # split-KV (fewer work items than CUs, >= 16 cached blocks): parts + merge
+    (1, 200, 1024, 0, 4, 2, 128),  # 4 items, 2 parts
+    (2, 300, 2048, 5, 8, 2, 128),  # 32 items, 4 parts, GQA 4:1, ragged query block
+    (1, 200, 1100, 0, 4, 4, 128),  # start_pos not a multiple of 64
+    (1, 256, 2048, 0, 8, 2, 64),   # on the zero-padded head_dim-64 route
+    (1, 512, 7680, 0, 8, 2, 128),  # chunk after 7680 cached positions: 15 parts
 ])
 def test_prefill_shapes(dev, stream, dtype, B, S, start, extra, NH, NKV, Dh):
     rng = np.random.default_rng(S * 7 + start)

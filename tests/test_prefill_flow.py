@@ -233,6 +233,19 @@ def test_trans_hazard_check_finds_a_planted_case():
     assert not trans_hazards(["v_exp_f32 v40, v40", "v_exp_f32 v42, v42", "v_add_f32 v41, v41, v40"])
 
 
+@pytest.mark.parametrize("partial", [False, True])
 @pytest.mark.parametrize("dt", ["bf16", "f16"])
-def test_no_trans_forwarding_hazard(dt):
-    assert trans_hazards(G.Gen(dt).program()) == []
+def test_no_trans_forwarding_hazard(dt, partial):
+    assert trans_hazards(G.Gen(dt, partial).program()) == []
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+def test_split_part_program_differs_only_in_the_epilogue(dt):
+    """The split-KV part program runs the same loop; only the code after the loop
+    (f32 partial rows instead of normalized 16-bit O) differs."""
+    full, part = G.Gen(dt).program(), G.Gen(dt, True).program()
+    cut = next(i for i, l in enumerate(full) if l.startswith("v_rcp_f32"))
+    assert part[:cut] == full[:cut]
+    assert not any(l.startswith("v_rcp_f32") for l in part)
+    stores = [l for l in part if l.startswith("global_store")]
+    assert len(stores) == 17 and stores[-1].endswith("offset:512")

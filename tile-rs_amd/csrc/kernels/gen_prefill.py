@@ -102,8 +102,9 @@ INF = 10 ** 9
 
 
 class Gen:
-    def __init__(self, dt):
+    def __init__(self, dt, partial=False):
         self.dt = dt
+        self.partial = partial
         self.mn, self.cvt = names(dt)
         self.uid = 0
         self.ool = []
@@ -499,14 +500,25 @@ class Gen:
                 "s_mov_b64 s[66:67], exec"]
         out += [f"v_mov_b32 v32, {st('l')}", f"v_mov_b32 v33, {st('l')}", "s_nop 1",
                 "v_permlane32_swap_b32 v32, v33", "s_nop 1",
-                "v_add_f32 v32, v32, v33", "v_rcp_f32 v34, v32", "s_nop 0",
-                f"s_mov_b64 exec, {o('ok')}"]
-        for dtl in range(4):
-            for q4 in range(4):
-                a = O_BASE + 16 * dtl + 4 * q4
-                out += [f"v_mul_f32 v{36 + k}, v34, v{a + k}" for k in range(4)]
-                out += [f"{self.cvt} v40, v36, v37", f"{self.cvt} v41, v38, v39",
-                        f"global_store_dwordx2 {o('op')}, v[40:41], off offset:{64 * dtl + 16 * q4}"]
+                "v_add_f32 v32, v32, v33"]
+        if self.partial:
+            # Split-KV part: the unnormalized O row in f32 (this lane's 64 values, 4 at a
+            # time: d = 32 dtl + 8 q4 + 4 g + 0..3), then {l, m} after the 128 values,
+            # written by the lanes of half 0 (op = record + 16 g bytes).
+            out += [f"v_mov_b32 v33, {st('m')}", f"s_mov_b64 exec, {o('ok')}"]
+            for dtl in range(4):
+                for q4 in range(4):
+                    a = O_BASE + 16 * dtl + 4 * q4
+                    out.append(f"global_store_dwordx4 {o('op')}, v[{a}:{a + 3}], off offset:{128 * dtl + 32 * q4}")
+            out += ["s_mov_b32 exec_hi, 0", f"global_store_dwordx2 {o('op')}, v[32:33], off offset:512"]
+        else:
+            out += ["v_rcp_f32 v34, v32", "s_nop 0", f"s_mov_b64 exec, {o('ok')}"]
+            for dtl in range(4):
+                for q4 in range(4):
+                    a = O_BASE + 16 * dtl + 4 * q4
+                    out += [f"v_mul_f32 v{36 + k}, v34, v{a + k}" for k in range(4)]
+                    out += [f"{self.cvt} v40, v36, v37", f"{self.cvt} v41, v38, v39",
+                            f"global_store_dwordx2 {o('op')}, v[40:41], off offset:{64 * dtl + 16 * q4}"]
         out += ["s_mov_b64 exec, s[66:67]"]
         end = self.label("end")
         out += [f"s_branch {end}"]
@@ -523,9 +535,10 @@ def cstr(lines):
 def main(path):
     lines = ["// Generated by gen_prefill.py: prefill main loop (gfx950 asm).", "#pragma once"]
     for dt in ("bf16", "f16"):
-        g = Gen(dt)
-        prog = g.program()
-        lines.append(f'#define TH_PREFILL_ASM_{dt.upper()} "{cstr(prog)}"')
+        for partial in (False, True):
+            prog = Gen(dt, partial).program()
+            name = dt.upper() + ("_PART" if partial else "")
+            lines.append(f'#define TH_PREFILL_ASM_{name} "{cstr(prog)}"')
     clob = [f'"v{k}"' for k in range(16, 256)] + [f'"s{k}"' for k in range(48, 96)]
     lines.append("#define TH_PREFILL_ASM_CLOBBERS " + ",".join(clob))
     text = "\n".join(lines) + "\n"

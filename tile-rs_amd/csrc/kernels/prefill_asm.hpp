@@ -19,14 +19,23 @@ constexpr int BKV = 64;   // kv positions per ring stage
 constexpr int NT = 512;   // 8 waves x 32 query rows
 constexpr int NS = 5;     // ring stages (5 x 32 KB = all of LDS)
 
-template <int DT>
+// Split-KV parts (PART): the workgroup covers K/V blocks [j0, j1) of its query block
+// (j1 = ~0u: through the last) and writes, per query row, the unnormalized O in f32
+// plus the row's sum l and running max m (log2 units) to part_out: a record of
+// kPartRec floats {O[128], l, m, pad, pad} at row index q_row.  j0 * 64 must not exceed
+// start_pos, so that every row of the part has an unmasked position (finite m).
+constexpr int kPartRec = 132;
+
+template <int DT, bool PART = false>
 __device__ __forceinline__ void prefill_tile(const uint16_t* __restrict__ Q,
                                              const uint16_t* __restrict__ K,
                                              const uint16_t* __restrict__ V,
                                              uint16_t* __restrict__ O, uint32_t seq_len,
                                              uint32_t start_pos, uint32_t max_seq, uint32_t nh,
                                              uint32_t nkv, float scale_log2, uint32_t bh,
-                                             uint32_t qb, bool head_major = false) {
+                                             uint32_t qb, bool head_major = false,
+                                             uint32_t j0 = 0, uint32_t j1 = ~0u,
+                                             float* __restrict__ part_out = nullptr) {
   u32x4* arena = lds::dma_lds_arena<NS * 2 * BKV * D * 2>();
   typedef __attribute__((address_space(3))) const void* lds_cptr;
   const uint32_t lds_base =
@@ -47,20 +56,27 @@ __device__ __forceinline__ void prefill_tile(const uint16_t* __restrict__ Q,
   const size_t q_row = head_major ? (static_cast<size_t>(b) * nh + h) * seq_len + qc
                                   : (static_cast<size_t>(b) * seq_len + qc) * nh + h;
   const uint16_t* qp = Q + q_row * D + 8 * g;
-  uint16_t* op = O + q_row * D + 4 * g;
+  void* op = PART ? static_cast<void*>(part_out + q_row * kPartRec + 4 * g)
+                 : static_cast<void*>(O + q_row * D + 4 * g);
   const uint64_t ok = __builtin_amdgcn_ballot_w64(qt < seq_len);
   // score (kt, r) of lane is kv position kv0 + 32kt + 8(r/4) + r%4 + 4g: masked
   // when that offset exceeds lim - kv0
-  const int lim = static_cast<int>(start_pos + qt) - 4 * g;
-
-  const uint64_t kbase = reinterpret_cast<uint64_t>(K + (static_cast<size_t>(b) * nkv + kvh) * max_seq * D);
-  const uint64_t vbase = reinterpret_cast<uint64_t>(V + (static_cast<size_t>(b) * nkv + kvh) * max_seq * D);
-  const uint32_t kvlast = kv_len - 1;   // DMA rows are clamped here (in bounds; masked)
+  // The loop sees blocks j0 .. j1-1 as 0 .. nb-1: positions, the mask limit and the
+  // block indices below are taken relative to position 64 * j0.
   const uint32_t q_hi_wg = min(q0 + BQ, seq_len);
-  const uint32_t nb = (start_pos + q_hi_wg + BKV - 1) / BKV;
-  const uint32_t jd = __builtin_amdgcn_readfirstlane((start_pos + q0 + 32 * wave + 1) / BKV);
+  const uint32_t nb_all = (start_pos + q_hi_wg + BKV - 1) / BKV;
+  const uint32_t jend = min(j1, nb_all);
+  const uint32_t nb = jend - j0;
+  const uint32_t p0 = j0 * BKV;
+  const int lim = static_cast<int>(start_pos + qt - p0) - 4 * g;
+
+  const uint64_t kbase = reinterpret_cast<uint64_t>(K + ((static_cast<size_t>(b) * nkv + kvh) * max_seq + p0) * D);
+  const uint64_t vbase = reinterpret_cast<uint64_t>(V + ((static_cast<size_t>(b) * nkv + kvh) * max_seq + p0) * D);
+  // DMA rows are clamped here (in bounds; masked or past the part)
+  const uint32_t kvlast = min(kv_len, jend * BKV) - 1 - p0;
+  const uint32_t jd = __builtin_amdgcn_readfirstlane((start_pos + q0 + 32 * wave + 1) / BKV - j0);
   // the wave's last kv block with an unmasked score (row q0 + 32 wave + 31)
-  const uint32_t jl = __builtin_amdgcn_readfirstlane((start_pos + q0 + 32 * wave + 31) / BKV);
+  const uint32_t jl = __builtin_amdgcn_readfirstlane((start_pos + q0 + 32 * wave + 31) / BKV - j0);
 
   // LDS read offsets: K fragment rows (l32) and chunk g; V^T transposed reads
   const uint32_t klane = 16u * (256u * (l32 >> 4) + 16u * g + (l32 & 15));
@@ -89,7 +105,11 @@ __device__ __forceinline__ void prefill_tile(const uint16_t* __restrict__ Q,
                  "s"(jd), "s"(lds_base), "s"(wave2k), "s"(scale_log2), "s"(lratio), "s"(ok), \
                  "s"(jl)                                                                   \
                : TH_PREFILL_ASM_CLOBBERS, "vcc", "scc", "m0", "memory")
-  if constexpr (DT == kBF16) TH_PREFILL_OPS(TH_PREFILL_ASM_BF16); else TH_PREFILL_OPS(TH_PREFILL_ASM_F16);
+  if constexpr (PART) {
+    if constexpr (DT == kBF16) TH_PREFILL_OPS(TH_PREFILL_ASM_BF16_PART); else TH_PREFILL_OPS(TH_PREFILL_ASM_F16_PART);
+  } else {
+    if constexpr (DT == kBF16) TH_PREFILL_OPS(TH_PREFILL_ASM_BF16); else TH_PREFILL_OPS(TH_PREFILL_ASM_F16);
+  }
 #undef TH_PREFILL_OPS
 }
 
@@ -105,6 +125,58 @@ attn_prefill_asm(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
   uint32_t bh, qb;
   prefill_work(blockIdx.x, batch, nh, nkv, nqb, bh, qb);
   prefill_tile<DT>(Q, K, V, O, seq_len, start_pos, max_seq, nh, nkv, scale_log2, bh, qb);
+}
+// Split-KV prefill for launches with fewer work items than CUs (chunked prefill after a
+// long cache).  Workgroup w = item * nsplit + part; part p < nsplit-1 covers blocks
+// [p c, (p+1) c), the last one [(nsplit-1) c, end), with c * (nsplit - 1) * 64 <=
+// start_pos (checked on the host).  Partials go to ws: [nsplit][rows][kPartRec] f32.
+template <int DT>
+__global__ void __launch_bounds__(NT, 1)
+attn_prefill_split(const uint16_t* __restrict__ Q, const uint16_t* __restrict__ K,
+                   const uint16_t* __restrict__ V, float* __restrict__ ws, uint32_t batch,
+                   uint32_t seq_len, uint32_t start_pos, uint32_t max_seq, uint32_t nh,
+                   uint32_t nkv, float scale_log2, uint32_t nsplit, uint32_t chunk) {
+  const uint32_t nqb = (seq_len + BQ - 1) / BQ;
+  const uint32_t item = blockIdx.x / nsplit, part = blockIdx.x % nsplit;
+  uint32_t bh, qb;
+  prefill_work(item, batch, nh, nkv, nqb, bh, qb);
+  const size_t rows = static_cast<size_t>(batch) * seq_len * nh;
+  const uint32_t j0 = part * chunk, j1 = part + 1 == nsplit ? ~0u : j0 + chunk;
+  prefill_tile<DT, true>(Q, K, V, nullptr, seq_len, start_pos, max_seq, nh, nkv, scale_log2, bh,
+                         qb, false, j0, j1, ws + part * rows * kPartRec);
+}
+
+// Merge the split parts of each query row: O = sum_p 2^(m_p - M) O_p / sum_p 2^(m_p - M) l_p
+// with M = max_p m_p.  32 threads per row, four O values each; 8 rows per workgroup.
+template <int DT>
+__global__ void __launch_bounds__(256)
+attn_prefill_combine(const float* __restrict__ ws, uint16_t* __restrict__ O, size_t rows,
+                     uint32_t nsplit) {
+  const size_t row = static_cast<size_t>(blockIdx.x) * 8 + (threadIdx.x >> 5);
+  if (row >= rows) return;
+  const int c = threadIdx.x & 31;
+  const size_t pstride = rows * kPartRec;
+  const float* rec = ws + row * kPartRec;
+  float M = -INFINITY;
+  for (uint32_t p = 0; p < nsplit; ++p) M = fmaxf(M, rec[p * pstride + D + 1]);
+  float den = 0.0f, num[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (uint32_t p = 0; p < nsplit; ++p) {
+    const float* r = rec + p * pstride;
+    const float w = exp2f(r[D + 1] - M);
+    den = __builtin_fmaf(w, r[D], den);
+    const float4 o = *reinterpret_cast<const float4*>(r + 4 * c);
+    num[0] = __builtin_fmaf(w, o.x, num[0]);
+    num[1] = __builtin_fmaf(w, o.y, num[1]);
+    num[2] = __builtin_fmaf(w, o.z, num[2]);
+    num[3] = __builtin_fmaf(w, o.w, num[3]);
+  }
+  const float inv = 1.0f / den;
+  u32x2 out;
+  out[0] = static_cast<uint32_t>(f32_to_u16<DT>(num[0] * inv)) |
+           (static_cast<uint32_t>(f32_to_u16<DT>(num[1] * inv)) << 16);
+  out[1] = static_cast<uint32_t>(f32_to_u16<DT>(num[2] * inv)) |
+           (static_cast<uint32_t>(f32_to_u16<DT>(num[3] * inv)) << 16);
+  *reinterpret_cast<u32x2*>(O + row * D + 4 * c) = out;
 }
 }  // namespace pfa
 }  // namespace th

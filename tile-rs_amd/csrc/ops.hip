@@ -608,6 +608,31 @@ int th_attention_prefill(const void* q, const void* k, const void* v, void* o, u
     auto O = static_cast<uint16_t*>(o);
     uint32_t kv_rows = max_seq;   // cache rows per (batch, kv head) seen by the kernel
     const uint64_t rows_q = static_cast<uint64_t>(batch) * seq_len * num_heads;
+    // Split-KV: too few work items to fill the chip (a short chunk after a long cache)
+    // split each item's cached blocks below start_pos into parts whose partial (O, l, m)
+    // rows a second kernel merges.  Each part keeps >= 8 cached blocks; every part but the
+    // last starts and ends below start_pos, so every row of a part has unmasked keys.
+    const uint32_t cus = current_cu_count();
+    const uint32_t cached = start_pos / th::pfa::BKV;
+    uint32_t nsplit = 1, chunk = 0;
+    if (blocks < cus && cached >= 16) {
+      nsplit = static_cast<uint32_t>(std::min<uint64_t>((cus + blocks - 1) / blocks, cached / 8));
+      nsplit = std::min<uint32_t>(nsplit, 16);
+      if (nsplit >= 2) {
+        const uint32_t nb_max = (start_pos + seq_len + th::pfa::BKV - 1) / th::pfa::BKV;
+        chunk = std::min((nb_max + nsplit - 1) / nsplit, cached / (nsplit - 1));
+      } else {
+        nsplit = 1;
+      }
+    }
+    const uint64_t split_bytes =
+        nsplit > 1 ? static_cast<uint64_t>(nsplit) * rows_q * th::pfa::kPartRec * 4 : 0;
+    float* part_ws = nullptr;
+    if (split_bytes && !pad) {
+      void* ws = nullptr;
+      TH_TRY(th::stream_scratch(as_stream(s), split_bytes, &ws));
+      part_ws = static_cast<float*>(ws);
+    }
     if (pad) {
       // Only the live cache rows (positions < start_pos + seq_len) are read, so only
       // those are copied: the padded cache holds kv_len rows per (batch, kv head).
@@ -615,8 +640,10 @@ int th_attention_prefill(const void* q, const void* k, const void* v, void* o, u
       const uint64_t rows_kv = static_cast<uint64_t>(batch) * num_kv_heads * kv_len;
       constexpr uint64_t RB = th::pfa::D * 2;  // bytes of a padded row
       void* ws = nullptr;
-      TH_TRY(th::stream_scratch(as_stream(s), (2 * rows_q + 2 * rows_kv) * RB, &ws));
+      const uint64_t pad_bytes = (2 * rows_q + 2 * rows_kv) * RB;
+      TH_TRY(th::stream_scratch(as_stream(s), pad_bytes + split_bytes, &ws));
       auto* base = static_cast<uint16_t*>(ws);
+      if (split_bytes) part_ws = reinterpret_cast<float*>(static_cast<char*>(ws) + pad_bytes);
       uint16_t* Qp = base;
       uint16_t* Op = Qp + rows_q * th::pfa::D;
       uint16_t* Kp = Op + rows_q * th::pfa::D;
@@ -633,12 +660,29 @@ int th_attention_prefill(const void* q, const void* k, const void* v, void* o, u
       O = Op;
       kv_rows = kv_len;
     }
-    if (dtype == TH_BF16)
+    if (nsplit > 1) {
+      const dim3 sgrid(static_cast<uint32_t>(blocks * nsplit));
+      const dim3 cgrid(static_cast<uint32_t>((rows_q + 7) / 8));
+      if (dtype == TH_BF16) {
+        hipLaunchKernelGGL(th::pfa::attn_prefill_split<th::kBF16>, sgrid, block, 0, as_stream(s), Q,
+                           K, V, part_ws, batch, seq_len, start_pos, kv_rows, num_heads,
+                           num_kv_heads, sl2, nsplit, chunk);
+        hipLaunchKernelGGL(th::pfa::attn_prefill_combine<th::kBF16>, cgrid, dim3(256), 0,
+                           as_stream(s), part_ws, O, static_cast<size_t>(rows_q), nsplit);
+      } else {
+        hipLaunchKernelGGL(th::pfa::attn_prefill_split<th::kF16>, sgrid, block, 0, as_stream(s), Q,
+                           K, V, part_ws, batch, seq_len, start_pos, kv_rows, num_heads,
+                           num_kv_heads, sl2, nsplit, chunk);
+        hipLaunchKernelGGL(th::pfa::attn_prefill_combine<th::kF16>, cgrid, dim3(256), 0,
+                           as_stream(s), part_ws, O, static_cast<size_t>(rows_q), nsplit);
+      }
+    } else if (dtype == TH_BF16) {
       hipLaunchKernelGGL(th::pfa::attn_prefill_asm<th::kBF16>, grid, block, 0, as_stream(s), Q, K, V,
                          O, batch, seq_len, start_pos, kv_rows, num_heads, num_kv_heads, sl2);
-    else
+    } else {
       hipLaunchKernelGGL(th::pfa::attn_prefill_asm<th::kF16>, grid, block, 0, as_stream(s), Q, K, V,
                          O, batch, seq_len, start_pos, kv_rows, num_heads, num_kv_heads, sl2);
+    }
     TH_TRY(launch_status("attention_prefill launch"));
     if (pad) {
       copy_rows16_launch(O, th::pfa::D, o, head_dim, head_dim, rows_q, as_stream(s));
