@@ -209,7 +209,8 @@ int th_attention_prefill(const void* q, const void* k, const void* v, void* o, u
  * `workspace` may be NULL (the library keeps one per device, grown on demand;
  * calls that overlap on one device then race on it) or a device buffer of at
  * least th_attention_decode_workspace_size(...) bytes (non-zero for head_dim 128
- * and for head dims below 128 that are multiples of 8, which run padded). */
+ * and for head dims below 128 that are multiples of 8: 64 runs natively, the others
+ * run padded to 128; the size covers 128-column records either way). */
 size_t th_attention_decode_workspace_size(uint32_t batch, uint32_t seq_len, uint32_t head_dim,
                                           uint32_t num_heads, uint32_t num_kv_heads);
 int th_attention_decode(const void* q, const void* k, const void* v, void* o, uint32_t batch,
@@ -223,7 +224,8 @@ int th_attention_decode(const void* q, const void* k, const void* v, void* o, ui
  * as th_attention_decode.  The split partials go to a fixed 8 MiB array in each
  * GPU's memory that is loaded with the library's code object and held until the
  * process ends; a plan whose partials would need more returns TH_MEMORY_ERROR,
- * and head dims below 128 (which run on padded copies) return TH_KERNEL_ERROR.
+ * and head dims below 128 other than 64 (which run on padded copies) return
+ * TH_KERNEL_ERROR.
  * Every call on one GPU shares that GPU's array, so calls that overlap on one
  * GPU (on different streams, or replays of captured graphs running at the same
  * time) race on it; calls ordered on one stream do not. */

@@ -552,8 +552,8 @@ def test_decode_golden_vectors(dev, stream, golden):
     (1, 1, 0, 4, 4, 128, True),       # one position
     (3, 513, 7, 16, 1, 128, True),    # G=16, chunk boundary + 1
     (2, 1024, 0, 8, 8, 128, False),   # MHA
-    (2, 777, 0, 4, 2, 64, False),     # head_dim 64: live rows zero-padded to 128, split
-    (1, 9000, 40, 8, 1, 64, True),    # head_dim 64, G=8, rows past seq_len skipped by the copy
+    (2, 777, 0, 4, 2, 64, False),     # head_dim 64 (native kernel), split
+    (1, 9000, 40, 8, 1, 64, True),    # head_dim 64, G=8, rows past seq_len not read
     (64, 600, 0, 8, 8, 96, False),    # head_dim 96, unsplit
     (1, 300, 0, 4, 2, 60, False),     # head_dim 60 (not a multiple of 8) -> general kernel
     (1, 200, 0, 6, 2, 128, False),   # G=3 -> general kernel
@@ -561,7 +561,10 @@ def test_decode_golden_vectors(dev, stream, golden):
     (1, 66000, 0, 2, 1, 128, True),   # 129 chunks: the merge stages partials in two passes
     (16, 4196, 0, 16, 8, 128, False),  # 128 items x 9 chunks: splits of several chunks each
     (64, 1500, 0, 8, 8, 128, True),   # 512 items: one workgroup per item walks all chunks
-    (1, 5000, 9, 8, 2, 64, True),     # head_dim 64, split, caller's workspace (padded size)
+    (1, 5000, 9, 8, 2, 64, True),     # head_dim 64, split, caller's workspace (128-wide records)
+    (64, 1100, 0, 32, 8, 64, False),  # head_dim 64, 512 items, unsplit
+    (3, 2100, 5, 16, 1, 64, True),    # head_dim 64, G=16
+    (2, 700, 0, 8, 4, 80, False),     # head_dim 80: zero-padded to 128
 ])
 def test_decode_shapes(dev, stream, dtype, B, L, extra, NH, NKV, Dh, ws):
     rng = np.random.default_rng(L * 3 + NH)

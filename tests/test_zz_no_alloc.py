@@ -17,8 +17,7 @@ pytestmark = pytest.mark.gpu
 D = th.TileDtype
 
 
-def _decode_pair(dev, stream, B, L, max_seq, NH, NKV, dtype, seed):
-    Dh = 128
+def _decode_pair(dev, stream, B, L, max_seq, NH, NKV, dtype, seed, Dh=128):
     nq, nkv = B * NH * Dh, B * NKV * max_seq * Dh
     bufs = [dev.alloc(n, dtype) for n in (nq, nkv, nkv)]
     for i, (b, n) in enumerate(zip(bufs, (nq, nkv, nkv))):
@@ -64,11 +63,19 @@ def test_decode_static_unsplit_and_empty(dev, stream):
     assert not o.copy_to_host(stream).any()
 
 
+def test_decode_static_head_dim_64(dev, stream):
+    """head_dim 64 runs natively (no padded copies), so the static entry serves it."""
+    a, b = _decode_pair(dev, stream, 1, 9000, 9000, 8, 2, D.BF16, 0x5eed3, Dh=64)
+    assert np.array_equal(a, b)
+    a, b = _decode_pair(dev, stream, 2, 500, 512, 4, 4, D.BF16, 0x5eed4, Dh=64)
+    assert np.array_equal(a, b)
+
+
 def test_decode_static_rejects_padded_head_dim(dev, stream):
-    q = dev.alloc(4 * 64, D.BF16)
-    kv = dev.alloc(4 * 64 * 64, D.BF16)
+    q = dev.alloc(4 * 96, D.BF16)
+    kv = dev.alloc(4 * 64 * 96, D.BF16)
     rc = th.lib().th_attention_decode_static(
         C.c_void_p(q.as_raw_ptr()), C.c_void_p(kv.as_raw_ptr()), C.c_void_p(kv.as_raw_ptr()),
-        C.c_void_p(q.as_raw_ptr()), 1, 64, 64, 64, 4, 4, int(D.BF16), stream.handle)
+        C.c_void_p(q.as_raw_ptr()), 1, 64, 64, 96, 4, 4, int(D.BF16), stream.handle)
     assert rc != 0
     assert b"padded" in th.lib().th_last_error()

@@ -710,8 +710,10 @@ static void decode_plan(uint32_t items, uint32_t nchunks, uint32_t* n_split, uin
   *n_split = (nchunks + *cps - 1) / *cps;
 }
 
+// The MFMA decode: head_dim 128 or 64 (both native), G = 1..16 query heads per kv head.
 static bool decode_fast(uint32_t head_dim, uint32_t nh, uint32_t nkv, th_dtype dtype) {
-  if (dtype == TH_F32 || head_dim != th::dec::D || nkv == 0 || nh % nkv != 0) return false;
+  if (dtype == TH_F32 || (head_dim != th::dec::D && head_dim != 64) || nkv == 0 || nh % nkv != 0)
+    return false;
   const uint32_t g = nh / nkv;
   return g == 1 || g == 2 || g == 4 || g == 8 || g == 16;
 }
@@ -719,7 +721,8 @@ static bool decode_fast(uint32_t head_dim, uint32_t nh, uint32_t nkv, th_dtype d
 size_t th_attention_decode_workspace_size(uint32_t batch, uint32_t seq_len, uint32_t head_dim,
                                           uint32_t num_heads, uint32_t num_kv_heads) {
   (void)num_kv_heads;
-  // head dims below 128 (multiples of 8) run the 128-wide kernel on padded copies
+  // 128 and 64 run natively; other head dims below 128 (multiples of 8) run the
+  // 128-wide kernel on padded copies.  Records are sized for 128 columns either way.
   if (head_dim > th::dec::D || head_dim == 0 || (head_dim != th::dec::D && head_dim % 8 != 0))
     return 0;
   return static_cast<size_t>(batch) * num_heads * decode_chunks(seq_len) * (th::dec::D + 2) *
@@ -728,29 +731,29 @@ size_t th_attention_decode_workspace_size(uint32_t batch, uint32_t seq_len, uint
 
 }  // extern "C"
 
-template <int DT, int G>
+template <int DT, int G, int HD>
 static void decode_split_launch(const void* q, const void* k, const void* v, void* o, float* ws,
                                 uint32_t batch, uint32_t seq_len, uint32_t max_seq, uint32_t nh,
                                 uint32_t nkv, uint32_t n_split, uint32_t cps, float sl2,
                                 hipStream_t s) {
   const dim3 grid(batch * nkv * n_split), block(th::dec::NT);
-  hipLaunchKernelGGL((th::attn_decode_split<DT, G>), grid, block, 0, s,
+  hipLaunchKernelGGL((th::attn_decode_split<DT, G, HD>), grid, block, 0, s,
                      static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
                      static_cast<const uint16_t*>(v), static_cast<uint16_t*>(o), ws, seq_len,
                      max_seq, nh, nkv, n_split, cps, sl2);
 }
 
-template <int DT>
+template <int DT, int HD>
 static void decode_launch_g(uint32_t g, const void* q, const void* k, const void* v, void* o,
                             float* ws, uint32_t batch, uint32_t seq_len, uint32_t max_seq,
                             uint32_t nh, uint32_t nkv, uint32_t n_split, uint32_t cps, float sl2,
                             hipStream_t s) {
   switch (g) {
-    case 1: decode_split_launch<DT, 1>(q, k, v, o, ws, batch, seq_len, max_seq, nh, nkv, n_split, cps, sl2, s); break;
-    case 2: decode_split_launch<DT, 2>(q, k, v, o, ws, batch, seq_len, max_seq, nh, nkv, n_split, cps, sl2, s); break;
-    case 4: decode_split_launch<DT, 4>(q, k, v, o, ws, batch, seq_len, max_seq, nh, nkv, n_split, cps, sl2, s); break;
-    case 8: decode_split_launch<DT, 8>(q, k, v, o, ws, batch, seq_len, max_seq, nh, nkv, n_split, cps, sl2, s); break;
-    default: decode_split_launch<DT, 16>(q, k, v, o, ws, batch, seq_len, max_seq, nh, nkv, n_split, cps, sl2, s); break;
+    case 1: decode_split_launch<DT, 1, HD>(q, k, v, o, ws, batch, seq_len, max_seq, nh, nkv, n_split, cps, sl2, s); break;
+    case 2: decode_split_launch<DT, 2, HD>(q, k, v, o, ws, batch, seq_len, max_seq, nh, nkv, n_split, cps, sl2, s); break;
+    case 4: decode_split_launch<DT, 4, HD>(q, k, v, o, ws, batch, seq_len, max_seq, nh, nkv, n_split, cps, sl2, s); break;
+    case 8: decode_split_launch<DT, 8, HD>(q, k, v, o, ws, batch, seq_len, max_seq, nh, nkv, n_split, cps, sl2, s); break;
+    default: decode_split_launch<DT, 16, HD>(q, k, v, o, ws, batch, seq_len, max_seq, nh, nkv, n_split, cps, sl2, s); break;
   }
 }
 
@@ -791,32 +794,43 @@ static int static_scratch_address(float** out) {
   return TH_OK;
 }
 
-// The 128-wide MFMA decode: split kernel, then (n_split > 1) the LSE combine of the
-// partials in ws.  Launches only; no allocation.
-static int decode_run(const void* Q, const void* K, const void* V, void* O, float* ws,
-                      uint32_t batch, uint32_t seq_len, uint32_t max_seq, uint32_t num_heads,
-                      uint32_t num_kv_heads, uint32_t n_split, uint32_t cps, float sl2,
-                      th_dtype dtype, hipStream_t s) {
+// The MFMA decode (head_dim 128 or 64): split kernel, then (n_split > 1) the LSE
+// combine of the partials in ws.  Launches only; no allocation.
+template <int HD>
+static void decode_run_hd(const void* Q, const void* K, const void* V, void* O, float* ws,
+                          uint32_t batch, uint32_t seq_len, uint32_t max_seq, uint32_t num_heads,
+                          uint32_t num_kv_heads, uint32_t n_split, uint32_t cps, float sl2,
+                          th_dtype dtype, hipStream_t s) {
   const uint32_t g = num_heads / num_kv_heads;
   if (dtype == TH_BF16)
-    decode_launch_g<th::kBF16>(g, Q, K, V, O, ws, batch, seq_len, max_seq, num_heads,
-                               num_kv_heads, n_split, cps, sl2, s);
+    decode_launch_g<th::kBF16, HD>(g, Q, K, V, O, ws, batch, seq_len, max_seq, num_heads,
+                                   num_kv_heads, n_split, cps, sl2, s);
   else
-    decode_launch_g<th::kF16>(g, Q, K, V, O, ws, batch, seq_len, max_seq, num_heads,
-                              num_kv_heads, n_split, cps, sl2, s);
-  TH_TRY(launch_status("attention_decode launch"));
+    decode_launch_g<th::kF16, HD>(g, Q, K, V, O, ws, batch, seq_len, max_seq, num_heads,
+                                  num_kv_heads, n_split, cps, sl2, s);
   // with one split each workgroup covered its whole sequence and wrote O
   if (n_split > 1) {
     const dim3 cgrid(batch * num_heads), cblock(th::dec::CT);
     if (dtype == TH_BF16)
-      hipLaunchKernelGGL(th::attn_decode_combine<th::kBF16>, cgrid, cblock, 0, s, ws,
+      hipLaunchKernelGGL((th::attn_decode_combine<th::kBF16, HD>), cgrid, cblock, 0, s, ws,
                          static_cast<uint16_t*>(O), num_heads, num_kv_heads, n_split);
     else
-      hipLaunchKernelGGL(th::attn_decode_combine<th::kF16>, cgrid, cblock, 0, s, ws,
+      hipLaunchKernelGGL((th::attn_decode_combine<th::kF16, HD>), cgrid, cblock, 0, s, ws,
                          static_cast<uint16_t*>(O), num_heads, num_kv_heads, n_split);
-    TH_TRY(launch_status("attention_decode combine launch"));
   }
-  return TH_OK;
+}
+
+static int decode_run(const void* Q, const void* K, const void* V, void* O, float* ws,
+                      uint32_t batch, uint32_t seq_len, uint32_t max_seq, uint32_t head_dim,
+                      uint32_t num_heads, uint32_t num_kv_heads, uint32_t n_split, uint32_t cps,
+                      float sl2, th_dtype dtype, hipStream_t s) {
+  if (head_dim == 64)
+    decode_run_hd<64>(Q, K, V, O, ws, batch, seq_len, max_seq, num_heads, num_kv_heads, n_split,
+                      cps, sl2, dtype, s);
+  else
+    decode_run_hd<th::dec::D>(Q, K, V, O, ws, batch, seq_len, max_seq, num_heads, num_kv_heads,
+                              n_split, cps, sl2, dtype, s);
+  return launch_status("attention_decode launch");
 }
 
 extern "C" {
@@ -841,7 +855,7 @@ int th_attention_decode(const void* q, const void* k, const void* v, void* o, ui
   }
   const bool fast = decode_fast(head_dim, num_heads, num_kv_heads, dtype) && aligned16(q) &&
                     aligned16(k) && aligned16(v);
-  // Head dims below 128 (multiples of 8): Q and the live rows of K and V (the first
+  // Other head dims below 128 (multiples of 8): Q and the live rows of K and V (the first
   // seq_len of each (batch, kv_head)) are copied zero-padded to 128 columns into the
   // stream's scratch, the MFMA decode runs on the copies (zero columns change no
   // score and give zero outputs) and O's first head_dim columns are copied back.
@@ -902,8 +916,9 @@ int th_attention_decode(const void* q, const void* k, const void* v, void* o, ui
   } else if (n_split > 1) {
     TH_TRY(th::device_scratch(need, &ws));
   }
-  TH_TRY(decode_run(Q, K, V, O, static_cast<float*>(ws), batch, seq_len, max_seq, num_heads,
-                    num_kv_heads, n_split, cps, scale * th::kLog2e, dtype, as_stream(s)));
+  TH_TRY(decode_run(Q, K, V, O, static_cast<float*>(ws), batch, seq_len, max_seq,
+                    pad ? th::dec::D : head_dim, num_heads, num_kv_heads, n_split, cps,
+                    scale * th::kLog2e, dtype, as_stream(s)));
   if (pad) {
     copy_rows16_launch(O, th::dec::D, o, head_dim, head_dim,
                        static_cast<uint64_t>(batch) * num_heads, as_stream(s));
@@ -937,7 +952,7 @@ int th_attention_decode_static(const void* q, const void* k, const void* v, void
   const bool fast = decode_fast(head_dim, num_heads, num_kv_heads, dtype) && aligned16(q) &&
                     aligned16(k) && aligned16(v);
   if (!fast) {
-    if (head_dim < th::dec::D && head_dim % 8 == 0 && dtype != TH_F32)
+    if (head_dim < th::dec::D && head_dim % 8 == 0 && dtype != TH_F32 && head_dim != 64)
       return fail(TH_KERNEL_ERROR,
                   "attention_decode_static: head_dim " + std::to_string(head_dim) +
                       " runs on zero-padded copies that need allocated memory; use "
@@ -955,7 +970,7 @@ int th_attention_decode_static(const void* q, const void* k, const void* v, void
   float* ws = nullptr;
   if (n_split > 1) {
     const uint64_t need =
-        static_cast<uint64_t>(batch) * num_heads * n_split * (th::dec::D + 2) * sizeof(float);
+        static_cast<uint64_t>(batch) * num_heads * n_split * (head_dim + 2) * sizeof(float);
     if (need > kDecodeStaticBytes)
       return fail(TH_MEMORY_ERROR, "attention_decode_static: the split partials need " +
                                        std::to_string(need) + " bytes, more than the " +
@@ -963,8 +978,8 @@ int th_attention_decode_static(const void* q, const void* k, const void* v, void
                                        "-byte fixed scratch; use th_attention_decode");
     TH_TRY(static_scratch_address(&ws));
   }
-  return decode_run(q, k, v, o, ws, batch, seq_len, max_seq, num_heads, num_kv_heads, n_split,
-                    cps, scale * th::kLog2e, dtype, as_stream(s));
+  return decode_run(q, k, v, o, ws, batch, seq_len, max_seq, head_dim, num_heads, num_kv_heads,
+                    n_split, cps, scale * th::kLog2e, dtype, as_stream(s));
 }
 
 int th_fill_random(void* dst, uint64_t n, th_dtype dtype, int dist, float p0, float p1,
