@@ -260,7 +260,7 @@ def test_prefill_bf16(dev, stream, launcher, S, start, NH, NKV, Dh):
 
 
 @pytest.mark.parametrize("L,NH,NKV,Dh", [(700, 8, 2, 128), (1100, 16, 16, 128), (300, 6, 2, 128),
-                                         (257, 4, 1, 64)])
+                                         (257, 4, 1, 64), (9000, 8, 2, 64), (600, 6, 2, 64)])
 def test_decode_bf16(dev, stream, launcher, L, NH, NKV, Dh):
     B, max_seq = 3, L + 5
     rng = np.random.default_rng(L + NH)

@@ -276,11 +276,11 @@ static __device__ uint32_t decode_arrivals[dsplit::kMaxItems];
 
 // O rows of item bk = sum_s 2^(m_s - M) O_s / sum_s 2^(m_s - M) l_s over its
 // n_split records (as decode_tile writes them), for all G heads of the item.
-template <int DT, int G>
+template <int DT, int G, int HD = dec::D>
 __device__ __forceinline__ void decode_merge(const float* __restrict__ ws, uint16_t* __restrict__ O,
                                              uint32_t bk, uint32_t nh, uint32_t nkv,
                                              uint32_t n_split) {
-  constexpr int D = dec::D, NT = dec::NT, R = D + 2;
+  constexpr int D = HD, NT = dec::NT, R = D + 2;
   constexpr int NP = G * D / 2;                  // output pairs (d, d+1)
   constexpr int NG = NP >= NT ? 1 : NT / NP;     // thread groups splitting the records
   constexpr int UNR = 8;
@@ -352,7 +352,7 @@ __device__ __forceinline__ void decode_merge(const float* __restrict__ ws, uint1
   __syncthreads();  // s_w / s_den / s_part are reused by the next item
 }
 
-template <int DT, int G>
+template <int DT, int G, int HD = dec::D>
 __device__ __forceinline__ void decode_group(const uint16_t* q, const uint16_t* k,
                                              const uint16_t* v, uint16_t* o, uint32_t batch,
                                              uint32_t seq_len, uint32_t max_seq, uint32_t nh,
@@ -361,7 +361,7 @@ __device__ __forceinline__ void decode_group(const uint16_t* q, const uint16_t* 
   const uint32_t items = batch * nkv;
   uint32_t n_split = (gridDim.x + items - 1) / items;
   n_split = min(n_split, min(nchunks, dsplit::kMaxSplit));
-  const size_t per_split = static_cast<size_t>(items) * G * (dec::D + 2);
+  const size_t per_split = static_cast<size_t>(items) * G * (HD + 2);
   n_split = min(static_cast<size_t>(n_split), dsplit::kPartialFloats / per_split);
   if (items > dsplit::kMaxItems || n_split < 2) n_split = 1;
   const uint32_t cps = (nchunks + n_split - 1) / n_split;
@@ -371,8 +371,8 @@ __device__ __forceinline__ void decode_group(const uint16_t* q, const uint16_t* 
     const uint32_t bk = w / n_split, split = w % n_split;
     const uint32_t c0 = split * cps, c1 = min(nchunks, c0 + cps);
     // unsplit: the workgroup covers the whole sequence and writes O itself
-    decode_tile<DT, G>(q, k, v, o, n_split > 1 ? decode_partials : nullptr, seq_len, max_seq, nh,
-                       nkv, n_split, scale_log2, bk, split, c0, c1);
+    decode_tile<DT, G, 4, 8, HD>(q, k, v, o, n_split > 1 ? decode_partials : nullptr, seq_len,
+                                 max_seq, nh, nkv, n_split, scale_log2, bk, split, c0, c1);
     if (n_split == 1) continue;
     // decode_tile ends on a barrier: every wave's partial stores are issued.  The
     // release fence makes them visible device-wide before the arrival counts.
@@ -383,10 +383,25 @@ __device__ __forceinline__ void decode_group(const uint16_t* q, const uint16_t* 
     __syncthreads();
     if (s_last) {
       __threadfence();   // acquire: the other splits' partials
-      decode_merge<DT, G>(decode_partials, o, bk, nh, nkv, n_split);
+      decode_merge<DT, G, HD>(decode_partials, o, bk, nh, nkv, n_split);
       if (threadIdx.x == 0) decode_arrivals[bk] = 0;   // ready for the next launch
     }
     __syncthreads();   // s_last is rewritten by the next item
+  }
+}
+
+// The MFMA decode for head_dim HD (128 or 64); false: no instance for this group size.
+template <int DT, int HD>
+__device__ __forceinline__ bool decode_mfma(uint32_t g, const uint16_t* Q, const uint16_t* K,
+                                            const uint16_t* V, uint16_t* O, uint32_t batch,
+                                            uint32_t seq_len, uint32_t max_seq, uint32_t nh,
+                                            uint32_t nkv, float sl2) {
+  switch (g) {
+    case 1: decode_group<DT, 1, HD>(Q, K, V, O, batch, seq_len, max_seq, nh, nkv, sl2); return true;
+    case 2: decode_group<DT, 2, HD>(Q, K, V, O, batch, seq_len, max_seq, nh, nkv, sl2); return true;
+    case 4: decode_group<DT, 4, HD>(Q, K, V, O, batch, seq_len, max_seq, nh, nkv, sl2); return true;
+    case 8: decode_group<DT, 8, HD>(Q, K, V, O, batch, seq_len, max_seq, nh, nkv, sl2); return true;
+    default: return false;
   }
 }
 
@@ -398,19 +413,16 @@ __device__ __forceinline__ void decode(const void* q, const void* k, const void*
   const float scale = 1.0f / __builtin_sqrtf(static_cast<float>(head_dim));
   const uint32_t g = nh / nkv;
   if constexpr (DT != kF32) {
-    if (head_dim == dec::D && seq_len > 0) {
+    if ((head_dim == dec::D || head_dim == 64) && seq_len > 0) {
       const float sl2 = scale * kLog2e;
       auto Q = static_cast<const uint16_t*>(q);
       auto K = static_cast<const uint16_t*>(k);
       auto V = static_cast<const uint16_t*>(v);
       auto O = static_cast<uint16_t*>(o);
-      switch (g) {
-        case 1: decode_group<DT, 1>(Q, K, V, O, batch, seq_len, max_seq, nh, nkv, sl2); return;
-        case 2: decode_group<DT, 2>(Q, K, V, O, batch, seq_len, max_seq, nh, nkv, sl2); return;
-        case 4: decode_group<DT, 4>(Q, K, V, O, batch, seq_len, max_seq, nh, nkv, sl2); return;
-        case 8: decode_group<DT, 8>(Q, K, V, O, batch, seq_len, max_seq, nh, nkv, sl2); return;
-        default: break;
-      }
+      if (head_dim == 64 ? decode_mfma<DT, 64>(g, Q, K, V, O, batch, seq_len, max_seq, nh, nkv, sl2)
+                         : decode_mfma<DT, dec::D>(g, Q, K, V, O, batch, seq_len, max_seq, nh, nkv,
+                                                   sl2))
+        return;
     }
   }
   for (uint32_t w = blockIdx.x; w < batch * nh; w += gridDim.x)
