@@ -136,3 +136,13 @@ def test_prefill_split_kv(dev, stream):
     o = dev.alloc(B * S * NH * Dh, D.BF16)
     same_bits(lambda: th.attention_prefill(q, k, v, o, B, S, start, max_seq, Dh, NH, NKV, D.BF16,
                                            stream), o, stream)
+
+
+def test_prefill_head_dim_64(dev, stream):
+    B, S, NH, NKV, Dh = 2, 2048, 16, 4, 64
+    q = rnd(dev, stream, B * S * NH * Dh, D.BF16, 0xE9)
+    k = rnd(dev, stream, B * NKV * S * Dh, D.BF16, 0xEA)
+    v = rnd(dev, stream, B * NKV * S * Dh, D.BF16, 0xEB)
+    o = dev.alloc(B * S * NH * Dh, D.BF16)
+    same_bits(lambda: th.attention_prefill(q, k, v, o, B, S, 0, S, Dh, NH, NKV, D.BF16, stream), o,
+              stream)

@@ -242,7 +242,7 @@ def test_attention_gqa_head_major(dev, stream, launcher, name, NH, NKV, S, Dh, d
         assert_attn_close(got, ref, "head-major gqa")
 
 
-@pytest.mark.parametrize("S,start,NH,NKV,Dh", [(200, 0, 4, 2, 128), (70, 9, 2, 1, 64)])
+@pytest.mark.parametrize("S,start,NH,NKV,Dh", [(200, 0, 4, 2, 128), (70, 9, 2, 1, 64), (600, 40, 8, 2, 64)])
 def test_prefill_bf16(dev, stream, launcher, S, start, NH, NKV, Dh):
     B, max_seq = 2, start + S + 3
     rng = np.random.default_rng(S)

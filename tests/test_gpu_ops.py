@@ -448,7 +448,9 @@ def test_prefill_golden_vectors(dev, stream, golden):
     (1, 256, 0, 0, 2, 2, 128),     # one full query block
     (2, 300, 0, 4, 4, 1, 128),     # ragged, GQA 4:1
     (1, 100, 37, 0, 8, 2, 128),    # chunked prefill, start_pos > 0
-    (1, 600, 0, 0, 2, 2, 64),      # head_dim 64: zero-padded to 128 for the MFMA kernel
+    (1, 600, 0, 0, 2, 2, 64),      # head_dim 64 (native kernel)
+    (2, 1000, 0, 0, 8, 2, 64),     # head_dim 64, GQA 4:1, grouped work order
+    (1, 1500, 100, 7, 4, 4, 64),   # head_dim 64, long loop, start_pos not a multiple of 64
     (2, 300, 40, 3, 8, 2, 96),     # head_dim 96, GQA 4:1, start_pos > 0, padded
     (1, 257, 0, 0, 4, 4, 80),      # head_dim 80, padded
     (1, 70, 3, 0, 2, 1, 60),       # head_dim 60 (not a multiple of 8) -> general kernel
@@ -457,7 +459,8 @@ def test_prefill_golden_vectors(dev, stream, golden):
     (1, 130, 0, 0, 2, 1, 128),     # three KV blocks, ragged query block
     (1, 1500, 100, 7, 4, 4, 128),  # long loop, start_pos not a multiple of 64
     (1, 100, 37, 3000, 8, 2, 128), # chunk of a long cache (max_seq >> start_pos + S)
-    (1, 200, 300, 4000, 4, 2, 64), # padded head_dim: only live cache rows are copied
+    (1, 200, 300, 4000, 4, 2, 64), # head_dim 64, chunk of a long cache
+    (1, 200, 300, 4000, 4, 2, 96), # padded head_dim: only live cache rows are copied
     (2, 600, 0, 0, 32, 8, 128),    # 16 (batch, kv head) units on 8 XCDs: grouped work order
     (1, 520, 64, 0, 16, 8, 128),   # 8 units, GQA 2:1, start_pos > 0
     (4, 300, 0, 0, 16, 4, 128),    # 16 units, GQA 4:1, ragged query block
@@ -465,7 +468,8 @@ def test_prefill_golden_vectors(dev, stream, golden):
     (1, 200, 1024, 0, 4, 2, 128),  # 4 items, 2 parts
     (2, 300, 2048, 5, 8, 2, 128),  # 32 items, 4 parts, GQA 4:1, ragged query block
     (1, 200, 1100, 0, 4, 4, 128),  # start_pos not a multiple of 64
-    (1, 256, 2048, 0, 8, 2, 64),   # on the zero-padded head_dim-64 route
+    (1, 256, 2048, 0, 8, 2, 64),   # head_dim 64 (native parts and merge)
+    (1, 256, 2048, 0, 8, 2, 80),   # on the zero-padded head_dim-80 route
     (1, 512, 7680, 0, 8, 2, 128),  # chunk after 7680 cached positions: 15 parts
 ])
 def test_prefill_shapes(dev, stream, dtype, B, S, start, extra, NH, NKV, Dh):

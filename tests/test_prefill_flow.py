@@ -130,19 +130,21 @@ class Wave:
 
 
 PROG = G.Gen("bf16").program()
+PROGS = {128: PROG, 64: G.Gen("bf16", False, 64).program()}
 
 SHAPES = [(1, 0), (40, 0), (64, 0), (65, 0), (200, 0), (256, 0), (300, 0), (700, 0),
           (1000, 0), (130, 5), (256, 64), (100, 1000), (513, 77)]
 
 
+@pytest.mark.parametrize("head_dim", [128, 64])
 @pytest.mark.parametrize("seq_len,start_pos", SHAPES)
-def test_every_wave_passes_the_same_barriers(seq_len, start_pos):
+def test_every_wave_passes_the_same_barriers(seq_len, start_pos, head_dim):
     rng = random.Random(seq_len * 131 + start_pos)
     for qb in range((seq_len + BQ - 1) // BQ):
         counts = set()
         for wave in range(8):
             ops = operands(seq_len, start_pos, qb, wave)
-            w = Wave(PROG, ops, rng).run()
+            w = Wave(PROGS[head_dim], ops, rng).run()
             nb = ops["nb"]
             counts.add(len(w.barriers))
             # one barrier after the prologue, then one per period j = 0 .. nb-2
@@ -159,18 +161,21 @@ def test_every_wave_passes_the_same_barriers(seq_len, start_pos):
         assert len(counts) == 1
 
 
-def test_waves_past_the_diagonal_drain():
+@pytest.mark.parametrize("head_dim", [128, 64])
+def test_waves_past_the_diagonal_drain(head_dim):
     """A wave whose rows end before the workgroup's last block skips the compute of the
     fully masked periods (wave 0 of a 256-row block: 3 of its 4 diagonal periods)."""
     ops = operands(256, 0, 0, 0)
     assert ops["jl"] == 0 and ops["nb"] == 4
-    w0 = Wave(PROG, ops, random.Random(1)).run()
-    w7 = Wave(PROG, operands(256, 0, 0, 7), random.Random(1)).run()
+    w0 = Wave(PROGS[head_dim], ops, random.Random(1)).run()
+    w7 = Wave(PROGS[head_dim], operands(256, 0, 0, 7), random.Random(1)).run()
     assert len(w0.barriers) == len(w7.barriers) == 4
-    # wave 0: S(0), the PV of its only block (16 + 16) and at most 4 x 4 residual
-    # MFMAs of its split steps; wave 7: S(0), three periods and the last PV block
-    assert w0.mfmas <= 16 + 16 + 16
-    assert w7.mfmas >= 16 + 3 * 32 + 16
+    # MFMAs per block: n QK and n PV (n = 16 at head_dim 128, 8 at 64); wave 0: S(0),
+    # the PV of its only block and at most 4 residual steps of n/4; wave 7: S(0), three
+    # periods and the last PV block
+    n = head_dim // 8
+    assert w0.mfmas <= n + n + n
+    assert w7.mfmas >= n + 3 * 2 * n + n
 
 
 # ---------------------------------------------------------------------------
@@ -233,19 +238,21 @@ def test_trans_hazard_check_finds_a_planted_case():
     assert not trans_hazards(["v_exp_f32 v40, v40", "v_exp_f32 v42, v42", "v_add_f32 v41, v41, v40"])
 
 
+@pytest.mark.parametrize("head_dim", [128, 64])
 @pytest.mark.parametrize("partial", [False, True])
 @pytest.mark.parametrize("dt", ["bf16", "f16"])
-def test_no_trans_forwarding_hazard(dt, partial):
-    assert trans_hazards(G.Gen(dt, partial).program()) == []
+def test_no_trans_forwarding_hazard(dt, partial, head_dim):
+    assert trans_hazards(G.Gen(dt, partial, head_dim).program()) == []
 
 
+@pytest.mark.parametrize("head_dim", [128, 64])
 @pytest.mark.parametrize("dt", ["bf16", "f16"])
-def test_split_part_program_differs_only_in_the_epilogue(dt):
+def test_split_part_program_differs_only_in_the_epilogue(dt, head_dim):
     """The split-KV part program runs the same loop; only the code after the loop
     (f32 partial rows instead of normalized 16-bit O) differs."""
-    full, part = G.Gen(dt).program(), G.Gen(dt, True).program()
+    full, part = G.Gen(dt, False, head_dim).program(), G.Gen(dt, True, head_dim).program()
     cut = next(i for i, l in enumerate(full) if l.startswith("v_rcp_f32"))
     assert part[:cut] == full[:cut]
     assert not any(l.startswith("v_rcp_f32") for l in part)
     stores = [l for l in part if l.startswith("global_store")]
-    assert len(stores) == 17 and stores[-1].endswith("offset:512")
+    assert len(stores) == head_dim // 8 + 1 and stores[-1].endswith(f"offset:{4 * head_dim}")

@@ -56,7 +56,6 @@ from pathlib import Path
 NS = 5          # LDS ring stages of 64 KV positions (K 16 KB + V 16 KB each)
 PD = 6          # fragment prefetch distance (fragments in flight ahead of their MFMA)
 RING = 8        # fragment ring size (4 VGPRs per fragment)
-NLD = 4         # DMA instructions per lane per KV block
 
 # operand numbers of the asm statement (see prefill_asm.hpp)
 OP = dict(qp=0, op=1, lim=2, klane=3, vlane=4, krow=5, kcol=6, vrow=7, vcol=8,
@@ -102,9 +101,20 @@ INF = 10 ** 9
 
 
 class Gen:
-    def __init__(self, dt, partial=False):
+    def __init__(self, dt, partial=False, d=128):
+        assert d in (128, 64)
         self.dt = dt
         self.partial = partial
+        self.D = d
+        self.NDS = d // 16          # 16-deep QK MFMA steps along the head dim
+        self.NDT = d // 32          # 32-wide O^T tiles (PV MFMAs per 16-position step)
+        self.RB = 2 * d             # bytes of a K or V row
+        self.KRG = 16 * self.RB     # bytes of a K row group (16 rows, all chunks)
+        self.KB = 64 * self.RB      # bytes of the K (or V) half of a stage
+        self.SS = 2 * self.KB       # bytes of a ring stage
+        self.NLDK = d // 64         # K (and V) DMA loads per wave and block
+        self.NLD = 2 * self.NLDK
+        self.SHIFT = 8 if d == 128 else 7
         self.mn, self.cvt = names(dt)
         self.uid = 0
         self.ool = []
@@ -116,13 +126,13 @@ class Gen:
     # ---------------- fragment streams ----------------
     def qk_frags(self, par):
         out = []
-        for i in range(16):
+        for i in range(2 * self.NDS):
             ds, kt = i // 2, i % 2
             d0 = S_BASE[par] + 16 * kt
             q0 = Q_BASE + 4 * ds
             src_c = "0" if ds == 0 else vr(d0, d0 + 15)
             out.append(dict(
-                reads=lambda R, kt=kt, ds=ds: [f"ds_read_b128 {vr(R, R + 3)}, {KADDR} offset:{8192 * kt + 512 * ds}"],
+                reads=lambda R, kt=kt, ds=ds: [f"ds_read_b128 {vr(R, R + 3)}, {KADDR} offset:{2 * self.KRG * kt + 512 * ds}"],
                 mfma=lambda R, d0=d0, q0=q0, src_c=src_c:
                     f"{self.mn} {vr(d0, d0 + 15)}, {vr(R, R + 3)}, {vr(q0, q0 + 3)}, {src_c}",
                 pdep=None))
@@ -130,14 +140,14 @@ class Gen:
 
     def pv_frags(self):
         out = []
-        for k in range(16):
-            stp, dtl = k // 4, k % 4
+        for k in range(4 * self.NDT):
+            stp, dtl = k // self.NDT, k % self.NDT
             ob = O_BASE + 16 * dtl
             pb = P_BASE + 4 * stp
             va = f"v{VADDR[dtl]}"
             out.append(dict(
-                reads=lambda R, va=va, stp=stp: [f"ds_read_b64_tr_b16 {vr(R, R + 1)}, {va} offset:{4096 * stp}",
-                                                 f"ds_read_b64_tr_b16 {vr(R + 2, R + 3)}, {va} offset:{4096 * stp + 2048}"],
+                reads=lambda R, va=va, stp=stp: [f"ds_read_b64_tr_b16 {vr(R, R + 1)}, {va} offset:{16 * self.RB * stp}",
+                                                 f"ds_read_b64_tr_b16 {vr(R + 2, R + 3)}, {va} offset:{16 * self.RB * stp + 8 * self.RB}"],
                 mfma=lambda R, ob=ob, pb=pb: f"{self.mn} {vr(ob, ob + 15)}, {vr(R, R + 3)}, {vr(pb, pb + 3)}, {vr(ob, ob + 15)}",
                 pdep=stp))
         return out
@@ -204,10 +214,10 @@ class Gen:
             ops.append(dict(lines=lines, deadline=deadline, earliest=-1))
 
         def pdl(q):
-            return (pv0 + 4 * (q // 4) - 2) if q % 4 == 3 else INF
+            return (pv0 + self.NDT * (q // 4) - 2) if q % 4 == 3 else INF
         lg, lb = self.label("grow"), self.label("growb")
         body = ["s_nop 7", "s_nop 7", "s_nop 7"]
-        for k in range(64):
+        for k in range(16 * self.NDT):
             body.append(f"v_mul_f32 v{O_BASE + k}, {alpha}, v{O_BASE + k}")
         self.ool.append([f"{lg}:"] + body + [f"s_branch {lb}"])
         add(["s_cmp_lg_u64 s[70:71], 0", f"s_cbranch_scc1 {lg}", f"{lb}:"], pv0 - 1)
@@ -262,11 +272,11 @@ class Gen:
         for t in range(4):
             skip = self.label("rskip")
             out += [f"s_cmp_lg_u64 {SPLIT_MASK[t]}, 0", f"s_cbranch_scc0 {skip}"]
-            for dtl in range(4):
+            for dtl in range(self.NDT):
                 R = RING_BASE + 4 * dtl
                 va = f"v{VADDR[dtl]}"
-                out += [f"ds_read_b64_tr_b16 {vr(R, R + 1)}, {va} offset:{4096 * t}",
-                        f"ds_read_b64_tr_b16 {vr(R + 2, R + 3)}, {va} offset:{4096 * t + 2048}"]
+                out += [f"ds_read_b64_tr_b16 {vr(R, R + 1)}, {va} offset:{16 * self.RB * t}",
+                        f"ds_read_b64_tr_b16 {vr(R + 2, R + 3)}, {va} offset:{16 * self.RB * t + 8 * self.RB}"]
             for q in range(4 * t, 4 * t + 4):
                 if self.dt == "bf16":
                     out += [f"v_lshlrev_b32 {TA}, 16, {P[q]}", f"v_and_b32 {TB}, 0xffff0000, {P[q]}"]
@@ -277,10 +287,10 @@ class Gen:
                         f"{self.cvt} {P[q]}, {TA}, {TB}"]
             out.append("s_nop 2")
             pb = P_BASE + 4 * t
-            for dtl in range(4):
+            for dtl in range(self.NDT):
                 R = RING_BASE + 4 * dtl
                 ob = O_BASE + 16 * dtl
-                out.append(f"s_waitcnt lgkmcnt({2 * (3 - dtl)})")
+                out.append(f"s_waitcnt lgkmcnt({2 * (self.NDT - 1 - dtl)})")
                 out.append(f"{self.mn} {vr(ob, ob + 15)}, {vr(R, R + 3)}, {vr(pb, pb + 3)}, {vr(ob, ob + 15)}")
             # the ring slots are refilled by the next split step: its reads wait for these MFMAs
             out += ["s_nop 7", "s_nop 7", f"{skip}:"]
@@ -349,35 +359,36 @@ class Gen:
         ex0 = ["s_mov_b64 exec, s[74:75]"] if masked_exec else []
         ex1 = ["s_mov_b64 exec, s[76:77]"] if masked_exec else []
         groups = [[f"v_add_u32 {DK}, s63, {o('krow')}", f"v_min_u32 {DK}, {o('kvlast')}, {DK}",
-                   f"v_lshl_add_u32 {DK}, {DK}, 8, {o('kcol')}", f"s_add_u32 s64, s62, {o('wave2k')}"]]
-        for j in range(2):
+                   f"v_lshl_add_u32 {DK}, {DK}, {self.SHIFT}, {o('kcol')}", f"s_add_u32 s64, s62, {o('wave2k')}"]]
+        for j in range(self.NLDK):
             groups.append([f"s_add_u32 m0, s64, {1024 * j}"] + ex0 +
                           [f"global_load_lds_dwordx4 {DK}, s[{48 + 2 * j}:{49 + 2 * j}]"] + ex1)
-        for j in range(2):
+        for j in range(self.NLDK):
             groups.append([f"v_add3_u32 {DV[j]}, s63, {o('vrow')}, {4 * j}", f"v_min_u32 {DV[j]}, {o('kvlast')}, {DV[j]}",
-                           f"v_lshl_add_u32 {DV[j]}, {DV[j]}, 8, {o('vcol')}"])
-            groups.append([f"s_add_u32 m0, s64, {16384 + 1024 * j}"] + ex0 +
+                           f"v_lshl_add_u32 {DV[j]}, {DV[j]}, {self.SHIFT}, {o('vcol')}"])
+            groups.append([f"s_add_u32 m0, s64, {self.KB + 1024 * j}"] + ex0 +
                           [f"global_load_lds_dwordx4 {DV[j]}, s[56:57]"] + ex1)
         return groups
 
     def rotate(self, sreg):
-        return [f"s_add_u32 {sreg}, {sreg}, 32768", f"s_cmp_ge_u32 {sreg}, s65",
+        return [f"s_add_u32 {sreg}, {sreg}, {self.SS}", f"s_cmp_ge_u32 {sreg}, s65",
                 f"s_cselect_b32 {sreg}, {o('lds')}, {sreg}"]
 
     def addr_k(self, sreg):
         return [f"v_add_u32 {KADDR}, {sreg}, {o('klane')}"]
 
     def addr_v(self, sreg):
-        out = ["s_add_u32 s68, " + sreg + ", 16384", f"v_add_u32 v{VADDR[0]}, s68, {o('vlane')}"]
-        for d in range(1, 4):
+        out = ["s_add_u32 s68, " + sreg + f", {self.KB}", f"v_add_u32 v{VADDR[0]}, s68, {o('vlane')}"]
+        for d in range(1, self.NDT):
             out.append(f"v_xor_b32 v{VADDR[d]}, {d << 6}, v{VADDR[0]}")
         return out
 
     # ---------------- bodies ----------------
     def period(self, par, masked):
         frags = self.qk_frags(1 - par) + self.pv_frags()
-        ops = [dict(lines=g, deadline=12, earliest=-1) for g in self.dma_lines(True)]
-        ops += self.phase_b(par, pv0=16) + self.phase_a(1 - par, masked, earliest=18)
+        nqk = 2 * self.NDS
+        ops = [dict(lines=g, deadline=min(12, nqk - 2), earliest=-1) for g in self.dma_lines(True)]
+        ops += self.phase_b(par, pv0=nqk) + self.phase_a(1 - par, masked, earliest=nqk + 2)
         pre = self.addr_k("s60") + self.addr_v("s61")
         body = self.schedule(frags, ops)
         tail = ["s_nop 7", "s_nop 7"] + self.split_tail(par)
@@ -391,7 +402,7 @@ class Gen:
 
     def pre_body(self):
         frags = self.qk_frags(0)
-        ops = self.phase_a(0, True, earliest=18)
+        ops = self.phase_a(0, True, earliest=2 * self.NDS + 2)
         return self.addr_k("s61") + self.schedule(frags, ops)
 
     def vm_wait_cases(self, sreg_count, cases, tag):
@@ -403,7 +414,7 @@ class Gen:
             else:
                 nxt = self.label(tag)
                 out += [f"s_cmp_ge_u32 {sreg_count}, {k}", f"s_cbranch_scc0 {nxt}",
-                        f"s_waitcnt vmcnt({NLD * k})", f"s_branch {ends}", f"{nxt}:"]
+                        f"s_waitcnt vmcnt({self.NLD * k})", f"s_branch {ends}", f"{nxt}:"]
         out.append(f"{ends}:")
         return out
 
@@ -429,7 +440,7 @@ class Gen:
         last: PV(jl) with the period's DMA and barrier, without S(jl+1) (all masked);
         then the drain."""
         frags = self.pv_frags()
-        ops = [dict(lines=g, deadline=12, earliest=-1) for g in self.dma_lines(True)]
+        ops = [dict(lines=g, deadline=min(12, 4 * self.NDT - 2), earliest=-1) for g in self.dma_lines(True)]
         ops += self.phase_b(par, pv0=0)
         body = self.schedule(frags, ops, pre_quota=10 ** 6)
         return (self.loop_top(last_label) + self.addr_v("s61") + body + ["s_nop 7", "s_nop 7"] +
@@ -450,26 +461,26 @@ class Gen:
 
     def program(self):
         out = [f"v_mov_b32 {NINF}, 0xff800000"]
-        out += [f"v_mov_b32 v{O_BASE + k}, 0" for k in range(64)]
-        for ds in range(8):
+        out += [f"v_mov_b32 v{O_BASE + k}, 0" for k in range(16 * self.NDT)]
+        for ds in range(self.NDS):
             q0 = Q_BASE + 4 * ds
             out.append(f"global_load_dwordx4 {vr(q0, q0 + 3)}, {o('qp')}, off offset:{32 * ds}")
         out += [f"v_mov_b32 {st('m')}, {NINF}", f"v_mov_b32 {st('l')}, 0", f"v_mov_b32 {st('lim')}, {o('lim')}"]
         out += ["s_mov_b64 s[48:49], " + o("kbase"), "s_mov_b64 s[56:57], " + o("vbase"),
                 "s_add_u32 s50, s48, 64", "s_addc_u32 s51, s49, 0"]
-        out += [f"s_add_u32 s65, {o('lds')}, {NS * 32768}"]
+        out += [f"s_add_u32 s65, {o('lds')}, {NS * self.SS}"]
         out += [f"s_mov_b32 s62, {o('lds')}", "s_mov_b32 s63, 0"]
         for s in range(NS):
             skip = self.label("pd")
             out += [f"s_cmp_lt_u32 {s}, {o('nb')}", f"s_cbranch_scc0 {skip}"]
             for g in self.dma_lines(False):
                 out += g
-            out += [f"{skip}:", "s_add_u32 s62, s62, 32768", "s_add_u32 s63, s63, 64"]
+            out += [f"{skip}:", f"s_add_u32 s62, s62, {self.SS}", "s_add_u32 s63, s63, 64"]
         out += [f"s_min_u32 s64, {o('nb')}, {NS}", "s_sub_u32 s64, s64, 1"]
         out += self.vm_wait_cases("s64", list(range(NS)), "w0")
         out += ["s_barrier"]
-        out += [f"s_mov_b32 s61, {o('lds')}", f"s_add_u32 s60, {o('lds')}, 32768",
-                f"s_add_u32 s62, {o('lds')}, {(NS - 2) * 32768}", f"s_mov_b32 s63, {(NS - 2) * 64}",
+        out += [f"s_mov_b32 s61, {o('lds')}", f"s_add_u32 s60, {o('lds')}, {self.SS}",
+                f"s_add_u32 s62, {o('lds')}, {(NS - 2) * self.SS}", f"s_mov_b32 s63, {(NS - 2) * 64}",
                 "s_mov_b32 s58, 0", f"s_sub_u32 s59, {o('nb')}, 1"]
         out += self.pre_body()
         top = [self.label("top0"), self.label("top1")]
@@ -506,14 +517,14 @@ class Gen:
             # time: d = 32 dtl + 8 q4 + 4 g + 0..3), then {l, m} after the 128 values,
             # written by the lanes of half 0 (op = record + 16 g bytes).
             out += [f"v_mov_b32 v33, {st('m')}", f"s_mov_b64 exec, {o('ok')}"]
-            for dtl in range(4):
+            for dtl in range(self.NDT):
                 for q4 in range(4):
                     a = O_BASE + 16 * dtl + 4 * q4
                     out.append(f"global_store_dwordx4 {o('op')}, v[{a}:{a + 3}], off offset:{128 * dtl + 32 * q4}")
-            out += ["s_mov_b32 exec_hi, 0", f"global_store_dwordx2 {o('op')}, v[32:33], off offset:512"]
+            out += ["s_mov_b32 exec_hi, 0", f"global_store_dwordx2 {o('op')}, v[32:33], off offset:{4 * self.D}"]
         else:
             out += ["v_rcp_f32 v34, v32", "s_nop 0", f"s_mov_b64 exec, {o('ok')}"]
-            for dtl in range(4):
+            for dtl in range(self.NDT):
                 for q4 in range(4):
                     a = O_BASE + 16 * dtl + 4 * q4
                     out += [f"v_mul_f32 v{36 + k}, v34, v{a + k}" for k in range(4)]
@@ -534,11 +545,12 @@ def cstr(lines):
 
 def main(path):
     lines = ["// Generated by gen_prefill.py: prefill main loop (gfx950 asm).", "#pragma once"]
-    for dt in ("bf16", "f16"):
-        for partial in (False, True):
-            prog = Gen(dt, partial).program()
-            name = dt.upper() + ("_PART" if partial else "")
-            lines.append(f'#define TH_PREFILL_ASM_{name} "{cstr(prog)}"')
+    for d in (128, 64):
+        for dt in ("bf16", "f16"):
+            for partial in (False, True):
+                prog = Gen(dt, partial, d).program()
+                name = dt.upper() + ("_PART" if partial else "") + ("" if d == 128 else "_D64")
+                lines.append(f'#define TH_PREFILL_ASM_{name} "{cstr(prog)}"')
     clob = [f'"v{k}"' for k in range(16, 256)] + [f'"s{k}"' for k in range(48, 96)]
     lines.append("#define TH_PREFILL_ASM_CLOBBERS " + ",".join(clob))
     text = "\n".join(lines) + "\n"

@@ -230,14 +230,21 @@ __device__ __forceinline__ void prefill(const void* q, const void* k, const void
   if constexpr (DT != kF32) {
     const uintptr_t align = reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(k) |
                             reinterpret_cast<uintptr_t>(v) | reinterpret_cast<uintptr_t>(o);
-    if (head_dim == pfa::D && (align & 15) == 0) {
+    if ((head_dim == pfa::D || head_dim == 64) && (align & 15) == 0) {
       const uint32_t nqb = (seq_len + pfa::BQ - 1) / pfa::BQ;
       for (uint32_t w = blockIdx.x; w < batch * nh * nqb; w += gridDim.x) {
         uint32_t bh, qb;
         prefill_work(w, batch, nh, nkv, nqb, bh, qb);
-        pfa::prefill_tile<DT>(static_cast<const uint16_t*>(q), static_cast<const uint16_t*>(k),
-                              static_cast<const uint16_t*>(v), static_cast<uint16_t*>(o), seq_len,
-                              start_pos, max_seq, nh, nkv, scale * kLog2e, bh, qb, HM);
+        auto qq = static_cast<const uint16_t*>(q);
+        auto kk = static_cast<const uint16_t*>(k);
+        auto vv = static_cast<const uint16_t*>(v);
+        auto oo = static_cast<uint16_t*>(o);
+        if (head_dim == 64)
+          pfa::prefill_tile<DT, false, 64>(qq, kk, vv, oo, seq_len, start_pos, max_seq, nh, nkv,
+                                           scale * kLog2e, bh, qb, HM);
+        else
+          pfa::prefill_tile<DT>(qq, kk, vv, oo, seq_len, start_pos, max_seq, nh, nkv,
+                                scale * kLog2e, bh, qb, HM);
         __syncthreads();  // every wave is done with the ring before the next item's DMA
       }
       return;

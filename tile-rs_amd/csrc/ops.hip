@@ -575,6 +575,45 @@ static void copy_rows16_launch(const void* src, uint32_t src_ld, void* dst, uint
                      dst_ld / 8, cols / 8, rows, grp, src_grp);
 }
 
+}  // extern "C"
+
+// The prefill kernels for head dim HD: one pass, or (nsplit > 1) split-KV parts and
+// their merge.
+template <int HD>
+static void prefill_launch(th_dtype dtype, const uint16_t* Q, const uint16_t* K, const uint16_t* V,
+                           uint16_t* O, float* part_ws, uint32_t batch, uint32_t seq_len,
+                           uint32_t start_pos, uint32_t kv_rows, uint32_t nh, uint32_t nkv,
+                           float sl2, uint64_t blocks, uint64_t rows_q, uint32_t nsplit,
+                           uint32_t chunk, hipStream_t s) {
+  const dim3 block(th::pfa::NT);
+  if (nsplit > 1) {
+    constexpr uint32_t rpb = 256 / (HD / 4);   // rows per merge workgroup
+    const dim3 sgrid(static_cast<uint32_t>(blocks * nsplit));
+    const dim3 cgrid(static_cast<uint32_t>((rows_q + rpb - 1) / rpb));
+    if (dtype == TH_BF16) {
+      hipLaunchKernelGGL((th::pfa::attn_prefill_split<th::kBF16, HD>), sgrid, block, 0, s, Q, K, V,
+                         part_ws, batch, seq_len, start_pos, kv_rows, nh, nkv, sl2, nsplit, chunk);
+      hipLaunchKernelGGL((th::pfa::attn_prefill_combine<th::kBF16, HD>), cgrid, dim3(256), 0, s,
+                         part_ws, O, static_cast<size_t>(rows_q), nsplit);
+    } else {
+      hipLaunchKernelGGL((th::pfa::attn_prefill_split<th::kF16, HD>), sgrid, block, 0, s, Q, K, V,
+                         part_ws, batch, seq_len, start_pos, kv_rows, nh, nkv, sl2, nsplit, chunk);
+      hipLaunchKernelGGL((th::pfa::attn_prefill_combine<th::kF16, HD>), cgrid, dim3(256), 0, s,
+                         part_ws, O, static_cast<size_t>(rows_q), nsplit);
+    }
+    return;
+  }
+  const dim3 grid(static_cast<uint32_t>(blocks));
+  if (dtype == TH_BF16)
+    hipLaunchKernelGGL((th::pfa::attn_prefill_asm<th::kBF16, HD>), grid, block, 0, s, Q, K, V, O,
+                       batch, seq_len, start_pos, kv_rows, nh, nkv, sl2);
+  else
+    hipLaunchKernelGGL((th::pfa::attn_prefill_asm<th::kF16, HD>), grid, block, 0, s, Q, K, V, O,
+                       batch, seq_len, start_pos, kv_rows, nh, nkv, sl2);
+}
+
+extern "C" {
+
 int th_attention_prefill(const void* q, const void* k, const void* v, void* o, uint32_t batch,
                          uint32_t seq_len, uint32_t start_pos, uint32_t max_seq,
                          uint32_t head_dim, uint32_t num_heads, uint32_t num_kv_heads,
@@ -589,18 +628,19 @@ int th_attention_prefill(const void* q, const void* k, const void* v, void* o, u
   if (head_dim == 0) return fail(TH_KERNEL_ERROR, "attention_prefill: head_dim == 0");
   const float scale = 1.0f / std::sqrt(static_cast<float>(head_dim));  // rsqrt(float(head_dim))
   const bool vec16 = aligned16(q) && aligned16(k) && aligned16(v) && aligned16(o);
-  const bool fast = dtype != TH_F32 && head_dim == th::pfa::D && vec16;
+  // head_dim 128 and 64 run natively
+  const bool fast = dtype != TH_F32 && (head_dim == th::pfa::D || head_dim == 64) && vec16;
   // Head dims below 128 (multiples of 8) run the same kernel on copies zero-padded
   // to 128 columns: the zero columns add nothing to Q.K^T and give zero O columns,
   // so the result is that of the narrower head (with its own 1/sqrt(D) scale).
   // Half the MFMA work is padding, against a general kernel ~500x slower
   // (measured for D = 64, S = 2048-4096).
-  const bool pad = dtype != TH_F32 && head_dim < th::pfa::D && head_dim % 8 == 0 && vec16;
+  const bool pad = !fast && dtype != TH_F32 && head_dim < th::pfa::D && head_dim % 8 == 0 && vec16;
+  const uint32_t hd = fast ? head_dim : th::pfa::D;   // the kernel's head dim
   if (fast || pad) {
     const uint64_t nqb = (seq_len + th::pfa::BQ - 1) / th::pfa::BQ;
     const uint64_t blocks = nqb * batch * num_heads;
     if (blocks > 0x7fffffffu) return fail(TH_KERNEL_ERROR, "attention_prefill: grid too large");
-    const dim3 grid(static_cast<uint32_t>(blocks)), block(th::pfa::NT);
     const float sl2 = scale * th::kLog2e;
     auto Q = static_cast<const uint16_t*>(q);
     auto K = static_cast<const uint16_t*>(k);
@@ -626,7 +666,7 @@ int th_attention_prefill(const void* q, const void* k, const void* v, void* o, u
       }
     }
     const uint64_t split_bytes =
-        nsplit > 1 ? static_cast<uint64_t>(nsplit) * rows_q * th::pfa::kPartRec * 4 : 0;
+        nsplit > 1 ? static_cast<uint64_t>(nsplit) * rows_q * th::pfa::part_rec(hd) * 4 : 0;
     float* part_ws = nullptr;
     if (split_bytes && !pad) {
       void* ws = nullptr;
@@ -660,29 +700,13 @@ int th_attention_prefill(const void* q, const void* k, const void* v, void* o, u
       O = Op;
       kv_rows = kv_len;
     }
-    if (nsplit > 1) {
-      const dim3 sgrid(static_cast<uint32_t>(blocks * nsplit));
-      const dim3 cgrid(static_cast<uint32_t>((rows_q + 7) / 8));
-      if (dtype == TH_BF16) {
-        hipLaunchKernelGGL(th::pfa::attn_prefill_split<th::kBF16>, sgrid, block, 0, as_stream(s), Q,
-                           K, V, part_ws, batch, seq_len, start_pos, kv_rows, num_heads,
-                           num_kv_heads, sl2, nsplit, chunk);
-        hipLaunchKernelGGL(th::pfa::attn_prefill_combine<th::kBF16>, cgrid, dim3(256), 0,
-                           as_stream(s), part_ws, O, static_cast<size_t>(rows_q), nsplit);
-      } else {
-        hipLaunchKernelGGL(th::pfa::attn_prefill_split<th::kF16>, sgrid, block, 0, as_stream(s), Q,
-                           K, V, part_ws, batch, seq_len, start_pos, kv_rows, num_heads,
-                           num_kv_heads, sl2, nsplit, chunk);
-        hipLaunchKernelGGL(th::pfa::attn_prefill_combine<th::kF16>, cgrid, dim3(256), 0,
-                           as_stream(s), part_ws, O, static_cast<size_t>(rows_q), nsplit);
-      }
-    } else if (dtype == TH_BF16) {
-      hipLaunchKernelGGL(th::pfa::attn_prefill_asm<th::kBF16>, grid, block, 0, as_stream(s), Q, K, V,
-                         O, batch, seq_len, start_pos, kv_rows, num_heads, num_kv_heads, sl2);
-    } else {
-      hipLaunchKernelGGL(th::pfa::attn_prefill_asm<th::kF16>, grid, block, 0, as_stream(s), Q, K, V,
-                         O, batch, seq_len, start_pos, kv_rows, num_heads, num_kv_heads, sl2);
-    }
+    if (hd == 64)
+      prefill_launch<64>(dtype, Q, K, V, O, part_ws, batch, seq_len, start_pos, kv_rows, num_heads,
+                         num_kv_heads, sl2, blocks, rows_q, nsplit, chunk, as_stream(s));
+    else
+      prefill_launch<th::pfa::D>(dtype, Q, K, V, O, part_ws, batch, seq_len, start_pos, kv_rows,
+                                 num_heads, num_kv_heads, sl2, blocks, rows_q, nsplit, chunk,
+                                 as_stream(s));
     TH_TRY(launch_status("attention_prefill launch"));
     if (pad) {
       copy_rows16_launch(O, th::pfa::D, o, head_dim, head_dim, rows_q, as_stream(s));
