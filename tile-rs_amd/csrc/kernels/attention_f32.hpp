@@ -38,8 +38,10 @@ constexpr int NT = 256;
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 
+// 16-byte aligned: V tiles go in, and the per-wave factors come out, as 16-byte LDS
+// accesses
 template <int D>
-struct Lds {
+struct alignas(16) Lds {
   float k[2][BKV * (D + 2)];
   float v[2][BKV * (D + 8)];
   float stat[NT / 64][32];   // per-wave query factors (rescale, then 1 / sum)

@@ -29,7 +29,8 @@ constexpr int NT = 256;
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-struct Lds {
+// 16-byte aligned: row-major B tiles go in with 16-byte LDS writes
+struct alignas(16) Lds {
   float a[2][BK * LD];
   float b[2][BK * LD];
 };
