@@ -378,8 +378,10 @@ __device__ __forceinline__ void decode_group(const uint16_t* q, const uint16_t* 
     const uint32_t bk = w / n_split, split = w % n_split;
     const uint32_t c0 = split * cps, c1 = min(nchunks, c0 + cps);
     // unsplit: the workgroup covers the whole sequence and writes O itself
-    decode_tile<DT, G, 4, 8, HD>(q, k, v, o, n_split > 1 ? decode_partials : nullptr, seq_len,
-                                 max_seq, nh, nkv, n_split, scale_log2, bk, split, c0, c1);
+    // one LDS arena for every (G, HD) this kernel may run: the largest, not the sum
+    decode_tile<DT, G, 4, 8, HD, 8, dec::D>(q, k, v, o, n_split > 1 ? decode_partials : nullptr,
+                                            seq_len, max_seq, nh, nkv, n_split, scale_log2, bk,
+                                            split, c0, c1);
     if (n_split == 1) continue;
     // decode_tile ends on a barrier: every wave's partial stores are issued.  The
     // release fence makes them visible device-wide before the arrival counts.
