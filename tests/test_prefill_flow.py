@@ -256,3 +256,80 @@ def test_split_part_program_differs_only_in_the_epilogue(dt, head_dim):
     assert not any(l.startswith("v_rcp_f32") for l in part)
     stores = [l for l in part if l.startswith("global_store")]
     assert len(stores) == head_dim // 8 + 1 and stores[-1].endswith(f"offset:{4 * head_dim}")
+
+
+# ---------------------------------------------------------------------------
+# Static checks of the program text: the asm statement gets no checking from the
+# compiler beyond assembling each line, so a branch to a label outside the
+# program, a register the statement does not own, or an accumulation register
+# (AGPR: the unified register file then has to hold 256 VGPRs plus the AGPRs,
+# more than a 512-thread workgroup may use) would only show on the GPU.
+# ---------------------------------------------------------------------------
+BRANCHES = ("s_branch", "s_cbranch_scc0", "s_cbranch_scc1", "s_cbranch_vccz", "s_cbranch_vccnz",
+            "s_cbranch_execz", "s_cbranch_execnz")
+CLOBBER_V = set(range(16, 256))
+CLOBBER_S = set(range(48, 96))
+
+
+def sregs(text):
+    out = set()
+    for a, b in re.findall(r"\bs\[(\d+):(\d+)\]", text):
+        out |= set(range(int(a), int(b) + 1))
+    out |= {int(a) for a in re.findall(r"\bs(\d+)\b", text)}
+    return out
+
+
+def static_problems(prog):
+    lines = [l.strip() for l in prog]
+    defs = [l[:-1] for l in lines if l.endswith(":")]
+    bad = [f"label defined twice: {d}" for d in set(defs) if defs.count(d) > 1]
+    labels = set(defs)
+    for ln in lines:
+        op = ln.split()[0] if ln else ""
+        if op.startswith("s_branch") or op.startswith("s_cbranch") or op.startswith("s_setpc") \
+                or op.startswith("s_swappc"):
+            if op not in BRANCHES:
+                bad.append("unexpected control transfer: " + ln)
+            elif ln.split()[1] not in labels:
+                bad.append("branch outside the program: " + ln)
+        if ln.endswith(":") or not op:
+            continue
+        body = ln.split(None, 1)[1] if " " in ln else ""
+        if re.search(r"\ba\[\d+:\d+\]|\ba\d+\b|accvgpr", ln):
+            bad.append("AGPR operand: " + ln)
+        if vregs(body) - CLOBBER_V:
+            bad.append("VGPR outside the clobber list: " + ln)
+        if sregs(body) - CLOBBER_S:
+            bad.append("SGPR outside the clobber list: " + ln)
+        for a, b in re.findall(r"\bv\[(\d+):(\d+)\]", body):
+            if int(a) % 2:
+                bad.append("odd-aligned VGPR tuple: " + ln)
+    return bad
+
+
+def test_static_check_finds_planted_cases():
+    assert static_problems(["s_branch L9_0"])
+    assert static_problems(["L1:", "L1:"])
+    assert static_problems(["v_accvgpr_write_b32 a3, v40"])
+    assert static_problems(["v_mfma_f32_32x32x16_bf16 a[0:15], v[40:43], v[44:47], a[0:15]"])
+    assert static_problems(["v_mov_b32 v3, v40"])
+    assert static_problems(["s_mov_b32 s20, s48"])
+    assert static_problems(["ds_read_b64 v[41:42], v40"])
+    assert static_problems(["s_setpc_b64 s[48:49]"])
+    assert not static_problems(["L1:", "s_cbranch_scc1 L1", "v_mov_b32 v40, %3"])
+
+
+@pytest.mark.parametrize("head_dim", [128, 64])
+@pytest.mark.parametrize("partial", [False, True])
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+def test_program_text_is_self_contained(dt, partial, head_dim):
+    prog = G.Gen(dt, partial, head_dim).program()
+    assert static_problems(prog) == []
+    # m0 is saved on entry and restored as the last instruction (single exit)
+    assert prog[0] == "s_mov_b32 s52, m0" and prog[-1] == "s_mov_b32 m0, s52"
+    assert not any("s52" in l for l in prog[1:-1])
+
+
+def test_clobber_list_matches_the_checked_sets():
+    text = Path(G.__file__).read_text()
+    assert 'for k in range(16, 256)' in text and 'for k in range(48, 96)' in text

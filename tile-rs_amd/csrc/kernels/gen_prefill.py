@@ -460,7 +460,9 @@ class Gen:
         return out
 
     def program(self):
-        out = [f"v_mov_b32 {NINF}, 0xff800000"]
+        # m0 (the LDS address of the DMA loads) belongs to the compiler: it is saved
+        # here and restored at the single exit, so the asm statement preserves it
+        out = ["s_mov_b32 s52, m0", f"v_mov_b32 {NINF}, 0xff800000"]
         out += [f"v_mov_b32 v{O_BASE + k}, 0" for k in range(16 * self.NDT)]
         for ds in range(self.NDS):
             q0 = Q_BASE + 4 * ds
@@ -535,7 +537,7 @@ class Gen:
         out += [f"s_branch {end}"]
         for blk in self.ool:
             out += blk
-        out += [f"{end}:", "s_waitcnt vmcnt(0)"]
+        out += [f"{end}:", "s_waitcnt vmcnt(0)", "s_mov_b32 m0, s52"]
         return out
 
 

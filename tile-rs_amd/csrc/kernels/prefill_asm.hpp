@@ -114,7 +114,7 @@ __device__ __forceinline__ void prefill_tile(const uint16_t* __restrict__ Q,
                  "v"(vrow), "v"(vcol), "s"(kbase), "s"(vbase), "s"(kvlast), "s"(nb),       \
                  "s"(jd), "s"(lds_base), "s"(wave2k), "s"(scale_log2), "s"(lratio), "s"(ok), \
                  "s"(jl)                                                                   \
-               : TH_PREFILL_ASM_CLOBBERS, "vcc", "scc", "m0", "memory")
+               : TH_PREFILL_ASM_CLOBBERS, "vcc", "scc", "memory")
   if constexpr (HD == 64) {
     if constexpr (PART) {
       if constexpr (DT == kBF16) TH_PREFILL_OPS(TH_PREFILL_ASM_BF16_PART_D64); else TH_PREFILL_OPS(TH_PREFILL_ASM_F16_PART_D64);

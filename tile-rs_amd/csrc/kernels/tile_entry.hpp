@@ -20,6 +20,14 @@
 #include "prefill_asm.hpp"
 #include "softmax.hpp"
 
+#ifndef TH_BUILD_STAMP
+#define TH_BUILD_STAMP "unstamped"
+#endif
+// Every emitted code object carries the hash of the sources it was compiled
+// from (passed by the build), so a test can check that the code object it loads
+// was built from the tree it runs in.
+extern "C" __device__ __attribute__((used)) const char __th_build_stamp[] = "th-src:" TH_BUILD_STAMP;
+
 namespace th {
 namespace entry {
 

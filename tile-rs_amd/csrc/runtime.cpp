@@ -137,7 +137,12 @@ extern "C" {
 
 const char* th_last_error(void) { return th::g_last_error.c_str(); }
 
-const char* th_version(void) { return "tilers_hip 0.1.0 (gfx950)"; }
+#ifndef TH_BUILD_STAMP
+#define TH_BUILD_STAMP "unstamped"
+#endif
+// The stamp is a hash of the sources this library was built from (written by the
+// build); tests and smoke() compare it with the tree they run in.
+const char* th_version(void) { return "tilers_hip 0.1.0 (gfx950) th-src:" TH_BUILD_STAMP; }
 
 int th_backend_is_hip(const char* codegen_path) {
   return codegen_path != nullptr && std::strcmp(codegen_path, "hip") == 0;

@@ -97,6 +97,10 @@ struct th_registry_s {
   std::vector<Entry> targets;
 };
 
+#ifndef TH_BUILD_STAMP
+#define TH_BUILD_STAMP "unstamped"
+#endif
+
 extern "C" {
 
 const char* th_target_name(void) { return "hip"; }
@@ -215,6 +219,8 @@ int th_compile(const char* src, size_t len, const char* out_path, const char* in
                                      "-Xclang",
                                      "-packed-fp32-ops",
                                      "-Wno-unused-command-line-argument",
+                                     // the stamp of the sources this library was built from
+                                     "-DTH_BUILD_STAMP=\"" TH_BUILD_STAMP "\"",
                                      "-I",
                                      inc,
                                      src_path,
