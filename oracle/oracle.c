@@ -330,6 +330,22 @@ ORC_EXPORT void orc_causal_mask_f32(const float* x, float* y, int64_t rows, int6
 enum { ORC_EXP = 0, ORC_LOG, ORC_TANH, ORC_ABS, ORC_SQRT, ORC_RSQRT, ORC_SIGMOID, ORC_RELU,
        ORC_NEG };
 
+/* arith.maximumf / arith.minimumf (the float body of linalg.max / linalg.min and of */
+/* the relu, clamp and max-reduce generics): IEEE 754-2019 maximum / minimum.  A NaN */
+/* operand gives NaN; -0 orders below +0; otherwise the larger (smaller) value.      */
+static float maximumf(float a, float b) {
+    if (a != a) return a;
+    if (b != b) return b;
+    if (a == b) return signbit(a) ? b : a; /* equal values, or +0 against -0 */
+    return a > b ? a : b;
+}
+static float minimumf(float a, float b) {
+    if (a != a) return a;
+    if (b != b) return b;
+    if (a == b) return signbit(a) ? a : b;
+    return a < b ? a : b;
+}
+
 static double unary1(int op, double x) {
     switch (op) {
         case ORC_EXP: return exp(x);
@@ -339,7 +355,7 @@ static double unary1(int op, double x) {
         case ORC_SQRT: return sqrt(x);
         case ORC_RSQRT: return 1.0 / sqrt(x);
         case ORC_SIGMOID: return 1.0 / (exp(-x) + 1.0);
-        case ORC_RELU: return x > 0.0 ? x : 0.0;
+        case ORC_RELU: return (double)maximumf((float)x, 0.0f); /* maximumf(%in, 0.0) */
         default: return -x;
     }
 }
@@ -348,15 +364,21 @@ ORC_EXPORT void orc_unary_f32(int op, const float* x, float* y, int64_t n) {
     for (int64_t i = 0; i < n; ++i) y[i] = (float)unary1(op, (double)x[i]);
 }
 
-/* op 0 = min, 1 = max (exact in f32) */
+/* op 0 = min (linalg.min -> minimumf), 1 = max (linalg.max -> maximumf); exact in f32 */
 ORC_EXPORT void orc_minmax_f32(int op, const float* a, const float* b, float* y, int64_t n) {
-    for (int64_t i = 0; i < n; ++i) y[i] = op ? (a[i] > b[i] ? a[i] : b[i]) : (a[i] < b[i] ? a[i] : b[i]);
+    for (int64_t i = 0; i < n; ++i) y[i] = op ? maximumf(a[i], b[i]) : minimumf(a[i], b[i]);
+}
+
+/* clamp (mlir_to_linalg.rs:906-955): minimumf(maximumf(x, lo), hi) */
+ORC_EXPORT void orc_clamp_f32(const float* x, float* y, int64_t n, float lo, float hi) {
+    for (int64_t i = 0; i < n; ++i) y[i] = minimumf(maximumf(x[i], lo), hi);
 }
 
 /* ------------------------------------------------------------------------ */
 /* Row reductions, dimension 1 of a rows x cols f32 tensor (mlir_to_linalg.rs:*/
-/* 1496-1573): op 0 sum (init 0), 1 max (init -inf), 2 absmax = max of |x|   */
-/* (linalg.abs then the max reduce).  The sum is carried in double and       */
+/* 1496-1573): op 0 sum (init 0), 1 max (init -inf, combiner maximumf, so a  */
+/* NaN in the row gives NaN), 2 absmax = the max reduce of linalg.abs(x).    */
+/* The sum is carried in double and                                          */
 /* rounded once.  op 3 argmax (:1576-1660): running (value, index) from      */
 /* (-inf, 0), replaced when x > value (ordered compare), so the result is    */
 /* the first index of the maximum and 0 for a row with no value above -inf.   */
@@ -377,10 +399,7 @@ ORC_EXPORT void orc_reduce_rows_f32(int op, const float* x, void* y, int64_t row
             ((int32_t*)y)[r] = idx;
         } else {
             float m = bits_f32(0xff800000u);
-            for (int64_t c = 0; c < cols; ++c) {
-                const float v = op == 2 ? fabsf(xr[c]) : xr[c];
-                if (v > m) m = v;
-            }
+            for (int64_t c = 0; c < cols; ++c) m = maximumf(m, op == 2 ? fabsf(xr[c]) : xr[c]);
             ((float*)y)[r] = m;
         }
     }
@@ -460,11 +479,33 @@ ORC_EXPORT void orc_attention_prefill(const void* q, const void* k, const void* 
     const int64_t group = nh / nkv;
     const float scale = 1.0f / sqrtf((float)D);
     const int64_t total = nbh * nq;
+    const int64_t L = start_pos + seq_len; /* positions any selected row can see */
+    if (total <= 0 || L <= 0) return;
+    /* The (b, kv_head) units the selected heads read, widened once: K transposed to   */
+    /* [D][L] so that PB consecutive positions' dot products advance together (each    */
+    /* one still a sequential fmaf chain over t = 0..D-1, the same operations in the   */
+    /* same order as one dot at a time), V as [L][D].                                  */
+    const int64_t u0 = (bh0 / nh) * nkv + (bh0 % nh) / group;
+    const int64_t bl = bh0 + nbh - 1;
+    const int64_t u1 = (bl / nh) * nkv + (bl % nh) / group + 1;
+    const int64_t nu = u1 - u0;
+    float* kt = (float*)malloc(sizeof(float) * (size_t)(nu * D * L));
+    float* vf = (float*)malloc(sizeof(float) * (size_t)(nu * L * D));
+    #pragma omp parallel for schedule(static) collapse(2)
+    for (int64_t u = 0; u < nu; ++u)
+        for (int64_t pos = 0; pos < L; ++pos) {
+            const int64_t src = ((u0 + u) * max_seq + pos) * D;
+            for (int64_t t = 0; t < D; ++t) {
+                kt[(u * D + t) * L + pos] = load_elem(k, src + t, dtype);
+                vf[(u * L + pos) * D + t] = load_elem(v, src + t, dtype);
+            }
+        }
+    enum { PB = 16 };
     #pragma omp parallel
     {
         float* qv = (float*)malloc(sizeof(float) * (size_t)D);
-        float* sc = (float*)malloc(sizeof(float) * (size_t)(start_pos + seq_len));
-        float* p = (float*)malloc(sizeof(float) * (size_t)(start_pos + seq_len));
+        float* sc = (float*)malloc(sizeof(float) * (size_t)(L + PB));
+        float* p = (float*)malloc(sizeof(float) * (size_t)L);
         float* acc = (float*)malloc(sizeof(float) * (size_t)D);
         #pragma omp for schedule(dynamic, 4)
         for (int64_t w = 0; w < total; ++w) {
@@ -474,21 +515,35 @@ ORC_EXPORT void orc_attention_prefill(const void* q, const void* k, const void* 
             const int64_t kvh = h / group;
             const int64_t abs_pos = start_pos + qi;
             const int64_t q_off = ((b * seq_len + qi) * nh + h) * D;
-            const int64_t kv_base = (b * nkv + kvh) * max_seq * D;
+            const int64_t u = b * nkv + kvh - u0;
+            const float* ku = kt + u * D * L;
+            const float* vu = vf + u * L * D;
             const int64_t n = abs_pos + 1; /* positions 0..abs_pos are unmasked */
             for (int64_t t = 0; t < D; ++t) qv[t] = load_elem(q, q_off + t, dtype);
-            for (int64_t pos = 0; pos < n; ++pos) {
+            int64_t pos = 0;
+            for (; pos + PB <= n; pos += PB) {
+                float dot[PB];
+                for (int j = 0; j < PB; ++j) dot[j] = 0.0f;
+                for (int64_t t = 0; t < D; ++t) {
+                    const float qt = qv[t];
+                    const float* kr = ku + t * L + pos;
+                    #pragma omp simd
+                    for (int j = 0; j < PB; ++j) dot[j] = fmaf(qt, kr[j], dot[j]);
+                }
+                for (int j = 0; j < PB; ++j) sc[pos + j] = dot[j] * scale;
+            }
+            for (; pos < n; ++pos) {
                 float dot = 0.0f;
-                for (int64_t t = 0; t < D; ++t)
-                    dot = fmaf(qv[t], load_elem(k, kv_base + pos * D + t, dtype), dot);
+                for (int64_t t = 0; t < D; ++t) dot = fmaf(qv[t], ku[t * L + pos], dot);
                 sc[pos] = dot * scale;
             }
             softmax_row(sc, p, n);
             for (int64_t t = 0; t < D; ++t) acc[t] = 0.0f;
-            for (int64_t pos = 0; pos < n; ++pos) {
-                const float pp = p[pos];
-                for (int64_t t = 0; t < D; ++t)
-                    acc[t] = fmaf(pp, load_elem(v, kv_base + pos * D + t, dtype), acc[t]);
+            for (int64_t ps = 0; ps < n; ++ps) {
+                const float pp = p[ps];
+                const float* vr = vu + ps * D;
+                #pragma omp simd
+                for (int64_t t = 0; t < D; ++t) acc[t] = fmaf(pp, vr[t], acc[t]);
             }
             for (int64_t t = 0; t < D; ++t) store_elem(o, q_off + t, out_dtype, acc[t]);
         }
@@ -497,6 +552,8 @@ ORC_EXPORT void orc_attention_prefill(const void* q, const void* k, const void* 
         free(p);
         free(acc);
     }
+    free(kt);
+    free(vf);
 }
 
 /* ------------------------------------------------------------------------ */

@@ -50,6 +50,7 @@ def lib():
         L.orc_causal_mask_f32.argtypes = [vp, vp, i64, i64]
         L.orc_unary_f32.argtypes = [i, vp, vp, i64]
         L.orc_minmax_f32.argtypes = [i, vp, vp, vp, i64]
+        L.orc_clamp_f32.argtypes = [vp, vp, i64, C.c_float, C.c_float]
         L.orc_reduce_rows_f32.argtypes = [i, vp, vp, i64, i64]
         L.orc_transpose_f32.argtypes = [vp, vp, i64, i64]
         L.orc_matvec_f32.argtypes = [vp, vp, vp, i64, i64]
@@ -185,6 +186,13 @@ def minmax_f32(op: str, a: np.ndarray, b: np.ndarray) -> np.ndarray:
     b = np.ascontiguousarray(b, np.float32)
     y = np.empty_like(a)
     lib().orc_minmax_f32(1 if op == "max" else 0, _ptr(a), _ptr(b), _ptr(y), a.size)
+    return y
+
+
+def clamp_f32(x: np.ndarray, lo: float, hi: float) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.empty_like(x)
+    lib().orc_clamp_f32(_ptr(x), _ptr(y), x.size, lo, hi)
     return y
 
 

@@ -29,6 +29,8 @@ def _check_stamps():
     assert _build.code_object_stamp(_build.library_path()) == want
     for stem in EXAMPLES:
         assert _build.code_object_stamp(_build.example_path(stem)) == want, stem
+    for stem in _build.REF_HOT_PATH:
+        assert _build.code_object_stamp(_build.ref_fixture_path(stem)) == want, stem
 
 
 def test_built_artefacts_carry_the_tree_stamp():

@@ -166,7 +166,7 @@ def test_elementwise_fallback():
     assert "/ (1.0f + expf(-" in out.source            # silu
     assert "(col <= row ?" in out.source                 # causal mask: keep col <= row
     assert "0x1p-3f" in out.source                       # scale 0.125, exact
-    assert "fminf(fmaxf(" in out.source                  # clamp
+    assert "th::minimumf(th::maximumf(" in out.source    # clamp: NaN-propagating min/max
 
 
 def test_long_rows_lower_to_one_workgroup_per_row():
@@ -375,7 +375,7 @@ def test_attention_gqa_lowers_to_the_head_major_prefill():
 def test_new_ops_lower_to_their_entries():
     out = th.emit((EXAMPLES / "ops_extra.mlir").read_text())
     src = out.source
-    for evidence in ("logf(", "tanhf(", "fabsf(", "(1.0f / sqrtf(", "(1.0f / (expf(-", "fminf(",
+    for evidence in ("logf(", "tanhf(", "fabsf(", "(1.0f / sqrtf(", "(1.0f / (expf(-", "th::minimumf(", "th::maximumf(",
                      "th::entry::reduce_rows<th::entry::kRowSum>", "kRowMax>", "kRowAbsMax>",
                      "kRowArgMax>", "th::entry::transpose(", "th::entry::matvec("):
         assert evidence in src, evidence
@@ -419,6 +419,38 @@ LOOP_BODY = (
     "    %t = llvm.call @__tile_load_f32(%src, %one, %cols) : (!llvm.ptr<1>, i32, i32) -> i32\n"
     "    %y = llvm.call @__tile_softmax_f32(%t, %t, %one, %cols) : (i32, i32, i32, i32) -> i32\n"
     "    llvm.call @__tile_store_f32(%dst, %y, %one, %cols) : (!llvm.ptr<1>, i32, i32, i32) -> ()\n")
+
+
+def _shift_body(load_off: str, store_off: str) -> str:
+    """A loop body that loads arg0 at `load_off` and stores arg0 at `store_off` (both i64
+    SSA names defined in the body): a read and a write of the same buffer."""
+    return ("    %iw = llvm.zext %i : i32 to i64\n"
+            "    %off = llvm.mul %iw, %cols64 : i64\n"
+            "    %one64 = llvm.mlir.constant(1 : i64) : i64\n"
+            "    %ip = llvm.add %iw, %one64 : i64\n"
+            "    %offp = llvm.mul %ip, %cols64 : i64\n"
+            f"    %src = llvm.getelementptr %arg0[{load_off}] : (!llvm.ptr<1>, i64) -> !llvm.ptr<1>, f32\n"
+            f"    %dst = llvm.getelementptr %arg0[{store_off}] : (!llvm.ptr<1>, i64) -> !llvm.ptr<1>, f32\n"
+            "    %t = llvm.call @__tile_load_f32(%src, %one, %cols) : (!llvm.ptr<1>, i32, i32) -> i32\n"
+            "    %y = llvm.call @__tile_softmax_f32(%t, %t, %one, %cols) : (i32, i32, i32, i32) -> i32\n"
+            "    llvm.call @__tile_store_f32(%dst, %y, %one, %cols) : (!llvm.ptr<1>, i32, i32, i32) -> ()\n")
+
+
+@pytest.mark.parametrize("load_off,store_off", [("%offp", "%off"), ("%off", "%offp")])
+def test_loop_carried_dependence_is_rejected(load_off, store_off):
+    """tile.rs:2187-2210 runs the loop body in order; the hip target runs iterations in
+    parallel.  A loop that stores buffer p one tile behind (or ahead of) where it loads
+    p has a loop-carried dependence, so parallel iterations would race: rejected."""
+    with pytest.raises(th.HalError) as e:
+        th.emit(loop_module(_shift_body(load_off, store_off)))
+    assert "loop-carried dependence" in str(e.value)
+
+
+def test_loop_in_place_update_is_lowered():
+    """Loading and storing the same tile of one buffer (an in-place update) has no
+    dependence between iterations."""
+    src = th.emit(loop_module(_shift_body("%off", "%off"))).source
+    assert "th::entry::softmax_rows<th::kF32, 4>(" in src
 
 
 def test_loop_example_lowers_to_a_tile_grid():

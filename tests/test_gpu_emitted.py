@@ -341,6 +341,50 @@ def test_elementwise_min_and_four_operand_mul(dev, stream, launcher):
     assert np.allclose(ob.copy_to_host(stream), orc.silu_mul(g, u), rtol=2e-6, atol=1e-7)
 
 
+def test_nan_and_signed_zero_follow_maximumf_minimumf(dev, stream, launcher):
+    """relu, max, min, clamp and the max / absmax row reductions lower as MLIR's
+    arith.maximumf / arith.minimumf (mlir_to_linalg.rs:429, :788, :951-955, :1543): a
+    NaN operand gives NaN and -0 orders below +0.  fmaxf / fminf would drop the NaN."""
+    tiles, n = 2, 1024
+    rng = np.random.default_rng(35)
+    a, b = (rng.standard_normal(tiles * n).astype(np.float32) for _ in range(2))
+    idx = np.arange(a.size)
+    nan_a, nan_b = idx % 17 == 0, idx % 23 == 5
+    z1 = (idx % 29 == 3) & ~nan_a & ~nan_b      # (-0, +0) pairs
+    z2 = (idx % 31 == 4) & ~nan_a & ~nan_b & ~z1  # (+0, -0) pairs
+    a[nan_a], b[nan_b] = np.nan, np.nan
+    a[z1], b[z1] = -0.0, 0.0
+    a[z2], b[z2] = 0.0, -0.0
+    ab, bb, yb = up(dev, stream, a, D.F32), up(dev, stream, b, D.F32), dev.alloc(a.size, D.F32)
+
+    def same_bits(got, ref, name):
+        """NaN where the oracle has NaN; every other value bit-identical (signed zeros too)."""
+        nan = np.isnan(ref)
+        assert np.array_equal(np.isnan(got), nan), f"{name}: NaN positions differ"
+        assert np.array_equal(got[~nan].view(np.uint32), ref[~nan].view(np.uint32)), name
+
+    for op in ("min", "max"):
+        launcher.launch(f"ew_{op}", th.LaunchGrid.blocks_only(tiles), [ptr(ab), ptr(bb), ptr(yb)], stream)
+        same_bits(yb.copy_to_host(stream), orc.minmax_f32(op, a, b), op)
+    launcher.launch("ew_relu", th.LaunchGrid.blocks_only(tiles), [ptr(ab), ptr(yb)], stream)
+    got = yb.copy_to_host(stream)
+    same_bits(got, orc.unary_f32("relu", a), "relu")
+    assert np.isnan(got[nan_a]).all() and not np.signbit(got[z1]).any()
+    launcher.launch("ew_clamp", th.LaunchGrid.blocks_only(tiles), [ptr(ab), ptr(yb)], stream)
+    same_bits(yb.copy_to_host(stream), orc.clamp_f32(a, -0.5, 0.75), "clamp")
+    R, C = 8, 1000
+    x = rng.standard_normal(5 * R * C).astype(np.float32)
+    x.reshape(-1, C)[2, 600] = np.nan
+    x.reshape(-1, C)[11, 3] = np.nan
+    xb, rb = up(dev, stream, x, D.F32), dev.alloc(5 * R, D.F32)
+    for op in ("reduce_max", "absmax"):
+        launcher.launch(f"row_{op}", th.LaunchGrid.blocks_only(5), [ptr(xb), ptr(rb)], stream)
+        got = rb.copy_to_host(stream)
+        ref = orc.reduce_rows_f32(op.replace("reduce_", ""), x, 5 * R, C)
+        assert np.isnan(got[[2, 11]]).all() and np.isnan(ref[[2, 11]]).all(), op
+        same_bits(got, ref, op)
+
+
 @pytest.mark.parametrize("op", ["reduce_sum", "reduce_max", "absmax", "argmax"])
 def test_row_reductions(dev, stream, launcher, op):
     tiles, R, C = 5, 8, 1000

@@ -428,6 +428,37 @@ def test_minmax_exact():
     assert np.array_equal(orc.minmax_f32("max", a, b), np.maximum(a, b))
 
 
+def test_maximumf_minimumf_nan_and_signed_zero():
+    """relu, min, max, clamp and the max reductions follow arith.maximumf / minimumf
+    (IEEE 754-2019 maximum / minimum): NaN propagates, -0 < +0.  numpy's maximum and
+    minimum propagate NaN too; the signed-zero rule is checked bit by bit."""
+    rng = np.random.default_rng(25)
+    a, b = (rng.standard_normal(1000).astype(np.float32) for _ in range(2))
+    a[::13] = np.nan
+    b[6::19] = np.nan
+    got_max, got_min = orc.minmax_f32("max", a, b), orc.minmax_f32("min", a, b)
+    assert np.array_equal(np.isnan(got_max), np.isnan(np.maximum(a, b)))
+    assert np.array_equal(np.isnan(got_min), np.isnan(np.minimum(a, b)))
+    ok = ~np.isnan(got_max)
+    assert np.array_equal(got_max[ok], np.maximum(a, b)[ok])
+    assert np.array_equal(got_min[ok], np.minimum(a, b)[ok])
+    z = np.float32([-0.0, 0.0, -0.0, 0.0])
+    w = np.float32([0.0, -0.0, -0.0, 0.0])
+    assert np.signbit(orc.minmax_f32("max", z, w)).tolist() == [False, False, True, False]
+    assert np.signbit(orc.minmax_f32("min", z, w)).tolist() == [True, True, True, False]
+    r = orc.unary_f32("relu", np.float32([-0.0, np.nan, -1.0, 2.0]))
+    assert not np.signbit(r[0]) and np.isnan(r[1]) and r[2] == 0.0 and r[3] == 2.0
+    c = orc.clamp_f32(np.float32([np.nan, -3.0, 0.1, 9.0, -0.0]), -0.5, 0.75)
+    assert np.isnan(c[0]) and c[1:4].tolist() == [-0.5, np.float32(0.1), 0.75] and np.signbit(c[4])
+    x = rng.standard_normal((4, 50)).astype(np.float32)
+    x[1, 30] = np.nan
+    x[3, :] = -0.0
+    x[3, 7] = 0.0
+    m = orc.reduce_rows_f32("max", x, 4, 50)
+    assert np.isnan(m[1]) and not np.isnan(m[[0, 2]]).any() and m[3] == 0 and not np.signbit(m[3])
+    assert np.isnan(orc.reduce_rows_f32("absmax", x, 4, 50)[1])
+
+
 def test_reduce_rows():
     rng = np.random.default_rng(23)
     R, C = 37, 301

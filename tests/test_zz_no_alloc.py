@@ -71,6 +71,16 @@ def test_decode_static_head_dim_64(dev, stream):
     assert np.array_equal(a, b)
 
 
+def test_decode_static_general_shapes(dev, stream):
+    """Shapes th_attention_decode runs on the general kernel (no scratch): the static
+    entry serves them too.  head_dim 96 with 3 query heads per kv head is not padded
+    (the MFMA decode takes groups of 1, 2, 4, 8 or 16)."""
+    a, b = _decode_pair(dev, stream, 2, 700, 704, 6, 2, D.BF16, 0x5eed5, Dh=96)
+    assert np.array_equal(a, b)
+    a, b = _decode_pair(dev, stream, 1, 300, 300, 3, 1, D.F16, 0x5eed6, Dh=96)
+    assert np.array_equal(a, b)
+
+
 def test_decode_static_rejects_padded_head_dim(dev, stream):
     q = dev.alloc(4 * 96, D.BF16)
     kv = dev.alloc(4 * 64 * 96, D.BF16)

@@ -120,6 +120,28 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+// IEEE 754-2019 maximum / minimum, the semantics of MLIR's arith.maximumf /
+// arith.minimumf (and of linalg.max / linalg.min on floats): NaN when either
+// operand is NaN, and -0 < +0.  gfx950 has them as v_maximum3_f32 / v_minimum3_f32.
+// (fmaxf / fminf are maxNum / minNum: they drop a NaN operand.)
+__device__ __forceinline__ float maximumf(float a, float b) {
+  return __builtin_elementwise_maximum(a, b);
+}
+__device__ __forceinline__ float minimumf(float a, float b) {
+  return __builtin_elementwise_minimum(a, b);
+}
+
+// wave_max with maximumf: a NaN in any lane reaches every lane
+__device__ __forceinline__ float wave_maximum(float v) {
+  v = maximumf(v, dpp_f32<0xb1>(v));
+  v = maximumf(v, dpp_f32<0x4e>(v));
+  v = maximumf(v, dpp_f32<0x141>(v));
+  v = maximumf(v, dpp_f32<0x140>(v));
+  v = maximumf(v, __shfl_xor(v, 16));
+  v = maximumf(v, __shfl_xor(v, 32));
+  return v;
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
   v += dpp_f32<0xb1>(v);
   v += dpp_f32<0x4e>(v);

@@ -457,8 +457,8 @@ enum RowReduce : int { kRowSum = 0, kRowMax = 1, kRowAbsMax = 2, kRowArgMax = 3 
 template <int OP>
 __device__ __forceinline__ void row_reduce_step(float v, uint32_t c, float& acc, uint32_t& idx) {
   if constexpr (OP == kRowSum) acc += v;
-  else if constexpr (OP == kRowMax) acc = fmaxf(acc, v);
-  else if constexpr (OP == kRowAbsMax) acc = fmaxf(acc, fabsf(v));
+  else if constexpr (OP == kRowMax) acc = maximumf(acc, v);        // reduce arith.maximumf
+  else if constexpr (OP == kRowAbsMax) acc = maximumf(acc, fabsf(v));
   else if (v > acc) { acc = v; idx = c; }   // strict: the first index of the maximum
 }
 
@@ -498,7 +498,7 @@ __device__ __forceinline__ void reduce_rows(const float* __restrict__ x, float* 
       }
       if (lane == 0) *reinterpret_cast<int32_t*>(yr) = static_cast<int32_t>(idx);
     } else {
-      acc = OP == kRowSum ? wave_sum(acc) : wave_max(acc);
+      acc = OP == kRowSum ? wave_sum(acc) : wave_maximum(acc);
       if (lane == 0) *yr = acc;
     }
   }

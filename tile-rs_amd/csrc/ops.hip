@@ -859,6 +859,17 @@ static int decode_run(const void* Q, const void* K, const void* V, void* O, floa
 
 extern "C" {
 
+// The shapes th_attention_decode runs on zero-padded 128-column copies (when the
+// native MFMA decode does not take them): 16-bit head dims below 128 that are
+// multiples of 8, with a group size the MFMA decode takes and 16-byte aligned views.
+static bool decode_pad(const void* q, const void* k, const void* v, const void* o,
+                       uint32_t head_dim, uint32_t num_heads, uint32_t num_kv_heads,
+                       th_dtype dtype) {
+  return head_dim < th::dec::D && head_dim % 8 == 0 &&
+         decode_fast(th::dec::D, num_heads, num_kv_heads, dtype) && aligned16(q) &&
+         aligned16(k) && aligned16(v) && aligned16(o);
+}
+
 int th_attention_decode(const void* q, const void* k, const void* v, void* o, uint32_t batch,
                         uint32_t seq_len, uint32_t max_seq, uint32_t head_dim, uint32_t num_heads,
                         uint32_t num_kv_heads, th_dtype dtype, void* workspace,
@@ -886,9 +897,7 @@ int th_attention_decode(const void* q, const void* k, const void* v, void* o, ui
   // The split partials use the caller's workspace as for head_dim 128.  The copies
   // read K and V once more, but the general kernel is 20-70x slower (measured for
   // head_dim 64).
-  const bool pad = !fast && head_dim < th::dec::D && head_dim % 8 == 0 &&
-                   decode_fast(th::dec::D, num_heads, num_kv_heads, dtype) && aligned16(q) &&
-                   aligned16(k) && aligned16(v) && aligned16(o);
+  const bool pad = !fast && decode_pad(q, k, v, o, head_dim, num_heads, num_kv_heads, dtype);
   if (!fast && !pad) {
     // one query per (batch, head): Q/O [B][1][NH][D]
     return attn_general_launch(q, k, v, o, batch, 1, 0, max_seq, seq_len, head_dim, num_heads,
@@ -976,7 +985,9 @@ int th_attention_decode_static(const void* q, const void* k, const void* v, void
   const bool fast = decode_fast(head_dim, num_heads, num_kv_heads, dtype) && aligned16(q) &&
                     aligned16(k) && aligned16(v);
   if (!fast) {
-    if (head_dim < th::dec::D && head_dim % 8 == 0 && dtype != TH_F32 && head_dim != 64)
+    // th_attention_decode would pad these shapes into allocated copies; every other
+    // shape it runs on the general kernel, which needs no scratch
+    if (decode_pad(q, k, v, o, head_dim, num_heads, num_kv_heads, dtype))
       return fail(TH_KERNEL_ERROR,
                   "attention_decode_static: head_dim " + std::to_string(head_dim) +
                       " runs on zero-padded copies that need allocated memory; use "

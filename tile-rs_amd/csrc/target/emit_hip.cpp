@@ -370,6 +370,20 @@ class Lowerer {
       if (st.dst.iv_stride != st.rows * st.cols)
         return fail("control flow: loop views must advance one tile (rows * cols) per iteration");
     if (k->stores.empty()) return fail("control flow: the loop body stores nothing");
+    // The reference runs the body in order (tile.rs:2187-2210); here the iterations
+    // run in parallel.  That is the same result only when no iteration reads what
+    // another writes: a stored argument may be loaded only at the store's own view
+    // (same offset, tile size and dtype: an in-place update), never shifted.
+    for (const Store& st : k->stores)
+      for (const auto& kv : k->tiles) {
+        const TileVal& t = kv.second;
+        if (t.op != "load" || t.src.arg != st.dst.arg) continue;
+        if (t.src.offset != st.dst.offset || t.src.iv_stride != st.dst.iv_stride ||
+            t.dtype != st.dtype || t.rows * t.cols != st.rows * st.cols)
+          return fail("control flow: the loop loads argument " + k->gm[st.dst.arg].name +
+                      " at another view than it stores it (a loop-carried dependence; "
+                      "the iterations are run in parallel)");
+      }
     // Every launched tile of such a kernel walks the same n tiles; a view that
     // also carried the per-tile offset would need that offset's stride, which
     // the folding cannot check.
@@ -739,6 +753,7 @@ void desc(std::ostringstream& os, const Kernel& k, unsigned threads, unsigned wg
     const unsigned long long tpw = tiles_per_wg ? tiles_per_wg : 1;
     tiles_per_wg = 1;
     if (k.loop.trip_arg >= 0) {
+      // callers with both slots in use reject run-time loop bounds before this point
       const unsigned slot = (scale_args & 0xffu) ? 8u : 0u;
       unsigned b = static_cast<unsigned>(k.loop.trip_arg + 1);
       if (k.args[k.loop.trip_arg].ty.find("i64") != std::string::npos) b |= th::kScaleWide;
@@ -1041,8 +1056,9 @@ bool emit_kernel(const Kernel& k, std::ostringstream& os, std::string* err) {
         else if (o == "sub_f32") e << in(0) << " - " << in(1);
         else if (o == "mul_f32" || o == "mul_f16") e << in(0) << " * " << in(1);
         else if (o == "div_f32") e << in(0) << " / " << in(1);
-        else if (o == "max_f32") e << "fmaxf(" << in(0) << ", " << in(1) << ")";
-        else if (o == "min_f32") e << "fminf(" << in(0) << ", " << in(1) << ")";
+        // linalg.max / linalg.min / arith.maximumf / arith.minimumf: NaN-propagating
+        else if (o == "max_f32") e << "th::maximumf(" << in(0) << ", " << in(1) << ")";
+        else if (o == "min_f32") e << "th::minimumf(" << in(0) << ", " << in(1) << ")";
         else if (o == "log_f32") e << "logf(" << in(0) << ")";
         else if (o == "tanh_f32") e << "tanhf(" << in(0) << ")";
         else if (o == "abs_f32") e << "fabsf(" << in(0) << ")";
@@ -1050,13 +1066,14 @@ bool emit_kernel(const Kernel& k, std::ostringstream& os, std::string* err) {
         else if (o == "rsqrt_f32") e << "(1.0f / sqrtf(" << in(0) << "))";
         // sigmoid and relu as the linalg bridge's generic bodies (mlir_to_linalg.rs:765-789)
         else if (o == "sigmoid_f32") e << "(1.0f / (expf(-" << in(0) << ") + 1.0f))";
-        else if (o == "relu_f32") e << "fmaxf(" << in(0) << ", 0.0f)";
+        else if (o == "relu_f32") e << "th::maximumf(" << in(0) << ", 0.0f)";
         else if (o == "exp_f32" || o == "exp_f16") e << "expf(" << in(0) << ")";
         else if (o == "neg_f32" || o == "neg_f16") e << "-" << in(0);
         else if (o == "silu_f32" || o == "silu_f16") e << in(0) << " / (1.0f + expf(-" << in(0) << "))";
         else if (o == "scale_f32") e << in(0) << " * " << fconst(t.scalars[0]);
         else if (o == "clamp_f32")
-          e << "fminf(fmaxf(" << in(0) << ", " << fconst(t.scalars[0]) << "), " << fconst(t.scalars[1]) << ")";
+          e << "th::minimumf(th::maximumf(" << in(0) << ", " << fconst(t.scalars[0]) << "), "
+            << fconst(t.scalars[1]) << ")";
         else if (o == "fill_f32") e << fconst(t.scalars[0]);
         else if (o == "causal_mask_f32") e << "(col <= row ? " << in(0) << " : -INFINITY)";
         else if (o == "cast_f32_f16") e << "th::f16_to_f32(th::f32_to_f16(" << in(0) << "))";
@@ -1262,6 +1279,15 @@ bool emit_kernel(const Kernel& k, std::ostringstream& os, std::string* err) {
     desc(os, k, 256, static_cast<unsigned>(flash ? (S + 127) / 128 : S), 1);
     return true;
   }
+  // The prefill and decode launch descriptors read their grid from two run-time
+  // scalars, which fills both scale slots; a loop bound taken from an argument
+  // would need a third.
+  if ((o == "attention_prefill_f32" || o == "attention_decode_f32") && k.loop.present &&
+      k.loop.trip_arg >= 0) {
+    *err = "mlir_to_hip: " + k.name + ": control flow: a loop with a run-time bound around " + o +
+           " is not lowered (its launch already scales with two run-time sizes)";
+    return false;
+  }
   if (o == "attention_prefill_f32") {
     const TileVal& q = k.tiles.at(hot->ins[0]);
     os << "causal GQA prefill " << dt_name(q.dtype) << " (runtime seq_len, start_pos, max_seq, head_dim, "
@@ -1299,9 +1325,10 @@ bool emit_kernel(const Kernel& k, std::ostringstream& os, std::string* err) {
     os << "  th::entry::prefill<" << dt_enum(q.dtype) << ", true>(" << in_ptr(0, ct) << ", "
        << in_ptr(1, ct) << ", " << in_ptr(2, ct) << ", " << out_ptr(ct) << ", th_tiles, " << u(S)
        << ", 0u, " << u(S) << ", " << u(HD) << ", " << u(NH) << ", " << u(NKV) << ");\n}\n";
-    // 16-bit with head_dim 128: the library's kernel, one workgroup per (head,
+    // 16-bit with head_dim 128 or 64: the library's kernel, one workgroup per (head,
     // 256-query block); otherwise one workgroup per (head, query)
-    const bool fast = q.dtype != F32 && HD == 128;
+    // (the asm kernel takes 16-bit head_dim 128 and 64, as entry::prefill dispatches)
+    const bool fast = q.dtype != F32 && (HD == 128 || HD == 64);
     long long wpt = fast ? NH * ((S + 255) / 256) : NH * S;
     if (wpt > (1 << 20)) wpt = 1 << 20;
     desc(os, k, 512, static_cast<unsigned>(wpt), 1);

@@ -70,12 +70,14 @@ def _stamp_files() -> list[Path]:
     roots = (CSRC, INCLUDE, PKG_DIR / "examples")
     files = [p for r in roots for p in r.rglob("*")
              if p.is_file() and p.suffix in STAMP_SUFFIXES and "__pycache__" not in p.parts]
+    files += [REF_MLIR_DIR / f"{stem}.mlir" for stem in REF_HOT_PATH]
     return sorted(files, key=lambda p: p.relative_to(ROOT.parent).as_posix())
 
 
 def source_stamp() -> str:
     """First 16 hex digits of a SHA-256 over csrc/ (kernels, emitter, runtime, the
-    prefill generator and its generated include), include/ and the example MLIR."""
+    prefill generator and its generated include), include/, the example MLIR and
+    the reference's hot-path MLIR test inputs that are compiled for the GPU tests."""
     h = hashlib.sha256()
     for p in _stamp_files():
         data = p.read_bytes()
@@ -176,6 +178,21 @@ def _compile_cpp(src: Path, obj: Path, stamp: str) -> None:
 EXAMPLES_DIR = PKG_DIR / "examples"
 EXAMPLES_OUT = LIB_DIR / "examples"
 
+# The reference's own MLIR test inputs for the tile ops of this path (stored as data
+# under tests/golden/ref_mlir by tests/golden/extract_ref_mlir.py): the linalg
+# bridge's MATMUL, SOFTMAX, ATTENTION, ATTENTION_DECODE_KERNEL, RMS_NORM and
+# ATTN_PREFILL_MLIR constants (mlir_to_linalg.rs:1941, :1957, :2088, :2550, :2629,
+# :2978) and the gpu emitter's softmax, matmul_f16 and attention_gqa tests
+# (mlir_to_gpu.rs:2185, :2612, :2995).  Each is emitted by the hip target and
+# compiled like the examples, so the GPU tests run them against the oracle.
+REF_MLIR_DIR = ROOT.parent / "tests" / "golden" / "ref_mlir"
+REF_OUT = LIB_DIR / "ref_fixtures"
+REF_HOT_PATH = (
+    "linalg__matmul", "linalg__softmax", "linalg__attention", "linalg__attention_decode_kernel",
+    "linalg__rms_norm", "linalg__attn_prefill_mlir", "gpu__softmax_mlir_0",
+    "gpu__matmul_f16_mlir_0", "gpu__attention_gqa_mlir_0",
+)
+
 
 def library_path() -> Path:
     return LIB_DIR / LIB_NAME
@@ -185,21 +202,32 @@ def example_path(stem: str) -> Path:
     return EXAMPLES_OUT / f"{stem}.hsaco"
 
 
+def ref_fixture_path(stem: str) -> Path:
+    return REF_OUT / f"{stem}.hsaco"
+
+
 def build_examples(verbose: bool = False) -> list:
-    """Emit every tilers_hip/examples/*.mlir through the hip target and compile the
-    HIP source into lib/examples/<stem>.hsaco (the code objects the launcher loads)."""
-    import ctypes as C
+    """Emit every tilers_hip/examples/*.mlir, and the reference's hot-path MLIR test
+    inputs, through the hip target and compile the HIP source into
+    lib/examples/<stem>.hsaco and lib/ref_fixtures/<stem>.hsaco (the code objects
+    the launcher loads)."""
     import importlib
 
     lib = importlib.import_module("tilers_hip")
     stamp = source_stamp()
     EXAMPLES_OUT.mkdir(parents=True, exist_ok=True)
+    REF_OUT.mkdir(parents=True, exist_ok=True)
     srcs = []
     for mlir in sorted(EXAMPLES_DIR.glob("*.mlir")):
         out = lib.emit(mlir.read_text())
         hip = EXAMPLES_OUT / f"{mlir.stem}.hip"
         hip.write_text(out.source)
         srcs.append((hip, example_path(mlir.stem)))
+    for stem in REF_HOT_PATH:
+        out = lib.emit((REF_MLIR_DIR / f"{stem}.mlir").read_text())
+        hip = REF_OUT / f"{stem}.hip"
+        hip.write_text(out.source)
+        srcs.append((hip, ref_fixture_path(stem)))
 
     def one(pair):
         hip, hsaco = pair
@@ -212,7 +240,7 @@ def build_examples(verbose: bool = False) -> list:
         built = list(ex.map(one, srcs))
     check_code_objects(built)
     if verbose:
-        print(f"built {len(built)} example code objects in {EXAMPLES_OUT}")
+        print(f"built {len(built)} code objects in {EXAMPLES_OUT} and {REF_OUT}")
     return built
 
 
