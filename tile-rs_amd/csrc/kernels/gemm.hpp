@@ -310,25 +310,33 @@ gemm_mfma_256(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, vo
 //
 // 256x256 tile per workgroup, eight waves (two per SIMD) each owning a 128x64
 // sub-tile of 4x2 v_mfma_f32_32x32x16 accumulators.  K is staged 32 at a time
-// through a ring of four LDS buffers (4 x 32 KB) filled by
+// through a ring of NS LDS buffers (4 x 32 KB by default) filled by
 // global_load_lds_dwordx4: each lane's 16 bytes go straight from L2/HBM into
-// LDS (no registers, no ds_write).  A stage is complete for a thread when its
-// vmcnt has dropped to the loads issued after it; one barrier per stage then
-// publishes every thread's part, and right after that barrier the freed buffer
-// is refilled with the stage four ahead, so three stages stay in flight under
-// the MFMAs (measured against two 64-k buffers: 2% faster at 4096^3, 6% for
-// 8192x4096x14336, bit-identical output).
+// LDS (no registers, no ds_write).
+//
+// Ping-pong schedule.  Waves 0-3 (group 0, one per SIMD) own rows 0-127 and
+// waves 4-7 (group 1) rows 128-255, so each SIMD holds one wave of each group.
+// Every K step has two phases per wave, each closed by a workgroup barrier:
+//   memory phase:  read the step's MFMA fragments (both 16-k sub-steps) from LDS
+//                  and wait for them; wait for this wave's share of the next
+//                  stage's DMA;
+//   compute phase: refill the buffer every wave has finished reading with the
+//                  stage NS-1 ahead, then issue the step's 16 MFMAs back to back.
+// Group 1 starts one phase late (an extra barrier before its first step, group 0
+// one after its last), so on every SIMD one wave's MFMA burst runs while the
+// other wave does its LDS reads and DMA issue.  Against both waves interleaving
+// reads and MFMAs with one barrier per step: 4096^3 bf16 118.9 -> 109.7 us on one
+// box, bit-identical output.
 //   A stage: [256 m][32 k], 64-byte rows; 16-byte chunk c of row r sits at
-//            c ^ ((r >> 2) & 3) -> conflict-free 128-bit MFMA reads
-//            (with 64-k stages: 128-byte rows, c ^ ((r ^ (r >> 3)) & 7)).
-//   B stage: row-major B needs no transpose anywhere: it stays [64 k][256 n]
+//            c ^ ((r >> 2) & 3) -> conflict-free 128-bit MFMA reads.
+//   B stage: row-major B needs no transpose anywhere: it stays [32 k][256 n]
 //            (512-byte rows, chunk c at c ^ 4*(k & 3), so the four k rows one
 //            half-wave reads land in four different 64-byte bank groups of the
 //            64-bank LDS) and the MFMA B operand is read with
 //            ds_read_b64_tr_b16, which hands each lane of a 16-lane group one
 //            n column of a 4 (k) x 16 (n) block: two reads give the eight
 //            consecutive k values of the 32x32x16 operand.
-//   B_TRANS: B stage is [256 n][64 k] like A.
+//   B_TRANS: B stage is [256 n][32 k] like A.
 // The swizzles are applied on the global side: each lane picks the global
 // chunk whose swizzled LDS slot is its own fixed slot (lane*16 bytes).
 // ---------------------------------------------------------------------------
@@ -373,8 +381,9 @@ __device__ __forceinline__ void gemm_dma_tile_256(const uint16_t* __restrict__ A
                                                   uint32_t ldk = 0) {
   using namespace gemm;
   const size_t lk = ldk ? ldk : K;
-  static_assert(KB == 32 || KB == 64, "stage K");
-  static_assert(WAVES == 4 || WAVES == 8, "2x2 or 2x4 waves");
+  static_assert(KB == 32, "stage K: two 16-k sub-steps per step");
+  static_assert(WAVES == 8, "ping-pong: two groups of one wave per SIMD");
+  static_assert(NS >= 3, "a refill lands at least one step ahead of its use");
   static_assert(NS * (BM + BN) * KB * 2 <= 160 * 1024, "LDS");
   constexpr int NTH = 64 * WAVES;          // threads
   constexpr int WN_W = WAVES / 2;          // waves along N
@@ -428,42 +437,78 @@ __device__ __forceinline__ void gemm_dma_tile_256(const uint16_t* __restrict__ A
     }
   };
 
-  // ---- fragment reads ----
+  // ---- fragment reads: a whole step (two 16-k sub-steps) per memory phase ----
   static_assert(MI == 1 || MI == 2 || MI == 4, "live row blocks");
   static_assert(EPI != kEpiSiluMul || MI == 4, "the staged epilogue covers whole tiles");
-  u32x4 fa[2][MI], fb[2][NI];
-  auto load_frags = [&](int stage, int ks, int set) {
-    const int chunk = 2 * ks + g;
+  static_assert(NI == 2, "two 32-column blocks per wave");
+  constexpr int KS = KB / 16;
+  u32x4 fa[KS][MI], fb[KS][NI];
+  auto load_frags = [&](int stage) {
     const u32x4* la = lds_a(stage);
     const u32x4* lb = lds_b(stage);
+    auto read_a = [&](int ks) {
 #pragma unroll
-    for (int mi = 0; mi < MI; ++mi) {
-      const int row = wm * 128 + mi * 32 + l32;
-      fa[set][mi] = la[row * CPR + (chunk ^ swa(row))];
-    }
+      for (int mi = 0; mi < MI; ++mi) {
+        const int row = wm * 128 + mi * 32 + l32;
+        fa[ks][mi] = la[row * CPR + ((2 * ks + g) ^ swa(row))];
+      }
+    };
     if constexpr (B_TRANS) {
 #pragma unroll
-      for (int ni = 0; ni < NI; ++ni) {
-        const int row = wn * TWN + ni * 32 + l32;
-        fb[set][ni] = lb[row * CPR + (chunk ^ swa(row))];
+      for (int ks = 0; ks < KS; ++ks) {
+        read_a(ks);
+#pragma unroll
+        for (int ni = 0; ni < NI; ++ni) {
+          const int row = wn * TWN + ni * 32 + l32;
+          fb[ks][ni] = lb[row * CPR + ((2 * ks + g) ^ swa(row))];
+        }
       }
+      lds::wait_lgkm0();
     } else {
+      // Lane (q, i) of each 16-lane group reads k rows 16 ks + 8 (q >> 1) + 4 r + (i >> 2)
+      // at column n = wn*64 + 32 ni + 16 (q & 1) + 4 (i & 3): one address per column
+      // block, the (ks, r) steps as immediate offsets (16 ks + 4 r rows of 512 bytes).
+      // The transposed reads are inline asm: the compiler would otherwise order them
+      // after every outstanding LDS DMA (vmcnt(0)), which this schedule orders itself
+      // with its stage waits and barriers.  A closing statement takes all eight
+      // results as operands and waits for them, so none is used before it has landed.
+      // Reads go A, B per 16-k sub-step.
       const int q = lane >> 4, i = lane & 15;
-      const char* base = reinterpret_cast<const char*>(lb);
+      const int k0 = 8 * (q >> 1) + (i >> 2);
+      uint32_t addr[NI];
 #pragma unroll
       for (int ni = 0; ni < NI; ++ni) {
         const int n = wn * TWN + ni * 32 + 16 * (q & 1) + 4 * (i & 3);
-#pragma unroll
-        for (int r = 0; r < 2; ++r) {
-          const int k = ks * 16 + 8 * (q >> 1) + 4 * r + (i >> 2);
-          const int off = k * 512 + (((n >> 3) ^ (4 * (k & 3))) << 4) + (n & 7) * 2;
-          const v4i16 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-              (lds_v4i16*)(const_cast<char*>(base) + off));
-          const u32x2 w = __builtin_bit_cast(u32x2, v);
-          fb[set][ni][2 * r] = w[0];
-          fb[set][ni][2 * r + 1] = w[1];
-        }
+        addr[ni] = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds::lds_void*)(lb))) +
+                   k0 * 512 + (((n >> 3) ^ (4 * (k0 & 3))) << 4) + (n & 7) * 2;
       }
+      u32x2 r[8];  // r[4 ni + 2 ks + half]
+      auto tr = [&](int ks) {
+#pragma unroll
+        for (int ni = 0; ni < NI; ++ni)
+#pragma unroll
+          for (int h = 0; h < 2; ++h)
+            asm volatile("ds_read_b64_tr_b16 %0, %1"
+                         : "=v"(r[4 * ni + 2 * ks + h])
+                         : "v"(addr[ni] + ks * 8192 + h * 2048)
+                         : "memory");
+      };
+      read_a(0);
+      tr(0);
+      read_a(1);
+      tr(1);
+      asm volatile("s_waitcnt lgkmcnt(0)"
+                   : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]), "+v"(r[4]), "+v"(r[5]),
+                     "+v"(r[6]), "+v"(r[7])
+                   :
+                   : "memory");
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+        for (int ni = 0; ni < NI; ++ni) {
+          const u32x2 lo = r[4 * ni + 2 * ks], hi = r[4 * ni + 2 * ks + 1];
+          fb[ks][ni] = u32x4{lo[0], lo[1], hi[0], hi[1]};
+        }
     }
   };
 
@@ -475,81 +520,39 @@ __device__ __forceinline__ void gemm_dma_tile_256(const uint16_t* __restrict__ A
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-  // Pipeline: all NS buffers are filled ahead.  In step kt the barrier sits
-  // before the MFMAs of the last sub-step (whose fragments are already in
-  // registers): every read of buffer kt%NS is then done, so right after the
-  // barrier the DMA for step kt+NS refills that buffer and the first fragments
-  // of step kt+1 are read, both under the last sub-step's MFMAs.
-  // Each sub-step is one scheduling region: the fragment reads it issues feed
-  // the NEXT sub-step, so they overlap this sub-step's MFMAs instead of being
-  // sunk next to their use (which would expose the LDS latency every sub-step).
-  constexpr int KS = KB / 16;
-  static_assert(KS % 2 == 0, "fragment sets alternate per sub-step");
-  constexpr int NM = MI * NI;                         // MFMAs per sub-step
-  constexpr int NR = MI + (B_TRANS ? NI : 2 * NI);    // LDS reads per sub-step
   const uint32_t nk = K / KB;
-  auto mfmas = [&](int set) {
-#pragma unroll
-    for (int mi = 0; mi < MI; ++mi)
-#pragma unroll
-      for (int ni = 0; ni < NI; ++ni)
-        acc[mi][ni] = mfma32x32x16<DT>(fa[set][mi], fb[set][ni], acc[mi][ni]);
-  };
-  // Fragment reads go first, two behind each MFMA, so the next sub-step's
-  // wait finds them done; the DMA issues (a whole step of slack) follow.
-  auto interleave = [&](int nvmem) {
-    int r = NR, v = nvmem;
-#pragma unroll
-    for (int i = 0; i < NM; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-      if (r >= 2) {
-        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // LDS read
-        r -= 2;
-      } else if (r == 1) {
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-        r = 0;
-      } else if (v >= 2) {
-        __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);  // VMEM (LDS DMA)
-        v -= 2;
-      } else if (v == 1) {
-        __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);
-        v = 0;
-      }
-    }
-  };
-  // One K step.  FILL: step kt+NS exists, so the freed buffer is refilled and
-  // the loop body has no branches.
-  auto step = [&](uint32_t kt, auto fill) {
+  const int grp = wave >> 2;
+  // One K step (FILL: a refill exists, so the body has no branches).  Barrier
+  // j of the workgroup closes group 0's phase j and group 1's phase j - 1: group
+  // 0 reads stage k in [B(2k-1), B(2k)) and computes in [B(2k), B(2k+1)), group 1
+  // one phase later.  Buffer (k-1) % NS is read by nobody after B(2k-1), so both
+  // groups refill it in their compute phase of step k.  Every wave waits for its
+  // share of stage k+1 at the end of its memory phase of step k, which precedes
+  // B(2k+1), the barrier after which group 0 reads stage k+1.
+  auto step = [&](uint32_t k, auto fill) {
     constexpr bool FILL = decltype(fill)::value;
-    const int cur = kt % NS;
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      const int set = ks & 1;
-      __builtin_amdgcn_sched_barrier(0);
-      if (ks + 1 < KS) {
-        load_frags(cur, ks + 1, set ^ 1);
-        mfmas(set);
-        interleave(0);
-      } else {
-        // this thread's reads of `cur` are complete; step kt+1's loads have landed
-        __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
-        if constexpr (FILL) {
-          wait_vm<(NS - 2) * 2 * NLA>();
-        } else if (kt + 1 < nk) {
-          wait_stages<2 * NLA, NS - 2>(min(nk - 2 - kt, static_cast<uint32_t>(NS - 2)));
-        }
-        bar();
-        __builtin_amdgcn_sched_barrier(0);
-        if constexpr (FILL) {
-          issue(cur, kt + NS);
-          load_frags((kt + 1) % NS, 0, set ^ 1);
-        } else if (kt + 1 < nk) {
-          load_frags((kt + 1) % NS, 0, set ^ 1);
-        }
-        mfmas(set);
-        interleave(FILL ? 2 * NLA : 0);
-      }
+    __builtin_amdgcn_sched_barrier(0);
+    load_frags(k % NS);
+    lds::wait_lgkm0();
+    if constexpr (FILL) {
+      // issued so far: stages up to k - 2 + NS; those past k + 1 stay in flight
+      wait_vm<(NS - 3) * 2 * NLA>();
+    } else if (k + 1 < nk) {
+      const uint32_t last = min(nk - 1, max(k + NS - 2, static_cast<uint32_t>(NS - 1)));
+      wait_stages<2 * NLA, NS - 2>(last - (k + 1));
     }
+    bar();
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (FILL) issue((k - 1) % NS, k - 1 + NS);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+      for (int mi = 0; mi < MI; ++mi)
+#pragma unroll
+        for (int ni = 0; ni < NI; ++ni)
+          acc[mi][ni] = mfma32x32x16<DT>(fa[ks][mi], fb[ks][ni], acc[mi][ni]);
+    __builtin_amdgcn_sched_barrier(0);
+    bar();
   };
 
   // A previous work item of this workgroup (grid-stride callers) may still be
@@ -560,9 +563,10 @@ __device__ __forceinline__ void gemm_dma_tile_256(const uint16_t* __restrict__ A
     if (s < nk) issue(s, s);
   wait_stages<2 * NLA, NS - 1>(min(nk - 1, static_cast<uint32_t>(NS - 1)));
   bar();
-  load_frags(0, 0, 0);
+  if (grp == 1) bar();
   uint32_t kt = 0;
-  for (; kt + NS < nk; ++kt) step(kt, std::true_type{});
+  if (kt < nk) step(kt++, std::false_type{});
+  for (; kt + NS - 1 < nk; ++kt) step(kt, std::true_type{});
   for (; kt < nk; ++kt) step(kt, std::false_type{});
   __builtin_amdgcn_sched_barrier(0);
 
@@ -570,24 +574,26 @@ __device__ __forceinline__ void gemm_dma_tile_256(const uint16_t* __restrict__ A
   // 8*(r/4) + 4*(l/32) + r%4, column l%32: a lane has four consecutive rows of
   // one column, so direct stores are 2- or 4-byte writes (64-128 contiguous
   // bytes per row and instruction).  For a plain store that is as fast as any
-  // rearrangement (measured): the tile's HBM writes bound it.
+  // rearrangement (measured): the tile's HBM writes bound it.  Each store keeps
+  // its own bounds test, so stores leave one at a time between address updates:
+  // at 4096^3 that is 4 us faster than issuing each 32x32 block's sixteen stores
+  // back to back (measured on one box, same schedule otherwise).  Both groups
+  // store after group 1's last compute phase: letting group 0 store during it was
+  // 3 us slower.
+  if (grp == 0) bar();
   if constexpr (EPI != kEpiSiluMul) {
-    auto store_all = [&](auto pred) {
 #pragma unroll
-      for (int mi = 0; mi < MI; ++mi)
+    for (int mi = 0; mi < MI; ++mi)
 #pragma unroll
-        for (int ni = 0; ni < NI; ++ni) {
-          const uint32_t col = n0 + wn * TWN + ni * 32 + l32;
+      for (int ni = 0; ni < NI; ++ni) {
+        const uint32_t col = n0 + wn * TWN + ni * 32 + l32;
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const uint32_t row = m0 + wm * 128 + mi * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
-            if (!decltype(pred)::value || (row < M && col < N))
-              store_out<EPI, DT_OUT>(C, up, static_cast<size_t>(row) * N + col, acc[mi][ni][r]);
-          }
+        for (int r = 0; r < 16; ++r) {
+          const uint32_t row = m0 + wm * 128 + mi * 32 + 8 * (r >> 2) + 4 * g + (r & 3);
+          if (row < M && col < N)
+            store_out<EPI, DT_OUT>(C, up, static_cast<size_t>(row) * N + col, acc[mi][ni][r]);
         }
-    };
-    if (edge) store_all(std::true_type{});
-    else store_all(std::false_type{});
+      }
     return;
   }
   // With the SiLU*Mul epilogue the UP operand makes scattered 2-byte reads as
