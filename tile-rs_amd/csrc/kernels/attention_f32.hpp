@@ -19,12 +19,21 @@
 // (B operand, LDS row f(r, h)) alike.  O's accumulator rows are queries, so the
 // per-query rescale factors and final sums go through a 32-float LDS slot per
 // wave.  The head dimension is split between lane halves in the S^T product as
-// d = 4 (ks / 2) + 2 (ks % 2) + h, so each lane fills its Q^T registers from
-// 16-byte loads of its query row.
+// d = 4 (ks / 2) + 2 h + ks % 2, so a lane's K values for steps 2m and 2m+1 are
+// adjacent (one 8-byte LDS read) and its Q^T registers fill from 16-byte loads of
+// its query row.  In O += P . V, 32-column block c of O holds head dims
+// d = ND n + c (n = l32, ND = D / 32 blocks), so a lane reads its V values for all
+// blocks as ND adjacent floats (one 16-byte read at D 128) and writes its O row
+// piece as one 16-byte store.
 //
-// LDS rows: K [32][D + 2] (positions 0..31 of a K-step read in one bank each,
-// the two lane halves one bank apart), V [32][D + 8] (rows f(r, 0) and f(r, 1)
-// are 4 apart: 32 banks apart).
+// LDS rows: K [32][D + 2] (an 8-byte read of positions 0..31 covers the 64 banks
+// once per lane half), V [32][D] (each 16-byte read takes 128 contiguous bytes per
+// eight lanes).  Reading K and V one float per lane, paired by the compiler into
+// two-address reads, cost one bank-conflict cycle per MFMA (27% of LDS-active
+// cycles).
+//
+// Work order: the 128-query blocks of one problem run on one XCD, so its K and V
+// are read from HBM about once and then served by that XCD's L2.
 #pragma once
 
 #include "common.hpp"
@@ -43,7 +52,7 @@ typedef float f32x2 __attribute__((ext_vector_type(2)));
 template <int D>
 struct alignas(16) Lds {
   float k[2][BKV * (D + 2)];
-  float v[2][BKV * (D + 8)];
+  float v[2][BKV * D];
   float stat[NT / 64][32];   // per-wave query factors (rescale, then 1 / sum)
 };
 template <int D>
@@ -62,7 +71,7 @@ __device__ __forceinline__ void attn_f32_tile(const float* __restrict__ Q,
                                               uint32_t qb) {
   using namespace af32;
   static_assert(D == 64 || D == 128, "head_dim 64 or 128");
-  constexpr int LK = D + 2, LV = D + 8;
+  constexpr int LK = D + 2, LV = D;
   constexpr int KP = BKV * D / 2 / NT;   // float2 pieces of K per thread
   constexpr int VP = BKV * D / 4 / NT;   // float4 pieces of V per thread
   constexpr int ND = D / 32;             // 32-wide column blocks of O
@@ -82,8 +91,8 @@ __device__ __forceinline__ void attn_f32_tile(const float* __restrict__ Q,
 #pragma unroll
     for (int j = 0; j < D / 4; ++j) {
       const f32x4 x = *reinterpret_cast<const f32x4*>(qr + 4 * j);
-      qf[2 * j] = x[h];
-      qf[2 * j + 1] = x[2 + h];
+      qf[2 * j] = x[2 * h];
+      qf[2 * j + 1] = x[2 * h + 1];
     }
   }
 
@@ -136,10 +145,13 @@ __device__ __forceinline__ void attn_f32_tile(const float* __restrict__ Q,
     f32x16 st;
 #pragma unroll
     for (int r = 0; r < 16; ++r) st[r] = 0.0f;
-    const float* kr = s.k[cur] + l32 * LK + h;
+    const float* kr = s.k[cur] + l32 * LK + 2 * h;
 #pragma unroll
-    for (int ks = 0; ks < D / 2; ++ks)
-      st = __builtin_amdgcn_mfma_f32_32x32x2f32(kr[4 * (ks >> 1) + 2 * (ks & 1)], qf[ks], st, 0, 0, 0);
+    for (int m = 0; m < D / 4; ++m) {
+      const f32x2 k2 = *reinterpret_cast<const f32x2*>(kr + 4 * m);
+      st = __builtin_amdgcn_mfma_f32_32x32x2f32(k2[0], qf[2 * m], st, 0, 0, 0);
+      st = __builtin_amdgcn_mfma_f32_32x32x2f32(k2[1], qf[2 * m + 1], st, 0, 0, 0);
+    }
     // ---- online softmax of query l32 over positions f(r, h) ----
     const uint32_t kv0 = jb * BKV;
     float mx = -INFINITY;
@@ -174,13 +186,23 @@ __device__ __forceinline__ void attn_f32_tile(const float* __restrict__ Q,
 #pragma unroll
         for (int r = 0; r < 16; ++r) acc[c][r] *= a4[r >> 2][r & 3];
     }
-    const float* vr = s.v[cur] + (4 * h) * LV + l32;
+    const float* vr = s.v[cur] + (4 * h) * LV + ND * l32;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const float* vrow = vr + (8 * (r >> 2) + (r & 3)) * LV;
+      float vv[ND];
+      if constexpr (ND == 4) {
+        const f32x4 x = *reinterpret_cast<const f32x4*>(vrow);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) vv[c] = x[c];
+      } else {
+        const f32x2 x = *reinterpret_cast<const f32x2*>(vrow);
+        vv[0] = x[0];
+        vv[1] = x[1];
+      }
 #pragma unroll
       for (int c = 0; c < ND; ++c)
-        acc[c] = __builtin_amdgcn_mfma_f32_32x32x2f32(st[r], vrow[32 * c], acc[c], 0, 0, 0);
+        acc[c] = __builtin_amdgcn_mfma_f32_32x32x2f32(st[r], vv[c], acc[c], 0, 0, 0);
     }
     if (jb + 1 < nb) store(cur ^ 1);
     __syncthreads();   // also orders this block's stat reads before the next writes
@@ -192,18 +214,36 @@ __device__ __forceinline__ void attn_f32_tile(const float* __restrict__ Q,
   __builtin_amdgcn_s_waitcnt(0xc07f);
   __builtin_amdgcn_wave_barrier();
   const uint32_t qw = qb * BQ + 32 * wave;
+  const bool o16 = (reinterpret_cast<uintptr_t>(O) & 15) == 0;
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
     const int qi = 8 * (r >> 2) + 4 * h + (r & 3);
     const float inv = s.stat[wave][qi];
     if (qw + qi < S) {
-      float* orow = O + base + static_cast<size_t>(qw + qi) * D + l32;
+      // columns ND l32 .. ND l32 + ND - 1 of the row
+      float* orow = O + base + static_cast<size_t>(qw + qi) * D + ND * l32;
+      f32x4 ov;
 #pragma unroll
-      for (int c = 0; c < ND; ++c) orow[32 * c] = acc[c][r] * inv;
+      for (int c = 0; c < 4; ++c) ov[c] = c < ND ? acc[c < ND ? c : 0][r] * inv : 0.0f;
+      if (ND == 4 && o16) {
+        *reinterpret_cast<f32x4*>(orow) = ov;
+      } else {
+#pragma unroll
+        for (int c = 0; c < ND; ++c) orow[c] = ov[c];
+      }
     }
   }
   __syncthreads();   // LDS is reused by the next work item
 }
+
+namespace af32 {
+// Work item of hardware block `bid` out of `total`: the hardware deals workgroups
+// to the 8 XCDs round-robin, so item ids are renumbered to give each XCD a
+// contiguous run (consecutive query blocks of one problem share its L2).
+__device__ __forceinline__ uint32_t xcd_item(uint32_t bid, uint32_t total) {
+  return total % 8 == 0 ? (bid % 8) * (total / 8) + bid / 8 : bid;
+}
+}  // namespace af32
 
 // Library kernel: grid = tiles * ceil(S / 128), S >= 1.
 template <int D>
@@ -211,7 +251,8 @@ __global__ void __launch_bounds__(af32::NT)
 attn_f32_mfma(const float* __restrict__ Q, const float* __restrict__ K, const float* __restrict__ V,
               float* __restrict__ O, uint32_t S, float scale_log2) {
   const uint32_t nqb = (S + af32::BQ - 1) / af32::BQ;
-  attn_f32_tile<D>(Q, K, V, O, S, scale_log2, blockIdx.x / nqb, blockIdx.x % nqb);
+  const uint32_t w = af32::xcd_item(blockIdx.x, gridDim.x);
+  attn_f32_tile<D>(Q, K, V, O, S, scale_log2, w / nqb, w % nqb);
 }
 
 }  // namespace th

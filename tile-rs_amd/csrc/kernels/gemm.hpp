@@ -62,16 +62,18 @@ __device__ __forceinline__ int swz(int row, int chunk) {
   return chunk ^ ((row ^ (row >> 3)) & 7);
 }
 
-// Map hardware block id -> (tile_m, tile_n).
+// Map hardware block id -> (tile_m, tile_n).  GM: tile-rows per group (an XCD's
+// contiguous run of ids covers GM rows and run / GM columns of tiles).
+template <int GM = GROUP_M>
 __device__ __forceinline__ void tile_coords(uint32_t bid, uint32_t tiles_m, uint32_t tiles_n,
                                             uint32_t& tm, uint32_t& tn) {
   const uint32_t total = tiles_m * tiles_n;
   uint32_t id = bid;
   if (total % NXCD == 0) id = (bid % NXCD) * (total / NXCD) + bid / NXCD;
-  const uint32_t per_group = GROUP_M * tiles_n;
+  const uint32_t per_group = GM * tiles_n;
   const uint32_t group = id / per_group;
-  const uint32_t first_m = group * GROUP_M;
-  const uint32_t gm = min(tiles_m - first_m, static_cast<uint32_t>(GROUP_M));
+  const uint32_t first_m = group * GM;
+  const uint32_t gm = min(tiles_m - first_m, static_cast<uint32_t>(GM));
   const uint32_t in_group = id % per_group;
   tm = first_m + in_group % gm;
   tn = in_group / gm;

@@ -24,6 +24,10 @@
 namespace th {
 namespace gf32 {
 constexpr int BM = 128, BN = 128, BK = 16;
+// Tile-rows per XCD group.  Four workgroups per CU run an XCD's whole run of
+// tiles at once (128 at 4096^3); groups 8 tall make that run 8 x 16 tiles, which
+// reads 8 A and 16 B panels instead of 4 and 32 (groups 4 tall).
+constexpr int GROUP_M = 8;
 constexpr int LD = 128 + 32;  // LDS row (floats)
 constexpr int NT = 256;
 
@@ -147,7 +151,7 @@ __device__ __forceinline__ void gemm_f32_tile_128(const float* __restrict__ A,
     }
 }
 
-// Library kernel: tiles in XCD-aware grouped order, batch = blockIdx.y with
+// Library kernel: tiles in XCD-aware grouped order (GROUP_M), batch = blockIdx.y with
 // element strides sa, sb, sc.
 template <int DT_OUT, bool B_TRANS, bool VEC, int EPI = 0>
 __global__ void __launch_bounds__(gf32::NT)
@@ -157,7 +161,7 @@ gemm_f32_mfma(const float* __restrict__ A, const float* __restrict__ B, void* __
   constexpr int OSZ = (DT_OUT == kF32) ? 4 : 2;
   const uint32_t tiles_m = (M + gf32::BM - 1) / gf32::BM, tiles_n = (N + gf32::BN - 1) / gf32::BN;
   uint32_t tm, tn;
-  gemm::tile_coords(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  gemm::tile_coords<gf32::GROUP_M>(blockIdx.x, tiles_m, tiles_n, tm, tn);
   const size_t co = static_cast<size_t>(blockIdx.y) * sc * OSZ;
   gemm_f32_tile_128<DT_OUT, B_TRANS, VEC, EPI>(
       A + blockIdx.y * sa, B + blockIdx.y * sb, static_cast<char*>(C) + co, M, N, K, tm, tn,

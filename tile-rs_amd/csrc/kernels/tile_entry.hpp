@@ -164,7 +164,7 @@ __device__ __forceinline__ void gemm_f32(const float* A, const float* B, void* C
   for (uint32_t w = blockIdx.x; w < per * batch; w += gridDim.x) {
     const uint32_t bi = w / per;
     uint32_t tm, tn;
-    gemm::tile_coords(w % per, tiles_m, tiles_n, tm, tn);
+    gemm::tile_coords<gf32::GROUP_M>(w % per, tiles_m, tiles_n, tm, tn);
     const size_t co = static_cast<size_t>(bi) * M * N * OSZ;
     const float* a = A + static_cast<size_t>(bi) * M * K;
     const float* b = B + static_cast<size_t>(bi) * K * N;
@@ -209,9 +209,12 @@ __device__ __forceinline__ void attention_tiles(const void* q, const void* k, co
       auto K = static_cast<const float*>(k);
       auto V = static_cast<const float*>(v);
       auto O = static_cast<float*>(o);
-      for (uint32_t w = blockIdx.x; w < tiles * nqb; w += gridDim.x) {
-        if (d == 64) attn_f32_tile<64>(Q, K, V, O, s, scale * kLog2e, w / nqb, w % nqb);
-        else attn_f32_tile<128>(Q, K, V, O, s, scale * kLog2e, w / nqb, w % nqb);
+      const uint32_t total = tiles * nqb;
+      for (uint32_t w = blockIdx.x; w < total; w += gridDim.x) {
+        // one item per workgroup: XCD-grouped order (as the library kernel)
+        const uint32_t it = gridDim.x == total ? af32::xcd_item(w, total) : w;
+        if (d == 64) attn_f32_tile<64>(Q, K, V, O, s, scale * kLog2e, it / nqb, it % nqb);
+        else attn_f32_tile<128>(Q, K, V, O, s, scale * kLog2e, it / nqb, it % nqb);
       }
       return;
     }
