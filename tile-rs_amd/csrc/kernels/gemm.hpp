@@ -4,13 +4,15 @@
 // (reference: crates/rustc_codegen_tile/src/mlir_to_linalg.rs:1345-1393).
 // Intrinsics: __tile_matmul_f16 (crates/tile_std/src/tile.rs:1983) with the
 // u16-tile result (tile.rs:2593) or the f32-tile result (`_acc_f32`,
-// tile.rs:2666); __tile_matmul_transposed_f16 (tile.rs:2028, :2694);
-// __tile_matmul_f32 (tile.rs:193, :2309) uses the f32 fallback kernel below.
+// tile.rs:2666); __tile_matmul_transposed_f16 (tile.rs:2028, :2694).
+// __tile_matmul_f32 (tile.rs:193, :2309) runs on the fp32 MFMA kernel of
+// gemm_f32.hpp; the FMA kernel at the end of this file serves only 16-bit shapes
+// the MFMA paths cannot take.
 //
 // Two MFMA paths (gfx950), both on 256x256 macro-tiles with
 // v_mfma_f32_32x32x16_{bf16,f16} and f32 accumulators:
-//  - gemm_dma_256 (the direct-to-LDS pipeline further down) for K a multiple
-//    of 32: the path every config shape takes;
+//  - gemm_dma_256 (the direct-to-LDS pipeline further down, ping-pong schedule)
+//    for K a multiple of 32: the path every config shape takes;
 //  - gemm_mfma_256, register-staged, for the other 16-bit shapes (K a multiple
 //    of 8): K staged 64 at a time through LDS with two buffers, four waves each
 //    owning a 128x128 sub-tile.  Global tiles are fetched into registers one
@@ -727,9 +729,9 @@ __device__ __forceinline__ void gemm_dot_tile_256(const uint16_t* __restrict__ A
   }
 }
 
-// Fallback for shapes the MFMA path does not take (K % 8 != 0, row-major B with
-// N % 8 != 0) and for f32 operands: 64x64 tile per 256-thread workgroup, each
-// thread a 4x4 block, K staged 16 at a time through LDS, f32 FMA.
+// Fallback for 16-bit shapes the MFMA paths do not take (K % 8 != 0, row-major B
+// with N % 8 != 0): 64x64 tile per 256-thread workgroup, each thread a 4x4 block,
+// K staged 16 at a time through LDS, f32 FMA.
 template <int DT, int DT_OUT, bool B_TRANS, int EPI = 0>
 __device__ __forceinline__ void gemm_fma_tile_64(const void* __restrict__ A,
                                                  const void* __restrict__ B, void* __restrict__ C,
