@@ -474,9 +474,8 @@ __device__ __forceinline__ void gemm_dma_tile_256(const uint16_t* __restrict__ A
       // block, the (ks, r) steps as immediate offsets (16 ks + 4 r rows of 512 bytes).
       // The transposed reads are inline asm: the compiler would otherwise order them
       // after every outstanding LDS DMA (vmcnt(0)), which this schedule orders itself
-      // with its stage waits and barriers.  A closing statement takes all eight
-      // results as operands and waits for them, so none is used before it has landed.
-      // Reads go A, B per 16-k sub-step.
+      // with its stage waits and barriers.  One statement issues all eight and waits
+      // for them, so no result is read (or copied) before it has landed.
       const int q = lane >> 4, i = lane & 15;
       const int k0 = 8 * (q >> 1) + (i >> 2);
       uint32_t addr[NI];
@@ -487,25 +486,22 @@ __device__ __forceinline__ void gemm_dma_tile_256(const uint16_t* __restrict__ A
                    k0 * 512 + (((n >> 3) ^ (4 * (k0 & 3))) << 4) + (n & 7) * 2;
       }
       u32x2 r[8];  // r[4 ni + 2 ks + half]
-      auto tr = [&](int ks) {
-#pragma unroll
-        for (int ni = 0; ni < NI; ++ni)
-#pragma unroll
-          for (int h = 0; h < 2; ++h)
-            asm volatile("ds_read_b64_tr_b16 %0, %1"
-                         : "=v"(r[4 * ni + 2 * ks + h])
-                         : "v"(addr[ni] + ks * 8192 + h * 2048)
-                         : "memory");
-      };
       read_a(0);
-      tr(0);
       read_a(1);
-      tr(1);
-      asm volatile("s_waitcnt lgkmcnt(0)"
-                   : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]), "+v"(r[4]), "+v"(r[5]),
-                     "+v"(r[6]), "+v"(r[7])
-                   :
-                   : "memory");
+      asm volatile(
+          "ds_read_b64_tr_b16 %0, %8\n"
+          "ds_read_b64_tr_b16 %1, %8 offset:2048\n"
+          "ds_read_b64_tr_b16 %2, %8 offset:8192\n"
+          "ds_read_b64_tr_b16 %3, %8 offset:10240\n"
+          "ds_read_b64_tr_b16 %4, %9\n"
+          "ds_read_b64_tr_b16 %5, %9 offset:2048\n"
+          "ds_read_b64_tr_b16 %6, %9 offset:8192\n"
+          "ds_read_b64_tr_b16 %7, %9 offset:10240\n"
+          "s_waitcnt lgkmcnt(0)"
+          : "=&v"(r[0]), "=&v"(r[1]), "=&v"(r[2]), "=&v"(r[3]), "=&v"(r[4]), "=&v"(r[5]),
+            "=&v"(r[6]), "=&v"(r[7])
+          : "v"(addr[0]), "v"(addr[1])
+          : "memory");
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
