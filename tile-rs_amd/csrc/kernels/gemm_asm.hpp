@@ -1,0 +1,111 @@
+// Dense 16-bit GEMM on whole 256 x 256 tiles: the library's kernel for row-major B with
+// M and N multiples of 256 and K a multiple of 128 (at least 256).
+//
+// The tile program is generated gfx950 assembly (gen_gemm.py, run by the build into
+// kernels/gen/gemm_asm.inc): four waves of 128 x 128 with AGPR accumulators, A fetched
+// in 64-deep double stages (whole 128-byte rows per DMA lane group), B in 32-deep
+// stages; layouts, schedule and waits are described in gen_gemm.py.  This wrapper maps
+// the workgroup to its tile and computes the per-lane and per-wave operands.
+// Semantics: C = A . B with f32 accumulation in k order per 32x32x16 MFMA
+// (crates/rustc_codegen_tile/src/mlir_to_linalg.rs:1345-1393), C rounded once (RNE) to
+// its dtype; the K order is that of gemm_dma_256, so both give the same bits.
+#pragma once
+
+#include "gemm.hpp"
+#include "kernels/gen/gemm_asm.inc"
+
+namespace th {
+namespace gasm {
+constexpr int NT = 256;   // 4 waves
+// Shapes the program takes: whole tiles, K in groups of four 32-deep steps (at least
+// two groups), and every per-lane byte offset within 32 bits.
+__host__ __device__ constexpr bool fits(uint64_t m, uint64_t n, uint64_t k, int out_size) {
+  return m % 256 == 0 && n % 256 == 0 && k % 128 == 0 && k >= 256 && m > 0 && n > 0 &&
+         256 * k * 2 < (1ull << 31) && 136 * n * out_size < (1ull << 31) && 32 * n * 2 < (1ull << 31);
+}
+}  // namespace gasm
+
+// Batch index = blockIdx.y (element strides sa, sb, sc).
+template <int DT, int DT_OUT>
+__global__ void __launch_bounds__(gasm::NT, 1)
+gemm_asm_256(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, void* __restrict__ C,
+             uint32_t M, uint32_t N, uint32_t K, uint64_t sa, uint64_t sb, uint64_t sc) {
+  static_assert(DT == kBF16 || DT == kF16, "16-bit operands");
+  constexpr uint32_t OSZ = (DT_OUT == kF32) ? 4 : 2;
+  uint32_t tm, tn;
+  gemm::tile_coords(blockIdx.x, M / 256, N / 256, tm, tn);
+  A += blockIdx.y * sa;
+  B += blockIdx.y * sb;
+  char* Cb = static_cast<char*>(C) + static_cast<size_t>(blockIdx.y) * sc * OSZ;
+  u32x4* arena = lds::dma_lds_arena<131072>();
+  typedef __attribute__((address_space(3))) const void* lds_cptr;
+  const uint32_t lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_cptr)(arena)));
+  const uint32_t m0 = tm * 256, n0 = tn * 256;
+  const uint32_t lane = threadIdx.x & 63;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t wm = wave >> 1, wn = wave & 1;
+  const uint32_t l32 = lane & 31, g = lane >> 5;
+  const uint64_t abase = reinterpret_cast<uint64_t>(A + static_cast<size_t>(m0) * K);
+  const uint64_t bbase = reinterpret_cast<uint64_t>(B + n0);
+  const uint64_t cbase = reinterpret_cast<uint64_t>(
+      Cb + (static_cast<size_t>(m0 + wm * 128) * N + n0 + wn * 128) * OSZ);
+  // A double stage [256 r][8 chunks]: chunk c of row r at c ^ sw(r)
+  auto swa = [](uint32_t r) { return (r & 7) ^ ((r >> 3) & 1); };
+  // DMA: A unit j of wave w = rows 64 w + 8 j + lane / 8, position lane % 8 (units 0
+  // and 1 here; the program derives the others); B unit j = k rows 2 (4 w + j) +
+  // lane / 32, position lane % 32 holding chunk (lane % 32) ^ 4 (k & 3).
+  uint32_t aoff[2], boff[4], ra[4], rb[4];
+#pragma unroll
+  for (uint32_t j = 0; j < 2; ++j) {
+    const uint32_t row = 64 * wave + 8 * j + lane / 8;
+    aoff[j] = row * K * 2 + (((lane & 7) ^ swa(row)) << 4);
+  }
+#pragma unroll
+  for (uint32_t j = 0; j < 4; ++j) {
+    const uint32_t kr = 2 * (4 * wave + j) + lane / 32;
+    boff[j] = kr * N * 2 + (((lane & 31) ^ (4 * (kr & 3))) << 4);
+  }
+  // Fragment reads.  A (k half h, sub-step ks): lane reads row 128 wm + 32 mi + l32,
+  // chunk 4 h + 2 ks + g (mi as an immediate: 4 KB per 32 rows).
+#pragma unroll
+  for (uint32_t h = 0; h < 2; ++h)
+#pragma unroll
+    for (uint32_t ks = 0; ks < 2; ++ks) {
+      const uint32_t row = wm * 128 + l32;
+      ra[2 * h + ks] = row * 128 + (((4 * h + 2 * ks + g) ^ swa(row)) << 4);
+    }
+  // B^T: lane (q, i) of a 16-lane group reads k rows 8 (q >> 1) + (i >> 2) (+4, +16,
+  // +20 as immediates) at column n = 128 wn + 32 ni + 16 (q & 1) + 4 (i & 3).
+  {
+    const uint32_t q = lane >> 4, i = lane & 15;
+    const uint32_t k0 = 8 * (q >> 1) + (i >> 2);
+#pragma unroll
+    for (uint32_t ni = 0; ni < 4; ++ni) {
+      const uint32_t n = wn * 128 + ni * 32 + 16 * (q & 1) + 4 * (i & 3);
+      rb[ni] = k0 * 512 + (((n >> 3) ^ (4 * (k0 & 3))) << 4) + (n & 7) * 2;
+    }
+  }
+  const uint32_t coff = ((4 * g) * N + l32) * OSZ;
+  const uint32_t nk = K / 32, bstep = 64 * N, nstride = N * OSZ, arow8 = 16 * K;
+  const uint32_t ldsa = lds + wave * 8192, ldsb = lds + 65536 + wave * 4096;
+#define TH_GEMM_ASM_OPS(STR)                                                                    \
+  asm volatile(STR                                                                              \
+               :                                                                                \
+               : "v"(aoff[0]), "v"(aoff[1]), "v"(boff[0]), "v"(boff[1]), "v"(boff[2]),         \
+                 "v"(boff[3]), "v"(ra[0]), "v"(ra[1]), "v"(ra[2]), "v"(ra[3]), "v"(rb[0]),      \
+                 "v"(rb[1]), "v"(rb[2]), "v"(rb[3]), "v"(coff), "s"(abase), "s"(bbase),         \
+                 "s"(cbase), "s"(nk), "s"(lds), "s"(ldsa), "s"(ldsb), "s"(bstep), "s"(nstride), \
+                 "s"(arow8)                                                                     \
+               : TH_GEMM_ASM_CLOBBERS, "vcc", "scc", "memory")
+  if constexpr (DT == kBF16) {
+    if constexpr (DT_OUT == kF32) TH_GEMM_ASM_OPS(TH_GEMM_ASM_BF16_F32);
+    else if constexpr (DT_OUT == kBF16) TH_GEMM_ASM_OPS(TH_GEMM_ASM_BF16_BF16);
+    else TH_GEMM_ASM_OPS(TH_GEMM_ASM_BF16_F16);
+  } else {
+    if constexpr (DT_OUT == kF32) TH_GEMM_ASM_OPS(TH_GEMM_ASM_F16_F32);
+    else if constexpr (DT_OUT == kBF16) TH_GEMM_ASM_OPS(TH_GEMM_ASM_F16_BF16);
+    else TH_GEMM_ASM_OPS(TH_GEMM_ASM_F16_F16);
+  }
+#undef TH_GEMM_ASM_OPS
+}
+}  // namespace th

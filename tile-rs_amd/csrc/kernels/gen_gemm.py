@@ -1,0 +1,255 @@
+"""Generate the dense 16-bit GEMM tile program (gfx950 assembly for one inline-asm
+statement; gemm_asm.hpp wraps it).
+
+Semantics: C = A . B with f32 accumulation (`linalg.fill 0` + `linalg.matmul`,
+/root/reference/crates/rustc_codegen_tile/src/mlir_to_linalg.rs:1345-1393), A row-major
+M x K, B row-major K x N, bf16 or f16 operands, C f32 or 16-bit (one rounding, RNE).
+
+Workgroup = 4 waves = one 256 x 256 tile; wave (wm, wn) = (w / 2, w % 2) owns rows
+128 wm .. +127 and columns 128 wn .. +127 as 4 x 4 blocks of 32 x 32, accumulated in
+a[0:255] (block (mi, ni) at a[16 (4 mi + ni)]) with v_mfma_f32_32x32x16.  One wave
+per SIMD: the 128 x 128 wave tile reads 64 KB of LDS fragments per 32-deep K step for
+the workgroup, a third less than eight waves of 128 x 64.
+
+K advances 32 per step.  LDS (128 KB), filled by global_load_lds_dwordx4 only:
+  A ring: 2 double stages x 32 KB at 0.  A double stage holds 64 k of the tile's 256
+          rows, [256 r][8 chunks of 16 B]: every DMA lane group reads whole 128-byte
+          rows of A (with 32-k stages each row would be half a cache line).  Chunk c
+          of row r sits at c ^ sw(r), sw(r) = (r & 7) ^ ((r >> 3) & 1), so the
+          ds_read_b128 of 16 lanes (16 rows, one chunk) covers all 64 banks.
+  B ring: 4 stages x 16 KB at 64 KB, [32 k][32 chunks]: chunk c of k-row r at
+          c ^ 4 (r & 3); read as B^T with ds_read_b64_tr_b16.
+Step k uses A double stage k/2 (buffer (k/2) % 2, k half k % 2) and B stage k
+(buffer k % 4).
+
+Schedule of step k (every wave):
+  s_waitcnt lgkmcnt(0)        this wave's fragments of step k have landed
+  s_waitcnt vmcnt(n)          this wave's DMA share of B stage k+1 and of A double
+                              stage (k+1)/2 has landed (n: loads issued after them)
+  s_barrier                   -> every share of those stages is in LDS, and every
+                              wave has finished reading step k's fragments
+  32 MFMAs of step k, with in between: the 24 fragment reads of step k+1 (into the
+  other register set) and the DMA issues: B stage k+4 into buffer k % 4 (free: step
+  k's reads are done) and, at odd k, A double stage (k+3)/2 into buffer ((k+3)/2) % 2
+  (free: its last reader, step k, is done).
+Per-wave issue order, steady state: even k: B(k+4); odd k: A((k+3)/2), B(k+4).  At
+the wait of even k the loads issued after B(k+1) are B(k+2), A(k/2+1), B(k+3) (16);
+at odd k those after A((k+1)/2) are B(k+2), B(k+3) (8).  The prologue issues B0, A0,
+B1, B2, A1, B3, which is the same sequence, so the steady waits hold from step 0.  A
+double stage is issued two steps before its first reader, a B stage three.  The loop
+runs in groups of four steps (static buffers); the last group issues no DMA and waits
+16, 4, 0.
+
+Registers: operands in v0-v15 and s-registers chosen by the compiler; v16-v19 A read
+bases [h][ks], v20-v23 B read bases [ni], v24-v31 A DMA offsets, v32-v47 epilogue,
+v[128:191] and v[192:255] the two fragment sets (A (ks, mi) at +4 (4 ks + mi), B
+(ks, ni) at +32 + 4 (4 ks + ni)); s[48:49] A pointer, s[50:51] B pointer, s[52:53] C
+base, s54 loop count, s55 saved m0, s56-s57 temps.
+
+Usage: python gen_gemm.py <out.inc>   (run by the library build)
+"""
+import sys
+from pathlib import Path
+
+OPN = ["aoffE", "aoffO", "boff0", "boff1", "boff2", "boff3", "ra00", "ra01", "ra10", "ra11",
+       "rb0", "rb1", "rb2", "rb3", "coff",
+       "abase", "bbase", "cbase", "nk", "lds", "ldsa", "ldsb", "bstep", "nstride", "arow8"]
+OP = {n: i for i, n in enumerate(OPN)}
+
+
+def o(n):
+    return f"%{OP[n]}"
+
+
+SA_, SB_, SC_ = "s[48:49]", "s[50:51]", "s[52:53]"
+SCNT, SROW = "s54", "s57"
+VA = [[16, 17], [18, 19]]        # A read bases [h][ks]
+VB = [20, 21, 22, 23]            # B read bases [ni]
+VAO = list(range(24, 32))        # A DMA offsets, unit j = 0..7
+FR = [128, 192]                  # fragment register sets
+
+
+def afr(s, ks, mi):
+    return FR[s] + 4 * (4 * ks + mi)
+
+
+def bfr(s, ks, ni):
+    return FR[s] + 32 + 4 * (4 * ks + ni)
+
+
+def acc(mi, ni):
+    b = 16 * (4 * mi + ni)
+    return f"a[{b}:{b + 15}]"
+
+
+def reads(k, s):
+    """Fragment reads of step k (mod 4) into register set s: B^T first (16
+    transposed 8-byte reads), then A (8 x 16 bytes)."""
+    ab, h, bb = (k // 2) % 2, k % 2, k % 4
+    out = []
+    for ks in range(2):
+        for ni in range(4):
+            f = bfr(s, ks, ni)
+            base = bb * 16384 + ks * 8192
+            out.append(f"ds_read_b64_tr_b16 v[{f}:{f + 1}], v{VB[ni]} offset:{base}")
+            out.append(f"ds_read_b64_tr_b16 v[{f + 2}:{f + 3}], v{VB[ni]} offset:{base + 2048}")
+    for ks in range(2):
+        for mi in range(4):
+            f = afr(s, ks, mi)
+            out.append(f"ds_read_b128 v[{f}:{f + 3}], v{VA[h][ks]} offset:{ab * 32768 + 4096 * mi}")
+    return out
+
+
+def dma_b(buf):
+    """This wave's four 1 KB units of the next B stage into buffer buf.  The LDS
+    destination (m0) needs one wait state after it is written."""
+    out = []
+    for j in range(4):
+        out.append([f"s_add_u32 m0, {o('ldsb')}, {buf * 16384 + j * 1024}", "s_nop 0",
+                    f"global_load_lds_dwordx4 {o('boff' + str(j))}, {SB_}"])
+    out.append([f"s_add_u32 s50, s50, {o('bstep')}", "s_addc_u32 s51, s51, 0"])
+    return out
+
+
+def dma_a(buf):
+    """This wave's eight 1 KB units (8 rows x 128 B each) of the next A double stage."""
+    out = []
+    for j in range(8):
+        out.append([f"s_add_u32 m0, {o('ldsa')}, {buf * 32768 + j * 1024}", "s_nop 0",
+                    f"global_load_lds_dwordx4 v{VAO[j]}, {SA_}"])
+    out.append(["s_add_u32 s48, s48, 128", "s_addc_u32 s49, s49, 0"])
+    return out
+
+
+def mfmas(s, mn):
+    out = []
+    for ks in range(2):
+        for mi in range(4):
+            for ni in range(4):
+                a, b = afr(s, ks, mi), bfr(s, ks, ni)
+                out.append(f"{mn} {acc(mi, ni)}, v[{a}:{a + 3}], v[{b}:{b + 3}], {acc(mi, ni)}")
+    return out
+
+
+def step(k4, mn, vm, rd, dm, bar=True):
+    """Step k with k % 4 == k4.  The reads of step k+1 are spread evenly over the 32
+    MFMAs, the DMA groups start after the first MFMA and spread likewise."""
+    out = ["s_waitcnt lgkmcnt(0)"]
+    if vm is not None:
+        out.append(f"s_waitcnt vmcnt({vm})")
+    if bar:
+        out.append("s_barrier")
+    M = mfmas(k4 & 1, mn)
+    R = reads((k4 + 1) % 4, (k4 + 1) & 1) if rd else []
+    D = []
+    if dm:
+        if k4 % 2 == 1:
+            D += dma_a(((k4 + 3) // 2) % 2)
+        D += dma_b(k4)
+    slots = [[] for _ in M]
+    for j, r in enumerate(R):
+        slots[(j * len(M)) // len(R)].append([r])
+    for j, d in enumerate(D):
+        slots[min(len(M) - 1, (j * len(M)) // len(D) + 1)].append(d)
+    for m, sl in zip(M, slots):
+        out.append(m)
+        for g in sl:
+            out.extend(g)
+    return out
+
+
+def epilogue(out_dt):
+    """C stores straight from the accumulators (f32) or through a packed conversion
+    (16-bit).  Accumulator r of a lane in a 32x32 block is row 8 (r/4) + 4 g + r % 4,
+    column l32: per store instruction the 32 lanes of a half write 32 consecutive
+    columns of one row.  coff = this lane's byte offset (row 4 g, column l32)."""
+    L = ["s_nop 7", "s_nop 7", "s_nop 7", "s_nop 7"]   # MFMA results -> readers
+    if out_dt == "f32":
+        for mi in range(4):
+            for r in range(16):
+                row = mi * 32 + 8 * (r >> 2) + (r & 3)
+                L.append(f"s_mul_i32 {SROW}, {o('nstride')}, {row}")
+                L.append(f"v_add_u32 v32, {SROW}, {o('coff')}")
+                for ni in range(4):
+                    L.append(f"global_store_dword v32, a{16 * (4 * mi + ni) + r}, {SC_} "
+                             f"offset:{128 * ni} nt")
+        return L
+    cvt = "v_cvt_pk_bf16_f32" if out_dt == "bf16" else "v_cvt_pk_f16_f32"
+    for mi in range(4):
+        for r in range(0, 16, 2):
+            row = mi * 32 + 8 * (r >> 2) + (r & 3)     # rows row and row + 1
+            L.append(f"s_mul_i32 {SROW}, {o('nstride')}, {row}")
+            L.append(f"v_add_u32 v32, {SROW}, {o('coff')}")
+            L.append(f"v_add_u32 v33, {o('nstride')}, v32")
+            for ni in range(4):
+                a = 16 * (4 * mi + ni) + r
+                t = 34 + 3 * ni
+                L += [f"v_accvgpr_read_b32 v{t}, a{a}", f"v_accvgpr_read_b32 v{t + 1}, a{a + 1}",
+                      f"{cvt} v{t + 2}, v{t}, v{t + 1}"]
+            for ni in range(4):
+                t = 34 + 3 * ni
+                L += [f"global_store_short v32, v{t + 2}, {SC_} offset:{64 * ni} nt",
+                      f"global_store_short_d16_hi v33, v{t + 2}, {SC_} offset:{64 * ni} nt"]
+    return L
+
+
+def program(dt, out_dt):
+    mn = "v_mfma_f32_32x32x16_bf16" if dt == "bf16" else "v_mfma_f32_32x32x16_f16"
+    L = ["s_mov_b32 s55, m0",
+         f"s_mov_b64 {SA_}, {o('abase')}", f"s_mov_b64 {SB_}, {o('bbase')}",
+         f"s_mov_b64 {SC_}, {o('cbase')}"]
+    for h in range(2):
+        for ks in range(2):
+            L.append(f"v_add_u32 v{VA[h][ks]}, {o('lds')}, {o('ra' + str(h) + str(ks))}")
+    for ni in range(4):
+        L.append(f"v_add_u32 v{VB[ni]}, {o('lds')}, {o('rb' + str(ni))}")
+        L.append(f"v_add_u32 v{VB[ni]}, 0x10000, v{VB[ni]}")
+    # A unit j of wave w holds rows 64 w + 8 j .. +7: the swizzle depends on j only
+    # through its parity, so units j and j & 1 differ by (j & ~1) x 8 rows
+    for j in range(8):
+        src = o("aoffE") if j % 2 == 0 else o("aoffO")
+        L.append(f"s_mul_i32 {SROW}, {o('arow8')}, {j & ~1}")
+        L.append(f"v_add_u32 v{VAO[j]}, {SROW}, {src}")
+    L += [f"v_accvgpr_write_b32 a{r}, 0" for r in range(256)]
+    for g in dma_b(0) + dma_a(0) + dma_b(1) + dma_b(2) + dma_a(1) + dma_b(3):
+        L.extend(g)
+    # B0 and A0 landed: loads issued after A0 are B1, B2, A1, B3 (4 + 4 + 8 + 4)
+    L += ["s_waitcnt vmcnt(20)", "s_barrier"] + reads(0, 0)
+    # steady groups: nk / 4 - 1 (nk >= 8, a multiple of 4: checked by the caller)
+    L += [f"s_lshr_b32 {SCNT}, {o('nk')}, 2", f"s_sub_u32 {SCNT}, {SCNT}, 1",
+          f"s_cmp_eq_u32 {SCNT}, 0", "s_cbranch_scc1 L_tail_%=", "L_top_%=:"]
+    for k4 in range(4):
+        L += step(k4, mn, 16 if k4 % 2 == 0 else 8, True, True)
+    L += [f"s_sub_u32 {SCNT}, {SCNT}, 1", f"s_cmp_lg_u32 {SCNT}, 0", "s_cbranch_scc1 L_top_%=",
+          "L_tail_%=:"]
+    L += step(0, mn, 16, True, False)
+    L += step(1, mn, 4, True, False)
+    L += step(2, mn, 0, True, False)
+    L += step(3, mn, None, False, False, bar=False)
+    L += epilogue(out_dt)
+    L += ["s_waitcnt vmcnt(0)", "s_mov_b32 m0, s55"]
+    return L
+
+
+def cstr(lines):
+    return "\\n\\t".join(lines)
+
+
+def main(path):
+    lines = ["// Generated by gen_gemm.py: 16-bit GEMM tile program (gfx950 asm).", "#pragma once"]
+    for dt in ("bf16", "f16"):
+        for out_dt in ("f32", "bf16", "f16"):
+            lines.append(f'#define TH_GEMM_ASM_{dt.upper()}_{out_dt.upper()} '
+                         f'"{cstr(program(dt, out_dt))}"')
+    clob = ([f'"v{k}"' for k in range(16, 256)] + [f'"a{k}"' for k in range(256)] +
+            [f'"s{k}"' for k in range(48, 58)])
+    lines.append("#define TH_GEMM_ASM_CLOBBERS " + ",".join(clob))
+    text = "\n".join(lines) + "\n"
+    p = Path(path)
+    if not p.exists() or p.read_text() != text:
+        p.parent.mkdir(parents=True, exist_ok=True)
+        p.write_text(text)
+
+
+if __name__ == "__main__":
+    main(sys.argv[1])

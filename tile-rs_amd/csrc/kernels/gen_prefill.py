@@ -360,13 +360,16 @@ class Gen:
         ex1 = ["s_mov_b64 exec, s[76:77]"] if masked_exec else []
         groups = [[f"v_add_u32 {DK}, s63, {o('krow')}", f"v_min_u32 {DK}, {o('kvlast')}, {DK}",
                    f"v_lshl_add_u32 {DK}, {DK}, {self.SHIFT}, {o('kcol')}", f"s_add_u32 s64, s62, {o('wave2k')}"]]
+        # an LDS DMA reads m0 one wait state after it is written (the exec write, when
+        # there is one, is that wait state)
+        w0 = ex0 or ["s_nop 0"]
         for j in range(self.NLDK):
-            groups.append([f"s_add_u32 m0, s64, {1024 * j}"] + ex0 +
+            groups.append([f"s_add_u32 m0, s64, {1024 * j}"] + w0 +
                           [f"global_load_lds_dwordx4 {DK}, s[{48 + 2 * j}:{49 + 2 * j}]"] + ex1)
         for j in range(self.NLDK):
             groups.append([f"v_add3_u32 {DV[j]}, s63, {o('vrow')}, {4 * j}", f"v_min_u32 {DV[j]}, {o('kvlast')}, {DV[j]}",
                            f"v_lshl_add_u32 {DV[j]}, {DV[j]}, {self.SHIFT}, {o('vcol')}"])
-            groups.append([f"s_add_u32 m0, s64, {self.KB + 1024 * j}"] + ex0 +
+            groups.append([f"s_add_u32 m0, s64, {self.KB + 1024 * j}"] + w0 +
                           [f"global_load_lds_dwordx4 {DV[j]}, s[56:57]"] + ex1)
         return groups
 

@@ -20,6 +20,7 @@
 #include "kernels/prefill_asm.hpp"
 #include "kernels/common.hpp"
 #include "kernels/gemm.hpp"
+#include "kernels/gemm_asm.hpp"
 #include "kernels/gemm_f32.hpp"
 #include "kernels/norm.hpp"
 #include "kernels/softmax.hpp"
@@ -244,6 +245,17 @@ bool gemm_dma() {
   return v;
 }
 
+// Whole-tile shapes with row-major B run on the generated-assembly kernel
+// (gemm_asm.hpp) unless TILERS_HIP_GEMM_ASM=0 (a debugging switch: the LDS-DMA
+// kernel, which gives the same bits, then runs them).
+bool gemm_asm() {
+  static const bool v = [] {
+    const char* e = std::getenv("TILERS_HIP_GEMM_ASM");
+    return !(e && std::atoi(e) == 0);
+  }();
+  return v;
+}
+
 // Split-K for shapes with too few 256 x 256 tiles to fill the chip (small M:
 // decode-time projections).  S slices of K (each a multiple of 32, at least 256
 // deep, S a divisor of K / 32) run as the batch dimension of the DMA kernel,
@@ -300,6 +312,13 @@ int gemm_mfma_go(const GemmArgs& g, dim3 grid) {
   if (gemm_dma() && out_vec && g.k % th::gemm::DBK == 0) {
     const uint32_t S = splitk_slices(g, grid.x);
     if (S > 1) return gemm_splitk<DT, DTO, EPI, BT>(g, grid.x, S);
+    if constexpr (!BT && EPI == th::gemm::kEpiStore) {
+      if (gemm_asm() && th::gasm::fits(g.m, g.n, g.k, static_cast<int>(OSZ))) {
+        hipLaunchKernelGGL((th::gemm_asm_256<DT, DTO>), grid, dim3(th::gasm::NT), 0, g.s, A, B,
+                           g.c, g.m, g.n, g.k, g.sa, g.sb, g.sc);
+        return launch_status("matmul (MFMA asm) launch");
+      }
+    }
     hipLaunchKernelGGL((th::gemm_dma_256<DT, DTO, BT, th::gemm::DBK, th::gemm::NSTAGE,
                                          th::gemm::DWAVES, EPI>),
                        grid, dim3(64 * th::gemm::DWAVES), 0, g.s, A, B, g.c, g.m, g.n, g.k, g.sa,

@@ -76,7 +76,7 @@ def _stamp_files() -> list[Path]:
 
 def source_stamp() -> str:
     """First 16 hex digits of a SHA-256 over csrc/ (kernels, emitter, runtime, the
-    prefill generator and its generated include), include/, the example MLIR and
+    prefill and GEMM generators and their generated includes), include/, the example MLIR and
     the reference's hot-path MLIR test inputs that are compiled for the GPU tests."""
     h = hashlib.sha256()
     for p in _stamp_files():
@@ -247,6 +247,7 @@ def build_examples(verbose: bool = False) -> list:
 GENERATED = [
     # (generator script, output) -- generated device code included by ops.hip
     (CSRC / "kernels" / "gen_prefill.py", CSRC / "kernels" / "gen" / "prefill_asm.inc"),
+    (CSRC / "kernels" / "gen_gemm.py", CSRC / "kernels" / "gen" / "gemm_asm.inc"),
 ]
 
 
