@@ -144,6 +144,22 @@ def test_matmul_launch_shapes_follow_the_entry():
     assert "__launch_bounds__(256) matmul_bf16_acc_f32(" in src
 
 
+def test_whole_tile_matmuls_lower_to_the_assembly_entry():
+    """The config GEMMs (4096^3 bf16 -> f32; 8192x4096x14336 f16 -> f16): whole 256x256
+    tiles, row-major B, K a multiple of 128 -> the generated-assembly entry, 256-thread
+    workgroups (one per CU), one per tile.  A K of 96 or an N of 384 keeps the DMA entry."""
+    src = th.emit((EXAMPLES / "config_gemms.mlir").read_text()).source
+    assert "th::entry::gemm_asm<th::kBF16, th::kF32>(" in src
+    assert "th::entry::gemm_asm<th::kF16, th::kF16>(" in src
+    assert "__launch_bounds__(256, 1) gemm_4096_bf16_acc_f32(" in src
+    assert "__th_desc_gemm_4096_bf16_acc_f32 = {th::kLaunchDescMagic, 256u, 256u, 1u," in src
+    assert "__th_desc_mlp_up_f16 = {th::kLaunchDescMagic, 256u, 1792u, 1u," in src
+    assert "th::entry::gemm_dma" not in src
+    k96 = (EXAMPLES / "matmul_bf16.mlir").read_text().replace("constant(256 : i32)",
+                                                                "constant(96 : i32)")
+    assert "th::entry::gemm_dma<" in th.emit(k96).source
+
+
 def test_matmul_shape_and_tile_offsets_are_exact():
     out = th.emit((EXAMPLES / "matmul_bf16.mlir").read_text())
     # M=512 K=256 N=384: th::entry::gemm_dma(..., M, N, K, tiles); 2 x 2 workgroups per tile

@@ -25,18 +25,19 @@ __host__ __device__ constexpr bool fits(uint64_t m, uint64_t n, uint64_t k, int 
 }
 }  // namespace gasm
 
-// Batch index = blockIdx.y (element strides sa, sb, sc).
+// Tile (tm, tn) of C = A . B by a workgroup of gasm::NT threads (launched with at most
+// one workgroup per CU: the program uses all 512 registers of each lane).  A, B
+// 16-byte aligned, C aligned to its element; gasm::fits(M, N, K, sizeof C) holds.  A
+// workgroup that runs several tiles passes a barrier between them (the next tile's
+// DMA refills buffers the previous one's last reads used).
 template <int DT, int DT_OUT>
-__global__ void __launch_bounds__(gasm::NT, 1)
-gemm_asm_256(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, void* __restrict__ C,
-             uint32_t M, uint32_t N, uint32_t K, uint64_t sa, uint64_t sb, uint64_t sc) {
+__device__ __forceinline__ void gemm_asm_tile(const uint16_t* __restrict__ A,
+                                              const uint16_t* __restrict__ B,
+                                              void* __restrict__ C, uint32_t M, uint32_t N,
+                                              uint32_t K, uint32_t tm, uint32_t tn) {
   static_assert(DT == kBF16 || DT == kF16, "16-bit operands");
   constexpr uint32_t OSZ = (DT_OUT == kF32) ? 4 : 2;
-  uint32_t tm, tn;
-  gemm::tile_coords(blockIdx.x, M / 256, N / 256, tm, tn);
-  A += blockIdx.y * sa;
-  B += blockIdx.y * sb;
-  char* Cb = static_cast<char*>(C) + static_cast<size_t>(blockIdx.y) * sc * OSZ;
+  char* Cb = static_cast<char*>(C);
   u32x4* arena = lds::dma_lds_arena<131072>();
   typedef __attribute__((address_space(3))) const void* lds_cptr;
   const uint32_t lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds_cptr)(arena)));
@@ -107,5 +108,18 @@ gemm_asm_256(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, voi
     else TH_GEMM_ASM_OPS(TH_GEMM_ASM_F16_F16);
   }
 #undef TH_GEMM_ASM_OPS
+}
+
+// Batch index = blockIdx.y (element strides sa, sb, sc).
+template <int DT, int DT_OUT>
+__global__ void __launch_bounds__(gasm::NT, 1)
+gemm_asm_256(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, void* __restrict__ C,
+             uint32_t M, uint32_t N, uint32_t K, uint64_t sa, uint64_t sb, uint64_t sc) {
+  constexpr uint32_t OSZ = (DT_OUT == kF32) ? 4 : 2;
+  uint32_t tm, tn;
+  gemm::tile_coords(blockIdx.x, M / 256, N / 256, tm, tn);
+  gemm_asm_tile<DT, DT_OUT>(A + blockIdx.y * sa, B + blockIdx.y * sb,
+                            static_cast<char*>(C) + static_cast<size_t>(blockIdx.y) * sc * OSZ, M,
+                            N, K, tm, tn);
 }
 }  // namespace th

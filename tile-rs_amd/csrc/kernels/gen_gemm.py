@@ -29,9 +29,9 @@ Schedule of step k (every wave):
   s_barrier                   -> every share of those stages is in LDS, and every
                               wave has finished reading step k's fragments
   32 MFMAs of step k, with in between: the 24 fragment reads of step k+1 (into the
-  other register set) and the DMA issues: B stage k+4 into buffer k % 4 (free: step
-  k's reads are done) and, at odd k, A double stage (k+3)/2 into buffer ((k+3)/2) % 2
-  (free: its last reader, step k, is done).
+  other register set, two per MFMA from the first) and the DMA issues: B stage k+4
+  into buffer k % 4 (free: step k's reads are done) and, at odd k, A double stage
+  (k+3)/2 into buffer ((k+3)/2) % 2 (free: its last reader, step k, is done).
 Per-wave issue order, steady state: even k: B(k+4); odd k: A((k+3)/2), B(k+4).  At
 the wait of even k the loads issued after B(k+1) are B(k+2), A(k/2+1), B(k+3) (16);
 at odd k those after A((k+1)/2) are B(k+2), B(k+3) (8).  The prologue issues B0, A0,
@@ -83,20 +83,20 @@ def acc(mi, ni):
 
 
 def reads(k, s):
-    """Fragment reads of step k (mod 4) into register set s: B^T first (16
-    transposed 8-byte reads), then A (8 x 16 bytes)."""
+    """Fragment reads of step k (mod 4) into register set s: A (8 x 16 bytes), then
+    B^T (16 transposed 8-byte reads)."""
     ab, h, bb = (k // 2) % 2, k % 2, k % 4
     out = []
+    for ks in range(2):
+        for mi in range(4):
+            f = afr(s, ks, mi)
+            out.append(f"ds_read_b128 v[{f}:{f + 3}], v{VA[h][ks]} offset:{ab * 32768 + 4096 * mi}")
     for ks in range(2):
         for ni in range(4):
             f = bfr(s, ks, ni)
             base = bb * 16384 + ks * 8192
             out.append(f"ds_read_b64_tr_b16 v[{f}:{f + 1}], v{VB[ni]} offset:{base}")
             out.append(f"ds_read_b64_tr_b16 v[{f + 2}:{f + 3}], v{VB[ni]} offset:{base + 2048}")
-    for ks in range(2):
-        for mi in range(4):
-            f = afr(s, ks, mi)
-            out.append(f"ds_read_b128 v[{f}:{f + 3}], v{VA[h][ks]} offset:{ab * 32768 + 4096 * mi}")
     return out
 
 
@@ -132,8 +132,9 @@ def mfmas(s, mn):
 
 
 def step(k4, mn, vm, rd, dm, bar=True):
-    """Step k with k % 4 == k4.  The reads of step k+1 are spread evenly over the 32
-    MFMAs, the DMA groups start after the first MFMA and spread likewise."""
+    """Step k with k % 4 == k4.  The reads of step k+1 go two after each of the first
+    12 MFMAs; the DMA groups start after the first MFMA and spread over the step
+    (measured against one read per MFMA and B^T reads first: 1 us less at 4096^3)."""
     out = ["s_waitcnt lgkmcnt(0)"]
     if vm is not None:
         out.append(f"s_waitcnt vmcnt({vm})")
@@ -148,7 +149,7 @@ def step(k4, mn, vm, rd, dm, bar=True):
         D += dma_b(k4)
     slots = [[] for _ in M]
     for j, r in enumerate(R):
-        slots[(j * len(M)) // len(R)].append([r])
+        slots[j // 2].append([r])
     for j, d in enumerate(D):
         slots[min(len(M) - 1, (j * len(M)) // len(D) + 1)].append(d)
     for m, sl in zip(M, slots):

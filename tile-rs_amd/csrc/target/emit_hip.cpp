@@ -875,14 +875,21 @@ bool matmul_entry(const Kernel& k, const TileVal& mm, const Store& st, const cha
   const int osz = out == F32 ? 4 : 2;
   const bool dma = mfma && K % 32 == 0 && N % 8 == 0 && (st.dst.offset * osz) % 16 == 0 &&
                    (!up || (up->src.offset * osz) % 16 == 0);
+  // whole 256 x 256 tiles, row-major B, plain store: the generated-assembly program
+  // (the shapes th::gasm::fits accepts: K in groups of four 32-deep steps, at least
+  // two, and per-lane byte offsets within 32 bits)
+  const bool gasm = dma && !bt && !up && M > 0 && N > 0 && M % 256 == 0 && N % 256 == 0 &&
+                    K % 128 == 0 && K >= 256 && 512LL * K < (1LL << 31) &&
+                    136LL * N * osz < (1LL << 31) && 64LL * N < (1LL << 31);
   os << "matmul " << M << "x" << K << "x" << N << (bt ? " (B transposed)" : "") << " " << dt_name(in)
      << " -> " << dt_name(out) << (up ? " with silu*mul epilogue" : "")
-     << (dma ? " -> th::entry::gemm_dma (MFMA, LDS-DMA)"
+     << (gasm ? " -> th::entry::gemm_asm (MFMA, generated assembly)"
+             : dma ? " -> th::entry::gemm_dma (MFMA, LDS-DMA)"
              : mfma ? " -> th::entry::gemm (MFMA)"
              : in == F32 ? " -> th::entry::gemm_f32 (fp32 MFMA)" : " -> th::entry::gemm_fma")
      << "\n";
-  const unsigned threads = dma ? 512 : 256;
-  signature(os, k, threads, {});
+  const unsigned threads = gasm ? 256 : dma ? 512 : 256;
+  signature(os, k, threads, {}, gasm ? 1 : 0);
   const std::string tmpl = std::string(dt_enum(in)) + ", " + dt_enum(out) + ", " +
                            (bt ? "true" : "false") + ", " + epi;
   // pipelined_for(depth >= 2): the LDS ring depth (4 or 5 stages; the staged
@@ -891,7 +898,12 @@ bool matmul_entry(const Kernel& k, const TileVal& mm, const Store& st, const cha
   const std::string tmpl_dma = ns ? tmpl + ", " + std::to_string(ns) : tmpl;
   const std::string tail = up ? ", th_tiles, " + view_ptr(*up, dt_ctype(out)) + ");\n}\n"
                               : ", th_tiles);\n}\n";
-  if (dma) {
+  if (gasm) {
+    os << "  th::entry::gemm_asm<" << dt_enum(in) << ", " << dt_enum(out) << ">("
+       << view_ptr(a, "uint16_t") << ", " << view_ptr(b, "uint16_t") << ", "
+       << store_ptr(st, dt_ctype(out)) << ", " << u(M) << ", " << u(N) << ", " << u(K) << tail;
+    desc(os, k, threads, static_cast<unsigned>((M / 256) * (N / 256)), 1);
+  } else if (dma) {
     os << "  th::entry::gemm_dma<" << tmpl_dma << ">(" << view_ptr(a, "uint16_t") << ", "
        << view_ptr(b, "uint16_t") << ", " << store_ptr(st, dt_ctype(out)) << ", " << u(M) << ", "
        << u(N) << ", " << u(K) << tail;
