@@ -2,13 +2,14 @@
 // M and N multiples of 256 and K a multiple of 128 (at least 256).
 //
 // The tile program is generated gfx950 assembly (gen_gemm.py, run by the build into
-// kernels/gen/gemm_asm.inc): four waves of 128 x 128 with AGPR accumulators, A fetched
+// kernels/gen/gemm_asm.inc): four waves of 128 x 128 with AGPR accumulators
+// (v_mfma_f32_16x16x32), A fetched
 // in 64-deep double stages (whole 128-byte rows per DMA lane group), B in 32-deep
 // stages; layouts, schedule and waits are described in gen_gemm.py.  This wrapper maps
 // the workgroup to its tile and computes the per-lane and per-wave operands.
-// Semantics: C = A . B with f32 accumulation in k order per 32x32x16 MFMA
-// (crates/rustc_codegen_tile/src/mlir_to_linalg.rs:1345-1393), C rounded once (RNE) to
-// its dtype; the K order is that of gemm_dma_256, so both give the same bits.
+// Semantics: C = A . B with f32 accumulation (crates/rustc_codegen_tile/src/
+// mlir_to_linalg.rs:1345-1393), C rounded once (RNE) to its dtype; K runs in the same
+// order as in gemm_dma_256, and both give the same bits (checked on both config shapes).
 #pragma once
 
 #include "gemm.hpp"
@@ -45,7 +46,6 @@ __device__ __forceinline__ void gemm_asm_tile(const uint16_t* __restrict__ A,
   const uint32_t lane = threadIdx.x & 63;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t wm = wave >> 1, wn = wave & 1;
-  const uint32_t l32 = lane & 31, g = lane >> 5;
   const uint64_t abase = reinterpret_cast<uint64_t>(A + static_cast<size_t>(m0) * K);
   const uint64_t bbase = reinterpret_cast<uint64_t>(B + n0);
   const uint64_t cbase = reinterpret_cast<uint64_t>(
@@ -55,7 +55,7 @@ __device__ __forceinline__ void gemm_asm_tile(const uint16_t* __restrict__ A,
   // DMA: A unit j of wave w = rows 64 w + 8 j + lane / 8, position lane % 8 (units 0
   // and 1 here; the program derives the others); B unit j = k rows 2 (4 w + j) +
   // lane / 32, position lane % 32 holding chunk (lane % 32) ^ 4 (k & 3).
-  uint32_t aoff[2], boff[4], ra[4], rb[4];
+  uint32_t aoff[2], boff[4], ra[2], rb[4];
 #pragma unroll
   for (uint32_t j = 0; j < 2; ++j) {
     const uint32_t row = 64 * wave + 8 * j + lane / 8;
@@ -66,35 +66,35 @@ __device__ __forceinline__ void gemm_asm_tile(const uint16_t* __restrict__ A,
     const uint32_t kr = 2 * (4 * wave + j) + lane / 32;
     boff[j] = kr * N * 2 + (((lane & 31) ^ (4 * (kr & 3))) << 4);
   }
-  // Fragment reads.  A (k half h, sub-step ks): lane reads row 128 wm + 32 mi + l32,
-  // chunk 4 h + 2 ks + g (mi as an immediate: 4 KB per 32 rows).
+  // Fragment reads (16x16x32 operands).  A (k half h): lane reads row 128 wm + 16 mi +
+  // lane % 16, chunk 4 h + lane / 16 (mi as an immediate: 2 KB per 16 rows).
 #pragma unroll
-  for (uint32_t h = 0; h < 2; ++h)
-#pragma unroll
-    for (uint32_t ks = 0; ks < 2; ++ks) {
-      const uint32_t row = wm * 128 + l32;
-      ra[2 * h + ks] = row * 128 + (((4 * h + 2 * ks + g) ^ swa(row)) << 4);
-    }
-  // B^T: lane (q, i) of a 16-lane group reads k rows 8 (q >> 1) + (i >> 2) (+4, +16,
-  // +20 as immediates) at column n = 128 wn + 32 ni + 16 (q & 1) + 4 (i & 3).
+  for (uint32_t h = 0; h < 2; ++h) {
+    const uint32_t row = wm * 128 + (lane & 15);
+    ra[h] = row * 128 + (((4 * h + (lane >> 4)) ^ swa(row)) << 4);
+  }
+  // B^T: lane (q, i) = (lane / 16, lane % 16) reads k rows 8 q + (i >> 2) (+4 as an
+  // immediate) at column n = 128 wn + 16 ni + 4 (i & 3); the address is per pair of
+  // column blocks p = ni / 2 (the odd block is 32 bytes on: the swizzle leaves bit 1 of
+  // the chunk index alone).
   {
     const uint32_t q = lane >> 4, i = lane & 15;
-    const uint32_t k0 = 8 * (q >> 1) + (i >> 2);
+    const uint32_t k0 = 8 * q + (i >> 2);
 #pragma unroll
-    for (uint32_t ni = 0; ni < 4; ++ni) {
-      const uint32_t n = wn * 128 + ni * 32 + 16 * (q & 1) + 4 * (i & 3);
-      rb[ni] = k0 * 512 + (((n >> 3) ^ (4 * (k0 & 3))) << 4) + (n & 7) * 2;
+    for (uint32_t p = 0; p < 4; ++p) {
+      const uint32_t n = wn * 128 + 32 * p + 4 * (i & 3);
+      rb[p] = k0 * 512 + (((n >> 3) ^ (4 * (k0 & 3))) << 4) + (n & 7) * 2;
     }
   }
-  const uint32_t coff = ((4 * g) * N + l32) * OSZ;
+  const uint32_t coff = ((4 * (lane >> 4)) * N + (lane & 15)) * OSZ;
   const uint32_t nk = K / 32, bstep = 64 * N, nstride = N * OSZ, arow8 = 16 * K;
   const uint32_t ldsa = lds + wave * 8192, ldsb = lds + 65536 + wave * 4096;
 #define TH_GEMM_ASM_OPS(STR)                                                                    \
   asm volatile(STR                                                                              \
                :                                                                                \
                : "v"(aoff[0]), "v"(aoff[1]), "v"(boff[0]), "v"(boff[1]), "v"(boff[2]),         \
-                 "v"(boff[3]), "v"(ra[0]), "v"(ra[1]), "v"(ra[2]), "v"(ra[3]), "v"(rb[0]),      \
-                 "v"(rb[1]), "v"(rb[2]), "v"(rb[3]), "v"(coff), "s"(abase), "s"(bbase),         \
+                 "v"(boff[3]), "v"(ra[0]), "v"(ra[1]), "v"(rb[0]), "v"(rb[1]), "v"(rb[2]),      \
+                 "v"(rb[3]), "v"(coff), "s"(abase), "s"(bbase),                                 \
                  "s"(cbase), "s"(nk), "s"(lds), "s"(ldsa), "s"(ldsb), "s"(bstep), "s"(nstride), \
                  "s"(arow8)                                                                     \
                : TH_GEMM_ASM_CLOBBERS, "vcc", "scc", "memory")

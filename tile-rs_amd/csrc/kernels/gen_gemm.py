@@ -6,10 +6,14 @@ Semantics: C = A . B with f32 accumulation (`linalg.fill 0` + `linalg.matmul`,
 M x K, B row-major K x N, bf16 or f16 operands, C f32 or 16-bit (one rounding, RNE).
 
 Workgroup = 4 waves = one 256 x 256 tile; wave (wm, wn) = (w / 2, w % 2) owns rows
-128 wm .. +127 and columns 128 wn .. +127 as 4 x 4 blocks of 32 x 32, accumulated in
-a[0:255] (block (mi, ni) at a[16 (4 mi + ni)]) with v_mfma_f32_32x32x16.  One wave
-per SIMD: the 128 x 128 wave tile reads 64 KB of LDS fragments per 32-deep K step for
-the workgroup, a third less than eight waves of 128 x 64.
+128 wm .. +127 and columns 128 wn .. +127 as 8 x 8 blocks of 16 x 16, accumulated in
+a[0:255] (block (mi, ni) at a[4 (8 mi + ni)]) with v_mfma_f32_16x16x32, one MFMA per
+block and 32-deep K step.  One wave per SIMD: the 128 x 128 wave tile reads 64 KB of
+LDS fragments per K step for the workgroup, a third less than eight waves of 128 x 64.
+The 16x16x32 form moves half the accumulator data of 32x32x16 per FLOP; the chip runs
+power-limited, and on random operands the same MFMA work takes 62.8-68.4 us instead of
+73.0-78.2 us (microbenchmark, 4096 x 32768 FLOP per SIMD).  Both forms round the same
+way here: C is bit-identical to the 32x32x16 program on both config shapes.
 
 K advances 32 per step.  LDS (128 KB), filled by global_load_lds_dwordx4 only:
   A ring: 2 double stages x 32 KB at 0.  A double stage holds 64 k of the tile's 256
@@ -28,10 +32,11 @@ Schedule of step k (every wave):
                               stage (k+1)/2 has landed (n: loads issued after them)
   s_barrier                   -> every share of those stages is in LDS, and every
                               wave has finished reading step k's fragments
-  32 MFMAs of step k, with in between: the 24 fragment reads of step k+1 (into the
-  other register set, two per MFMA from the first) and the DMA issues: B stage k+4
-  into buffer k % 4 (free: step k's reads are done) and, at odd k, A double stage
-  (k+3)/2 into buffer ((k+3)/2) % 2 (free: its last reader, step k, is done).
+  64 MFMAs of step k, with in between: the 24 fragment reads of step k+1 (into the
+  other register set, one after every second MFMA from the first) and the DMA issues:
+  B stage k+4 into buffer k % 4 (free: step k's reads are done) and, at odd k, A
+  double stage (k+3)/2 into buffer ((k+3)/2) % 2 (free: its last reader, step k, is
+  done).
 Per-wave issue order, steady state: even k: B(k+4); odd k: A((k+3)/2), B(k+4).  At
 the wait of even k the loads issued after B(k+1) are B(k+2), A(k/2+1), B(k+3) (16);
 at odd k those after A((k+1)/2) are B(k+2), B(k+3) (8).  The prologue issues B0, A0,
@@ -40,18 +45,23 @@ double stage is issued two steps before its first reader, a B stage three.  The 
 runs in groups of four steps (static buffers); the last group issues no DMA and waits
 16, 4, 0.
 
-Registers: operands in v0-v15 and s-registers chosen by the compiler; v16-v19 A read
-bases [h][ks], v20-v23 B read bases [ni], v24-v31 A DMA offsets, v32-v47 epilogue,
-v[128:191] and v[192:255] the two fragment sets (A (ks, mi) at +4 (4 ks + mi), B
-(ks, ni) at +32 + 4 (4 ks + ni)); s[48:49] A pointer, s[50:51] B pointer, s[52:53] C
-base, s54 loop count, s55 saved m0, s56-s57 temps.
+Fragments of a step: A block mi (16 rows x 32 k): lane l reads row 16 mi + l % 16,
+the 16 bytes of k 8 (l / 16) .. +7 (ds_read_b128); B block ni (32 k x 16 columns):
+lane l needs column 16 ni + l % 16 at k 8 (l / 16) .. +7, two ds_read_b64_tr_b16 of
+four k rows each.
+
+Registers: operands in v0-v15 and s-registers chosen by the compiler; v16-v17 A read
+bases [h], v20-v23 B read bases [ni / 2] (odd ni: +32 bytes), v24-v31 A DMA offsets,
+v32-v49 epilogue, v[128:191] and v[192:255] the two fragment sets (A mi at +4 mi, B ni
+at +32 + 4 ni); s[48:49] A pointer, s[50:51] B pointer, s[52:53] C base, s54 loop
+count, s55 saved m0, s56-s57 temps.
 
 Usage: python gen_gemm.py <out.inc>   (run by the library build)
 """
 import sys
 from pathlib import Path
 
-OPN = ["aoffE", "aoffO", "boff0", "boff1", "boff2", "boff3", "ra00", "ra01", "ra10", "ra11",
+OPN = ["aoffE", "aoffO", "boff0", "boff1", "boff2", "boff3", "ra0", "ra1",
        "rb0", "rb1", "rb2", "rb3", "coff",
        "abase", "bbase", "cbase", "nk", "lds", "ldsa", "ldsb", "bstep", "nstride", "arow8"]
 OP = {n: i for i, n in enumerate(OPN)}
@@ -63,40 +73,39 @@ def o(n):
 
 SA_, SB_, SC_ = "s[48:49]", "s[50:51]", "s[52:53]"
 SCNT, SROW = "s54", "s57"
-VA = [[16, 17], [18, 19]]        # A read bases [h][ks]
-VB = [20, 21, 22, 23]            # B read bases [ni]
+VA = [16, 17]                    # A read bases [h]
+VB = [20, 21, 22, 23]            # B read bases [ni / 2]
 VAO = list(range(24, 32))        # A DMA offsets, unit j = 0..7
 FR = [128, 192]                  # fragment register sets
 
 
-def afr(s, ks, mi):
-    return FR[s] + 4 * (4 * ks + mi)
+def afr(s, mi):
+    return FR[s] + 4 * mi
 
 
-def bfr(s, ks, ni):
-    return FR[s] + 32 + 4 * (4 * ks + ni)
+def bfr(s, ni):
+    return FR[s] + 32 + 4 * ni
 
 
 def acc(mi, ni):
-    b = 16 * (4 * mi + ni)
-    return f"a[{b}:{b + 15}]"
+    b = 4 * (8 * mi + ni)
+    return f"a[{b}:{b + 3}]"
 
 
 def reads(k, s):
-    """Fragment reads of step k (mod 4) into register set s: A (8 x 16 bytes), then
-    B^T (16 transposed 8-byte reads)."""
+    """Fragment reads of step k (mod 4) into register set s: A (8 blocks of 16 rows,
+    16 bytes per lane), then B^T (8 blocks of 16 columns, two transposed 8-byte reads
+    each)."""
     ab, h, bb = (k // 2) % 2, k % 2, k % 4
     out = []
-    for ks in range(2):
-        for mi in range(4):
-            f = afr(s, ks, mi)
-            out.append(f"ds_read_b128 v[{f}:{f + 3}], v{VA[h][ks]} offset:{ab * 32768 + 4096 * mi}")
-    for ks in range(2):
-        for ni in range(4):
-            f = bfr(s, ks, ni)
-            base = bb * 16384 + ks * 8192
-            out.append(f"ds_read_b64_tr_b16 v[{f}:{f + 1}], v{VB[ni]} offset:{base}")
-            out.append(f"ds_read_b64_tr_b16 v[{f + 2}:{f + 3}], v{VB[ni]} offset:{base + 2048}")
+    for mi in range(8):
+        f = afr(s, mi)
+        out.append(f"ds_read_b128 v[{f}:{f + 3}], v{VA[h]} offset:{ab * 32768 + 2048 * mi}")
+    for ni in range(8):
+        f = bfr(s, ni)
+        base = bb * 16384 + 32 * (ni & 1)
+        out.append(f"ds_read_b64_tr_b16 v[{f}:{f + 1}], v{VB[ni >> 1]} offset:{base}")
+        out.append(f"ds_read_b64_tr_b16 v[{f + 2}:{f + 3}], v{VB[ni >> 1]} offset:{base + 2048}")
     return out
 
 
@@ -123,18 +132,17 @@ def dma_a(buf):
 
 def mfmas(s, mn):
     out = []
-    for ks in range(2):
-        for mi in range(4):
-            for ni in range(4):
-                a, b = afr(s, ks, mi), bfr(s, ks, ni)
-                out.append(f"{mn} {acc(mi, ni)}, v[{a}:{a + 3}], v[{b}:{b + 3}], {acc(mi, ni)}")
+    for mi in range(8):
+        for ni in range(8):
+            a, b = afr(s, mi), bfr(s, ni)
+            out.append(f"{mn} {acc(mi, ni)}, v[{a}:{a + 3}], v[{b}:{b + 3}], {acc(mi, ni)}")
     return out
 
 
 def step(k4, mn, vm, rd, dm, bar=True):
-    """Step k with k % 4 == k4.  The reads of step k+1 go two after each of the first
-    12 MFMAs; the DMA groups start after the first MFMA and spread over the step
-    (measured against one read per MFMA and B^T reads first: 1 us less at 4096^3)."""
+    """Step k with k % 4 == k4.  The reads of step k+1 go one after every second MFMA
+    of the first 48 (measured at 4096^3 against 12, 24 and 64 MFMAs: 1-7 us less); the
+    DMA groups start after the first MFMA and spread over the step."""
     out = ["s_waitcnt lgkmcnt(0)"]
     if vm is not None:
         out.append(f"s_waitcnt vmcnt({vm})")
@@ -149,7 +157,7 @@ def step(k4, mn, vm, rd, dm, bar=True):
         D += dma_b(k4)
     slots = [[] for _ in M]
     for j, r in enumerate(R):
-        slots[j // 2].append([r])
+        slots[2 * j].append([r])
     for j, d in enumerate(D):
         slots[min(len(M) - 1, (j * len(M)) // len(D) + 1)].append(d)
     for m, sl in zip(M, slots):
@@ -161,47 +169,47 @@ def step(k4, mn, vm, rd, dm, bar=True):
 
 def epilogue(out_dt):
     """C stores straight from the accumulators (f32) or through a packed conversion
-    (16-bit).  Accumulator r of a lane in a 32x32 block is row 8 (r/4) + 4 g + r % 4,
-    column l32: per store instruction the 32 lanes of a half write 32 consecutive
-    columns of one row.  coff = this lane's byte offset (row 4 g, column l32)."""
+    (16-bit).  Accumulator r of lane l in a 16x16 block is row 4 (l / 16) + r, column
+    l % 16: per store instruction the 16 lanes of each quarter write 16 consecutive
+    columns of one row (the next block's store the other half of the 128-byte line).
+    coff = this lane's byte offset (row 4 (l / 16), column l % 16)."""
     L = ["s_nop 7", "s_nop 7", "s_nop 7", "s_nop 7"]   # MFMA results -> readers
     if out_dt == "f32":
-        for mi in range(4):
-            for r in range(16):
-                row = mi * 32 + 8 * (r >> 2) + (r & 3)
+        for mi in range(8):
+            for r in range(4):
+                row = mi * 16 + r
                 L.append(f"s_mul_i32 {SROW}, {o('nstride')}, {row}")
                 L.append(f"v_add_u32 v32, {SROW}, {o('coff')}")
-                for ni in range(4):
-                    L.append(f"global_store_dword v32, a{16 * (4 * mi + ni) + r}, {SC_} "
-                             f"offset:{128 * ni} nt")
+                for ni in range(8):
+                    L.append(f"global_store_dword v32, a{4 * (8 * mi + ni) + r}, {SC_} "
+                             f"offset:{64 * ni} nt")
         return L
     cvt = "v_cvt_pk_bf16_f32" if out_dt == "bf16" else "v_cvt_pk_f16_f32"
-    for mi in range(4):
-        for r in range(0, 16, 2):
-            row = mi * 32 + 8 * (r >> 2) + (r & 3)     # rows row and row + 1
+    for mi in range(8):
+        for r in range(0, 4, 2):
+            row = mi * 16 + r     # rows row and row + 1
             L.append(f"s_mul_i32 {SROW}, {o('nstride')}, {row}")
             L.append(f"v_add_u32 v32, {SROW}, {o('coff')}")
             L.append(f"v_add_u32 v33, {o('nstride')}, v32")
-            for ni in range(4):
-                a = 16 * (4 * mi + ni) + r
-                t = 34 + 3 * ni
+            for ni in range(8):
+                a = 4 * (8 * mi + ni) + r
+                t = 34 + 2 * ni
                 L += [f"v_accvgpr_read_b32 v{t}, a{a}", f"v_accvgpr_read_b32 v{t + 1}, a{a + 1}",
-                      f"{cvt} v{t + 2}, v{t}, v{t + 1}"]
-            for ni in range(4):
-                t = 34 + 3 * ni
-                L += [f"global_store_short v32, v{t + 2}, {SC_} offset:{64 * ni} nt",
-                      f"global_store_short_d16_hi v33, v{t + 2}, {SC_} offset:{64 * ni} nt"]
+                      f"{cvt} v{t}, v{t}, v{t + 1}"]
+            for ni in range(8):
+                t = 34 + 2 * ni
+                L += [f"global_store_short v32, v{t}, {SC_} offset:{32 * ni} nt",
+                      f"global_store_short_d16_hi v33, v{t}, {SC_} offset:{32 * ni} nt"]
     return L
 
 
 def program(dt, out_dt):
-    mn = "v_mfma_f32_32x32x16_bf16" if dt == "bf16" else "v_mfma_f32_32x32x16_f16"
+    mn = "v_mfma_f32_16x16x32_bf16" if dt == "bf16" else "v_mfma_f32_16x16x32_f16"
     L = ["s_mov_b32 s55, m0",
          f"s_mov_b64 {SA_}, {o('abase')}", f"s_mov_b64 {SB_}, {o('bbase')}",
          f"s_mov_b64 {SC_}, {o('cbase')}"]
     for h in range(2):
-        for ks in range(2):
-            L.append(f"v_add_u32 v{VA[h][ks]}, {o('lds')}, {o('ra' + str(h) + str(ks))}")
+        L.append(f"v_add_u32 v{VA[h]}, {o('lds')}, {o('ra' + str(h))}")
     for ni in range(4):
         L.append(f"v_add_u32 v{VB[ni]}, {o('lds')}, {o('rb' + str(ni))}")
         L.append(f"v_add_u32 v{VB[ni]}, 0x10000, v{VB[ni]}")
