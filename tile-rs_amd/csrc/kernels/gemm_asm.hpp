@@ -86,7 +86,9 @@ __device__ __forceinline__ void gemm_asm_tile(const uint16_t* __restrict__ A,
       rb[p] = k0 * 512 + (((n >> 3) ^ (4 * (k0 & 3))) << 4) + (n & 7) * 2;
     }
   }
-  const uint32_t coff = ((4 * (lane >> 4)) * N + (lane & 15)) * OSZ;
+  // C: after the epilogue's lane swap, lane l writes row 8 (l / 32), column l % 32 of
+  // each row group and pair of column blocks
+  const uint32_t coff = ((8 * (lane >> 5)) * N + (lane & 31)) * OSZ;
   const uint32_t nk = K / 32, bstep = 64 * N, nstride = N * OSZ, arow8 = 16 * K;
   const uint32_t ldsa = lds + wave * 8192, ldsb = lds + 65536 + wave * 4096;
 #define TH_GEMM_ASM_OPS(STR)                                                                    \
