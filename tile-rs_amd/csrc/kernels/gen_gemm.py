@@ -131,24 +131,42 @@ def dma_a(buf):
 
 
 def mfmas(s, mn):
+    """The step's 64 MFMAs, row block by row block, the column order reversed on odd rows
+    (each row's A fragment, and one B fragment across the turn, feed consecutive MFMAs;
+    0.6 us less at 4096^3 than the same order on every row)."""
     out = []
     for mi in range(8):
-        for ni in range(8):
+        for ni in (range(8) if mi % 2 == 0 else range(7, -1, -1)):
             a, b = afr(s, mi), bfr(s, ni)
             out.append(f"{mn} {acc(mi, ni)}, v[{a}:{a + 3}], v[{b}:{b + 3}], {acc(mi, ni)}")
     return out
 
 
-def step(k4, mn, vm, rd, dm, bar=True):
-    """Step k with k % 4 == k4.  The reads of step k+1 go one after every second MFMA
-    of the first 48 (measured at 4096^3 against 12, 24 and 64 MFMAs: 1-7 us less); the
-    DMA groups start after the first MFMA and spread over the step."""
+DEFER = 4   # MFMAs of each step issued after the next step's barrier
+
+
+def deferred(k4, mn):
+    """The last DEFER MFMAs of step k4: issued after the next step's waits and barrier,
+    they keep the MFMA pipe busy while the barrier resolves.  They read only registers
+    already loaded, and the next reads into their fragment set are issued after them."""
+    return mfmas(k4 & 1, mn)[64 - DEFER:]
+
+
+def step(k4, mn, vm, rd, dm, bar=True, carry=(), defer=True):
+    """Step k with k % 4 == k4: waits, barrier, the previous step's deferred MFMAs
+    (`carry`), then this step's MFMAs (all but the deferred ones when `defer`).  The
+    reads of step k+1 go one after every second MFMA of the first 48 (measured at
+    4096^3 against 12, 24 and 64 MFMAs: 1-7 us less); the DMA groups start after the
+    first MFMA and spread over the step."""
     out = ["s_waitcnt lgkmcnt(0)"]
     if vm is not None:
         out.append(f"s_waitcnt vmcnt({vm})")
     if bar:
         out.append("s_barrier")
+    out += list(carry)
     M = mfmas(k4 & 1, mn)
+    if defer:
+        M = M[:64 - DEFER]
     R = reads((k4 + 1) % 4, (k4 + 1) & 1) if rd else []
     D = []
     if dm:
@@ -167,7 +185,7 @@ def step(k4, mn, vm, rd, dm, bar=True):
     return out
 
 
-def epilogue(out_dt):
+def epilogue(out_dt, mis=range(8)):
     """C stores from the accumulators.  Accumulator r of lane l in a 16x16 block is row
     4 (l / 16) + r, column l % 16, so a store straight from one block writes 64-byte row
     pieces.  For each row r and pair of column blocks (2p, 2p+1) the two values go
@@ -177,9 +195,9 @@ def epilogue(out_dt):
     direct stores at 4096^3, same bits).  16-bit C packs rows r, r+1 first
     (v_cvt_pk_{bf16,f16}_f32, RNE) and writes them with short / short_d16_hi stores.
     coff = this lane's byte offset (row 8 (l / 32), column l % 32)."""
-    L = ["s_nop 7", "s_nop 7", "s_nop 7", "s_nop 7"]   # MFMA results -> readers
+    L = []
     if out_dt == "f32":
-        for mi in range(8):
+        for mi in mis:
             for r in range(4):
                 row = mi * 16 + r
                 L.append(f"s_mul_i32 {SROW}, {o('nstride')}, {row}")
@@ -197,7 +215,7 @@ def epilogue(out_dt):
                     L.append(f"global_store_dword v33, v{37 + 2 * p}, {SC_} offset:{128 * p} nt")
         return L
     cvt = "v_cvt_pk_bf16_f32" if out_dt == "bf16" else "v_cvt_pk_f16_f32"
-    for mi in range(8):
+    for mi in mis:
         for r in range(0, 4, 2):
             row = mi * 16 + r     # rows row, row + 1 (and + 4, + 5 after the swap)
             L.append(f"s_mul_i32 {SROW}, {o('nstride')}, {row}")
@@ -245,18 +263,32 @@ def program(dt, out_dt):
         L.extend(g)
     # B0 and A0 landed: loads issued after A0 are B1, B2, A1, B3 (4 + 4 + 8 + 4)
     L += ["s_waitcnt vmcnt(20)", "s_barrier"] + reads(0, 0)
-    # steady groups: nk / 4 - 1 (nk >= 8, a multiple of 4: checked by the caller)
+    # steady groups: nk / 4 - 1 (nk >= 8, a multiple of 4: checked by the caller; a
+    # launch outside that would skip the work and write nothing).  The first group
+    # enters at its step 1 after a copy of step 0 with nothing carried in.
     L += [f"s_lshr_b32 {SCNT}, {o('nk')}, 2", f"s_sub_u32 {SCNT}, {SCNT}, 1",
-          f"s_cmp_eq_u32 {SCNT}, 0", "s_cbranch_scc1 L_tail_%=", "L_top_%=:"]
-    for k4 in range(4):
-        L += step(k4, mn, 16 if k4 % 2 == 0 else 8, True, True)
-    L += [f"s_sub_u32 {SCNT}, {SCNT}, 1", f"s_cmp_lg_u32 {SCNT}, 0", "s_cbranch_scc1 L_top_%=",
-          "L_tail_%=:"]
-    L += step(0, mn, 16, True, False)
-    L += step(1, mn, 4, True, False)
-    L += step(2, mn, 0, True, False)
-    L += step(3, mn, None, False, False, bar=False)
-    L += epilogue(out_dt)
+          f"s_cmp_eq_u32 {SCNT}, 0", "s_cbranch_scc1 L_end_%="]
+    L += step(0, mn, 16, True, True) + ["s_branch L_b1_%="]
+    L += ["L_top_%=:"] + step(0, mn, 16, True, True, carry=deferred(3, mn))
+    L += ["L_b1_%=:"]
+    for k4 in (1, 2, 3):
+        L += step(k4, mn, 16 if k4 % 2 == 0 else 8, True, True, carry=deferred(k4 - 1, mn))
+    L += [f"s_sub_u32 {SCNT}, {SCNT}, 1", f"s_cmp_lg_u32 {SCNT}, 0", "s_cbranch_scc1 L_top_%="]
+    L += step(0, mn, 16, True, False, carry=deferred(3, mn))
+    L += step(1, mn, 4, True, False, carry=deferred(0, mn))
+    L += step(2, mn, 0, True, False, carry=deferred(1, mn))
+    # the last step: row block mi's stores start once the MFMAs of row block mi + 2
+    # have issued (16 MFMAs after its last one: its results are written), the last
+    # two row blocks' after the loop
+    L += ["s_waitcnt lgkmcnt(0)"] + deferred(2, mn)
+    M = mfmas(1, mn)
+    for mi in range(8):
+        L += M[8 * mi:8 * mi + 8]
+        if mi >= 2:
+            L += epilogue(out_dt, [mi - 2])
+    L += ["s_nop 7", "s_nop 7", "s_nop 7", "s_nop 7"]   # MFMA results -> readers
+    L += epilogue(out_dt, [6, 7])
+    L += ["L_end_%=:"]
     L += ["s_waitcnt vmcnt(0)", "s_mov_b32 m0, s55"]
     return L
 
