@@ -52,9 +52,11 @@ __device__ __forceinline__ void gemm_asm_tile(const uint16_t* __restrict__ A,
       Cb + (static_cast<size_t>(m0 + wm * 128) * N + n0 + wn * 128) * OSZ);
   // A double stage [256 r][8 chunks]: chunk c of row r at c ^ sw(r)
   auto swa = [](uint32_t r) { return (r & 7) ^ ((r >> 3) & 1); };
+  // B stage [32 k][32 chunks]: chunk c of k-row r at c ^ sb(r)
+  auto swb = [](uint32_t r) { return 4 * (r & 3) ^ 2 * ((r >> 3) & 1); };
   // DMA: A unit j of wave w = rows 64 w + 8 j + lane / 8, position lane % 8 (units 0
   // and 1 here; the program derives the others); B unit j = k rows 2 (4 w + j) +
-  // lane / 32, position lane % 32 holding chunk (lane % 32) ^ 4 (k & 3).
+  // lane / 32, position lane % 32 holding chunk (lane % 32) ^ sb(k).
   uint32_t aoff[2], boff[4], ra[2], rb[4];
 #pragma unroll
   for (uint32_t j = 0; j < 2; ++j) {
@@ -64,7 +66,7 @@ __device__ __forceinline__ void gemm_asm_tile(const uint16_t* __restrict__ A,
 #pragma unroll
   for (uint32_t j = 0; j < 4; ++j) {
     const uint32_t kr = 2 * (4 * wave + j) + lane / 32;
-    boff[j] = kr * N * 2 + (((lane & 31) ^ (4 * (kr & 3))) << 4);
+    boff[j] = kr * N * 2 + (((lane & 31) ^ swb(kr)) << 4);
   }
   // Fragment reads (16x16x32 operands).  A (k half h): lane reads row 128 wm + 16 mi +
   // lane % 16, chunk 4 h + lane / 16 (mi as an immediate: 2 KB per 16 rows).
@@ -74,16 +76,15 @@ __device__ __forceinline__ void gemm_asm_tile(const uint16_t* __restrict__ A,
     ra[h] = row * 128 + (((4 * h + (lane >> 4)) ^ swa(row)) << 4);
   }
   // B^T: lane (q, i) = (lane / 16, lane % 16) reads k rows 8 q + (i >> 2) (+4 as an
-  // immediate) at column n = 128 wn + 16 ni + 4 (i & 3); the address is per pair of
-  // column blocks p = ni / 2 (the odd block is 32 bytes on: the swizzle leaves bit 1 of
-  // the chunk index alone).
+  // immediate: same sb) at column n = 128 wn + 16 ni + 4 (i & 3); passed for the even
+  // blocks ni = 2p (the program flips chunk bit 1 for the odd ones).
   {
     const uint32_t q = lane >> 4, i = lane & 15;
     const uint32_t k0 = 8 * q + (i >> 2);
 #pragma unroll
     for (uint32_t p = 0; p < 4; ++p) {
       const uint32_t n = wn * 128 + 32 * p + 4 * (i & 3);
-      rb[p] = k0 * 512 + (((n >> 3) ^ (4 * (k0 & 3))) << 4) + (n & 7) * 2;
+      rb[p] = k0 * 512 + (((n >> 3) ^ swb(k0)) << 4) + (n & 7) * 2;
     }
   }
   // C: after the epilogue's lane swap, lane l writes row 8 (l / 32), column l % 32 of

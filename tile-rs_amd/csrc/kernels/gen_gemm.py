@@ -22,7 +22,11 @@ K advances 32 per step.  LDS (128 KB), filled by global_load_lds_dwordx4 only:
           of row r sits at c ^ sw(r), sw(r) = (r & 7) ^ ((r >> 3) & 1), so the
           ds_read_b128 of 16 lanes (16 rows, one chunk) covers all 64 banks.
   B ring: 4 stages x 16 KB at 64 KB, [32 k][32 chunks]: chunk c of k-row r at
-          c ^ 4 (r & 3); read as B^T with ds_read_b64_tr_b16.
+          c ^ sb(r), sb(r) = 4 (r & 3) ^ 2 ((r >> 3) & 1); read as B^T with
+          ds_read_b64_tr_b16.  A transposed read covers 32 lanes per cycle: the two
+          16-lane groups read k rows 8 apart, and bit 3 of the row in sb keeps their
+          16 chunks apart (without it the B reads took 2-way bank conflicts in half of
+          the LDS-active cycles).
 Step k uses A double stage k/2 (buffer (k/2) % 2, k half k % 2) and B stage k
 (buffer k % 4).
 
@@ -51,7 +55,7 @@ lane l needs column 16 ni + l % 16 at k 8 (l / 16) .. +7, two ds_read_b64_tr_b16
 four k rows each.
 
 Registers: operands in v0-v15 and s-registers chosen by the compiler; v16-v17 A read
-bases [h], v20-v23 B read bases [ni / 2] (odd ni: +32 bytes), v24-v31 A DMA offsets,
+bases [h], v52-v59 B read bases [ni], v24-v31 A DMA offsets,
 v32-v51 epilogue, v[128:191] and v[192:255] the two fragment sets (A mi at +4 mi, B ni
 at +32 + 4 ni); s[48:49] A pointer, s[50:51] B pointer, s[52:53] C base, s54 loop
 count, s55 saved m0, s56-s57 temps.
@@ -74,7 +78,7 @@ def o(n):
 SA_, SB_, SC_ = "s[48:49]", "s[50:51]", "s[52:53]"
 SCNT, SROW = "s54", "s57"
 VA = [16, 17]                    # A read bases [h]
-VB = [20, 21, 22, 23]            # B read bases [ni / 2]
+VB = list(range(52, 60))         # B read bases [ni]
 VAO = list(range(24, 32))        # A DMA offsets, unit j = 0..7
 FR = [128, 192]                  # fragment register sets
 
@@ -103,9 +107,9 @@ def reads(k, s):
         out.append(f"ds_read_b128 v[{f}:{f + 3}], v{VA[h]} offset:{ab * 32768 + 2048 * mi}")
     for ni in range(8):
         f = bfr(s, ni)
-        base = bb * 16384 + 32 * (ni & 1)
-        out.append(f"ds_read_b64_tr_b16 v[{f}:{f + 1}], v{VB[ni >> 1]} offset:{base}")
-        out.append(f"ds_read_b64_tr_b16 v[{f + 2}:{f + 3}], v{VB[ni >> 1]} offset:{base + 2048}")
+        base = bb * 16384
+        out.append(f"ds_read_b64_tr_b16 v[{f}:{f + 1}], v{VB[ni]} offset:{base}")
+        out.append(f"ds_read_b64_tr_b16 v[{f + 2}:{f + 3}], v{VB[ni]} offset:{base + 2048}")
     return out
 
 
@@ -249,9 +253,12 @@ def program(dt, out_dt):
          f"s_mov_b64 {SC_}, {o('cbase')}"]
     for h in range(2):
         L.append(f"v_add_u32 v{VA[h]}, {o('lds')}, {o('ra' + str(h))}")
-    for ni in range(4):
-        L.append(f"v_add_u32 v{VB[ni]}, {o('lds')}, {o('rb' + str(ni))}")
-        L.append(f"v_add_u32 v{VB[ni]}, 0x10000, v{VB[ni]}")
+    # block 2p + 1 is 16 columns on: chunk bit 1 flips (bytes ^ 32), whatever sb adds
+    for p in range(4):
+        ev, od = VB[2 * p], VB[2 * p + 1]
+        L += [f"v_add_u32 v{ev}, {o('lds')}, {o('rb' + str(p))}", f"v_add_u32 v{ev}, 0x10000, v{ev}",
+              f"v_xor_b32 v{od}, 32, {o('rb' + str(p))}", f"v_add_u32 v{od}, {o('lds')}, v{od}",
+              f"v_add_u32 v{od}, 0x10000, v{od}"]
     # A unit j of wave w holds rows 64 w + 8 j .. +7: the swizzle depends on j only
     # through its parity, so units j and j & 1 differ by (j & ~1) x 8 rows
     for j in range(8):
