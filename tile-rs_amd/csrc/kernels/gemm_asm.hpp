@@ -50,8 +50,8 @@ __device__ __forceinline__ void gemm_asm_tile(const uint16_t* __restrict__ A,
   const uint64_t bbase = reinterpret_cast<uint64_t>(B + n0);
   const uint64_t cbase = reinterpret_cast<uint64_t>(
       Cb + (static_cast<size_t>(m0 + wm * 128) * N + n0 + wn * 128) * OSZ);
-  // A double stage [256 r][8 chunks]: chunk c of row r at c ^ sw(r)
-  auto swa = [](uint32_t r) { return (r & 7) ^ ((r >> 3) & 1); };
+  // A double stage [256 r][8 chunks]: chunk c of row r at c ^ (r & 7)
+  auto swa = [](uint32_t r) { return r & 7; };
   // B stage [32 k][32 chunks]: chunk c of k-row r at c ^ sb(r)
   auto swb = [](uint32_t r) { return 4 * (r & 3) ^ 2 * ((r >> 3) & 1); };
   // DMA: A unit j of wave w = rows 64 w + 8 j + lane / 8, position lane % 8 (units 0

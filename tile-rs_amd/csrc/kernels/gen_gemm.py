@@ -19,8 +19,10 @@ K advances 32 per step.  LDS (128 KB), filled by global_load_lds_dwordx4 only:
   A ring: 2 double stages x 32 KB at 0.  A double stage holds 64 k of the tile's 256
           rows, [256 r][8 chunks of 16 B]: every DMA lane group reads whole 128-byte
           rows of A (with 32-k stages each row would be half a cache line).  Chunk c
-          of row r sits at c ^ sw(r), sw(r) = (r & 7) ^ ((r >> 3) & 1), so the
-          ds_read_b128 of 16 lanes (16 rows, one chunk) covers all 64 banks.
+          of row r sits at c ^ (r & 7): conflict-free for the fragment reads (16 rows
+          x 4 chunks per instruction), where (r & 7) ^ ((r >> 3) & 1) measured 2-way
+          bank conflicts and no swizzle 4-way (SQ_LDS_BANK_CONFLICT, probe of the
+          lane pattern).
   B ring: 4 stages x 16 KB at 64 KB, [32 k][32 chunks]: chunk c of k-row r at
           c ^ sb(r), sb(r) = 4 (r & 3) ^ 2 ((r >> 3) & 1); read as B^T with
           ds_read_b64_tr_b16.  A transposed read covers 32 lanes per cycle: the two
@@ -259,8 +261,8 @@ def program(dt, out_dt):
         L += [f"v_add_u32 v{ev}, {o('lds')}, {o('rb' + str(p))}", f"v_add_u32 v{ev}, 0x10000, v{ev}",
               f"v_xor_b32 v{od}, 32, {o('rb' + str(p))}", f"v_add_u32 v{od}, {o('lds')}, v{od}",
               f"v_add_u32 v{od}, 0x10000, v{od}"]
-    # A unit j of wave w holds rows 64 w + 8 j .. +7: the swizzle depends on j only
-    # through its parity, so units j and j & 1 differ by (j & ~1) x 8 rows
+    # A unit j of wave w holds rows 64 w + 8 j .. +7: units j and j & 1 differ by
+    # (j & ~1) x 8 rows (the swizzle depends on the row's low three bits only)
     for j in range(8):
         src = o("aoffE") if j % 2 == 0 else o("aoffO")
         L.append(f"s_mul_i32 {SROW}, {o('arow8')}, {j & ~1}")
