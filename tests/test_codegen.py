@@ -149,8 +149,8 @@ def test_whole_tile_matmuls_lower_to_the_assembly_entry():
     tiles, row-major B, K a multiple of 128 -> the generated-assembly entry, 256-thread
     workgroups (one per CU), one per tile.  A K of 96 or an N of 384 keeps the DMA entry."""
     src = th.emit((EXAMPLES / "config_gemms.mlir").read_text()).source
-    assert "th::entry::gemm_asm<th::kBF16, th::kF32>(" in src
-    assert "th::entry::gemm_asm<th::kF16, th::kF16>(" in src
+    assert "th::entry::gemm_asm<th::kBF16, th::kF32, false>(" in src
+    assert "th::entry::gemm_asm<th::kF16, th::kF16, false>(" in src
     assert "__launch_bounds__(256, 1) gemm_4096_bf16_acc_f32(" in src
     assert "__th_desc_gemm_4096_bf16_acc_f32 = {th::kLaunchDescMagic, 256u, 256u, 1u," in src
     assert "__th_desc_mlp_up_f16 = {th::kLaunchDescMagic, 256u, 1792u, 1u," in src
@@ -158,6 +158,12 @@ def test_whole_tile_matmuls_lower_to_the_assembly_entry():
     k96 = (EXAMPLES / "matmul_bf16.mlir").read_text().replace("constant(256 : i32)",
                                                                 "constant(96 : i32)")
     assert "th::entry::gemm_dma<" in th.emit(k96).source
+    # B stored N x K on whole tiles: the same entry's transposed program
+    t = (EXAMPLES / "matmul_f16_t.mlir").read_text()
+    for old, new in (("128 : i32", "256 : i32"), ("320 : i32", "512 : i32"),
+                     ("264 : i32", "768 : i32")):
+        t = t.replace(f"constant({old})", f"constant({new})")
+    assert "th::entry::gemm_asm<th::kF16, th::kF16, true>(" in th.emit(t).source
 
 
 def test_matmul_shape_and_tile_offsets_are_exact():

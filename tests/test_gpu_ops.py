@@ -260,21 +260,24 @@ def test_matmul_integer_bit_exact(dev, stream, in_dt, trans, m, k, n):
     assert np.array_equal(got, ref), f"max diff {np.abs(got - ref).max()}"
 
 
+@pytest.mark.parametrize("trans", [False, True])
 @pytest.mark.parametrize("in_dt", [D.BF16, D.F16])
 @pytest.mark.parametrize("out_dt", [D.F32, D.BF16, D.F16])
 @pytest.mark.parametrize("m,k,n,bsz", [(256, 256, 256, 1), (512, 384, 768, 1), (768, 1152, 512, 1),
                                        (256, 512, 512, 3)])
-def test_matmul_whole_tiles_bit_exact(dev, stream, in_dt, out_dt, m, k, n, bsz):
-    """Whole 256 x 256 tiles, row-major B, K a multiple of 128: the generated-assembly
-    kernel (K in 8, 12 and 36 steps of 32, and a batch).  Integer inputs keep every f32
-    partial sum exact, so C is the exact product rounded once to its dtype."""
+def test_matmul_whole_tiles_bit_exact(dev, stream, trans, in_dt, out_dt, m, k, n, bsz):
+    """Whole 256 x 256 tiles, K a multiple of 128, B row-major or stored N x K: the
+    generated-assembly kernel (K in 8, 12 and 36 steps of 32, and a batch).  Integer
+    inputs keep every f32 partial sum exact, so C is the exact product rounded once to
+    its dtype."""
     rng = np.random.default_rng(m + 3 * k + 5 * n + bsz)
     a = rng.integers(-4, 5, (bsz, m, k)).astype(np.float32)
     b = rng.integers(-4, 5, (bsz, k, n)).astype(np.float32)
+    bs = np.ascontiguousarray(b.transpose(0, 2, 1)) if trans else b
     ab = upload(dev, stream, orc.narrow(a.ravel(), ORC[in_dt]), in_dt)
-    bb = upload(dev, stream, orc.narrow(b.ravel(), ORC[in_dt]), in_dt)
+    bb = upload(dev, stream, orc.narrow(bs.ravel(), ORC[in_dt]), in_dt)
     cb = dev.alloc(bsz * m * n, out_dt)
-    th.matmul(ab, bb, cb, m, k, n, in_dt, out_dt, False, batch=bsz, stream=stream)
+    th.matmul(ab, bb, cb, m, k, n, in_dt, out_dt, trans, batch=bsz, stream=stream)
     raw = cb.copy_to_host(stream).reshape(bsz, m, n)
     for i in range(bsz):
         ref = (a[i].astype(np.int64) @ b[i].astype(np.int64)).astype(np.float32)

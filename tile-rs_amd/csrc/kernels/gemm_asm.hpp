@@ -1,5 +1,6 @@
-// Dense 16-bit GEMM on whole 256 x 256 tiles: the library's kernel for row-major B with
-// M and N multiples of 256 and K a multiple of 128 (at least 256).
+// Dense 16-bit GEMM on whole 256 x 256 tiles: the library's kernel for M and N multiples
+// of 256 and K a multiple of 128 (at least 256), B row-major (K x N) or stored N x K
+// (BT, __tile_matmul_transposed_f16: crates/tile_std/src/tile.rs:2028).
 //
 // The tile program is generated gfx950 assembly (gen_gemm.py, run by the build into
 // kernels/gen/gemm_asm.inc): four waves of 128 x 128 with AGPR accumulators
@@ -31,7 +32,7 @@ __host__ __device__ constexpr bool fits(uint64_t m, uint64_t n, uint64_t k, int 
 // 16-byte aligned, C aligned to its element; gasm::fits(M, N, K, sizeof C) holds.  A
 // workgroup that runs several tiles passes a barrier between them (the next tile's
 // DMA refills buffers the previous one's last reads used).
-template <int DT, int DT_OUT>
+template <int DT, int DT_OUT, bool BT = false>
 __device__ __forceinline__ void gemm_asm_tile(const uint16_t* __restrict__ A,
                                               const uint16_t* __restrict__ B,
                                               void* __restrict__ C, uint32_t M, uint32_t N,
@@ -47,7 +48,7 @@ __device__ __forceinline__ void gemm_asm_tile(const uint16_t* __restrict__ A,
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t wm = wave >> 1, wn = wave & 1;
   const uint64_t abase = reinterpret_cast<uint64_t>(A + static_cast<size_t>(m0) * K);
-  const uint64_t bbase = reinterpret_cast<uint64_t>(B + n0);
+  const uint64_t bbase = reinterpret_cast<uint64_t>(BT ? B + static_cast<size_t>(n0) * K : B + n0);
   const uint64_t cbase = reinterpret_cast<uint64_t>(
       Cb + (static_cast<size_t>(m0 + wm * 128) * N + n0 + wn * 128) * OSZ);
   // A double stage [256 r][8 chunks]: chunk c of row r at c ^ (r & 7)
@@ -63,10 +64,17 @@ __device__ __forceinline__ void gemm_asm_tile(const uint16_t* __restrict__ A,
     const uint32_t row = 64 * wave + 8 * j + lane / 8;
     aoff[j] = row * K * 2 + (((lane & 7) ^ swa(row)) << 4);
   }
+  if constexpr (BT) {
+    // B^T double stages: the same units and swizzle as A, over the tile's n rows
 #pragma unroll
-  for (uint32_t j = 0; j < 4; ++j) {
-    const uint32_t kr = 2 * (4 * wave + j) + lane / 32;
-    boff[j] = kr * N * 2 + (((lane & 31) ^ swb(kr)) << 4);
+    for (uint32_t j = 0; j < 2; ++j) boff[j] = aoff[j];
+    boff[2] = boff[3] = 0;
+  } else {
+#pragma unroll
+    for (uint32_t j = 0; j < 4; ++j) {
+      const uint32_t kr = 2 * (4 * wave + j) + lane / 32;
+      boff[j] = kr * N * 2 + (((lane & 31) ^ swb(kr)) << 4);
+    }
   }
   // Fragment reads (16x16x32 operands).  A (k half h): lane reads row 128 wm + 16 mi +
   // lane % 16, chunk 4 h + lane / 16 (mi as an immediate: 2 KB per 16 rows).
@@ -75,10 +83,18 @@ __device__ __forceinline__ void gemm_asm_tile(const uint16_t* __restrict__ A,
     const uint32_t row = wm * 128 + (lane & 15);
     ra[h] = row * 128 + (((4 * h + (lane >> 4)) ^ swa(row)) << 4);
   }
-  // B^T: lane (q, i) = (lane / 16, lane % 16) reads k rows 8 q + (i >> 2) (+4 as an
-  // immediate: same sb) at column n = 128 wn + 16 ni + 4 (i & 3); passed for the even
-  // blocks ni = 2p (the program flips chunk bit 1 for the odd ones).
-  {
+  if constexpr (BT) {
+    // B^T (k half h): lane reads n row 128 wn + 16 ni + lane % 16, chunk 4 h + lane / 16
+#pragma unroll
+    for (uint32_t h = 0; h < 2; ++h) {
+      const uint32_t row = wn * 128 + (lane & 15);
+      rb[h] = row * 128 + (((4 * h + (lane >> 4)) ^ swa(row)) << 4);
+    }
+    rb[2] = rb[3] = 0;
+  } else {
+    // B^T from row-major B: lane (q, i) = (lane / 16, lane % 16) reads k rows 8 q +
+    // (i >> 2) (+4 as an immediate: same sb) at column n = 128 wn + 16 ni + 4 (i & 3);
+    // passed for the even blocks ni = 2p (the program flips chunk bit 1 for the odd ones).
     const uint32_t q = lane >> 4, i = lane & 15;
     const uint32_t k0 = 8 * q + (i >> 2);
 #pragma unroll
@@ -91,7 +107,7 @@ __device__ __forceinline__ void gemm_asm_tile(const uint16_t* __restrict__ A,
   // each row group and pair of column blocks
   const uint32_t coff = ((8 * (lane >> 5)) * N + (lane & 31)) * OSZ;
   const uint32_t nk = K / 32, bstep = 64 * N, nstride = N * OSZ, arow8 = 16 * K;
-  const uint32_t ldsa = lds + wave * 8192, ldsb = lds + 65536 + wave * 4096;
+  const uint32_t ldsa = lds + wave * 8192, ldsb = lds + 65536 + wave * (BT ? 8192 : 4096);
 #define TH_GEMM_ASM_OPS(STR)                                                                    \
   asm volatile(STR                                                                              \
                :                                                                                \
@@ -101,7 +117,17 @@ __device__ __forceinline__ void gemm_asm_tile(const uint16_t* __restrict__ A,
                  "s"(cbase), "s"(nk), "s"(lds), "s"(ldsa), "s"(ldsb), "s"(bstep), "s"(nstride), \
                  "s"(arow8)                                                                     \
                : TH_GEMM_ASM_CLOBBERS, "vcc", "scc", "memory")
-  if constexpr (DT == kBF16) {
+  if constexpr (BT) {
+    if constexpr (DT == kBF16) {
+      if constexpr (DT_OUT == kF32) TH_GEMM_ASM_OPS(TH_GEMM_ASM_BF16_F32_BT);
+      else if constexpr (DT_OUT == kBF16) TH_GEMM_ASM_OPS(TH_GEMM_ASM_BF16_BF16_BT);
+      else TH_GEMM_ASM_OPS(TH_GEMM_ASM_BF16_F16_BT);
+    } else {
+      if constexpr (DT_OUT == kF32) TH_GEMM_ASM_OPS(TH_GEMM_ASM_F16_F32_BT);
+      else if constexpr (DT_OUT == kBF16) TH_GEMM_ASM_OPS(TH_GEMM_ASM_F16_BF16_BT);
+      else TH_GEMM_ASM_OPS(TH_GEMM_ASM_F16_F16_BT);
+    }
+  } else if constexpr (DT == kBF16) {
     if constexpr (DT_OUT == kF32) TH_GEMM_ASM_OPS(TH_GEMM_ASM_BF16_F32);
     else if constexpr (DT_OUT == kBF16) TH_GEMM_ASM_OPS(TH_GEMM_ASM_BF16_BF16);
     else TH_GEMM_ASM_OPS(TH_GEMM_ASM_BF16_F16);
@@ -114,14 +140,14 @@ __device__ __forceinline__ void gemm_asm_tile(const uint16_t* __restrict__ A,
 }
 
 // Batch index = blockIdx.y (element strides sa, sb, sc).
-template <int DT, int DT_OUT>
+template <int DT, int DT_OUT, bool BT = false>
 __global__ void __launch_bounds__(gasm::NT, 1)
 gemm_asm_256(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, void* __restrict__ C,
              uint32_t M, uint32_t N, uint32_t K, uint64_t sa, uint64_t sb, uint64_t sc) {
   constexpr uint32_t OSZ = (DT_OUT == kF32) ? 4 : 2;
   uint32_t tm, tn;
   gemm::tile_coords(blockIdx.x, M / 256, N / 256, tm, tn);
-  gemm_asm_tile<DT, DT_OUT>(A + blockIdx.y * sa, B + blockIdx.y * sb,
+  gemm_asm_tile<DT, DT_OUT, BT>(A + blockIdx.y * sa, B + blockIdx.y * sb,
                             static_cast<char*>(C) + static_cast<size_t>(blockIdx.y) * sc * OSZ, M,
                             N, K, tm, tn);
 }

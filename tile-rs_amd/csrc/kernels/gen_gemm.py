@@ -32,6 +32,13 @@ K advances 32 per step.  LDS (128 KB), filled by global_load_lds_dwordx4 only:
 Step k uses A double stage k/2 (buffer (k/2) % 2, k half k % 2) and B stage k
 (buffer k % 4).
 
+B stored N x K (`bt`, the transposed matmul): B^T rows are K-contiguous like A's, so
+B takes A's form: a ring of 2 double stages x 32 KB at 64 KB ([256 n][8 chunks],
+chunk c of row n at c ^ (n & 7)), read with ds_read_b128 like A, and refilled at the
+same odd steps.  Then the only wait is at odd k, for double stage (k+1)/2 of both
+operands, which nothing has been issued after (vmcnt(0)); it was issued two steps
+earlier.  The prologue issues A0, B0, A1, B1 and waits for A0, B0 (vmcnt(16)).
+
 Schedule of step k (every wave):
   s_waitcnt lgkmcnt(0)        this wave's fragments of step k have landed
   s_waitcnt vmcnt(n)          this wave's DMA share of B stage k+1 and of A double
@@ -82,6 +89,8 @@ SCNT, SROW = "s54", "s57"
 VA = [16, 17]                    # A read bases [h]
 VB = list(range(52, 60))         # B read bases [ni]
 VAO = list(range(24, 32))        # A DMA offsets, unit j = 0..7
+VBO = list(range(60, 68))        # B DMA offsets (bt), unit j = 0..7
+BT = [False]                     # the program being generated has B stored N x K
 FR = [128, 192]                  # fragment register sets
 
 
@@ -107,6 +116,11 @@ def reads(k, s):
     for mi in range(8):
         f = afr(s, mi)
         out.append(f"ds_read_b128 v[{f}:{f + 3}], v{VA[h]} offset:{ab * 32768 + 2048 * mi}")
+    if BT[0]:
+        for ni in range(8):
+            f = bfr(s, ni)
+            out.append(f"ds_read_b128 v[{f}:{f + 3}], v{VB[h]} offset:{ab * 32768 + 2048 * ni}")
+        return out
     for ni in range(8):
         f = bfr(s, ni)
         base = bb * 16384
@@ -116,9 +130,16 @@ def reads(k, s):
 
 
 def dma_b(buf):
-    """This wave's four 1 KB units of the next B stage into buffer buf.  The LDS
-    destination (m0) needs one wait state after it is written."""
+    """This wave's four 1 KB units of the next B stage into buffer buf (bt: eight units
+    of the next B double stage, like A).  The LDS destination (m0) needs one wait state
+    after it is written."""
     out = []
+    if BT[0]:
+        for j in range(8):
+            out.append([f"s_add_u32 m0, {o('ldsb')}, {buf * 32768 + j * 1024}", "s_nop 0",
+                        f"global_load_lds_dwordx4 v{VBO[j]}, {SB_}"])
+        out.append(["s_add_u32 s50, s50, 128", "s_addc_u32 s51, s51, 0"])
+        return out
     for j in range(4):
         out.append([f"s_add_u32 m0, {o('ldsb')}, {buf * 16384 + j * 1024}", "s_nop 0",
                     f"global_load_lds_dwordx4 {o('boff' + str(j))}, {SB_}"])
@@ -178,7 +199,10 @@ def step(k4, mn, vm, rd, dm, bar=True, carry=(), defer=True):
     if dm:
         if k4 % 2 == 1:
             D += dma_a(((k4 + 3) // 2) % 2)
-        D += dma_b(k4)
+            if BT[0]:
+                D += dma_b(((k4 + 3) // 2) % 2)
+        if not BT[0]:
+            D += dma_b(k4)
     slots = [[] for _ in M]
     for j, r in enumerate(R):
         slots[2 * j].append([r])
@@ -248,19 +272,38 @@ def epilogue(out_dt, mis=range(8)):
     return L
 
 
-def program(dt, out_dt):
+def vm(k4, steady):
+    """vmcnt of step k % 4 == k4 (None: no wait), steady: the group issues DMA."""
+    if BT[0]:
+        return 0 if k4 % 2 == 1 else None
+    if steady:
+        return 16 if k4 % 2 == 0 else 8
+    return [16, 4, 0, None][k4]
+
+
+def program(dt, out_dt, bt=False):
+    BT[0] = bt
     mn = "v_mfma_f32_16x16x32_bf16" if dt == "bf16" else "v_mfma_f32_16x16x32_f16"
     L = ["s_mov_b32 s55, m0",
          f"s_mov_b64 {SA_}, {o('abase')}", f"s_mov_b64 {SB_}, {o('bbase')}",
          f"s_mov_b64 {SC_}, {o('cbase')}"]
     for h in range(2):
         L.append(f"v_add_u32 v{VA[h]}, {o('lds')}, {o('ra' + str(h))}")
-    # block 2p + 1 is 16 columns on: chunk bit 1 flips (bytes ^ 32), whatever sb adds
-    for p in range(4):
-        ev, od = VB[2 * p], VB[2 * p + 1]
-        L += [f"v_add_u32 v{ev}, {o('lds')}, {o('rb' + str(p))}", f"v_add_u32 v{ev}, 0x10000, v{ev}",
-              f"v_xor_b32 v{od}, 32, {o('rb' + str(p))}", f"v_add_u32 v{od}, {o('lds')}, v{od}",
-              f"v_add_u32 v{od}, 0x10000, v{od}"]
+    if bt:
+        # B^T read bases [h] (rb0, rb1), DMA offsets like A's (boff0, boff1 = units 0, 1)
+        for h in range(2):
+            L += [f"v_add_u32 v{VB[h]}, {o('lds')}, {o('rb' + str(h))}",
+                  f"v_add_u32 v{VB[h]}, 0x10000, v{VB[h]}"]
+        for j in range(8):
+            L.append(f"s_mul_i32 {SROW}, {o('arow8')}, {j & ~1}")
+            L.append(f"v_add_u32 v{VBO[j]}, {SROW}, {o('boff' + str(j & 1))}")
+    else:
+        # block 2p + 1 is 16 columns on: chunk bit 1 flips (bytes ^ 32), whatever sb adds
+        for p in range(4):
+            ev, od = VB[2 * p], VB[2 * p + 1]
+            L += [f"v_add_u32 v{ev}, {o('lds')}, {o('rb' + str(p))}", f"v_add_u32 v{ev}, 0x10000, v{ev}",
+                  f"v_xor_b32 v{od}, 32, {o('rb' + str(p))}", f"v_add_u32 v{od}, {o('lds')}, v{od}",
+                  f"v_add_u32 v{od}, 0x10000, v{od}"]
     # A unit j of wave w holds rows 64 w + 8 j .. +7: units j and j & 1 differ by
     # (j & ~1) x 8 rows (the swizzle depends on the row's low three bits only)
     for j in range(8):
@@ -268,24 +311,29 @@ def program(dt, out_dt):
         L.append(f"s_mul_i32 {SROW}, {o('arow8')}, {j & ~1}")
         L.append(f"v_add_u32 v{VAO[j]}, {SROW}, {src}")
     L += [f"v_accvgpr_write_b32 a{r}, 0" for r in range(256)]
-    for g in dma_b(0) + dma_a(0) + dma_b(1) + dma_b(2) + dma_a(1) + dma_b(3):
-        L.extend(g)
-    # B0 and A0 landed: loads issued after A0 are B1, B2, A1, B3 (4 + 4 + 8 + 4)
-    L += ["s_waitcnt vmcnt(20)", "s_barrier"] + reads(0, 0)
+    if bt:
+        for g in dma_a(0) + dma_b(0) + dma_a(1) + dma_b(1):
+            L.extend(g)
+        # A0 and B0 landed: loads issued after B0 are A1, B1 (8 + 8)
+        L += ["s_waitcnt vmcnt(16)", "s_barrier"] + reads(0, 0)
+    else:
+        for g in dma_b(0) + dma_a(0) + dma_b(1) + dma_b(2) + dma_a(1) + dma_b(3):
+            L.extend(g)
+        # B0 and A0 landed: loads issued after A0 are B1, B2, A1, B3 (4 + 4 + 8 + 4)
+        L += ["s_waitcnt vmcnt(20)", "s_barrier"] + reads(0, 0)
     # steady groups: nk / 4 - 1 (nk >= 8, a multiple of 4: checked by the caller; a
     # launch outside that would skip the work and write nothing).  The first group
     # enters at its step 1 after a copy of step 0 with nothing carried in.
     L += [f"s_lshr_b32 {SCNT}, {o('nk')}, 2", f"s_sub_u32 {SCNT}, {SCNT}, 1",
           f"s_cmp_eq_u32 {SCNT}, 0", "s_cbranch_scc1 L_end_%="]
-    L += step(0, mn, 16, True, True) + ["s_branch L_b1_%="]
-    L += ["L_top_%=:"] + step(0, mn, 16, True, True, carry=deferred(3, mn))
+    L += step(0, mn, vm(0, True), True, True) + ["s_branch L_b1_%="]
+    L += ["L_top_%=:"] + step(0, mn, vm(0, True), True, True, carry=deferred(3, mn))
     L += ["L_b1_%=:"]
     for k4 in (1, 2, 3):
-        L += step(k4, mn, 16 if k4 % 2 == 0 else 8, True, True, carry=deferred(k4 - 1, mn))
+        L += step(k4, mn, vm(k4, True), True, True, carry=deferred(k4 - 1, mn))
     L += [f"s_sub_u32 {SCNT}, {SCNT}, 1", f"s_cmp_lg_u32 {SCNT}, 0", "s_cbranch_scc1 L_top_%="]
-    L += step(0, mn, 16, True, False, carry=deferred(3, mn))
-    L += step(1, mn, 4, True, False, carry=deferred(0, mn))
-    L += step(2, mn, 0, True, False, carry=deferred(1, mn))
+    for k4 in (0, 1, 2):
+        L += step(k4, mn, vm(k4, False), True, False, carry=deferred((k4 + 3) % 4, mn))
     # the last step: row block mi's stores start once the MFMAs of row block mi + 2
     # have issued (16 MFMAs after its last one: its results are written), the last
     # two row blocks' after the loop
@@ -308,10 +356,11 @@ def cstr(lines):
 
 def main(path):
     lines = ["// Generated by gen_gemm.py: 16-bit GEMM tile program (gfx950 asm).", "#pragma once"]
-    for dt in ("bf16", "f16"):
-        for out_dt in ("f32", "bf16", "f16"):
-            lines.append(f'#define TH_GEMM_ASM_{dt.upper()}_{out_dt.upper()} '
-                         f'"{cstr(program(dt, out_dt))}"')
+    for bt in (False, True):
+        for dt in ("bf16", "f16"):
+            for out_dt in ("f32", "bf16", "f16"):
+                lines.append(f'#define TH_GEMM_ASM_{dt.upper()}_{out_dt.upper()}{"_BT" if bt else ""} '
+                             f'"{cstr(program(dt, out_dt, bt))}"')
     clob = ([f'"v{k}"' for k in range(16, 256)] + [f'"a{k}"' for k in range(256)] +
             [f'"s{k}"' for k in range(48, 58)])
     lines.append("#define TH_GEMM_ASM_CLOBBERS " + ",".join(clob))

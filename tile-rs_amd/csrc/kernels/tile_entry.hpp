@@ -151,11 +151,11 @@ __device__ __forceinline__ void gemm_dma(const uint16_t* A, const uint16_t* B, v
   }
 }
 
-// Whole 256 x 256 tiles with row-major B and K a multiple of 128 (gasm::fits, checked
-// by the emitter): the library's generated-assembly tile program, 256 threads per
-// workgroup.  Operands that are not 16-byte aligned (checked at run time) take the
-// per-element kernel instead, which fits in the same workgroup.
-template <int DT, int DTO>
+// Whole 256 x 256 tiles with K a multiple of 128 (gasm::fits, checked by the emitter):
+// the library's generated-assembly tile program, 256 threads per workgroup.  Operands
+// that are not 16-byte aligned (checked at run time) take the per-element kernel
+// instead, which fits in the same workgroup.
+template <int DT, int DTO, bool BT = false>
 __device__ __forceinline__ void gemm_asm(const uint16_t* A, const uint16_t* B, void* C, uint32_t M,
                                          uint32_t N, uint32_t K, uint32_t batch) {
   constexpr int OSZ = (DTO == kF32) ? 4 : 2;
@@ -175,9 +175,9 @@ __device__ __forceinline__ void gemm_asm(const uint16_t* A, const uint16_t* B, v
     char* c = static_cast<char*>(C) + bi * sc;
     if (vec) {
       __syncthreads();  // the previous tile's last fragment reads are done
-      gemm_asm_tile<DT, DTO>(a, b, c, M, N, K, tm, tn);
+      gemm_asm_tile<DT, DTO, BT>(a, b, c, M, N, K, tm, tn);
     } else {
-      gemm_dot_tile_256<DT, DTO, false>(a, b, c, M, N, K, tm, tn);
+      gemm_dot_tile_256<DT, DTO, BT>(a, b, c, M, N, K, tm, tn);
     }
   }
 }

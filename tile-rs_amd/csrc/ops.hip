@@ -245,7 +245,7 @@ bool gemm_dma() {
   return v;
 }
 
-// Whole-tile shapes with row-major B run on the generated-assembly kernel
+// Whole-tile shapes (B row-major or stored N x K) run on the generated-assembly kernel
 // (gemm_asm.hpp) unless TILERS_HIP_GEMM_ASM=0 (a debugging switch: the LDS-DMA
 // kernel, which gives the same bits, then runs them).
 bool gemm_asm() {
@@ -312,10 +312,10 @@ int gemm_mfma_go(const GemmArgs& g, dim3 grid) {
   if (gemm_dma() && out_vec && g.k % th::gemm::DBK == 0) {
     const uint32_t S = splitk_slices(g, grid.x);
     if (S > 1) return gemm_splitk<DT, DTO, EPI, BT>(g, grid.x, S);
-    if constexpr (!BT && EPI == th::gemm::kEpiStore) {
+    if constexpr (EPI == th::gemm::kEpiStore) {
       if (gemm_asm() && th::gasm::fits(g.m, g.n, g.k, static_cast<int>(OSZ))) {
-        hipLaunchKernelGGL((th::gemm_asm_256<DT, DTO>), grid, dim3(th::gasm::NT), 0, g.s, A, B,
-                           g.c, g.m, g.n, g.k, g.sa, g.sb, g.sc);
+        hipLaunchKernelGGL((th::gemm_asm_256<DT, DTO, BT>), grid, dim3(th::gasm::NT), 0, g.s, A,
+                           B, g.c, g.m, g.n, g.k, g.sa, g.sb, g.sc);
         return launch_status("matmul (MFMA asm) launch");
       }
     }

@@ -875,10 +875,10 @@ bool matmul_entry(const Kernel& k, const TileVal& mm, const Store& st, const cha
   const int osz = out == F32 ? 4 : 2;
   const bool dma = mfma && K % 32 == 0 && N % 8 == 0 && (st.dst.offset * osz) % 16 == 0 &&
                    (!up || (up->src.offset * osz) % 16 == 0);
-  // whole 256 x 256 tiles, row-major B, plain store: the generated-assembly program
+  // whole 256 x 256 tiles, plain store: the generated-assembly program
   // (the shapes th::gasm::fits accepts: K in groups of four 32-deep steps, at least
   // two, and per-lane byte offsets within 32 bits)
-  const bool gasm = dma && !bt && !up && M > 0 && N > 0 && M % 256 == 0 && N % 256 == 0 &&
+  const bool gasm = dma && !up && M > 0 && N > 0 && M % 256 == 0 && N % 256 == 0 &&
                     K % 128 == 0 && K >= 256 && 512LL * K < (1LL << 31) &&
                     136LL * N * osz < (1LL << 31) && 64LL * N < (1LL << 31);
   os << "matmul " << M << "x" << K << "x" << N << (bt ? " (B transposed)" : "") << " " << dt_name(in)
@@ -899,7 +899,8 @@ bool matmul_entry(const Kernel& k, const TileVal& mm, const Store& st, const cha
   const std::string tail = up ? ", th_tiles, " + view_ptr(*up, dt_ctype(out)) + ");\n}\n"
                               : ", th_tiles);\n}\n";
   if (gasm) {
-    os << "  th::entry::gemm_asm<" << dt_enum(in) << ", " << dt_enum(out) << ">("
+    os << "  th::entry::gemm_asm<" << dt_enum(in) << ", " << dt_enum(out) << ", "
+       << (bt ? "true" : "false") << ">("
        << view_ptr(a, "uint16_t") << ", " << view_ptr(b, "uint16_t") << ", "
        << store_ptr(st, dt_ctype(out)) << ", " << u(M) << ", " << u(N) << ", " << u(K) << tail;
     desc(os, k, threads, static_cast<unsigned>((M / 256) * (N / 256)), 1);
