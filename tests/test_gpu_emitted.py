@@ -157,6 +157,25 @@ def test_matmul_transposed_f16_out(dev, stream, launcher):
     assert_gemm_close(got, orc.widen(orc.narrow(ref, orc.F16), orc.F16), "matmul_t_f16", u16_dtype=orc.F16)
 
 
+def test_matmul_transposed_whole_tiles(dev, stream, launcher):
+    """256x512x768 f16 with B stored N x K over two logical tiles: the generated-assembly
+    entry's transposed program."""
+    tiles, M, K, N = 2, 256, 512, 768
+    rng = np.random.default_rng(14)
+    a = orc.narrow(rng.standard_normal(tiles * M * K).astype(np.float32), orc.F16)
+    b = orc.narrow((rng.standard_normal(tiles * N * K) * 0.05).astype(np.float32), orc.F16)
+    ab, bb = up(dev, stream, a, D.F16), up(dev, stream, b, D.F16)
+    cb = dev.alloc(tiles * M * N, D.F16)
+    launcher.launch("matmul_t_f16_tiles", th.LaunchGrid.blocks_only(tiles), [ptr(ab), ptr(bb), ptr(cb)],
+                    stream)
+    got = orc.widen(cb.copy_to_host(stream), orc.F16).reshape(tiles, M, N)
+    for t in range(tiles):
+        ref = orc.matmul(a[t * M * K:(t + 1) * M * K], b[t * N * K:(t + 1) * N * K], M, K, N,
+                         orc.F16, orc.F32, b_trans=True)
+        assert_gemm_close(got[t], orc.widen(orc.narrow(ref, orc.F16), orc.F16),
+                          f"matmul_t_f16_tiles tile {t}", u16_dtype=orc.F16)
+
+
 def test_matmul_f32_fma_integer_exact(dev, stream, launcher):
     M, K, N = 96, 72, 80
     rng = np.random.default_rng(5)
