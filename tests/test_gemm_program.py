@@ -9,7 +9,10 @@ program text:
   LDS ring discipline.  Every wave runs the same program, so for each LDS buffer the
   walk checks that a fragment read sees a DMA fill that this wave waited for (vmcnt)
   before a barrier that precedes the read, and that a DMA into a buffer comes after a
-  barrier that follows the completion (lgkmcnt) of the last read of it.
+  barrier that follows the completion (lgkmcnt) of the last read of it.  The SiLU*Mul
+  program stages each wave's UP tile over the ring: its DMA must follow a barrier that
+  comes after every ring read and every ring fill completed, and its reads must follow
+  the wave's own wait for it.
 """
 import re
 import sys
@@ -24,6 +27,7 @@ OP = G.OP
 CLOBBER_V = set(range(16, 256))
 CLOBBER_A = set(range(256))
 CLOBBER_S = set(range(48, 58))
+CLOBBER_S_SILU = set(range(48, 60))
 
 
 def regs(text, kind):
@@ -34,7 +38,7 @@ def regs(text, kind):
     return out
 
 
-def static_problems(prog):
+def static_problems(prog, sregs=CLOBBER_S):
     lines = [l.strip() for l in prog]
     defs = [l[:-1] for l in lines if l.endswith(":")]
     bad = [f"label defined twice: {d}" for d in set(defs) if defs.count(d) > 1]
@@ -51,7 +55,7 @@ def static_problems(prog):
             bad.append("VGPR outside the clobber list: " + ln)
         if regs(body, "a") - CLOBBER_A:
             bad.append("AGPR outside the clobber list: " + ln)
-        if regs(body, "s") - CLOBBER_S:
+        if regs(body, "s") - sregs:
             bad.append("SGPR outside the clobber list: " + ln)
         for kind in ("v", "a"):
             for a, b in re.findall(rf"\b{kind}\[(\d+):(\d+)\]", body):
@@ -116,6 +120,27 @@ class Walk:
         self.lgkm.append(buf)
         self.read[buf] = (len(self.lgkm) - 1, self.t)
 
+    def on_up_dma(self):
+        for buf, (_, t) in self.read.items():
+            done = self.read_done.get(buf)
+            if done is None or done < t or not self.barrier_between(done, self.t):
+                self.problems.append(f"UP staging at t={self.t} over {buf} before its reads are done and synced")
+        for buf, (_, t) in self.fill.items():
+            if buf[0] == "U":
+                continue
+            done = self.fill_done.get(buf)
+            if done is None or done < t or not self.barrier_between(done, self.t):
+                self.problems.append(f"UP staging at t={self.t} over {buf} before its fill is done and synced")
+        self.vmem.append(("U", 0))
+        self.fill[("U", 0)] = (len(self.vmem) - 1, self.t)
+        self.dma += 1
+
+    def on_up_read(self):
+        f = self.fill.get(("U", 0))
+        done = self.fill_done.get(("U", 0))
+        if f is None or done is None or done < f[1]:
+            self.problems.append(f"UP read at t={self.t} before the wave's own UP DMA is waited")
+
     def on_dma(self, buf):
         r = self.read.get(buf)
         if r is not None:
@@ -139,7 +164,13 @@ class Walk:
             a = [x.strip() for x in rest.split(",")] if rest else []
             if op == "global_load_lds_dwordx4":
                 kind, imm = self.m0
-                self.on_dma(self.a_buf(imm) if kind == "A" else self.b_buf(imm))
+                if kind == "U":
+                    self.on_up_dma()
+                else:
+                    self.on_dma(self.a_buf(imm) if kind == "A" else self.b_buf(imm))
+            elif op == "ds_read_u16":
+                assert a[1].split()[0] == f"%{OP['uread']}", line
+                self.on_up_read()
             elif op.startswith("global_store"):
                 self.vmem.append(None)
                 self.stores += 1
@@ -167,8 +198,7 @@ class Walk:
             elif op.startswith("v_") or op == "s_nop":
                 pass
             elif op == "s_add_u32" and a[0] == "m0":
-                kind = "A" if a[1] == f"%{OP['ldsa']}" else "B"
-                assert a[1] in (f"%{OP['ldsa']}", f"%{OP['ldsb']}"), line
+                kind = {f"%{OP['ldsa']}": "A", f"%{OP['ldsb']}": "B", f"%{OP['ustage']}": "U"}[a[1]]
                 self.m0 = (kind, int(a[2], 0))
             elif op == "s_mov_b32" and "m0" in a:
                 pass
@@ -204,6 +234,17 @@ def test_program_text_is_self_contained(dt, out, bt):
     assert static_problems(prog) == []
     assert prog[0] == "s_mov_b32 s55, m0" and prog[-1] == "s_mov_b32 m0, s55"
     assert not any("s55" in l for l in prog[1:-1])
+    if out != "f32":
+        silu = G.program(dt, out, bt, silu=True)
+        assert static_problems(silu, CLOBBER_S_SILU) == []
+        assert silu[0] == "s_mov_b32 s55, m0" and silu[-1] == "s_mov_b32 m0, s55"
+        assert not any("s55" in l for l in silu[1:-1])
+
+
+def test_clobber_lists_match_the_checked_sets():
+    text = Path(G.__file__).read_text()
+    assert "for k in range(16, 256)" in text and "for k in range(256)" in text
+    assert "for k in range(48, 58)" in text and 'TH_GEMM_ASM_CLOBBERS, \\"s58\\", \\"s59\\"' in text
 
 
 def test_static_check_finds_planted_cases():
@@ -229,6 +270,25 @@ def test_ring_discipline_and_counts(nk, out, bt):
     assert w.dma == 8 * nk          # A: 8 units per 64-k double stage; B: 4 per 32-k stage (8 per 64 with bt)
     assert w.stores == 256
     assert w.vm_done == len(w.vmem)
+
+
+@pytest.mark.parametrize("bt", [False, True])
+@pytest.mark.parametrize("nk", [8, 12, 128])
+def test_silu_program_ring_discipline_and_counts(nk, bt):
+    w = Walk(G.program("f16", "f16", bt, silu=True), nk, bt).run()
+    assert w.problems == []
+    assert w.mfma == 64 * nk
+    assert w.dma == 8 * nk + 32      # the ring, then 32 UP units (128 rows x 256 B)
+    assert w.stores == 256
+    assert w.vm_done == len(w.vmem)
+
+
+def test_walk_finds_a_planted_early_up_staging():
+    """The UP staging needs the barrier that opens the last step: without it a slower
+    wave may still read its last fragments where this wave's UP lands."""
+    prog = G.program("f16", "f16", False, silu=True)
+    i = max(k for k, l in enumerate(prog) if l == "s_barrier")
+    assert Walk(prog[:i] + prog[i + 1:], 16, False).run().problems
 
 
 def test_walk_finds_a_planted_race():

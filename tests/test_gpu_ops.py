@@ -778,7 +778,10 @@ def test_matmul_silu_mul_golden_vectors(dev, stream, golden):
 
 @pytest.mark.parametrize("m,k,n,in_dt,out_dt,trans", [
     (512, 512, 768, D.BF16, D.F32, False),    # LDS-DMA pipeline
-    (256, 1024, 512, D.F16, D.F16, True),     # LDS-DMA pipeline, B stored N x K
+    (256, 1024, 512, D.F16, D.F16, True),     # generated-assembly program, B stored N x K
+    (512, 384, 768, D.BF16, D.BF16, False),   # generated-assembly program (whole tiles)
+    (256, 512, 256, D.F16, D.BF16, False),    # same, f16 operands, bf16 C and UP
+    (512, 256, 256, D.BF16, D.F16, True),     # same, B stored N x K
     (512, 96, 256, D.BF16, D.BF16, False),    # LDS-DMA pipeline, 3 stages of K
     (512, 80, 256, D.BF16, D.BF16, False),    # register-staged MFMA (K % 32 != 0)
     (300, 72, 136, D.F16, D.F32, False),      # ragged MFMA tiles
@@ -813,6 +816,32 @@ def test_matmul_silu_mul_unaligned_output(dev, stream):
 def test_matmul_silu_mul_batched(dev, stream):
     _swiglu_case(dev, stream, np.random.default_rng(77), 256, 128, 256, D.F16, D.F16, False,
                  batch=3)
+
+
+def test_matmul_silu_mul_whole_tiles_batched(dev, stream):
+    """Whole tiles over a batch of two (the assembly program; UP and C step by the
+    batch stride together)."""
+    _swiglu_case(dev, stream, np.random.default_rng(78), 256, 256, 512, D.BF16, D.BF16, False,
+                 batch=2)
+
+
+def test_matmul_silu_mul_saturated_gate(dev, stream):
+    """Gate values far past the exponential's range (|A.B| up to ~200): silu(x) -> x for
+    large x and -> -0 for large negative x, with no NaN from inf / inf."""
+    rng = np.random.default_rng(79)
+    m, k, n = 256, 256, 256
+    a = rand16(rng, m * k, D.F16, 4.0)
+    b = rand16(rng, k * n, D.F16, 4.0)
+    u = orc.narrow(rng.standard_normal(m * n).astype(np.float32), orc.F16)
+    ab, bb, ub = upload(dev, stream, a, D.F16), upload(dev, stream, b, D.F16), upload(dev, stream, u, D.F16)
+    cb = dev.alloc(m * n, D.F16)
+    th.matmul_silu_mul(ab, bb, ub, cb, m, k, n, D.F16, D.F16, False, stream=stream)
+    got = orc.widen(cb.copy_to_host(stream), orc.F16).reshape(m, n)
+    ref = orc.widen(orc.matmul_silu_mul(a, b, u, m, k, n, orc.F16, orc.F16), orc.F16).reshape(m, n)
+    assert np.isfinite(got).all()
+    g = orc.matmul(a, b, m, k, n, orc.F16, orc.F32).reshape(m, n)
+    assert np.abs(g).max() > 60
+    assert_gemm_close(got, ref, "swiglu saturated", u16_dtype=orc.F16)
 
 
 def test_matmul_silu_mul_config3_subset(dev, stream):

@@ -32,12 +32,16 @@ __host__ __device__ constexpr bool fits(uint64_t m, uint64_t n, uint64_t k, int 
 // 16-byte aligned, C aligned to its element; gasm::fits(M, N, K, sizeof C) holds.  A
 // workgroup that runs several tiles passes a barrier between them (the next tile's
 // DMA refills buffers the previous one's last reads used).
-template <int DT, int DT_OUT, bool BT = false>
+// SILU: C = silu(A . B) * UP (kEpiSiluMul), UP an M x N tensor of C's 16-bit dtype and
+// layout, 16-byte aligned.
+template <int DT, int DT_OUT, bool BT = false, bool SILU = false>
 __device__ __forceinline__ void gemm_asm_tile(const uint16_t* __restrict__ A,
                                               const uint16_t* __restrict__ B,
                                               void* __restrict__ C, uint32_t M, uint32_t N,
-                                              uint32_t K, uint32_t tm, uint32_t tn) {
+                                              uint32_t K, uint32_t tm, uint32_t tn,
+                                              const void* __restrict__ UP = nullptr) {
   static_assert(DT == kBF16 || DT == kF16, "16-bit operands");
+  static_assert(!SILU || DT_OUT != kF32, "the SiLU*Mul program writes 16-bit C");
   constexpr uint32_t OSZ = (DT_OUT == kF32) ? 4 : 2;
   char* Cb = static_cast<char*>(C);
   u32x4* arena = lds::dma_lds_arena<131072>();
@@ -108,6 +112,43 @@ __device__ __forceinline__ void gemm_asm_tile(const uint16_t* __restrict__ A,
   const uint32_t coff = ((8 * (lane >> 5)) * N + (lane & 31)) * OSZ;
   const uint32_t nk = K / 32, bstep = 64 * N, nstride = N * OSZ, arow8 = 16 * K;
   const uint32_t ldsa = lds + wave * 8192, ldsb = lds + 65536 + wave * (BT ? 8192 : 4096);
+  if constexpr (SILU) {
+    // UP: the wave's 128 x 128 tile, staged row-major in the wave's 32 KB of the ring
+    // (256-byte rows); DMA unit j = rows 4 j + lane / 16, chunk lane % 16.  Reads
+    // follow the epilogue's lane swap: lane l takes row 8 (l / 32) (+ immediates),
+    // column l % 32.
+    const uint64_t ubase = reinterpret_cast<uint64_t>(
+        static_cast<const char*>(UP) + (static_cast<size_t>(m0 + wm * 128) * N + n0 + wn * 128) * 2);
+    const uint32_t ustage = lds + wave * 32768;
+    const uint32_t uoff = (lane >> 4) * N * 2 + (lane & 15) * 16;
+    const uint32_t uread = ustage + 2048 * (lane >> 5) + 2 * (lane & 31);
+#define TH_GEMM_ASM_SILU_OPS(STR)                                                                \
+  asm volatile(STR                                                                              \
+               :                                                                                \
+               : "v"(aoff[0]), "v"(aoff[1]), "v"(boff[0]), "v"(boff[1]), "v"(boff[2]),         \
+                 "v"(boff[3]), "v"(ra[0]), "v"(ra[1]), "v"(rb[0]), "v"(rb[1]), "v"(rb[2]),      \
+                 "v"(rb[3]), "v"(coff), "s"(abase), "s"(bbase),                                 \
+                 "s"(cbase), "s"(nk), "s"(lds), "s"(ldsa), "s"(ldsb), "s"(bstep), "s"(nstride), \
+                 "s"(arow8), "s"(ubase), "s"(ustage), "v"(uoff), "v"(uread)                     \
+               : TH_GEMM_ASM_SILU_CLOBBERS, "vcc", "scc", "memory")
+    if constexpr (BT) {
+      if constexpr (DT == kBF16) {
+        if constexpr (DT_OUT == kBF16) TH_GEMM_ASM_SILU_OPS(TH_GEMM_ASM_SILU_BF16_BF16_BT);
+        else TH_GEMM_ASM_SILU_OPS(TH_GEMM_ASM_SILU_BF16_F16_BT);
+      } else {
+        if constexpr (DT_OUT == kBF16) TH_GEMM_ASM_SILU_OPS(TH_GEMM_ASM_SILU_F16_BF16_BT);
+        else TH_GEMM_ASM_SILU_OPS(TH_GEMM_ASM_SILU_F16_F16_BT);
+      }
+    } else if constexpr (DT == kBF16) {
+      if constexpr (DT_OUT == kBF16) TH_GEMM_ASM_SILU_OPS(TH_GEMM_ASM_SILU_BF16_BF16);
+      else TH_GEMM_ASM_SILU_OPS(TH_GEMM_ASM_SILU_BF16_F16);
+    } else {
+      if constexpr (DT_OUT == kBF16) TH_GEMM_ASM_SILU_OPS(TH_GEMM_ASM_SILU_F16_BF16);
+      else TH_GEMM_ASM_SILU_OPS(TH_GEMM_ASM_SILU_F16_F16);
+    }
+#undef TH_GEMM_ASM_SILU_OPS
+    return;
+  }
 #define TH_GEMM_ASM_OPS(STR)                                                                    \
   asm volatile(STR                                                                              \
                :                                                                                \
@@ -139,16 +180,18 @@ __device__ __forceinline__ void gemm_asm_tile(const uint16_t* __restrict__ A,
 #undef TH_GEMM_ASM_OPS
 }
 
-// Batch index = blockIdx.y (element strides sa, sb, sc).
-template <int DT, int DT_OUT, bool BT = false>
+// Batch index = blockIdx.y (element strides sa, sb, sc; UP, with SILU, strides like C).
+template <int DT, int DT_OUT, bool BT = false, bool SILU = false>
 __global__ void __launch_bounds__(gasm::NT, 1)
 gemm_asm_256(const uint16_t* __restrict__ A, const uint16_t* __restrict__ B, void* __restrict__ C,
-             uint32_t M, uint32_t N, uint32_t K, uint64_t sa, uint64_t sb, uint64_t sc) {
+             uint32_t M, uint32_t N, uint32_t K, uint64_t sa, uint64_t sb, uint64_t sc,
+             const void* __restrict__ UP = nullptr) {
   constexpr uint32_t OSZ = (DT_OUT == kF32) ? 4 : 2;
   uint32_t tm, tn;
   gemm::tile_coords(blockIdx.x, M / 256, N / 256, tm, tn);
-  gemm_asm_tile<DT, DT_OUT, BT>(A + blockIdx.y * sa, B + blockIdx.y * sb,
-                            static_cast<char*>(C) + static_cast<size_t>(blockIdx.y) * sc * OSZ, M,
-                            N, K, tm, tn);
+  const size_t coff = static_cast<size_t>(blockIdx.y) * sc * OSZ;
+  gemm_asm_tile<DT, DT_OUT, BT, SILU>(A + blockIdx.y * sa, B + blockIdx.y * sb,
+                                      static_cast<char*>(C) + coff, M, N, K, tm, tn,
+                                      SILU ? static_cast<const char*>(UP) + coff : nullptr);
 }
 }  // namespace th

@@ -76,7 +76,10 @@ from pathlib import Path
 
 OPN = ["aoffE", "aoffO", "boff0", "boff1", "boff2", "boff3", "ra0", "ra1",
        "rb0", "rb1", "rb2", "rb3", "coff",
-       "abase", "bbase", "cbase", "nk", "lds", "ldsa", "ldsb", "bstep", "nstride", "arow8"]
+       "abase", "bbase", "cbase", "nk", "lds", "ldsa", "ldsb", "bstep", "nstride", "arow8",
+       # the SiLU*Mul program only: UP tile base, wave's LDS staging region (m0 of the UP
+       # DMA), per-lane UP DMA offset, per-lane LDS read base
+       "ubase", "ustage", "uoff", "uread"]
 OP = {n: i for i, n in enumerate(OPN)}
 
 
@@ -272,6 +275,71 @@ def epilogue(out_dt, mis=range(8)):
     return L
 
 
+LOG2E_NEG = "0xbfb8aa3b"   # -log2(e) in f32
+
+
+def dma_up():
+    """The SiLU*Mul program's UP tile: 32 units of four 256-byte rows (the wave's 128 rows
+    x 128 columns, 16-bit) into the wave's 32 KB staging region, row-major."""
+    out = [[f"s_mov_b64 s[58:59], {o('ubase')}", f"s_lshl_b32 s56, {o('nstride')}, 2"]]
+    for j in range(32):
+        out.append([f"s_add_u32 m0, {o('ustage')}, {1024 * j}", "s_nop 0",
+                    f"global_load_lds_dwordx4 {o('uoff')}, s[58:59]",
+                    "s_add_u32 s58, s58, s56", "s_addc_u32 s59, s59, 0"])
+    return out
+
+
+def epilogue_silu(out_dt):
+    """C = silu(acc) * UP for 16-bit C, silu(x) = x / (1 + exp(-x)) as x * rcp(1 +
+    2^(-x log2 e)) in f32 (v_exp_f32, v_rcp_f32), one rounding at the end.  Values go
+    through the same lane swap as the f32 stores; UP comes from the staging region at
+    the same (row, column) and C is written with short stores (two rows of 32 columns
+    per store)."""
+    cvt = "v_cvt_pk_bf16_f32" if out_dt == "bf16" else "v_cvt_pk_f16_f32"
+    T = list(range(128, 136))     # temps: fragment registers, free after the last MFMAs
+    L = [f"s_lshl_b32 s56, {o('nstride')}, 2"]
+    for mi in range(8):
+        for r in range(4):
+            row = mi * 16 + r
+            L.append(f"s_mul_i32 {SROW}, {o('nstride')}, {row}")
+            L.append(f"v_add_u32 v32, {SROW}, {o('coff')}")
+            L.append("v_add_u32 v33, s56, v32")
+            for ni in range(8):
+                L.append(f"v_accvgpr_read_b32 v{36 + ni}, a{4 * (8 * mi + ni) + r}")
+            for p in range(4):
+                L.append(f"ds_read_u16 v{44 + 2 * p}, {o('uread')} offset:{256 * row + 64 * p}")
+                L.append(f"ds_read_u16 v{45 + 2 * p}, {o('uread')} offset:{256 * (row + 4) + 64 * p}")
+            L.append("s_nop 1")
+            for p in range(4):
+                L.append(f"v_permlane16_swap_b32 v{36 + 2 * p}, v{37 + 2 * p}")
+            L.append("s_nop 1")
+            G, U = [36 + k for k in range(8)], [44 + k for k in range(8)]
+            for k in range(8):
+                L.append(f"v_mul_f32 v{T[k]}, {LOG2E_NEG}, v{G[k]}")
+            for k in range(8):
+                L.append(f"v_exp_f32 v{T[k]}, v{T[k]}")
+            for k in range(8):
+                L.append(f"v_add_f32 v{T[k]}, 1.0, v{T[k]}")
+            for k in range(8):
+                L.append(f"v_rcp_f32 v{T[k]}, v{T[k]}")
+            for k in range(8):
+                L.append(f"v_mul_f32 v{T[k]}, v{G[k]}, v{T[k]}")
+            L.append("s_waitcnt lgkmcnt(0)")
+            for k in range(8):
+                if out_dt == "bf16":
+                    L.append(f"v_lshlrev_b32 v{U[k]}, 16, v{U[k]}")
+                else:
+                    L.append(f"v_cvt_f32_f16 v{U[k]}, v{U[k]}")
+            for k in range(8):
+                L.append(f"v_mul_f32 v{G[k]}, v{T[k]}, v{U[k]}")
+            for k in range(8):
+                L.append(f"{cvt} v{G[k]}, v{G[k]}, v{G[k]}")
+            for p in range(4):
+                L.append(f"global_store_short v32, v{36 + 2 * p}, {SC_} offset:{64 * p} nt")
+                L.append(f"global_store_short v33, v{37 + 2 * p}, {SC_} offset:{64 * p} nt")
+    return L
+
+
 def vm(k4, steady):
     """vmcnt of step k % 4 == k4 (None: no wait), steady: the group issues DMA."""
     if BT[0]:
@@ -281,7 +349,11 @@ def vm(k4, steady):
     return [16, 4, 0, None][k4]
 
 
-def program(dt, out_dt, bt=False):
+def program(dt, out_dt, bt=False, silu=False):
+    """silu: the SiLU*Mul epilogue (16-bit C): after the barrier that opens the last
+    step, when every wave has read its last fragments, each wave's UP tile is fetched
+    into its 32 KB of the (then idle) ring under the last step's MFMAs."""
+    assert not silu or out_dt != "f32"
     BT[0] = bt
     mn = "v_mfma_f32_16x16x32_bf16" if dt == "bf16" else "v_mfma_f32_16x16x32_f16"
     L = ["s_mov_b32 s55, m0",
@@ -337,14 +409,29 @@ def program(dt, out_dt, bt=False):
     # the last step: row block mi's stores start once the MFMAs of row block mi + 2
     # have issued (16 MFMAs after its last one: its results are written), the last
     # two row blocks' after the loop
-    L += ["s_waitcnt lgkmcnt(0)"] + deferred(2, mn)
-    M = mfmas(1, mn)
-    for mi in range(8):
-        L += M[8 * mi:8 * mi + 8]
-        if mi >= 2:
-            L += epilogue(out_dt, [mi - 2])
-    L += ["s_nop 7", "s_nop 7", "s_nop 7", "s_nop 7"]   # MFMA results -> readers
-    L += epilogue(out_dt, [6, 7])
+    if silu:
+        L += ["s_waitcnt lgkmcnt(0)", "s_barrier"] + deferred(2, mn)
+        M = mfmas(1, mn)
+        D = dma_up()
+        slots = [[] for _ in M]
+        for j, d in enumerate(D):
+            slots[min(len(M) - 1, (j * len(M)) // len(D))].append(d)
+        for m, sl in zip(M, slots):
+            L.append(m)
+            for g in sl:
+                L.extend(g)
+        # MFMA results -> readers; UP landed (no store issued yet)
+        L += ["s_nop 7", "s_nop 7", "s_nop 7", "s_nop 7", "s_waitcnt vmcnt(0)"]
+        L += epilogue_silu(out_dt)
+    else:
+        L += ["s_waitcnt lgkmcnt(0)"] + deferred(2, mn)
+        M = mfmas(1, mn)
+        for mi in range(8):
+            L += M[8 * mi:8 * mi + 8]
+            if mi >= 2:
+                L += epilogue(out_dt, [mi - 2])
+        L += ["s_nop 7", "s_nop 7", "s_nop 7", "s_nop 7"]   # MFMA results -> readers
+        L += epilogue(out_dt, [6, 7])
     L += ["L_end_%=:"]
     L += ["s_waitcnt vmcnt(0)", "s_mov_b32 m0, s55"]
     return L
@@ -361,9 +448,15 @@ def main(path):
             for out_dt in ("f32", "bf16", "f16"):
                 lines.append(f'#define TH_GEMM_ASM_{dt.upper()}_{out_dt.upper()}{"_BT" if bt else ""} '
                              f'"{cstr(program(dt, out_dt, bt))}"')
+    for bt in (False, True):
+        for dt in ("bf16", "f16"):
+            for out_dt in ("bf16", "f16"):
+                lines.append(f'#define TH_GEMM_ASM_SILU_{dt.upper()}_{out_dt.upper()}{"_BT" if bt else ""} '
+                             f'"{cstr(program(dt, out_dt, bt, silu=True))}"')
     clob = ([f'"v{k}"' for k in range(16, 256)] + [f'"a{k}"' for k in range(256)] +
             [f'"s{k}"' for k in range(48, 58)])
     lines.append("#define TH_GEMM_ASM_CLOBBERS " + ",".join(clob))
+    lines.append("#define TH_GEMM_ASM_SILU_CLOBBERS TH_GEMM_ASM_CLOBBERS, \"s58\", \"s59\"")
     text = "\n".join(lines) + "\n"
     p = Path(path)
     if not p.exists() or p.read_text() != text:

@@ -315,8 +315,15 @@ int gemm_mfma_go(const GemmArgs& g, dim3 grid) {
     if constexpr (EPI == th::gemm::kEpiStore) {
       if (gemm_asm() && th::gasm::fits(g.m, g.n, g.k, static_cast<int>(OSZ))) {
         hipLaunchKernelGGL((th::gemm_asm_256<DT, DTO, BT>), grid, dim3(th::gasm::NT), 0, g.s, A,
-                           B, g.c, g.m, g.n, g.k, g.sa, g.sb, g.sc);
+                           B, g.c, g.m, g.n, g.k, g.sa, g.sb, g.sc, nullptr);
         return launch_status("matmul (MFMA asm) launch");
+      }
+    } else if constexpr (DTO != th::kF32) {
+      // SiLU*Mul with 16-bit C (UP staged through LDS: 16-byte aligned, checked above)
+      if (gemm_asm() && th::gasm::fits(g.m, g.n, g.k, static_cast<int>(OSZ))) {
+        hipLaunchKernelGGL((th::gemm_asm_256<DT, DTO, BT, true>), grid, dim3(th::gasm::NT), 0, g.s,
+                           A, B, g.c, g.m, g.n, g.k, g.sa, g.sb, g.sc, g.up);
+        return launch_status("matmul silu*mul (MFMA asm) launch");
       }
     }
     hipLaunchKernelGGL((th::gemm_dma_256<DT, DTO, BT, th::gemm::DBK, th::gemm::NSTAGE,
