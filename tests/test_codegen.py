@@ -322,6 +322,15 @@ def test_fused_swiglu_takes_up_from_its_own_view():
     assert "silu*mul epilogue" in out
 
 
+def test_fused_swiglu_whole_tiles_16bit_lower_to_the_assembly_entry():
+    out = th.emit((EXAMPLES / "swiglu_gate_bf16.mlir").read_text()).source
+    fn = out[out.index("kernel swiglu_gate_f16"):]
+    assert "th::entry::gemm_asm<th::kF16, th::kF16, false, true>(" in fn
+    assert ("(reinterpret_cast<uint16_t*>(p3)), 256u, 512u, 512u, th_tiles, "
+            "(reinterpret_cast<const uint16_t*>(p2)));") in fn
+    assert "__launch_bounds__(256, 1) swiglu_gate_f16" in fn
+
+
 def test_fused_swiglu_rejects_up_in_another_dtype():
     text = (EXAMPLES / "swiglu_gate_bf16.mlir").read_text().replace(
         "%u = llvm.call @__tile_load_f32(%arg2", "%u = llvm.call @__tile_load_f16(%arg2")

@@ -214,6 +214,26 @@ def test_swiglu_gate_bf16_fused(dev, stream, launcher):
         assert_gemm_close(got[t], ref, f"emitted swiglu tile {t}")
 
 
+def test_swiglu_gate_f16_whole_tiles(dev, stream, launcher):
+    """256x512x512 f16 -> f16 over two logical tiles: the generated-assembly entry's
+    SiLU*Mul program."""
+    tiles, M, K, N = 2, 256, 512, 512
+    rng = np.random.default_rng(15)
+    a = orc.narrow(rng.standard_normal(tiles * M * K).astype(np.float32), orc.F16)
+    b = orc.narrow((rng.standard_normal(tiles * K * N) * 0.05).astype(np.float32), orc.F16)
+    u = orc.narrow(rng.standard_normal(tiles * M * N).astype(np.float32), orc.F16)
+    ab, bb, ub = up(dev, stream, a, D.F16), up(dev, stream, b, D.F16), up(dev, stream, u, D.F16)
+    cb = dev.alloc(tiles * M * N, D.F16)
+    launcher.launch("swiglu_gate_f16", th.LaunchGrid.blocks_only(tiles),
+                    [ptr(ab), ptr(bb), ptr(ub), ptr(cb)], stream)
+    got = orc.widen(cb.copy_to_host(stream), orc.F16).reshape(tiles, M, N)
+    for t in range(tiles):
+        ref = orc.matmul_silu_mul(a[t * M * K:(t + 1) * M * K], b[t * K * N:(t + 1) * K * N],
+                                  u[t * M * N:(t + 1) * M * N], M, K, N, orc.F16, orc.F16)
+        assert_gemm_close(got[t], orc.widen(ref, orc.F16).reshape(M, N),
+                          f"emitted swiglu f16 tile {t}", u16_dtype=orc.F16)
+
+
 def test_attention_f32_tiles(dev, stream, launcher, golden):
     g = golden("attention_f32.npz")
     s, d = (int(t) for t in g["sd"])

@@ -152,19 +152,22 @@ __device__ __forceinline__ void gemm_dma(const uint16_t* A, const uint16_t* B, v
 }
 
 // Whole 256 x 256 tiles with K a multiple of 128 (gasm::fits, checked by the emitter):
-// the library's generated-assembly tile program, 256 threads per workgroup.  Operands
-// that are not 16-byte aligned (checked at run time) take the per-element kernel
-// instead, which fits in the same workgroup.
-template <int DT, int DTO, bool BT = false>
+// the library's generated-assembly tile program, 256 threads per workgroup; SILU: the
+// SiLU*Mul program (16-bit C, UP laid out like C).  Operands that are not 16-byte
+// aligned (checked at run time) take the per-element kernel instead, which fits in the
+// same workgroup.
+template <int DT, int DTO, bool BT = false, bool SILU = false>
 __device__ __forceinline__ void gemm_asm(const uint16_t* A, const uint16_t* B, void* C, uint32_t M,
-                                         uint32_t N, uint32_t K, uint32_t batch) {
+                                         uint32_t N, uint32_t K, uint32_t batch,
+                                         const void* up = nullptr) {
   constexpr int OSZ = (DTO == kF32) ? 4 : 2;
   const uint32_t tiles_m = M / 256, tiles_n = N / 256;
   const uint32_t per = tiles_m * tiles_n;
   const size_t sa = static_cast<size_t>(M) * K * 2, sb = static_cast<size_t>(K) * N * 2;
   const size_t sc = static_cast<size_t>(M) * N * OSZ;
   const uintptr_t bits = reinterpret_cast<uintptr_t>(A) | reinterpret_cast<uintptr_t>(B) |
-                         reinterpret_cast<uintptr_t>(C) | sa | sb | sc;
+                         reinterpret_cast<uintptr_t>(C) | reinterpret_cast<uintptr_t>(up) | sa |
+                         sb | sc;
   const bool vec = (bits & 15) == 0;
   for (uint32_t w = blockIdx.x; w < per * batch; w += gridDim.x) {
     const uint32_t bi = w / per;
@@ -173,11 +176,13 @@ __device__ __forceinline__ void gemm_asm(const uint16_t* A, const uint16_t* B, v
     const uint16_t* a = A + static_cast<size_t>(bi) * M * K;
     const uint16_t* b = B + static_cast<size_t>(bi) * K * N;
     char* c = static_cast<char*>(C) + bi * sc;
+    const void* u = SILU ? static_cast<const char*>(up) + bi * sc : nullptr;
     if (vec) {
-      __syncthreads();  // the previous tile's last fragment reads are done
-      gemm_asm_tile<DT, DTO, BT>(a, b, c, M, N, K, tm, tn);
+      __syncthreads();  // the previous tile's last fragment reads (or UP reads) are done
+      gemm_asm_tile<DT, DTO, BT, SILU>(a, b, c, M, N, K, tm, tn, u);
     } else {
-      gemm_dot_tile_256<DT, DTO, BT>(a, b, c, M, N, K, tm, tn);
+      gemm_dot_tile_256<DT, DTO, BT, SILU ? gemm::kEpiSiluMul : gemm::kEpiStore>(a, b, c, M, N, K,
+                                                                               tm, tn, u);
     }
   }
 }

@@ -875,10 +875,10 @@ bool matmul_entry(const Kernel& k, const TileVal& mm, const Store& st, const cha
   const int osz = out == F32 ? 4 : 2;
   const bool dma = mfma && K % 32 == 0 && N % 8 == 0 && (st.dst.offset * osz) % 16 == 0 &&
                    (!up || (up->src.offset * osz) % 16 == 0);
-  // whole 256 x 256 tiles, plain store: the generated-assembly program
-  // (the shapes th::gasm::fits accepts: K in groups of four 32-deep steps, at least
-  // two, and per-lane byte offsets within 32 bits)
-  const bool gasm = dma && !up && M > 0 && N > 0 && M % 256 == 0 && N % 256 == 0 &&
+  // whole 256 x 256 tiles, plain store or SiLU*Mul into 16-bit C: the generated-assembly
+  // program (the shapes th::gasm::fits accepts: K in groups of four 32-deep steps, at
+  // least two, and per-lane byte offsets within 32 bits)
+  const bool gasm = dma && (!up || out != F32) && M > 0 && N > 0 && M % 256 == 0 && N % 256 == 0 &&
                     K % 128 == 0 && K >= 256 && 512LL * K < (1LL << 31) &&
                     136LL * N * osz < (1LL << 31) && 64LL * N < (1LL << 31);
   os << "matmul " << M << "x" << K << "x" << N << (bt ? " (B transposed)" : "") << " " << dt_name(in)
@@ -900,7 +900,7 @@ bool matmul_entry(const Kernel& k, const TileVal& mm, const Store& st, const cha
                               : ", th_tiles);\n}\n";
   if (gasm) {
     os << "  th::entry::gemm_asm<" << dt_enum(in) << ", " << dt_enum(out) << ", "
-       << (bt ? "true" : "false") << ">("
+       << (bt ? "true" : "false") << (up ? ", true" : "") << ">("
        << view_ptr(a, "uint16_t") << ", " << view_ptr(b, "uint16_t") << ", "
        << store_ptr(st, dt_ctype(out)) << ", " << u(M) << ", " << u(N) << ", " << u(K) << tail;
     desc(os, k, threads, static_cast<unsigned>((M / 256) * (N / 256)), 1);
