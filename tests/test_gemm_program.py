@@ -217,8 +217,10 @@ class Walk:
             elif op.startswith("s_cmp_"):
                 x, y = self.val(a[0]), self.val(a[1])
                 self.scc = int({"eq": x == y, "lg": x != y}[op.split("_")[2]])
-            elif op in ("s_cbranch_scc1", "s_branch"):
-                if op == "s_branch" or self.scc:
+            elif op == "s_bitcmp1_b32":
+                self.scc = (self.val(a[0]) >> self.val(a[1])) & 1
+            elif op in ("s_cbranch_scc0", "s_cbranch_scc1", "s_branch"):
+                if op == "s_branch" or self.scc == int(op[-1]):
                     pc = self.labels[a[0]]
             else:
                 raise AssertionError("unmodelled instruction: " + line)
