@@ -81,9 +81,9 @@ def test_budget_rule():
 
 def test_every_built_kernel_fits_its_workgroup():
     objs = [_build.example_path(s) for s in EXAMPLES]
-    ops_o = _build.OBJ_DIR / "ops.hip.o"
-    if ops_o.exists():
-        objs.append(ops_o)
+    for name in ("ops.hip.o", "ops_gemm.hip.o"):
+        if (_build.OBJ_DIR / name).exists():
+            objs.append(_build.OBJ_DIR / name)
     _build.check_code_objects(objs)
 
 

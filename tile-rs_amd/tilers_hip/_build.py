@@ -39,7 +39,7 @@ DEVICE_FLAGS = [
 ]
 HOST_CXX_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-Wall", "-Wextra"]
 
-HIP_SOURCES = ["ops.hip", "runtime.cpp"]
+HIP_SOURCES = ["ops.hip", "ops_gemm.hip", "runtime.cpp"]
 CPP_SOURCES = ["target/mlir_parse.cpp", "target/emit_hip.cpp", "target/registry.cpp"]
 
 
@@ -245,7 +245,7 @@ def build_examples(verbose: bool = False) -> list:
 
 
 GENERATED = [
-    # (generator script, output) -- generated device code included by ops.hip
+    # (generator script, output) -- generated device code included by ops.hip and ops_gemm.hip
     (CSRC / "kernels" / "gen_prefill.py", CSRC / "kernels" / "gen" / "prefill_asm.inc"),
     (CSRC / "kernels" / "gen_gemm.py", CSRC / "kernels" / "gen" / "gemm_asm.inc"),
 ]
