@@ -243,7 +243,10 @@ class GemmF32(Gemm):
 class Swiglu(Mlp):
     """Config 3's MLP shape with the gate epilogue fused: C = silu(A.B) * UP (f16)."""
     name = "swiglu"
-    emitted = None
+    emitted = ("config_gemms", "mlp_gate_f16")
+
+    def emitted_args(self, i):
+        return 1, [self.a, self.b, self.up, self.c], []
 
     def config(self):
         return {"workload": "MLP gate GEMM M=8192 K=4096 N=14336 with fused silu*mul "

@@ -154,6 +154,9 @@ def test_whole_tile_matmuls_lower_to_the_assembly_entry():
     assert "__launch_bounds__(256, 1) gemm_4096_bf16_acc_f32(" in src
     assert "__th_desc_gemm_4096_bf16_acc_f32 = {th::kLaunchDescMagic, 256u, 256u, 1u," in src
     assert "__th_desc_mlp_up_f16 = {th::kLaunchDescMagic, 256u, 1792u, 1u," in src
+    gate = src[src.index("kernel mlp_gate_f16"):]
+    assert "th::entry::gemm_asm<th::kF16, th::kF16, false, true>(" in gate
+    assert "__th_desc_mlp_gate_f16 = {th::kLaunchDescMagic, 256u, 1792u, 1u," in gate
     assert "th::entry::gemm_dma" not in src
     k96 = (EXAMPLES / "matmul_bf16.mlir").read_text().replace("constant(256 : i32)",
                                                                 "constant(96 : i32)")

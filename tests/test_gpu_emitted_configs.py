@@ -70,6 +70,26 @@ def test_config3_mlp_emitted(dev, stream, launcher):
                       "emitted config3", u16_dtype=orc.F16)
 
 
+def test_config3_swiglu_emitted(dev, stream, launcher):
+    """Config 3's shape with the gate epilogue through the emitter (the assembly entry's
+    SiLU*Mul program): 96 rows against the oracle."""
+    M, K, N = 8192, 4096, 14336
+    a = rnd(dev, stream, M * K, D.F16, "normal", 0.0, 1.0, SEED0 + 3)
+    b = rnd(dev, stream, K * N, D.F16, "normal", 0.0, 0.02, SEED0 + 103)
+    u = rnd(dev, stream, M * N, D.F16, "normal", 0.0, 1.0, SEED0 + 203)
+    c = dev.alloc(M * N, D.F16)
+    launcher.launch("mlp_gate_f16", th.LaunchGrid.blocks_only(1), [ptr(a), ptr(b), ptr(u), ptr(c)],
+                    stream)
+    ah = a.copy_to_host(stream).reshape(M, K)
+    bh, uh = b.copy_to_host(stream), u.copy_to_host(stream).reshape(M, N)
+    got = orc.widen(c.copy_to_host(stream), orc.F16).reshape(M, N)
+    for r0 in (0, 4064, 8160):
+        ref = orc.matmul_silu_mul(np.ascontiguousarray(ah[r0:r0 + 32]), bh,
+                                  np.ascontiguousarray(uh[r0:r0 + 32]), 32, K, N, orc.F16, orc.F16)
+        assert_gemm_close(got[r0:r0 + 32], orc.widen(ref, orc.F16).reshape(32, N),
+                          f"emitted config3 swiglu rows {r0}", u16_dtype=orc.F16)
+
+
 def test_config4_prefill_emitted(dev, stream, launcher, config4):
     c = config4                        # batch = logical tiles
     o = dev.alloc(c.n, D.BF16)
