@@ -69,6 +69,12 @@ v32-v51 epilogue, v[128:191] and v[192:255] the two fragment sets (A mi at +4 mi
 at +32 + 4 ni); s[48:49] A pointer, s[50:51] B pointer, s[52:53] C base, s54 loop
 count, s55 saved m0, s56-s57 temps.
 
+SiLU*Mul form (C = silu(A.B) * UP, 16-bit C and UP): the same loop; the last step opens
+with a barrier (every wave has read its last fragments), after which each wave DMAs its
+128 x 128 UP tile into its own 32 KB of the idle ring under the last step's MFMAs
+(s[58:59] the UP pointer), waits for it (no store has been issued yet, so vmcnt(0)
+covers exactly the UP loads), and runs epilogue_silu.  v[128:135] are its temps.
+
 Usage: python gen_gemm.py <out.inc>   (run by the library build)
 """
 import sys
