@@ -26,6 +26,7 @@
 #include "runtime.hpp"
 
 using th::fail;
+using namespace th::ops;
 
 namespace {
 

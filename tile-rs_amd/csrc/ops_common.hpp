@@ -7,7 +7,8 @@
 
 #include "runtime.hpp"
 
-namespace {
+namespace th {
+namespace ops {
 
 inline hipStream_t as_stream(th_stream s) { return static_cast<hipStream_t>(s); }
 
@@ -42,4 +43,5 @@ inline uint32_t current_cu_count() {
   return n;
 }
 
-}  // namespace
+}  // namespace ops
+}  // namespace th

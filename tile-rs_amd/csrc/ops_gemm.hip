@@ -16,6 +16,7 @@
 #include "ops_common.hpp"
 
 using th::fail;
+using namespace th::ops;
 
 namespace {
 
