@@ -168,7 +168,9 @@ int th_matmul(const void* a, const void* b, void* c, uint32_t m, uint32_t k, uin
  * -> __tile_mul_* (tile.rs:229, :1135; linalg mlir_to_linalg.rs:449-451,
  * :774-782, :425; the gpu target fuses silu+mul the same way,
  * mlir_to_gpu.rs:536-634).  UP has out_dtype and C's layout and strides;
- * arithmetic is f32 with one rounding at the output.  Other arguments as
+ * arithmetic is f32 with one rounding at the output (whole 256 x 256 tiles with
+ * 16-bit C evaluate exp and the division with the hardware's f32 exp2 and
+ * reciprocal, within the GEMM tolerance of the exact form).  Other arguments as
  * th_matmul. */
 int th_matmul_silu_mul(const void* a, const void* b, const void* up, void* c, uint32_t m,
                        uint32_t k, uint32_t n, th_dtype in_dtype, th_dtype out_dtype,
