@@ -49,13 +49,11 @@ bool gemm_dma() {
 
 // Whole-tile shapes (B row-major or stored N x K) run on the generated-assembly kernel
 // (gemm_asm.hpp) unless TILERS_HIP_GEMM_ASM=0 (a debugging switch: the LDS-DMA
-// kernel, which gives the same bits, then runs them).
+// kernel, which gives the same bits for the plain store, then runs them).  Read on
+// every call (a getenv, next to a kernel launch), so a process can compare the two.
 bool gemm_asm() {
-  static const bool v = [] {
-    const char* e = std::getenv("TILERS_HIP_GEMM_ASM");
-    return !(e && std::atoi(e) == 0);
-  }();
-  return v;
+  const char* e = std::getenv("TILERS_HIP_GEMM_ASM");
+  return !(e && std::atoi(e) == 0);
 }
 
 // Split-K for shapes with too few 256 x 256 tiles to fill the chip (small M:
