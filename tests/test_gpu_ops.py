@@ -825,6 +825,17 @@ def test_matmul_silu_mul_whole_tiles_batched(dev, stream):
                  batch=2)
 
 
+@pytest.mark.parametrize("trans", [False, True])
+@pytest.mark.parametrize("in_dt", [D.BF16, D.F16])
+@pytest.mark.parametrize("out_dt", [D.BF16, D.F16])
+def test_matmul_silu_mul_whole_tiles_every_variant(dev, stream, trans, in_dt, out_dt):
+    """Each of the assembly program's eight SiLU*Mul variants (operand dtype x C/UP dtype
+    x B layout) on two 256 x 256 tiles with K = 384 (12 steps of 32)."""
+    _swiglu_case(dev, stream, np.random.default_rng(90 + 4 * trans + 2 * (in_dt == D.F16) +
+                                                    (out_dt == D.F16)),
+                 256, 384, 512, in_dt, out_dt, trans)
+
+
 def test_matmul_silu_mul_saturated_gate(dev, stream):
     """Gate values far past the exponential's range (|A.B| up to ~200): silu(x) -> x for
     large x and -> -0 for large negative x, with no NaN from inf / inf."""
