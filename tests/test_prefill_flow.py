@@ -1,9 +1,9 @@
 """Control flow of the generated prefill main loop, checked on the CPU.
 
 kernels/gen_prefill.py emits the loop as one asm statement.  Every wave of a
-workgroup must pass the same number of s_barrier instructions, and before each
-barrier a wave must have waited for its own DMA share of the K/V block the next
-period reads.  Waves leave the compute loop at different blocks (the causal
+workgroup must pass the same number of s_barrier instructions (one per two K/V
+periods), and before each barrier a wave must have waited for its own DMA share of
+the K/V blocks the next two periods read.  Waves leave the compute loop at different blocks (the causal
 diagonal), so this walks the scalar instructions of the program for every wave of
 a range of (seq_len, start_pos, query block) shapes and checks both properties.
 Vector instructions are skipped; vector compares that write scalar masks (the
@@ -55,6 +55,7 @@ class Wave:
         self.barriers = []        # (s58, completed DMA kv0 set) at each barrier
         self.done_upto = 0        # vmem ops known complete (prefix length)
         self.mfmas = 0
+        self.kv = {}              # block (kv0) each DMA address register was computed for
 
     def val(self, tok):
         tok = tok.strip()
@@ -88,7 +89,10 @@ class Wave:
             a = [x.strip() for x in rest.split(",")] if rest else []
             if op.startswith("global_load") or op.startswith("global_store"):
                 real_dma = op == "global_load_lds_dwordx4" and self.exec != 0
-                self.vmem.append(self.s.get("s63", 0) if real_dma else None)
+                self.vmem.append(self.kv[a[0]] if real_dma else None)
+            elif op in ("v_add_u32", "v_add3_u32") and a[0] in ("v16", "v17", "v18") and a[1].startswith("s"):
+                # a DMA address: row = block kv0 (an SGPR) + lane offsets
+                self.kv[a[0]] = self.val(a[1])
             elif op.startswith("v_mfma"):
                 self.mfmas += 1
             elif op.startswith("v_cmp") and a and a[0].startswith("s["):
@@ -147,18 +151,32 @@ def test_every_wave_passes_the_same_barriers(seq_len, start_pos, head_dim):
             w = Wave(PROGS[head_dim], ops, rng).run()
             nb = ops["nb"]
             counts.add(len(w.barriers))
-            # one barrier after the prologue, then one per period j = 0 .. nb-2
-            assert len(w.barriers) == nb, (seq_len, start_pos, qb, wave, len(w.barriers), nb)
-            # before the barrier of period j this wave's DMA of block j+1 has landed
-            # (the prologue's barrier covers block 0)
+            # one barrier after the prologue, then one per even period j = 0 .. nb-2
+            want = 1 + (len(range(0, nb - 1, 2)) if nb >= 2 else 0)
+            assert len(w.barriers) == want, (seq_len, start_pos, qb, wave, len(w.barriers), want)
+            # before the barrier of even period j this wave's DMA of blocks j+1 and j+2
+            # (all that periods j and j+1 read) has been issued and has landed; the
+            # prologue's barrier covers block 0
+            issued = {kv for kv in w.vmem if kv is not None}
             for i, (j, done) in enumerate(w.barriers):
-                need = 0 if i == 0 else BKV * (j + 1)
-                issued = {kv for kv in w.vmem if kv is not None}
-                if need in issued:
-                    assert need in done, (seq_len, start_pos, qb, wave, i, j)
+                assert i == 0 or j % 2 == 0, (seq_len, start_pos, qb, wave, i, j)
+                for need in ([0] if i == 0 else [BKV * (j + 1), BKV * (j + 2)]):
+                    if need < BKV * nb:
+                        assert need in issued and need in done, (seq_len, start_pos, qb, wave, i, j, need)
             # every DMA of the ring was issued (blocks 0 .. nb-1, one real batch each)
             assert {kv for kv in w.vmem if kv is not None} >= set(range(0, BKV * nb, BKV))
         assert len(counts) == 1
+
+
+def test_walk_finds_a_missing_wait():
+    """Planted mistake: without the vmcnt(0) waits of the even loop tops, blocks j+1
+    and j+2 are not known to have landed at the barrier of period j."""
+    prog = [l for l in PROG if l.strip() != "s_waitcnt vmcnt(0)"]
+    ops = operands(1000, 0, 3, 7)
+    w = Wave(prog, ops, random.Random(3)).run()
+    missing = [(j, need) for i, (j, done) in enumerate(w.barriers) if i > 0
+               for need in (BKV * (j + 1), BKV * (j + 2)) if need < BKV * ops["nb"] and need not in done]
+    assert missing
 
 
 @pytest.mark.parametrize("head_dim", [128, 64])
@@ -169,7 +187,7 @@ def test_waves_past_the_diagonal_drain(head_dim):
     assert ops["jl"] == 0 and ops["nb"] == 4
     w0 = Wave(PROGS[head_dim], ops, random.Random(1)).run()
     w7 = Wave(PROGS[head_dim], operands(256, 0, 0, 7), random.Random(1)).run()
-    assert len(w0.barriers) == len(w7.barriers) == 4
+    assert len(w0.barriers) == len(w7.barriers) == 3
     # MFMAs per block: n QK and n PV (n = 16 at head_dim 128, 8 at 64); wave 0: S(0),
     # the PV of its only block and at most 4 residual steps of n/4; wave 7: S(0), three
     # periods and the last PV block

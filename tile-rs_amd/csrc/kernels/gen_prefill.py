@@ -24,13 +24,18 @@ A 16-position PV step whose largest probability exceeds 1/ratio of the row's
 running sum also gets its 16-bit residual P - hi(P) multiplied in (out of line,
 only for those steps: 4 MFMAs per step instead of 16 per block).  Scores
 are double-buffered by block parity, so the loop is unrolled by two.  One
-s_barrier per period recycles the LDS stage of block j-1 for block j+NS-1.
+s_barrier per two periods, at even j: before it each wave waits for its DMA share
+of blocks j+1 and j+2 (all it reads until the next barrier); after it every wave
+has finished period j-1, so the stages of blocks j-2 and j-1 are free, and period j
+refills the first with block j+3, period j+1 the second with block j+4 (one DMA
+block per period, each issued one or two periods before the barrier that publishes
+it).  Measured at config 4 against one barrier per period: 10-17 us faster, same
+bits; issuing both blocks in the even period was not faster.
 A wave whose rows end before the workgroup's last block (the causal diagonal:
 wave 0 of a 256-row block needs one of the last four blocks) leaves the compute
 loop after its last unmasked block jl (whose period runs PV(jl) without the
-all-masked S(jl+1)) and drains: each remaining period only
-waits for its DMA share, passes the barrier and issues the next DMA, so every
-wave passes the same barriers (tests/test_prefill_flow.py walks the scalar
+all-masked S(jl+1)) and drains: each remaining period only does the period's
+waits, barrier and DMA issue, so every wave passes the same barriers (tests/test_prefill_flow.py walks the scalar
 control flow of this program for every wave and checks it).
 
 Register map (VGPRs only; the asm statement clobbers v16-v255, s48-s95):
@@ -43,8 +48,10 @@ Register map (VGPRs only; the asm statement clobbers v16-v255, s48-s95):
   v251 K address, v252-255 V^T addresses.
 SGPRs: s[48:51] K bases (+0,+64), s[56:57] V base, s58 j, s59 nb-1 (jl and jd are
   operands), s60 stage of
-  block j+1, s61 stage of block j, s62 DMA stage, s63 DMA kv0, s64 s68 temps,
-  s65 stage end, s[66:67] saved exec, s[70:71] grow mask, s[74:75] DMA exec,
+  block j+1, s61 stage of block j, s62 s63 DMA stage and kv0 of an even period,
+  s53 s54 those of the odd period after it, s64 s68 temps,
+  s65 stage end, s[66:67] saved exec, s[70:71] grow mask, s[74:75] s[92:93] DMA exec
+  (even, odd period),
   s[76:77] full exec, s[78:79] split mask (any step), s[80:81] mask compare,
   s[84:91] split masks of the four PV steps.
 
@@ -354,12 +361,12 @@ class Gen:
         return out
 
     # ---------------- DMA ----------------
-    def dma_lines(self, masked_exec):
-        """Block s63 into the stage at s62: two K and two V loads per lane."""
-        ex0 = ["s_mov_b64 exec, s[74:75]"] if masked_exec else []
+    def dma_lines(self, masked_exec, st_="s62", kv="s63", ex="s[74:75]"):
+        """Block kv into the stage at st_: two K and two V loads per lane."""
+        ex0 = [f"s_mov_b64 exec, {ex}"] if masked_exec else []
         ex1 = ["s_mov_b64 exec, s[76:77]"] if masked_exec else []
-        groups = [[f"v_add_u32 {DK}, s63, {o('krow')}", f"v_min_u32 {DK}, {o('kvlast')}, {DK}",
-                   f"v_lshl_add_u32 {DK}, {DK}, {self.SHIFT}, {o('kcol')}", f"s_add_u32 s64, s62, {o('wave2k')}"]]
+        groups = [[f"v_add_u32 {DK}, {kv}, {o('krow')}", f"v_min_u32 {DK}, {o('kvlast')}, {DK}",
+                   f"v_lshl_add_u32 {DK}, {DK}, {self.SHIFT}, {o('kcol')}", f"s_add_u32 s64, {st_}, {o('wave2k')}"]]
         # an LDS DMA reads m0 one wait state after it is written (the exec write, when
         # there is one, is that wait state)
         w0 = ex0 or ["s_nop 0"]
@@ -367,7 +374,7 @@ class Gen:
             groups.append([f"s_add_u32 m0, s64, {1024 * j}"] + w0 +
                           [f"global_load_lds_dwordx4 {DK}, s[{48 + 2 * j}:{49 + 2 * j}]"] + ex1)
         for j in range(self.NLDK):
-            groups.append([f"v_add3_u32 {DV[j]}, s63, {o('vrow')}, {4 * j}", f"v_min_u32 {DV[j]}, {o('kvlast')}, {DV[j]}",
+            groups.append([f"v_add3_u32 {DV[j]}, {kv}, {o('vrow')}, {4 * j}", f"v_min_u32 {DV[j]}, {o('kvlast')}, {DV[j]}",
                            f"v_lshl_add_u32 {DV[j]}, {DV[j]}, {self.SHIFT}, {o('vcol')}"])
             groups.append([f"s_add_u32 m0, s64, {self.KB + 1024 * j}"] + w0 +
                           [f"global_load_lds_dwordx4 {DV[j]}, s[56:57]"] + ex1)
@@ -390,7 +397,10 @@ class Gen:
     def period(self, par, masked):
         frags = self.qk_frags(1 - par) + self.pv_frags()
         nqk = 2 * self.NDS
-        ops = [dict(lines=g, deadline=min(12, nqk - 2), earliest=-1) for g in self.dma_lines(True)]
+        # every period j issues block j+3: even ones from s62/s63 (exec s[74:75]), odd
+        # ones from s53/s54 (exec s[92:93]); the even loop top sets both
+        dma = self.dma_lines(True) if par == 0 else self.dma_lines(True, "s53", "s54", "s[92:93]")
+        ops = [dict(lines=g, deadline=min(12, nqk - 2), earliest=-1) for g in dma]
         ops += self.phase_b(par, pv0=nqk) + self.phase_a(1 - par, masked, earliest=nqk + 2)
         pre = self.addr_k("s60") + self.addr_v("s61")
         body = self.schedule(frags, ops)
@@ -421,21 +431,32 @@ class Gen:
         out.append(f"{ends}:")
         return out
 
-    def loop_top(self, last_label):
+    def loop_top(self, last_label, par):
+        """Even periods j: wait for this wave's share of blocks j+1 and j+2, barrier
+        (every wave has finished period j-1, so the stages of blocks j-2 and j-1 are
+        free), DMA pointers and exec masks for blocks j+3 and j+4.  Odd periods: no
+        wait, barrier or DMA."""
         out = ["s_cmp_ge_u32 s58, s59", f"s_cbranch_scc1 {last_label}"]
-        # loads issued after block j+1: prologue blocks past it plus the last two
-        # loop DMAs (each iteration issues one, real or with no lanes)
-        out += [f"s_min_u32 s64, {o('nb')}, {NS}", "s_sub_u32 s64, s64, 2", "s_sub_u32 s64, s64, s58",
-                "s_max_i32 s64, s64, 0", "s_min_u32 s68, s58, 2", "s_add_u32 s64, s64, s68"]
-        out += self.vm_wait_cases("s64", list(range(4)), "wl")
+        if par == 1:
+            return out + [f"v_subrev_u32 {st('lim')}, 64, {st('lim')}"]
+        # at j = 0 the prologue's blocks 3 .. min(nb, NS)-1 were issued after blocks 1, 2;
+        # later, blocks j+1 and j+2 are the last ones issued (period j-2)
+        w0, wd = self.label("wz"), self.label("wd")
+        out += ["s_cmp_eq_u32 s58, 0", f"s_cbranch_scc0 {w0}",
+                f"s_min_u32 s64, {o('nb')}, {NS}", "s_sub_u32 s64, s64, 3", "s_max_i32 s64, s64, 0"]
+        out += self.vm_wait_cases("s64", list(range(NS - 2)), "wl")
+        out += [f"s_branch {wd}", f"{w0}:", "s_waitcnt vmcnt(0)", f"{wd}:"]
         out += ["s_barrier"]
         skip = self.label("dsk")
-        out += self.rotate("s62") + ["s_add_u32 s63, s63, 64", "s_mov_b64 s[76:77], exec",
-                                     "s_mov_b64 s[74:75], 0",
-                                     "s_cmp_eq_u32 s58, 0", f"s_cbranch_scc1 {skip}",
-                                     f"s_add_u32 s64, s58, {NS - 1}", f"s_cmp_ge_u32 s64, {o('nb')}",
-                                     f"s_cbranch_scc1 {skip}", "s_mov_b64 s[74:75], exec", f"{skip}:",
-                                     f"v_subrev_u32 {st('lim')}, 64, {st('lim')}"]
+        out += ["s_mov_b32 s62, s53", "s_mov_b32 s63, s54"] + self.rotate("s62") + ["s_add_u32 s63, s63, 64",
+                "s_mov_b32 s53, s62", "s_mov_b32 s54, s63"] + self.rotate("s53") + ["s_add_u32 s54, s54, 64",
+                "s_mov_b64 s[76:77], exec", "s_mov_b64 s[74:75], 0", "s_mov_b64 s[92:93], 0",
+                "s_cmp_eq_u32 s58, 0", f"s_cbranch_scc1 {skip}",
+                "s_add_u32 s64, s58, 3", f"s_cmp_ge_u32 s64, {o('nb')}", f"s_cbranch_scc1 {skip}",
+                "s_mov_b64 s[74:75], exec",
+                "s_add_u32 s64, s58, 4", f"s_cmp_ge_u32 s64, {o('nb')}", f"s_cbranch_scc1 {skip}",
+                "s_mov_b64 s[92:93], exec", f"{skip}:",
+                f"v_subrev_u32 {st('lim')}, 64, {st('lim')}"]
         return out
 
     def fin(self, par, last_label, drain):
@@ -443,23 +464,27 @@ class Gen:
         last: PV(jl) with the period's DMA and barrier, without S(jl+1) (all masked);
         then the drain."""
         frags = self.pv_frags()
-        ops = [dict(lines=g, deadline=min(12, 4 * self.NDT - 2), earliest=-1) for g in self.dma_lines(True)]
+        npv = 4 * self.NDT
+        ops = [dict(lines=g, deadline=min(12, npv - 2), earliest=-1) for g in
+               (self.dma_lines(True) if par == 0 else self.dma_lines(True, "s53", "s54", "s[92:93]"))]
         ops += self.phase_b(par, pv0=0)
         body = self.schedule(frags, ops, pre_quota=10 ** 6)
-        return (self.loop_top(last_label) + self.addr_v("s61") + body + ["s_nop 7", "s_nop 7"] +
-                self.split_tail(par) + ["s_add_u32 s58, s58, 1", f"s_branch {drain}"])
+        return (self.loop_top(last_label, par) + self.addr_v("s61") + body + ["s_nop 7", "s_nop 7"] +
+                self.split_tail(par) + ["s_add_u32 s58, s58, 1", f"s_branch {drain[1 - par]}"])
 
-    def drain(self, label, epi):
-        """Periods after the wave's last unmasked block: the same vmcnt wait, barrier
-        and DMA issue as a loop period (so every wave passes the same barriers and
+    def drain(self, labels, epi):
+        """Periods after the wave's last unmasked block: the same waits, barriers and
+        DMA issues as the loop's periods (so every wave passes the same barriers and
         fills its share of the ring), no MFMA, softmax or LDS reads; the final PV
-        block is skipped as well."""
+        block is skipped as well.  labels: entry at an even / odd period."""
         done = self.label("dlast")
-        top = self.loop_top(done)
-        out = [f"{label}:"] + top
+        out = [f"{labels[0]}:"] + self.loop_top(done, 0)
         for g in self.dma_lines(True):
             out += g
-        out += ["s_add_u32 s58, s58, 1", f"s_branch {label}", f"{done}:", f"s_branch {epi}"]
+        out += ["s_add_u32 s58, s58, 1", f"{labels[1]}:"] + self.loop_top(done, 1)
+        for g in self.dma_lines(True, "s53", "s54", "s[92:93]"):
+            out += g
+        out += ["s_add_u32 s58, s58, 1", f"s_branch {labels[0]}", f"{done}:", f"s_branch {epi}"]
         return out
 
     def program(self):
@@ -485,21 +510,21 @@ class Gen:
         out += self.vm_wait_cases("s64", list(range(NS)), "w0")
         out += ["s_barrier"]
         out += [f"s_mov_b32 s61, {o('lds')}", f"s_add_u32 s60, {o('lds')}, {self.SS}",
-                f"s_add_u32 s62, {o('lds')}, {(NS - 2) * self.SS}", f"s_mov_b32 s63, {(NS - 2) * 64}",
+                f"s_add_u32 s53, {o('lds')}, {2 * self.SS}", "s_mov_b32 s54, 128",
                 "s_mov_b32 s58, 0", f"s_sub_u32 s59, {o('nb')}, 1"]
         out += self.pre_body()
         top = [self.label("top0"), self.label("top1")]
         last = [self.label("last0"), self.label("last1")]
         epi = self.label("epi")
-        drain = self.label("drain")
+        drain = [self.label("drain0"), self.label("drain1")]
         fin = [self.label("fin0"), self.label("fin1")]
         for par in (0, 1):
             msk, nxt = self.label("msk"), self.label("nxt")
             # past the wave's last block (jl) every score is masked: only the ring
             # duties (DMA share, barrier) remain
-            out += [f"{top[par]}:", f"s_cmp_gt_u32 s58, {o('jl')}", f"s_cbranch_scc1 {drain}",
+            out += [f"{top[par]}:", f"s_cmp_gt_u32 s58, {o('jl')}", f"s_cbranch_scc1 {drain[par]}",
                     f"s_cmp_eq_u32 s58, {o('jl')}", f"s_cbranch_scc1 {fin[par]}"]
-            out += self.loop_top(last[par])
+            out += self.loop_top(last[par], par)
             out += ["s_add_u32 s64, s58, 1", f"s_cmp_ge_u32 s64, {o('jd')}", f"s_cbranch_scc1 {msk}"]
             out += self.period(par, False)
             out += [f"s_branch {nxt}", f"{msk}:"]
