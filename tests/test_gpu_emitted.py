@@ -298,6 +298,24 @@ def test_prefill_bf16(dev, stream, launcher, S, start, NH, NKV, Dh):
     assert_attn_close(got, ref, "emitted prefill")
 
 
+@pytest.mark.parametrize("S,start,NH,NKV,Dh", [(300, 20, 8, 2, 128), (520, 64, 4, 4, 64)])
+def test_prefill_bf16_same_bits_as_library(dev, stream, launcher, S, start, NH, NKV, Dh):
+    """The emitted prefill runs the library's kernel with the same scale (its head-dim-128
+    path folds 1/sqrt(128) at compile time): the two outputs match bit for bit."""
+    B, max_seq = 2, start + S + 5
+    rng = np.random.default_rng(S + Dh)
+    q = orc.narrow(rng.standard_normal(B * S * NH * Dh).astype(np.float32), orc.BF16)
+    k = orc.narrow(rng.standard_normal(B * NKV * max_seq * Dh).astype(np.float32), orc.BF16)
+    v = orc.narrow(rng.standard_normal(B * NKV * max_seq * Dh).astype(np.float32), orc.BF16)
+    bufs = [up(dev, stream, t, D.BF16) for t in (q, k, v)]
+    oe, ol = dev.alloc(q.size, D.BF16), dev.alloc(q.size, D.BF16)
+    scal = [C.c_uint32(x) for x in (S, start, max_seq, Dh, NH, NKV)]
+    launcher.launch("prefill_bf16", th.LaunchGrid.blocks_only(B), [ptr(b) for b in bufs] + [ptr(oe)] + scal,
+                    stream)
+    th.attention_prefill(*bufs, ol, B, S, start, max_seq, Dh, NH, NKV, D.BF16, stream)
+    np.testing.assert_array_equal(oe.copy_to_host(stream), ol.copy_to_host(stream))
+
+
 @pytest.mark.parametrize("L,NH,NKV,Dh", [(700, 8, 2, 128), (1100, 16, 16, 128), (300, 6, 2, 128),
                                          (257, 4, 1, 64), (9000, 8, 2, 64), (600, 6, 2, 64)])
 def test_decode_bf16(dev, stream, launcher, L, NH, NKV, Dh):

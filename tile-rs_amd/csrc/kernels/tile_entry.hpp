@@ -280,13 +280,34 @@ __device__ __forceinline__ void prefill(const void* q, const void* k, const void
                             reinterpret_cast<uintptr_t>(v) | reinterpret_cast<uintptr_t>(o);
     if ((head_dim == pfa::D || head_dim == 64) && (align & 15) == 0) {
       const uint32_t nqb = (seq_len + pfa::BQ - 1) / pfa::BQ;
+      auto qq = static_cast<const uint16_t*>(q);
+      auto kk = static_cast<const uint16_t*>(k);
+      auto vv = static_cast<const uint16_t*>(v);
+      auto oo = static_cast<uint16_t*>(o);
+      if (gridDim.x >= batch * nh * nqb) {
+        // One item per workgroup (the launcher's grid), each head dim on a path of its
+        // own that returns: the asm statement clobbers v16-v255 and s48-s95, and values
+        // live across it (the loop's state below) or shared by the two paths' operand
+        // math are spilled to scratch around every item (2-3% at config 4).
+        if (blockIdx.x >= batch * nh * nqb) return;
+        if (head_dim == pfa::D) {
+          // the same value as `scale` at head_dim 128 (sqrt and divide correctly rounded)
+          const float s128 = 1.0f / __builtin_sqrtf(static_cast<float>(pfa::D));
+          uint32_t bh, qb;
+          prefill_work(blockIdx.x, batch, nh, nkv, nqb, bh, qb);
+          pfa::prefill_tile<DT>(qq, kk, vv, oo, seq_len, start_pos, max_seq, nh, nkv,
+                                s128 * kLog2e, bh, qb, HM);
+          return;
+        }
+        uint32_t bh, qb;
+        prefill_work(blockIdx.x, batch, nh, nkv, nqb, bh, qb);
+        pfa::prefill_tile<DT, false, 64>(qq, kk, vv, oo, seq_len, start_pos, max_seq, nh, nkv,
+                                         scale * kLog2e, bh, qb, HM);
+        return;
+      }
       for (uint32_t w = blockIdx.x; w < batch * nh * nqb; w += gridDim.x) {
         uint32_t bh, qb;
         prefill_work(w, batch, nh, nkv, nqb, bh, qb);
-        auto qq = static_cast<const uint16_t*>(q);
-        auto kk = static_cast<const uint16_t*>(k);
-        auto vv = static_cast<const uint16_t*>(v);
-        auto oo = static_cast<uint16_t*>(o);
         if (head_dim == 64)
           pfa::prefill_tile<DT, false, 64>(qq, kk, vv, oo, seq_len, start_pos, max_seq, nh, nkv,
                                            scale * kLog2e, bh, qb, HM);
