@@ -169,6 +169,21 @@ __device__ __forceinline__ void gemm_asm(const uint16_t* A, const uint16_t* B, v
                          reinterpret_cast<uintptr_t>(C) | reinterpret_cast<uintptr_t>(up) | sa |
                          sb | sc;
   const bool vec = (bits & 15) == 0;
+  if (vec && gridDim.x >= per * batch) {
+    // One tile per workgroup (the launcher's grid) on a path that returns: the asm
+    // statement clobbers most registers, and values live across it (the loop's state
+    // below) are spilled to scratch and reloaded before every tile.
+    const uint32_t w = blockIdx.x;
+    if (w >= per * batch) return;
+    const uint32_t bi = w / per;
+    uint32_t tm, tn;
+    gemm::tile_coords(w % per, tiles_m, tiles_n, tm, tn);
+    gemm_asm_tile<DT, DTO, BT, SILU>(A + static_cast<size_t>(bi) * M * K,
+                                     B + static_cast<size_t>(bi) * K * N,
+                                     static_cast<char*>(C) + bi * sc, M, N, K, tm, tn,
+                                     SILU ? static_cast<const char*>(up) + bi * sc : nullptr);
+    return;
+  }
   for (uint32_t w = blockIdx.x; w < per * batch; w += gridDim.x) {
     const uint32_t bi = w / per;
     uint32_t tm, tn;
