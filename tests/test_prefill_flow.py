@@ -351,3 +351,82 @@ def test_program_text_is_self_contained(dt, partial, head_dim):
 def test_clobber_list_matches_the_checked_sets():
     text = Path(G.__file__).read_text()
     assert 'for k in range(16, 256)' in text and 'for k in range(48, 96)' in text
+
+
+# ---------------------------------------------------------------------------
+# K stage layout: the DMA lanes' (row, chunk) targets and the fragment reads must
+# agree.  The lane operands klane, krow and kcol are restated from
+# kernels/prefill_asm.hpp; the read registers, their XORs and the immediates are
+# taken from the generated program.
+# ---------------------------------------------------------------------------
+def k_layout(head_dim, klane, krow, kcol, prog):
+    rb = 2 * head_dim
+    lds = {}
+    for w in range(8):
+        for j in range(head_dim // 64):
+            for lane in range(64):
+                addr = (2048 if head_dim == 128 else 1024) * w + 1024 * j + 16 * lane
+                assert kcol(w, lane) + 16 <= rb
+                assert addr not in lds
+                lds[addr] = (krow(w, lane) + 8 * j, kcol(w, lane) // 16)
+    assert sorted(lds.values()) == [(r, c) for r in range(64) for c in range(head_dim // 8)]
+    # the period's K fragment reads in issue order, and each base register's XOR
+    xor = {G.KADDR: 0}
+    for ln in prog:
+        m = re.fullmatch(r"v_xor_b32 (v\d+), (\d+), " + G.KADDR, ln.strip())
+        if m:
+            xor[m.group(1)] = int(m.group(2))
+    reads = [re.fullmatch(r"ds_read_b128 v\[\d+:\d+\], (v\d+) offset:(\d+)", ln.strip()) for ln in prog]
+    reads = [(m.group(1), int(m.group(2))) for m in reads if m and m.group(1) in xor]
+    nds = head_dim // 16
+    frags = reads[:2 * nds]            # S(0) in the prologue: (ds, kt) in issue order
+    bad = []
+    for i, (reg, off) in enumerate(frags):
+        ds, kt = i // 2, i % 2
+        for lane in range(64):
+            a = (klane(lane) ^ xor[reg]) + off
+            want = (32 * kt + (lane & 31), 2 * ds + (lane >> 5))
+            if lds.get(a) != want:
+                bad.append((ds, kt, lane, lds.get(a), want))
+        # a ds_read_b128 conflict window: lanes l .. l+7 with l+16 .. l+23 (measured:
+        # the GEMM's A layout, c ^ (r & 7) over 16 rows, has no conflicts; this K layout
+        # with c ^ (r & 7) over 32 rows had 32% of LDS-active cycles in conflicts)
+        for base in (0, 8, 32, 40):
+            lanes = list(range(base, base + 8)) + list(range(base + 16, base + 24))
+            pos = [((klane(l) ^ xor[reg]) + off) % 256 // 16 for l in lanes]
+            if len(set(pos)) != len(pos):
+                bad.append(("conflict", ds, kt, base))
+    return bad
+
+
+def kswz(r):
+    return ((r >> 1) & 3) | ((r >> 2) & 4)
+
+
+def klane_hpp(lane):
+    l32, g = lane & 31, lane >> 5
+    return 128 * l32 + 16 * (g ^ kswz(l32))
+
+
+@pytest.mark.parametrize("head_dim", [128, 64])
+def test_k_stage_layout(head_dim):
+    krow = lambda w, lane: (16 * (w & 3) if head_dim == 128 else 8 * w) + (lane >> 3)
+    kcol = lambda w, lane: (128 * (w >> 2) if head_dim == 128 else 0) + 16 * ((lane & 7) ^ kswz(krow(w, lane)))
+    assert k_layout(head_dim, klane_hpp, krow, kcol, PROGS[head_dim]) == []
+
+
+def test_k_stage_layout_check_finds_a_planted_mistake():
+    """The unswizzled chunk order on the DMA side: reads land on the wrong chunks."""
+    krow = lambda w, lane: 16 * (w & 3) + (lane >> 3)
+    kcol = lambda w, lane: 128 * (w >> 2) + 16 * (lane & 7)
+    assert k_layout(128, klane_hpp, krow, kcol, PROGS[128])
+
+
+def test_k_stage_conflict_check_finds_the_rows_16_apart():
+    """Swizzle r & 7: the reads find the right data but rows r and r + 16 share banks in
+    one conflict window."""
+    krow = lambda w, lane: 16 * (w & 3) + (lane >> 3)
+    kcol = lambda w, lane: 128 * (w >> 2) + 16 * ((lane & 7) ^ (krow(w, lane) & 7))
+    klane = lambda lane: 128 * (lane & 31) + 16 * ((lane >> 5) ^ (lane & 7))
+    bad = k_layout(128, klane, krow, kcol, PROGS[128])
+    assert bad and all(b[0] == "conflict" for b in bad)

@@ -9,8 +9,12 @@ as a flash-attention online softmax in base 2 with lazy rescaling.
 Workgroup = 8 waves = 256 query rows of one (batch, head); wave w owns rows
 [32w, 32w+32) and runs two per SIMD.  KV advances 64 positions at a time through
 a ring of NS LDS stages filled by global_load_lds_dwordx4 (no register staging):
-  K stage [4 row groups][16 chunks][16 rows] x 16 B, so the 32 rows x 16 B that
-           one MFMA A operand needs sit at one lane address plus an immediate;
+  K stage [2 halves][64 rows][8 chunks] x 16 B (head_dim 64: one half), chunk c of
+           row r at c ^ f(r), f(r) = bits 1-2 and 4 of r (prefill_asm.hpp): one DMA
+           instruction writes 8 rows x 128 bytes, so every K fetch is a whole cache
+           line (4 us faster at config 4 than 16 rows x 64 bytes, same bits); a
+           fragment read is one of four lane bases (XOR 32 q, q = ds & 3) plus an
+           immediate, without bank conflicts (another 2-5 us);
   V stage [64 kv][128 d] row-major with chunk c of row r at c ^ 4(r & 3), read as
            V^T with ds_read_b64_tr_b16.
 Per wave and period j (S = scores of 64 kv x 32 queries, as S^T accumulators):
@@ -39,14 +43,15 @@ waits, barrier and DMA issue, so every wave passes the same barriers (tests/test
 control flow of this program for every wave and checks it).
 
 Register map (VGPRs only; the asm statement clobbers v16-v255, s48-s95):
-  v16 v17 v18 DMA offsets, v19 v20 temps, v[24:27] v[28:31] per-step score maxima
+  v16 v17 v18 DMA offsets, v19 v20 temps, v21-v23 K fragment bases 1-3,
+  v[24:27] v[28:31] per-step score maxima
   (by block parity),
   v[32:63] S (even blocks), v[64:95] S (odd blocks), v[96:111] P,
   v[112:143] fragment ring (8 x 4), v[144:207] O^T (4 d-tiles x 16),
   v[208:239] Q^T fragments (8 x 4),
   v240-247 m l lim mblk mnew alpha ls0 ls1, v248 v249 temps, v250 -inf,
   v251 K address, v252-255 V^T addresses.
-SGPRs: s[48:51] K bases (+0,+64), s[56:57] V base, s58 j, s59 nb-1 (jl and jd are
+SGPRs: s[48:49] K base, s[56:57] V base, s58 j, s59 nb-1 (jl and jd are
   operands), s60 stage of
   block j+1, s61 stage of block j, s62 s63 DMA stage and kv0 of an even period,
   s53 s54 those of the odd period after it, s64 s68 temps,
@@ -81,6 +86,9 @@ O_BASE = 144
 Q_BASE = 208
 STB = 240
 X0, X1, NINF, KADDR = "v248", "v249", "v250", "v251"
+# K fragment bases: lane base XOR 32 q for q = ds & 3 (chunk 2 ds + g is stored at
+# (2 ds + g) ^ f(row), so ds & 3 enters as an XOR of chunk bits 1-2)
+KADDRS = [KADDR, "v21", "v22", "v23"]
 # Raw score maxima of the block's four 16-position PV steps (this lane's 8 scores of
 # each), by block parity: the residual split is decided, and run, per step.
 STEPMAX = [24, 28]
@@ -139,7 +147,7 @@ class Gen:
             q0 = Q_BASE + 4 * ds
             src_c = "0" if ds == 0 else vr(d0, d0 + 15)
             out.append(dict(
-                reads=lambda R, kt=kt, ds=ds: [f"ds_read_b128 {vr(R, R + 3)}, {KADDR} offset:{2 * self.KRG * kt + 512 * ds}"],
+                reads=lambda R, kt=kt, ds=ds: [f"ds_read_b128 {vr(R, R + 3)}, {KADDRS[ds & 3]} offset:{8192 * (ds >> 2) + 4096 * kt}"],
                 mfma=lambda R, d0=d0, q0=q0, src_c=src_c:
                     f"{self.mn} {vr(d0, d0 + 15)}, {vr(R, R + 3)}, {vr(q0, q0 + 3)}, {src_c}",
                 pdep=None))
@@ -371,8 +379,12 @@ class Gen:
         # there is one, is that wait state)
         w0 = ex0 or ["s_nop 0"]
         for j in range(self.NLDK):
+            if j:
+                # K unit j holds 8 more rows at the same columns (the swizzle follows r & 7)
+                groups.append([f"v_add3_u32 {DK}, {kv}, {o('krow')}, {8 * j}", f"v_min_u32 {DK}, {o('kvlast')}, {DK}",
+                               f"v_lshl_add_u32 {DK}, {DK}, {self.SHIFT}, {o('kcol')}"])
             groups.append([f"s_add_u32 m0, s64, {1024 * j}"] + w0 +
-                          [f"global_load_lds_dwordx4 {DK}, s[{48 + 2 * j}:{49 + 2 * j}]"] + ex1)
+                          [f"global_load_lds_dwordx4 {DK}, s[48:49]"] + ex1)
         for j in range(self.NLDK):
             groups.append([f"v_add3_u32 {DV[j]}, {kv}, {o('vrow')}, {4 * j}", f"v_min_u32 {DV[j]}, {o('kvlast')}, {DV[j]}",
                            f"v_lshl_add_u32 {DV[j]}, {DV[j]}, {self.SHIFT}, {o('vcol')}"])
@@ -385,7 +397,10 @@ class Gen:
                 f"s_cselect_b32 {sreg}, {o('lds')}, {sreg}"]
 
     def addr_k(self, sreg):
-        return [f"v_add_u32 {KADDR}, {sreg}, {o('klane')}"]
+        out = [f"v_add_u32 {KADDR}, {sreg}, {o('klane')}"]
+        for q in range(1, 4):
+            out.append(f"v_xor_b32 {KADDRS[q]}, {32 * q}, {KADDR}")
+        return out
 
     def addr_v(self, sreg):
         out = ["s_add_u32 s68, " + sreg + f", {self.KB}", f"v_add_u32 v{VADDR[0]}, s68, {o('vlane')}"]
@@ -496,8 +511,7 @@ class Gen:
             q0 = Q_BASE + 4 * ds
             out.append(f"global_load_dwordx4 {vr(q0, q0 + 3)}, {o('qp')}, off offset:{32 * ds}")
         out += [f"v_mov_b32 {st('m')}, {NINF}", f"v_mov_b32 {st('l')}, 0", f"v_mov_b32 {st('lim')}, {o('lim')}"]
-        out += ["s_mov_b64 s[48:49], " + o("kbase"), "s_mov_b64 s[56:57], " + o("vbase"),
-                "s_add_u32 s50, s48, 64", "s_addc_u32 s51, s49, 0"]
+        out += ["s_mov_b64 s[48:49], " + o("kbase"), "s_mov_b64 s[56:57], " + o("vbase")]
         out += [f"s_add_u32 s65, {o('lds')}, {NS * self.SS}"]
         out += [f"s_mov_b32 s62, {o('lds')}", "s_mov_b32 s63, 0"]
         for s in range(NS):

@@ -28,7 +28,8 @@ __host__ __device__ constexpr int part_rec(int hd) { return hd + 4; }
 
 // HD: head dim, 128 or 64.  Both use the same 160 KB LDS allocation (a kernel that
 // instantiates both keeps one); at 64 the 5-stage ring fills half of it.  K stage
-// [4 row groups][HD/8 chunks][16 rows] x 16 B; V stage row-major with 16-byte chunk c
+// [HD/128 halves][64 rows][8 chunks] x 16 B, chunk c of row r at c ^ kswz(r) (below; HD
+// 64: one half); V stage row-major with 16-byte chunk c
 // of row r at c ^ 4(r & 3) (HD 128) or c ^ 4((r >> 1) & 1) (HD 64): the four rows a
 // transposed read touches then fall in distinct banks.
 template <int DT, bool PART = false, int HD = D>
@@ -87,20 +88,27 @@ __device__ __forceinline__ void prefill_tile(const uint16_t* __restrict__ Q,
 
   // LDS read offsets: K fragment rows (l32) and chunk g; V^T transposed reads
   auto vswz = [](uint32_t r) { return HD == 128 ? 4 * (r & 3) : 4 * ((r >> 1) & 1); };
-  const uint32_t klane = 16u * (16u * (HD / 8) * (l32 >> 4) + 16u * g + (l32 & 15));
+  // K fragment (32 rows x 16 B): lane reads row l32, chunk 2 ds + g (the program XORs
+  // 32 (ds & 3) and adds the row block and half as immediates).  The chunk swizzle
+  // kswz(r) takes rows 1-2 and 4: a ds_read_b128 conflict window pairs lanes l .. l+7
+  // with l+16 .. l+23 (rows r and r + 16), which then fall in distinct banks (with
+  // r & 7 instead: 32% of LDS-active cycles in bank conflicts, measured).
+  auto kswz = [](uint32_t r) { return ((r >> 1) & 3u) | ((r >> 2) & 4u); };
+  const uint32_t klane = 128u * l32 + 16u * (static_cast<uint32_t>(g) ^ kswz(l32));
   uint32_t vlane;
   {
     const uint32_t d = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
     const uint32_t kv = 4 * ((lane >> 4) >> 1) + ((lane & 15) >> 2);
     vlane = kv * RB + (((d >> 3) ^ vswz(kv)) << 4) + (d & 7) * 2;
   }
-  // DMA in 1 KB units (HD/64 of K and as many of V per wave and block).  HD 128: K unit
-  // bi = 2 wave + j holds rows 16(bi/4) + lane%16, chunk 4(bi%4) + lane/16; V unit bi
-  // holds row 4 bi + lane/16, chunk lane%16 ^ swizzle.  HD 64: K unit wave holds rows
-  // 16(wave/2) + lane%16, chunk 4(wave%2) + lane/16; V unit wave holds row
-  // 8 wave + lane/8, chunk lane%8 ^ swizzle.
-  const uint32_t krow = 16 * (wave >> 1) + (lane & 15);
-  const uint32_t kcol = (HD == 128 ? 128 : 64) * (wave & 1) + 16 * (lane >> 4);
+  // DMA in 1 KB units (HD/64 of K and as many of V per wave and block).  K unit u
+  // holds half u / 8, rows 8 (u % 8) + lane / 8, chunk (lane % 8) ^ kswz(row) of the
+  // half (whole 128-byte lines; unit j = 1 is 8 rows on, same kswz); HD 128: units
+  // 2 wave + j, HD 64: unit wave.  V unit bi
+  // holds row 4 bi + lane/16, chunk lane%16 ^ swizzle (HD 128), or row 8 wave + lane/8,
+  // chunk lane%8 ^ swizzle (HD 64).
+  const uint32_t krow = (HD == 128 ? 16 * (wave & 3) : 8 * wave) + (lane >> 3);
+  const uint32_t kcol = (HD == 128 ? 128 * (wave >> 2) : 0) + 16 * ((lane & 7) ^ kswz(krow));
   const uint32_t vrow = HD == 128 ? 8 * wave + (lane >> 4) : 8 * wave + (lane >> 3);
   const uint32_t vcol = HD == 128 ? 16 * ((lane & 15) ^ vswz(vrow)) : 16 * ((lane & 7) ^ vswz(vrow));
   const uint32_t wave2k = (HD == 128 ? 2048 : 1024) * wave;
